@@ -1,0 +1,174 @@
+#!/usr/bin/env python3
+"""Slot-scan fwd+bwd throughput on one MI355X (BASELINE metric, config 2).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config3]
+
+One step = one hard-address slot scan forward (kv_scan_c) plus its backward (torch.autograd.grad of the two
+snapshot outputs against fixed upstream gradients) over one synthetic batch already resident in HBM:
+B=64, T=1024 (65,536 tokens), H=6 heads, N=192 slots, DK=DV=128, G=8, temp=16, per-token fr, occ_bin,
+hard, detached address (the reference's training setting, run_sh25.sh:213, 222-224).  k, q, v are bf16
+N(0,1) with k and q L2-normalised, gate = sigmoid(N(0,1.5)) bf16, fr ~ U[0,2) bf16, upstream gradients
+N(0,1) drawn in bf16 and passed as fp32 -- all drawn on the GPU from a seeded generator (seed 1).
+
+Prints ONE JSON line.  `value` is tokens/s over the K timed steps; `roofline` is the dominant kernel's
+algorithmic HBM bytes per launch over its average launch time, measured with HIP events recorded inside the
+library on the launch stream during the timed region; `step_roofline` applies the same formula to the
+whole step's algorithmic bytes; `cpu_baseline` is the repository's CPU oracle (numpy, fp32, one thread)
+timed on a bounded B-slice of the same workload on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "smal-memory-llm_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E, published
+
+WORKLOADS = {
+    "config2": dict(B=64, T=1024, H=6, N=192, D=128, G=8),
+    "config3": dict(B=64, T=1024, H=6, N=96, D=128, G=8),
+}
+
+
+def algorithmic_bytes(B, T, H, N, D, G):
+    """Per-kernel and per-step algorithmic HBM bytes (inputs read once, outputs written once; logs, Dn and
+    staging are implementation choices and are not counted).  Token tensors bf16, snapshots fp32, gate and
+    fr bf16 as the caller holds them (the kernels read the fp32 copies the wrapper makes: 4 B each)."""
+    tok = B * T * H
+    NB = (T + G - 1) // G
+    snap = B * NB * H * N * D * 4
+    row = tok * D * 2
+    per_kernel = {
+        "chain_fwd": 2 * row + 2 * tok * 4 + snap,          # q, k, gate, fr in; kbuf out
+        "rows_fwd": row + tok * 4 + snap,                   # v, gate in; vbuf out
+        "rows_bwd": 2 * snap + 2 * row + tok * 4 + 2 * row,  # dkbuf, dvbuf, k, v, gate in; dk, dv out
+        "chain_bwd": row + 2 * tok * 4 + row + 2 * tok * 4,  # q, gate, fr in; dq, dgate, dfr out
+    }
+    step = (3 * row + 2 * tok * 2 + 2 * snap) + (2 * snap + 3 * row + 2 * tok * 2 + 3 * row + 2 * tok * 2)
+    return per_kernel, step
+
+
+def cpu_baseline(W, seed=1, Bs=3):
+    """The fp32 numpy oracle (oracle/scan_oracle.py), fwd+bwd on a B-slice of the same workload."""
+    import numpy as np
+    from oracle import scan_oracle as SO
+    T, H, N, D, G = W["T"], W["H"], W["N"], W["D"], W["G"]
+    rng = np.random.default_rng(seed)
+    f = np.float32
+    unit = lambda x: (x / np.linalg.norm(x, axis=-1, keepdims=True)).astype(f)
+    k = unit(rng.standard_normal((Bs, T, H, D)).astype(f))
+    q = unit(rng.standard_normal((Bs, T, H, D)).astype(f))
+    v = rng.standard_normal((Bs, T, H, D)).astype(f)
+    g = (1 / (1 + np.exp(-1.5 * rng.standard_normal((Bs, T, H))))).astype(f)
+    fr = rng.uniform(0, 2, (Bs, T, H)).astype(f)
+    NB = (T + G - 1) // G
+    dkb = rng.standard_normal((Bs, NB, H, N, D)).astype(f)
+    dvb = rng.standard_normal((Bs, NB, H, N, D)).astype(f)
+    t0 = time.perf_counter()
+    kb, vb, info = SO.scan_forward(k, v, g, fr, N, 16.0, G=G, hard=True, q=q, occ_bin=True, dtype=f)
+    SO.scan_backward(k, v, g, fr, N, 16.0, kb, vb, info, dkb, dvb, G=G, hard=True, q=q, occ_bin=True,
+                     detach_addr=True, dtype=f)
+    dt = time.perf_counter() - t0
+    return dict(value=round(Bs * T / dt, 1), unit="tokens/s", cores=1, kind="port",
+                sample=f"B={Bs} slice of the workload (T={T}, H={H}, N={N}, D={D}, G={G}), fp32 numpy oracle "
+                       f"fwd+bwd, {dt:.1f} s", seconds=round(dt, 2))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="config2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the scan has no cross-GPU exchange and this build runs on "
+              "single-GPU boxes (every (batch, head) chain is independent; see the sharding note in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import slotkern_hip as KH
+    import slotscan_lib as L
+
+    W = WORKLOADS[args.workload]
+    B, T, H, N, D, G = (W[x] for x in ("B", "T", "H", "N", "D", "G"))
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(1)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=gen)
+    unit = lambda x: x / x.norm(dim=-1, keepdim=True)
+    k = unit(rn(B, T, H, D)).to(torch.bfloat16).requires_grad_()
+    q = unit(rn(B, T, H, D)).to(torch.bfloat16).requires_grad_()
+    v = rn(B, T, H, D).to(torch.bfloat16).requires_grad_()
+    gate = torch.sigmoid(rn(B, T, H) * 1.5).to(torch.bfloat16).requires_grad_()
+    fr = (torch.rand(B, T, H, device=dev, generator=gen) * 2).to(torch.bfloat16).requires_grad_()
+    temp = torch.tensor(16.0, device=dev, requires_grad=True)
+    NB = (T + G - 1) // G
+    dkb = rn(B, NB, H, N, D).to(torch.bfloat16).float()
+    dvb = rn(B, NB, H, N, D).to(torch.bfloat16).float()
+    inputs = (k, q, v, gate, fr, temp)
+
+    def step():
+        kb, vb = KH.kv_scan_c(k, v, gate, fr, N, temp, G=G, hard=True, hard_gate=False, detach_addr=True, q=q,
+                              occ_bin=True)
+        return torch.autograd.grad((kb, vb), inputs, (dkb, dvb))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    L.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    L.profile(False)
+    prof = L.profile_read()
+    ms = (t1 - t0) * 1e3 / args.steps
+    tokens = B * T
+    per_kernel_bytes, step_bytes = algorithmic_bytes(B, T, H, N, D, G)
+    kern_ms = {name: tot / cnt for name, (tot, cnt) in prof.items()}
+    dom = max((n for n in kern_ms if n in per_kernel_bytes), key=lambda n: kern_ms[n])
+    ach = per_kernel_bytes[dom] / (kern_ms[dom] * 1e-3) / 1e9
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"{dom}_{args.workload}_traffic.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+    out = {
+        "metric": "slot-scan fwd+bwd tokens/s at B64 T1024 H6 S192 d128; % HBM/MFMA roofline",
+        "value": round(tokens / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 state, bf16 tokens",
+        "data": "synthetic (seeded GPU generator, seed 1)",
+        "config": {"workload": args.workload, "B": B, "T": T, "H": H, "N": N, "D": D, "G": G, "temp": 16.0,
+                   "mode": "hard, detach_addr, occ_bin, per-token fr", "tokens_per_step": tokens},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": per_kernel_bytes[dom],
+                     "avg_launch_ms": round(kern_ms[dom], 4)},
+        "step_roofline": {"algorithmic_bytes": step_bytes,
+                          "achieved": round(step_bytes / (ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBPS,
+                          "unit": "GB/s", "frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
+        "kernels_ms": {n: round(x, 4) for n, x in kern_ms.items()},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(W)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

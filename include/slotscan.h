@@ -1,0 +1,104 @@
+/* C-ABI of the MI355X (gfx950) slot-scan library, libslotscan.so.
+ *
+ * The reference reaches its scan kernels through torch.cuda._compile_kernel launches made by the autograd
+ * function _KVScanC (/root/reference/gqa25/slotkern_cuda.py:482-533).  This library exports one entry point
+ * per direction instead of per kernel: slotscan_fwd replaces the addr_fwd + val_fwd launch pair
+ * (slotkern_cuda.py:505-509), slotscan_bwd replaces rows_bwd + addr_bwd (slotkern_cuda.py:525-532) and adds a
+ * fixed-order reduction for dtemp and the scalar dfr (the reference uses atomicAdd, slotkern_cuda.py:437-442).
+ *
+ * Conventions
+ *   - Every pointer is a device pointer, allocated by the caller (torch's caching allocator in the Python
+ *     binding).  The library allocates nothing, synchronises nothing, and launches on `stream`
+ *     (a hipStream_t; NULL = the legacy default stream).
+ *   - Token tensors k, q, v are (B, T, H, D) contiguous, all of `dtype` (SLOTSCAN_F32 or SLOTSCAN_BF16);
+ *     gate is (B, T, H) fp32; fr is (B, T, H) fp32 when fr_per_token, else one fp32; temp is one fp32.
+ *   - Snapshots kbuf, vbuf are (B, ceil(T/G), H, N, D) fp32: the PRE-write state at t = 0, G, 2G, ...
+ *     (slotkern_kvg.py:258-259).  Final state kfin, vfin (B*H, N, D) and ofin (B*H, N) fp32.
+ *   - Undo log: am (B, T, H) int32 = the written row; kold, vold (B, T, H, D) fp32 and oold (B, T, H) fp32 =
+ *     that row's key, value and occupancy BEFORE the write (the reference's saved tensors,
+ *     slotkern_cuda.py:502-504, 510).
+ *   - Return value: 0 on success, else one of the SLOTSCAN_ERR_* codes; slotscan_last_error() then holds a
+ *     message (per calling thread).
+ *   - Semantics: hard address, detached address gradient (slotkern_cuda.py:536-543); hard_gate is applied by
+ *     the caller by passing the binarised gate (slotkern_cuda.py:490).
+ */
+#ifndef SLOTSCAN_H
+#define SLOTSCAN_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SLOTSCAN_F32 0
+#define SLOTSCAN_BF16 1
+
+#define SLOTSCAN_MAX_SLOTS 192
+
+#define SLOTSCAN_ERR_SHAPE 1
+#define SLOTSCAN_ERR_DTYPE 2
+#define SLOTSCAN_ERR_NULL 3
+#define SLOTSCAN_ERR_ALIGN 4
+#define SLOTSCAN_ERR_HIP 5
+
+/* Message of the last failing call on this thread. */
+const char* slotscan_last_error(void);
+
+/* Largest slot count N the kernels are built for. */
+int slotscan_max_slots(int64_t D);
+
+/* Forward scan.  Replaces _KVScanC.forward's two launches (slotkern_cuda.py:484-512).
+ *   k0, v0, o0   optional carried state (B*H, N, D) / (B*H, N); NULL = the all-zero, all-free start
+ *                (the reference always starts from zero, slotkern_cuda.py:83-87, 190-192)
+ *   kold, vold, oold  the undo log; all NULL for a forward that will not be differentiated
+ *   am, kfin, vfin, ofin  always written (am drives the value replay; the final state is the carry out). */
+int slotscan_fwd(const void* k, const void* q, const void* v, int dtype,
+                 const float* gate, const float* fr, int fr_per_token, const float* temp,
+                 int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                 float eps, int occ_bin,
+                 const float* k0, const float* v0, const float* o0,
+                 float* kbuf, float* vbuf, int32_t* am,
+                 float* kold, float* vold, float* oold,
+                 float* kfin, float* vfin, float* ofin, void* stream);
+
+/* Bytes of device workspace slotscan_bwd needs: the row adjoint Dn (B*H, N, T) fp32 plus (B*H, 2) fp32
+ * per-chain partials.  The reference allocates Dn inside _KVScanC.backward (slotkern_cuda.py:524). */
+size_t slotscan_bwd_workspace(int64_t B, int64_t T, int64_t H, int64_t N);
+
+/* Backward scan.  Replaces _KVScanC.backward's launches (slotkern_cuda.py:514-533).
+ *   dkbuf, dvbuf  upstream gradients of kbuf, vbuf (fp32, same layout; pass zeros for a missing one)
+ *   workspace     >= slotscan_bwd_workspace(...) bytes, 256-byte aligned
+ *   dk, dq, dv    (B, T, H, D) in `dtype`: the store-path key gradient, the search-query gradient and the
+ *                 value gradient (when the caller's q IS k, it adds dk and dq, slotkern_cuda.py:543)
+ *   dgate         (B, T, H) fp32;  dfr  (B, T, H) fp32 if fr_per_token else one fp32;  dtemp  one fp32. */
+int slotscan_bwd(const void* k, const void* q, const void* v, int dtype,
+                 const float* gate, const float* fr, int fr_per_token, const float* temp,
+                 int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                 float eps, int occ_bin,
+                 const int32_t* am, const float* kold, const float* vold, const float* oold,
+                 const float* kfin, const float* vfin, const float* ofin,
+                 const float* dkbuf, const float* dvbuf, void* workspace,
+                 void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
+                 void* stream);
+
+/* Per-kernel timing (the reference's kvu/prof_cuda.py:9-20 wraps each compiled kernel's launch in CUDA
+ * events; this is the same facility inside the library).  While enabled, every kernel launch is bracketed
+ * by two hipEvents recorded on its stream.  slotscan_profile_read waits for the recorded events, writes
+ * the summed milliseconds and launch counts per kernel id (SLOTSCAN_K_*) into total_ms[nk] / count[nk],
+ * and clears the records.  Returns 0, or SLOTSCAN_ERR_HIP if an event query failed. */
+#define SLOTSCAN_K_CHAIN_FWD 0
+#define SLOTSCAN_K_ROWS_FWD 1
+#define SLOTSCAN_K_ROWS_BWD 2
+#define SLOTSCAN_K_CHAIN_BWD 3
+#define SLOTSCAN_K_REDUCE 4
+#define SLOTSCAN_K_READ_FWD 5
+#define SLOTSCAN_K_READ_BWD 6
+#define SLOTSCAN_NK 8
+int slotscan_profile(int enable);
+int slotscan_profile_read(double* total_ms, int64_t* count, int nk);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SLOTSCAN_H */

@@ -1,0 +1,185 @@
+"""Key-matched slot scan on MI355X: the reference's slotkern_* entry points, backed by libslotscan.so.
+
+Drop-in surface (same names, arguments, layouts and autograd contract as the reference):
+    kv_scan_c(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False,
+              q=None, nw=None, nwb=None, occ_bin=False) -> (kbuf, vbuf)       gqa25/slotkern_cuda.py:536-543
+    kv_scan_g(...same...)                                                     gqa25/slotkern_kvg.py:257-265
+    scan_kv(k, v, gate, fr, N, temp, G=1, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None)
+                                                                              gqa25/slotkern_kv.py:29-41
+    kv_scan(k, v, gate, fr, N, temp, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
+            occ_bin=False)                                                    gqa25/slotkern_kvt.py:298-302
+plus kv_scan_stream(...) -- forward only, with a carried (K, V, o) state in and out, for chunked streaming.
+
+Layouts: k, q (B,T,H,DK); v (B,T,H,DV); gate (B,T,H); fr one value or (B,T,H) (per-token when fr.dim()==3,
+slotkern_cuda.py:491); temp a float or 0-d tensor.  Returns fp32 kbuf (B,ceil(T/G),H,N,DK) and vbuf
+(B,ceil(T/G),H,N,DV): the PRE-write state at t = 0, G, 2G, ... (slotkern_kvg.py:258-259).
+
+Autograd: gradients for k, v, gate, fr, temp and q.  When q is None, k is passed as both the stored key and
+the search query and autograd adds the two paths (slotkern_cuda.py:543).  hard_gate is straight-through:
+the forward uses [gate > 0.5] and dgate flows to gate unchanged (slotkern_cuda.py:490, 533).  dfr has fr's
+shape; dtemp is 0-d.  A missing upstream gradient is zeros (slotkern_cuda.py:521-522).  The op computes in
+fp32; bf16 token inputs are read as bf16 and their gradients written as bf16 (autograd would cast them to
+the input dtype anyway); other dtypes are cast to fp32 first.
+
+Supported mode: hard=True with detach_addr=True, DK == DV in {64, 128}, N <= 192 -- the model's training
+setting (run_sh25.sh:213, 222-223) and exactly the mode the reference's CUDA kernels cover
+(slotkern_cuda.py:540).  Other modes raise NotImplementedError: there is no Triton or CPU fallback here.
+"""
+import torch
+
+import slotscan_lib as L
+
+_SUPPORTED_D = (64, 128)
+
+
+def _unsupported(hard, detach_addr, DK, DV, N):
+    if not hard:
+        return "the soft write address (hard=False) is not implemented by the HIP scan"
+    if not detach_addr:
+        return "an attached address gradient (detach_addr=False) is not implemented by the HIP scan"
+    if DK != DV or DK not in _SUPPORTED_D:
+        return f"the HIP scan needs DK == DV in {_SUPPORTED_D} (got DK={DK}, DV={DV})"
+    if N > L.lib().slotscan_max_slots(DK):
+        return f"the HIP scan supports at most {L.lib().slotscan_max_slots(DK)} slots (got N={N})"
+    return None
+
+
+def _prep(k, q, v, gate, fr, temp, hard_gate):
+    if not (k.is_cuda and q.is_cuda and v.is_cuda):
+        raise RuntimeError("the HIP slot scan runs on GPU tensors only (no CPU path in this package)")
+    dt = k.dtype if (k.dtype in (torch.float32, torch.bfloat16) and q.dtype == k.dtype and v.dtype == k.dtype) \
+        else torch.float32
+    k_, q_, v_ = (x.contiguous().to(dt) for x in (k, q, v))
+    g = (gate > 0.5).to(torch.float32).contiguous() if hard_gate else gate.contiguous().to(torch.float32)
+    frt = fr.dim() == 3
+    if frt:
+        if fr.shape != gate.shape:
+            raise ValueError(f"per-token fr must be shaped like the gate: {tuple(fr.shape)} vs {tuple(gate.shape)}")
+        fr_ = fr.contiguous().to(torch.float32)
+    else:
+        fr_ = fr.to(torch.float32).reshape(1).contiguous()
+    temp_ = torch.as_tensor(temp, dtype=torch.float32, device=k.device).reshape(1).contiguous()
+    return dt, k_, q_, v_, g, fr_, frt, temp_
+
+
+def _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, state=None):
+    B, T, H, D = k_.shape
+    NB = (T + G - 1) // G
+    dev = k_.device
+    f32 = torch.float32
+    e = lambda *s, dtype=f32: torch.empty(*s, device=dev, dtype=dtype)
+    kbuf, vbuf = e(B, NB, H, N, D), e(B, NB, H, N, D)
+    am = e(B, T, H, dtype=torch.int32)
+    kold = vold = oold = None
+    if logs:
+        kold, vold, oold = e(B, T, H, D), e(B, T, H, D), e(B, T, H)
+    kfin, vfin, ofin = e(B * H, N, D), e(B * H, N, D), e(B * H, N)
+    k0 = v0 = o0 = None
+    if state is not None:
+        k0, v0, o0 = (x.contiguous().to(f32) for x in state)
+        if k0.shape != (B * H, N, D) or v0.shape != (B * H, N, D) or o0.shape != (B * H, N):
+            raise ValueError("state must be (K (B*H,N,D), V (B*H,N,D), o (B*H,N))")
+    rc = L.lib().slotscan_fwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
+                              int(frt), L.ptr(temp_), B, T, H, N, D, G, float(eps), int(bool(occ_bin)),
+                              L.ptr(k0), L.ptr(v0), L.ptr(o0), L.ptr(kbuf), L.ptr(vbuf), L.ptr(am),
+                              L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(kfin), L.ptr(vfin), L.ptr(ofin),
+                              L.stream_of(dev))
+    L.check(rc, "slotscan_fwd")
+    return kbuf, vbuf, am, kold, vold, oold, kfin, vfin, ofin
+
+
+class _KVScanHip(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, k, q, v, gate, fr, temp, N, G, hard_gate, eps, occ_bin):
+        D = k.shape[-1]
+        if v.shape[-1] != D:
+            raise ValueError("the HIP scan needs DK == DV")
+        dt, k_, q_, v_, g, fr_, frt, temp_ = _prep(k, q, v, gate, fr, temp, hard_gate)
+        logs = any(ctx.needs_input_grad[:6])
+        kbuf, vbuf, am, kold, vold, oold, kfin, vfin, ofin = _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps,
+                                                                  occ_bin, dt, logs)
+        if logs:
+            ctx.save_for_backward(k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, kfin, vfin, ofin)
+        ctx.meta = (int(N), int(G), frt, float(eps), bool(occ_bin), dt, tuple(fr.shape), torch.is_tensor(temp))
+        return kbuf, vbuf
+
+    @staticmethod
+    def backward(ctx, dkbuf, dvbuf):
+        k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, kfin, vfin, ofin = ctx.saved_tensors
+        N, G, frt, eps, occ_bin, dt, fr_shape, temp_is_tensor = ctx.meta
+        B, T, H, D = k_.shape
+        NB = (T + G - 1) // G
+        dev = k_.device
+        f32 = torch.float32
+        z = lambda: torch.zeros(B, NB, H, N, D, device=dev, dtype=f32)
+        dkbuf = z() if dkbuf is None else dkbuf.contiguous().to(f32)
+        dvbuf = z() if dvbuf is None else dvbuf.contiguous().to(f32)
+        ws = torch.empty(L.lib().slotscan_bwd_workspace(B, T, H, N), device=dev, dtype=torch.uint8)
+        dk, dq, dv = torch.empty_like(k_), torch.empty_like(q_), torch.empty_like(v_)
+        dg = torch.empty(B, T, H, device=dev, dtype=f32)
+        dfr = torch.empty_like(fr_)
+        dtemp = torch.empty(1, device=dev, dtype=f32)
+        rc = L.lib().slotscan_bwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
+                                  int(frt), L.ptr(temp_), B, T, H, N, D, G, float(eps), int(occ_bin),
+                                  L.ptr(am), L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(kfin), L.ptr(vfin),
+                                  L.ptr(ofin), L.ptr(dkbuf), L.ptr(dvbuf), L.ptr(ws),
+                                  L.ptr(dk), L.ptr(dq), L.ptr(dv), L.ptr(dg), L.ptr(dfr), L.ptr(dtemp),
+                                  L.stream_of(dev))
+        L.check(rc, "slotscan_bwd")
+        dfr = dfr.reshape(fr_shape) if not frt else dfr
+        dtemp = dtemp.reshape(()) if temp_is_tensor else None
+        return dk, dq, dv, dg, dfr, dtemp, None, None, None, None, None
+
+
+def kv_scan_c(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
+              nw=None, nwb=None, occ_bin=False):
+    """Hard + detached-address slot scan on gfx950 (the mode slotkern_cuda.kv_scan_c runs on its own kernels,
+    slotkern_cuda.py:536-543).  nw / nwb (the reference's warp counts) are accepted and ignored: the launch
+    shape here is fixed by the gfx950 design, not tuned per call."""
+    why = _unsupported(hard, detach_addr, k.shape[-1], v.shape[-1], N)
+    if why:
+        raise NotImplementedError(why)
+    return _KVScanHip.apply(k, k if q is None else q, v, gate, fr, temp, N, int(G), bool(hard_gate), eps,
+                            bool(occ_bin))
+
+
+def kv_scan_g(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
+              nw=None, nwb=None, occ_bin=False):
+    """Same contract as the reference's stride-G scan (slotkern_kvg.py:257-265), on the gfx950 kernels."""
+    return kv_scan_c(k, v, gate, fr, N, temp, G=G, hard=hard, hard_gate=hard_gate, eps=eps,
+                     detach_addr=detach_addr, q=q, occ_bin=occ_bin)
+
+
+def scan_kv(k, v, gate, fr, N, temp, G=1, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None):
+    """slotkern_kv.scan_kv's signature (slotkern_kv.py:29-41).  Errors are raised, never swallowed."""
+    return kv_scan_c(k, v, gate, fr, N, temp, G=G, hard=hard, hard_gate=hard_gate, eps=eps,
+                     detach_addr=detach_addr, q=q)
+
+
+def kv_scan(k, v, gate, fr, N, temp, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
+            occ_bin=False):
+    """slotkern_kvt.kv_scan's signature (G = 1).  Like the reference, occ_bin is refused here
+    (slotkern_kvt.py:300-301)."""
+    if occ_bin:
+        raise NotImplementedError("occ_bin is implemented in kv_scan_g only (the G=1 entry point refuses it, "
+                                  "as the reference's does)")
+    return kv_scan_c(k, v, gate, fr, N, temp, G=1, hard=hard, hard_gate=hard_gate, eps=eps,
+                     detach_addr=detach_addr, q=q)
+
+
+@torch.no_grad()
+def kv_scan_stream(k, v, gate, fr, N, temp, G=8, hard_gate=False, eps=1e-4, q=None, occ_bin=False, state=None):
+    """Forward-only hard scan over one chunk of a long stream, with the slot state carried across calls.
+
+    state: None (all rows free) or the (K (B*H,N,D), V (B*H,N,D), o (B*H,N)) fp32 triple returned by the
+    previous chunk.  Returns (kbuf, vbuf, state_out).  Scanning a sequence chunk by chunk this way gives
+    bitwise the same snapshots as one call over the whole sequence when every chunk length is a multiple
+    of G (the reference has no carry: it restarts from zero per call, memlm_sh.py:676)."""
+    why = _unsupported(True, True, k.shape[-1], v.shape[-1], N)
+    if why:
+        raise NotImplementedError(why)
+    qq = k if q is None else q
+    dt, k_, q_, v_, g, fr_, frt, temp_ = _prep(k, qq, v, gate, fr, temp, hard_gate)
+    kbuf, vbuf, _am, _ko, _vo, _oo, kfin, vfin, ofin = _fwd(k_, q_, v_, g, fr_, frt, temp_, int(N), int(G), eps,
+                                                            occ_bin, dt, logs=False, state=state)
+    return kbuf, vbuf, (kfin, vfin, ofin)
