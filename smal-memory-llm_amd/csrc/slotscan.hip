@@ -23,35 +23,39 @@
 //              and runs its adjoint: dgate, dq, per-token dfr, and per-chain dtemp / scalar-dfr partials
 //              that a fixed-order reduction (reduce_parts) sums -- no float atomics anywhere.
 //
-// gfx950 mapping.  A chain workgroup is 256 lanes = 4 waves = 16 row groups of 16 lanes (one DPP row per
-// slot row); row n lives in row group n % 16 as register slice i = n / 16.  Row dot products reduce with 4
-// DPP stages, the argmax reduces the 4 row groups of a wave with readlane and the 4 waves through one
-// ping-pong LDS slot, so a step costs ONE workgroup barrier.  Token inputs (q, k, gate, fr, and in the
-// backward the undo log and Dn) are staged in LDS 16 steps ahead in double-buffered chunks.  Row norms are
-// kept per row and recomputed only for the written row.
+// gfx950 mapping of the chain kernels.  A chain workgroup is 192 lanes = 3 waves = 12 row groups of 16
+// lanes (one DPP row each); a row group holds P slot rows (P = 16 at N <= 192), lane c keeping elements
+// {4c..4c+3, 64+4c..} of every one of them, in the same register order in every lane (so the written
+// row's register index is wave-uniform and the update never diverges).  The per-step dot products
+// <K_n, q_t> are finished with a DPP REDUCE-SCATTER instead of a 16-lane all-reduce, after which each
+// lane holds the complete dot product of ONE row: all per-row scalar work (score, occupancy, softmax,
+// adjoint) is done once per row instead of 16 times.  Rows increase with the lane index, so the argmax
+// tie rule (lowest index) is a ballot plus a find-first-set.  The 3 waves meet in one ping-pong LDS slot: ONE workgroup barrier per step.  A barrier
+// every step makes the step time the per-SIMD sum of issued instructions, so the design minimises
+// per-wave work: the next step's dot products are computed before the barrier with the current keys and
+// only the one rewritten row is corrected afterwards; row norms use v_rsq; the key snapshots are not
+// written by the chain at all (the row replay emits them, perfectly coalesced).  Token inputs (q, k, gate,
+// fr; in the backward also the undo log and Dn) are staged in LDS as fp32 in double-buffered chunks.
 #include "slot_common.h"
 
 using namespace slot;
 typedef uint64_t u64;
 typedef uint32_t u32;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-#define SLOT_CT 16          // tokens per staged chunk in the chain kernels
-#define SLOT_BIGI 0x7fffffff
+#define SLOT_CT 16          // tokens per staged chunk
+#define CHAIN_WAVES 3
+#define CHAIN_THREADS (64 * CHAIN_WAVES)
 
-#define CHAIN_ATTR __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2)))
+#define CHAIN_ATTR __global__ __attribute__((amdgpu_flat_work_group_size(CHAIN_THREADS, CHAIN_THREADS), amdgpu_waves_per_eu(2)))
 #define ROWS_ATTR __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 
 namespace {
 
 constexpr int CT = SLOT_CT;
 
-__device__ __forceinline__ u64 umax64(u64 a, u64 b) { return a > b ? a : b; }
 __device__ __forceinline__ float readlanef(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-__device__ __forceinline__ u32 readlaneu(u32 v, int l) { return (u32)__builtin_amdgcn_readlane((int)v, l); }
-__device__ __forceinline__ u64 readlane64(u64 v, int l) {
-    return ((u64)readlaneu((u32)(v >> 32), l) << 32) | readlaneu((u32)v, l);
 }
 
 template <int EPL>
@@ -76,70 +80,148 @@ __device__ __forceinline__ void st_slice(TO* row, const float* s, int c) {
     for (int jj = 0; jj < EPL / 4; jj++)
         st4(row + 4 * c + 64 * jj, make_float4(s[4 * jj], s[4 * jj + 1], s[4 * jj + 2], s[4 * jj + 3]));
 }
+// streaming store of a row slice: vector non-temporal stores (full 16-byte pieces)
 template <int EPL>
 __device__ __forceinline__ void st_slice_nt(float* row, const float* s, int c) {
 #pragma unroll
-    for (int jj = 0; jj < EPL / 4; jj++)
-        st4_nt(row + 4 * c + 64 * jj, make_float4(s[4 * jj], s[4 * jj + 1], s[4 * jj + 2], s[4 * jj + 3]));
+    for (int jj = 0; jj < EPL / 4; jj++) {
+        f32x4 v = {s[4 * jj], s[4 * jj + 1], s[4 * jj + 2], s[4 * jj + 3]};
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(row + 4 * c + 64 * jj));
+    }
 }
 template <int EPL>
-__device__ __forceinline__ float norm_inv(const float* x) {
-    float kk = 0.f;
+__device__ __forceinline__ void ld_slice_nt(float* d, const float* row, int c) {
 #pragma unroll
-    for (int e = 0; e < EPL; e++) kk = fmaf(x[e], x[e], kk);
-    kk = rowsum16(kk);
-    return 1.f / fmaxf(sqrtf(kk), 1e-6f);
+    for (int jj = 0; jj < EPL / 4; jj++) {
+        f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + 4 * c + 64 * jj));
+        d[4 * jj + 0] = v.x; d[4 * jj + 1] = v.y; d[4 * jj + 2] = v.z; d[4 * jj + 3] = v.w;
+    }
+}
+// 4 raw token elements (fp32 or bf16 bits in a uint4 lane word group) -> fp32 into LDS
+__device__ __forceinline__ void stage_store(float* dst, uint4 raw, bool bf) {
+    if (bf) {   // 8 bf16 values
+        float4 lo = make_float4(__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                                __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u));
+        float4 hi = make_float4(__uint_as_float(raw.z << 16), __uint_as_float(raw.z & 0xffff0000u),
+                                __uint_as_float(raw.w << 16), __uint_as_float(raw.w & 0xffff0000u));
+        reinterpret_cast<float4*>(dst)[0] = lo;
+        reinterpret_cast<float4*>(dst)[1] = hi;
+    } else {
+        *reinterpret_cast<uint4*>(dst) = raw;
+    }
 }
 
-// online-softmax merge of (max, sum e^(z-max), sum e^(z-max) w)
-__device__ __forceinline__ void smerge(float& M, float& S, float& SD, float m2, float s2, float sd2) {
-    if (m2 == -INFINITY) return;
-    if (M == -INFINITY) { M = m2; S = s2; SD = sd2; return; }
-    const float m = fmaxf(M, m2);
-    const float a1 = expf(M - m), a2 = expf(m2 - m);
-    S = S * a1 + s2 * a2;
-    SD = SD * a1 + sd2 * a2;
-    M = m;
+// ------------------------------------------------------------------ DPP reduce-scatter over a row group
+// Every lane holds partial sums x[0..P) of the same P slot rows of its row group.  Four stages pair lanes
+// with row_mirror (lane^15), row_half_mirror (lane^7), lane^2 and lane^1; the first log2(P) stages SPLIT
+// (a lane keeps the half of the remaining slots picked by lane bit 3, 2, 1, 0 and receives its partner's
+// partial of that half), the rest add.  Afterwards lane c holds the full 16-lane sum of slot c >> (4 -
+// log2 P): each lane owns one row, so all per-row scalar work runs once per row.
+template <int P> struct RS {
+    static constexpr int SH = P == 16 ? 0 : P == 8 ? 1 : P == 4 ? 2 : P == 2 ? 3 : 4;
+};
+template <int CTRL> __device__ __forceinline__ void rs_stage(float* x, int V, bool hi) {
+    const int half = V / 2;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (j < half) {
+            const float snd = hi ? x[j] : x[j + half];
+            const float kp = hi ? x[j + half] : x[j];
+            x[j] = kp + dppf<CTRL>(snd);
+        }
+    }
+}
+template <int P> __device__ __forceinline__ float rs_reduce(float* x, int c) {
+    // stage 0: row_mirror / lane bit 3
+    if constexpr (P >= 2) rs_stage<SLOT_DPP_MIR>(x, P, c & 8); else x[0] += dppf<SLOT_DPP_MIR>(x[0]);
+    // stage 1: row_half_mirror / lane bit 2
+    if constexpr (P >= 4) rs_stage<SLOT_DPP_HMIR>(x, P / 2, c & 4); else x[0] += dppf<SLOT_DPP_HMIR>(x[0]);
+    // stage 2: lane^2 / lane bit 1
+    if constexpr (P >= 8) rs_stage<SLOT_DPP_XOR2>(x, P / 4, c & 2); else x[0] += dppf<SLOT_DPP_XOR2>(x[0]);
+    // stage 3: lane^1 / lane bit 0
+    if constexpr (P >= 16) rs_stage<SLOT_DPP_XOR1>(x, P / 8, c & 1); else x[0] += dppf<SLOT_DPP_XOR1>(x[0]);
+    return x[0];
+}
+
+// 1 / max(sqrt(x), 1e-6) as one v_rsq_f32 (sqrt(x) < 1e-6 exactly when x < 1e-12)
+__device__ __forceinline__ float rsq_clamped(float x) { return __builtin_amdgcn_rsqf(fmaxf(x, 1e-12f)); }
+
+// one hard write of a row slice: x <- (1 - g) x + g v, as ONE explicit fma so that the chain, the row
+// replay and any other kernel that re-applies the log produce bitwise the same state
+__device__ __forceinline__ float blend(float x, float v, float g, float omw) { return fmaf(g, v, omw * x); }
+
+__device__ __forceinline__ float wavemax(float v) {
+    v = rowmax16(v);
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Row layout of a chain workgroup.  Lane `lane` of wave `w`: row group r = lane >> 4, c = lane & 15;
+// register slot j holds row rowbase + j (the same order in every lane); after a reduce-scatter the lane
+// owns row rowbase + (c >> SH).  Rows therefore increase with the lane index, and the lowest lane of each
+// row (the "primary" lane, c % 2^SH == 0) is the one a ballot's find-first-set returns.
+template <int P> struct ChainRows {
+    int rowbase, n_me;
+    bool prim;
+    __device__ __forceinline__ ChainRows(int tid) {
+        const int w = tid >> 6, lane = tid & 63, r = lane >> 4, c = lane & 15;
+        rowbase = (w * 4 + r) * P;
+        n_me = rowbase + (c >> RS<P>::SH);
+        prim = (c & ((1 << RS<P>::SH) - 1)) == 0;
+    }
+    __device__ __forceinline__ int row(int j) const { return rowbase + j; }
+};
+template <int P> __device__ __forceinline__ int row_of_lane(int wave, int lane) {
+    return (wave * 4 + (lane >> 4)) * P + ((lane & 15) >> RS<P>::SH);
 }
 
 // =========================================================================================== chain_fwd
 struct ChainFwdArgs {
     const void* q; const void* k; const float* gate; const float* fr; const float* temp;
     const float* k0; const float* o0;
-    float* kbuf; int32_t* am; float* kold; float* oold; float* kfin; float* ofin;
-    int T, H, N, G, NB; float eps; int frt, occb;
+    int32_t* am; float* kold; float* oold; float* kfin; float* ofin;
+    int T, H, N; float eps; int frt, occb;
 };
 
-template <int D, int RPT, typename TI>
+template <int D, int P, typename TI>
 CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
-    constexpr int CT = (sizeof(TI) == 4 && RPT >= 12) ? 8 : SLOT_CT;   // fewer staging registers at N > 128
     constexpr int EPL = D / 16;
-    constexpr int RU = D * (int)sizeof(TI) / 16;      // uint4 per token row
-    constexpr int NU = CT * 2 * RU;                    // uint4 per staged chunk: (q row, k row) per token
-    constexpr int UPT = (NU + 255) / 256;
-    __shared__ __align__(16) TI s_tok[2][CT][2][D];
+    constexpr int EPU = 16 / (int)sizeof(TI);          // token elements per uint4
+    constexpr int RU = D / EPU;                         // uint4 per token row
+    constexpr int NU = CT * 2 * RU;                     // uint4 per staged chunk: (q row, k row) per token
+    constexpr int UPT = (NU + CHAIN_THREADS - 1) / CHAIN_THREADS;
+    constexpr bool BF = sizeof(TI) == 2;
+    __shared__ __align__(16) float s_tok[2][CT][2][D];
     __shared__ float s_g[2][CT], s_fr[2][CT];
-    __shared__ uint4 s_red[2][4];
+    __shared__ uint4 s_red[2][CHAIN_WAVES];
 
-    const int T = a.T, H = a.H, N = a.N, G = a.G;
+    const int T = a.T, H = a.H, N = a.N;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
-    const int tid = threadIdx.x, rg = tid >> 4, c = tid & 15, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = tid & 15;
+    const ChainRows<P> R(tid);
     const TI* __restrict__ qp = (const TI*)a.q;
     const TI* __restrict__ kp = (const TI*)a.k;
-    const size_t tok0 = (size_t)b * T * H + h;         // token (b, t, h) = tok0 + t * H
+    const size_t tok0 = (size_t)b * T * H + h;          // token (b, t, h) = tok0 + t * H
 
-    float K[RPT][EPL], o[RPT], kinv[RPT];
+    float K[P][EPL];
+    float o_me = 0.f, kinv_me;
+    {
+        float x[P];
 #pragma unroll
-    for (int i = 0; i < RPT; i++) {
-        const int n = rg + 16 * i;
-        o[i] = 0.f;
+        for (int j = 0; j < P; j++) {
+            const int n = R.row(j);
 #pragma unroll
-        for (int e = 0; e < EPL; e++) K[i][e] = 0.f;
-        if (n < N) {
-            if (a.k0) ld_slice<EPL>(K[i], a.k0 + ((size_t)bh * N + n) * D, c);
-            if (a.o0) o[i] = a.o0[(size_t)bh * N + n];
+            for (int e = 0; e < EPL; e++) K[j][e] = 0.f;
+            if (a.k0 && n < N) ld_slice<EPL>(K[j], a.k0 + ((size_t)bh * N + n) * D, c);
+            float kk = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) kk = fmaf(K[j][e], K[j][e], kk);
+            x[j] = kk;
         }
-        kinv[i] = norm_inv<EPL>(K[i]);
+        kinv_me = rsq_clamped(rs_reduce<P>(x, c));
+        if (a.o0 && R.n_me < N) o_me = a.o0[(size_t)bh * N + R.n_me];
     }
 
     uint4 rq[UPT];
@@ -147,7 +229,7 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
     auto load_chunk = [&](int ch) {
 #pragma unroll
         for (int m = 0; m < UPT; m++) {
-            const int u = tid + 256 * m;
+            const int u = tid + CHAIN_THREADS * m;
             rq[m] = make_uint4(0u, 0u, 0u, 0u);
             if (u < NU) {
                 const int j = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
@@ -162,127 +244,158 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
         }
     };
     auto store_chunk = [&](int buf) {
-        uint4* dst = reinterpret_cast<uint4*>(&s_tok[buf][0][0][0]);
 #pragma unroll
         for (int m = 0; m < UPT; m++) {
-            const int u = tid + 256 * m;
-            if (u < NU) dst[u] = rq[m];
+            const int u = tid + CHAIN_THREADS * m;
+            if (u < NU) {
+                const int j = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
+                stage_store(&s_tok[buf][j][arr][w * EPU], rq[m], BF);
+            }
         }
         if (tid < CT) s_g[buf][tid] = rs;
         else if (tid < 2 * CT) s_fr[buf][tid - CT] = rs;
+    };
+    // this lane's row dotted with a query slice, completed by the reduce-scatter
+    auto dot_me = [&](const float* qv) -> float {
+        float x[P];
+#pragma unroll
+        for (int jr = 0; jr < P; jr++) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) d = fmaf(K[jr][e], qv[e], d);
+            x[jr] = d;
+        }
+        return rs_reduce<P>(x, c);
+    };
+    auto qinv_of = [&](const float* qv) -> float {
+        float qq = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) qq = fmaf(qv[e], qv[e], qq);
+        return rsq_clamped(rowsum16(qq));
     };
 
     const float temp = a.temp[0];
     const float fr_s = a.frt ? 0.f : a.fr[0];
     const float eps = a.eps;
     const bool occb = a.occb != 0, frt = a.frt != 0;
+    const bool valid_me = R.n_me < N;
 
     load_chunk(0);
     store_chunk(0);
     __syncthreads();
     load_chunk(1);
+    float qv[EPL];
+    ld_slice<EPL>(qv, &s_tok[0][0][0][0], c);
+    float qinv = qinv_of(qv);
+    float dme = dot_me(qv);                             // <K_me, q_t> for the current keys
     int par = 0, j = 0, buf = 0;
     for (int t = 0; t < T; t++) {
-        if (t % G == 0) {                                   // the PRE-write key state of block t / G
-            float* kb = a.kbuf + ((size_t)(b * a.NB + t / G) * H + h) * N * D;
-#pragma unroll
-            for (int i = 0; i < RPT; i++) {
-                const int n = rg + 16 * i;
-                if (n < N) st_slice_nt<EPL>(kb + (size_t)n * D, K[i], c);
-            }
-        }
-        float qv[EPL];
-        ld_slice<EPL>(qv, &s_tok[buf][j][0][0], c);
-        float qq = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; e++) qq = fmaf(qv[e], qv[e], qq);
-        qq = rowsum16(qq);
-        const float qinv = 1.f / fmaxf(sqrtf(qq), 1e-6f);
         const float g = s_g[buf][j];
         const float frv = frt ? s_fr[buf][j] : fr_s;
-
-        // per-row score and this thread's candidates: best occupied (z, -n) and lowest free n (with its z)
-        u64 bo = 0, bfr = 0;
-#pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int n = rg + 16 * i;
-            float d = 0.f;
-#pragma unroll
-            for (int e = 0; e < EPL; e++) d = fmaf(K[i][e], qv[e], d);
-            d = rowsum16(d);
-            const float s = temp * ((d * kinv[i]) * qinv);
-            const bool taken = o[i] >= eps;
-            const float occ = occb ? (taken ? 1.f : 0.f) : o[i];
-            const float z = s - frv * occ;
-            if (n < N) {
-                if (taken) bo = umax64(bo, ((u64)fkey(z) << 32) | (u32)(~n));
-                else bfr = umax64(bfr, ((u64)(u32)(~n) << 32) | fkey(z));
+        const float s = temp * ((dme * kinv_me) * qinv);
+        const bool taken = o_me >= eps;
+        const float occ = occb ? (taken ? 1.f : 0.f) : o_me;
+        const float z = s - frv * occ;
+        {   // this wave's candidates: best occupied (z, lowest row) and lowest free row; mo and mf are
+            // wave-uniform, so the readlane runs outside divergent code
+            const float zo = (valid_me && taken) ? z : -INFINITY;
+            const float wm = wavemax(zo);
+            const u64 mo = __ballot(valid_me && taken && zo == wm);
+            const u64 mf = __ballot(valid_me && !taken);
+            int bo = -1, fo = -1;
+            float fz = 0.f;
+            if (mo) bo = row_of_lane<P>(wave, __builtin_ctzll(mo));
+            if (mf) {
+                const int lf = __builtin_ctzll(mf);
+                fo = row_of_lane<P>(wave, lf);
+                fz = readlanef(z, lf);
             }
+            if (lane == 0) s_red[par][wave] = make_uint4(__float_as_uint(wm), (u32)bo, (u32)fo, __float_as_uint(fz));
         }
-        {   // the 4 row groups of this wave sit at lanes 0, 16, 32, 48
-            u64 wo = 0, wf = 0;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                wo = umax64(wo, readlane64(bo, 16 * r));
-                wf = umax64(wf, readlane64(bfr, 16 * r));
-            }
-            if (lane == 0) s_red[par][wave] = make_uint4((u32)(wo >> 32), (u32)wo, (u32)(wf >> 32), (u32)wf);
+        // next step's query, its norm and its dot products with the CURRENT keys; after the write below
+        // only the rewritten row's dot is recomputed
+        float qinv_n = 0.f, dnext = 0.f;
+        if (t + 1 < T) {
+            const int jn = j + 1 == CT ? 0 : j + 1, bn = j + 1 == CT ? (buf ^ 1) : buf;
+            ld_slice<EPL>(qv, &s_tok[bn][jn][0][0], c);
+            qinv_n = qinv_of(qv);
+            dnext = dot_me(qv);
         }
-        if (j == CT - 1) {                                  // refill: chunk t/CT+1 -> LDS, fetch t/CT+2
+        if (j == CT - 2) {                                  // refill: chunk t/CT+1 -> LDS, fetch t/CT+2
             store_chunk(buf ^ 1);
             load_chunk(t / CT + 2);
         }
         __syncthreads();
-        u64 BO = 0, BF = 0;
+        uint4 r[CHAIN_WAVES];
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const uint4 x = s_red[par][w];
-            BO = umax64(BO, ((u64)x.x << 32) | x.y);
-            BF = umax64(BF, ((u64)x.z << 32) | x.w);
+        for (int w = 0; w < CHAIN_WAVES; w++) r[w] = s_red[par][w];
+        // waves in order = rows in order: strict '>' keeps the lowest row on ties
+        float bz = -INFINITY, fz = 0.f;
+        int bo = -1, fo = -1;
+#pragma unroll
+        for (int w = 0; w < CHAIN_WAVES; w++) {
+            const float z2 = __uint_as_float(r[w].x);
+            const int o2 = (int)r[w].y, f2 = (int)r[w].z;
+            const bool tk = o2 >= 0 && (bo < 0 || z2 > bz);
+            bz = tk ? z2 : bz;
+            bo = tk ? o2 : bo;
+            const bool tf = f2 >= 0 && fo < 0;
+            fo = tf ? f2 : fo;
+            fz = tf ? __uint_as_float(r[w].w) : fz;
         }
         par ^= 1;
-        // the lowest free row competes as (its z, -its index)
-        const u64 fc = BF ? (((u64)(u32)BF << 32) | (BF >> 32)) : 0;
-        const int amv = (int)(~(u32)umax64(BO, fc));
+        const int amv = __builtin_amdgcn_readfirstlane((fo >= 0 && (bo < 0 || fz > bz || (fz == bz && fo < bo))) ? fo : bo);
         const size_t ix = tok0 + (size_t)t * H;
         if (tid == 0) a.am[ix] = amv;
-        const float omw = 1.f - g;
+        if (amv >= R.rowbase && amv < R.rowbase + P) {      // this row group holds the written row
+            const int sl = amv & (P - 1);                   // its register slot: the same in every lane
+            const float omw = 1.f - g;
+            float kv[EPL];
+            ld_slice<EPL>(kv, &s_tok[buf][j][1][0], c);
+            float part = 0.f, pd = 0.f;
 #pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int n = rg + 16 * i;
-            if (n == amv) {
-                if (a.kold) {
-                    st_slice<EPL>(a.kold + ix * D, K[i], c);
-                    if (c == 0) a.oold[ix] = o[i];
+            for (int jr = 0; jr < P; jr++) {
+                if (jr == sl) {
+                    if (a.kold) st_slice<EPL>(a.kold + ix * D, K[jr], c);
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) {
+                        K[jr][e] = blend(K[jr][e], kv[e], g, omw);
+                        part = fmaf(K[jr][e], K[jr][e], part);
+                        pd = fmaf(K[jr][e], qv[e], pd);
+                    }
                 }
-                float kv[EPL];
-                ld_slice<EPL>(kv, &s_tok[buf][j][1][0], c);
-#pragma unroll
-                for (int e = 0; e < EPL; e++) K[i][e] = omw * K[i][e] + g * kv[e];
-                o[i] = omw * o[i] + g;
-                kinv[i] = norm_inv<EPL>(K[i]);
+            }
+            const float kk = rowsum16(part);
+            const float kd = rowsum16(pd);
+            if (R.n_me == amv) {
+                if (a.oold && R.prim) a.oold[ix] = o_me;
+                o_me = omw * o_me + g;
+                kinv_me = rsq_clamped(kk);
+                dnext = kd;
             }
         }
+        dme = dnext;
+        qinv = qinv_n;
         if (++j == CT) { j = 0; buf ^= 1; }
     }
 #pragma unroll
-    for (int i = 0; i < RPT; i++) {
-        const int n = rg + 16 * i;
-        if (n < N) {
-            st_slice<EPL>(a.kfin + ((size_t)bh * N + n) * D, K[i], c);
-            if (c == 0) a.ofin[(size_t)bh * N + n] = o[i];
-        }
+    for (int jr = 0; jr < P; jr++) {
+        const int n = R.row(jr);
+        if (n < N) st_slice<EPL>(a.kfin + ((size_t)bh * N + n) * D, K[jr], c);
     }
+    if (valid_me && R.prim) a.ofin[(size_t)bh * N + R.n_me] = o_me;
 }
 
 // =========================================================================================== rows_fwd
 struct RowsFwdArgs {
-    const void* v; const float* gate; const int32_t* am; const float* v0;
-    float* vbuf; float* vold; float* vfin;
+    const void* k; const void* v; const float* gate; const int32_t* am; const float* k0; const float* v0;
+    float* kbuf; float* vbuf; float* vold; float* vfin;
     int T, H, N, G, NB;
 };
 
-// 512 lanes = 32 rows of one chain per workgroup; grid (B*H, ceil(N/32)).
+// 512 lanes = 32 rows of one chain per workgroup; grid (B*H, ceil(N/32)).  Replays every row's key and
+// value from the address log (the same blend as the chain, so the keys match its state bitwise) and emits
+// both snapshots with full-row non-temporal stores.
 template <int D, typename TI>
 ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     constexpr int EPL = D / 16;
@@ -294,14 +407,19 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     const int tid = threadIdx.x, rg = tid >> 4, c = tid & 15;
     const int n = blockIdx.y * 32 + rg;
     const bool live = n < N;
+    const TI* __restrict__ kp = (const TI*)a.k;
     const TI* __restrict__ vp = (const TI*)a.v;
     const size_t tok0 = (size_t)b * T * H + h;
-    float V[EPL];
+    float K[EPL], V[EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; e++) V[e] = 0.f;
+    for (int e = 0; e < EPL; e++) { K[e] = 0.f; V[e] = 0.f; }
+    if (live && a.k0) ld_slice<EPL>(K, a.k0 + ((size_t)bh * N + n) * D, c);
     if (live && a.v0) ld_slice<EPL>(V, a.v0 + ((size_t)bh * N + n) * D, c);
-    float* vb0 = a.vbuf + ((size_t)b * a.NB * H + h) * N * D + (size_t)n * D;
-    const size_t vbstride = (size_t)H * N * D;
+    const size_t roff = ((size_t)b * a.NB * H + h) * N * D + (size_t)(live ? n : 0) * D;
+    float* kb = a.kbuf + roff;
+    float* vb = a.vbuf + roff;
+    const size_t sstride = (size_t)H * N * D;
+    int gc = 0;
     for (int t0 = 0; t0 < T; t0 += TC) {
         const int tn = min(TC, T - t0);
         __syncthreads();
@@ -313,16 +431,22 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
         __syncthreads();
         if (!live) continue;
         for (int jt = 0; jt < tn; jt++) {
-            const int t = t0 + jt;
-            if (t % G == 0) st_slice_nt<EPL>(vb0 + (size_t)(t / G) * vbstride, V, c);
+            if (gc == 0) {
+                st_slice_nt<EPL>(kb, K, c);
+                st_slice_nt<EPL>(vb, V, c);
+                kb += sstride;
+                vb += sstride;
+            }
+            if (++gc == G) gc = 0;
             if (s_am[jt] == n) {
-                const size_t ix = tok0 + (size_t)t * H;
+                const size_t ix = tok0 + (size_t)(t0 + jt) * H;
                 const float g = s_g[jt], omw = 1.f - g;
-                float vv[EPL];
+                float kk[EPL], vv[EPL];
+                ld_slice<EPL>(kk, kp + ix * D, c);
                 ld_slice<EPL>(vv, vp + ix * D, c);
                 if (a.vold) st_slice<EPL>(a.vold + ix * D, V, c);
 #pragma unroll
-                for (int e = 0; e < EPL; e++) V[e] = omw * V[e] + g * vv[e];
+                for (int e = 0; e < EPL; e++) { K[e] = blend(K[e], kk[e], g, omw); V[e] = blend(V[e], vv[e], g, omw); }
             }
         }
     }
@@ -338,18 +462,26 @@ struct RowsBwdArgs {
     int T, H, N, G, NB;
 };
 
-// 512 lanes = 32 rows per workgroup, grid (B*H, ceil(N/32)); reverse in t.  The chain's k_t, v_t are
-// staged through LDS in chunks of CT tokens, double buffered one chunk ahead.  Dn is written (B*H, N, T):
-// lane c of a row group keeps Dn for t with t % 16 == c and the group stores 16 consecutive t at once.
+// 512 lanes = 32 rows per workgroup, grid (B*H, ceil(N/32)); reverse in t, in 16-step chunks aligned to
+// t % 16 == 0, one workgroup barrier per chunk.  k_t, v_t are staged through LDS (fp32) one chunk ahead.
+// Per step a lane forms <k_t, dK> + <v_t, dV> - (<K, dK> + <V, dV>) over its 8 elements (the bracket is
+// kept up to date at the rare events that change it: a write to this row, a block boundary) and parks it
+// in an LDS tile; at the end of the chunk lane c sums the 16 lanes' partials of step 16m + c and stores
+// Dn (B*H, N, T), 64 contiguous bytes per row.  The upstream snapshot gradient is prefetched two blocks
+// ahead.  The step loop is not unrolled, which keeps the rare write/boundary paths from multiplying
+// register copies.
 template <int D, typename TI>
 ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
     constexpr int EPL = D / 16;
-    constexpr int RU = D * (int)sizeof(TI) / 16;
-    constexpr int NU = CT * 2 * RU;
+    constexpr int EPU = 16 / (int)sizeof(TI);
+    constexpr int RU = D / EPU;
+    constexpr int NU = 16 * 2 * RU;
     constexpr int UPT = (NU + 511) / 512;
-    __shared__ __align__(16) TI s_tok[2][CT][2][D];
-    __shared__ int s_am[2][CT];
-    __shared__ float s_g[2][CT];
+    constexpr bool BF = sizeof(TI) == 2;
+    __shared__ __align__(16) float s_tok[2][16][2][D];
+    __shared__ int s_am[2][16];
+    __shared__ float s_g[2][16];
+    __shared__ __align__(16) float s_part[32][16][17];   // [row group][step][lane], padded
 
     const int T = a.T, H = a.H, N = a.N, G = a.G;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
@@ -364,100 +496,127 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
     const size_t tok0 = (size_t)b * T * H + h;
 
     uint4 rq[UPT];
-    int ram = 0;
+    int ram = -1;
     float rgt = 0.f;
-    auto load_chunk = [&](int ch) {
+    auto load_chunk = [&](int m) {                      // chunk m: t in [16m, 16m + 16)
 #pragma unroll
-        for (int m = 0; m < UPT; m++) {
-            const int u = tid + 512 * m;
-            rq[m] = make_uint4(0u, 0u, 0u, 0u);
-            if (u < NU) {
-                const int j = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
-                const int t = T - 1 - (ch * CT + j);
-                if (t >= 0) rq[m] = reinterpret_cast<const uint4*>((arr ? vp : kp) + (tok0 + (size_t)t * H) * D)[w];
+        for (int u2 = 0; u2 < UPT; u2++) {
+            const int u = tid + 512 * u2;
+            rq[u2] = make_uint4(0u, 0u, 0u, 0u);
+            if (u < NU && m >= 0) {
+                const int i = u / (2 * RU), arr = (u / RU) & 1, w = u % RU, t = 16 * m + i;
+                if (t < T) rq[u2] = reinterpret_cast<const uint4*>((arr ? vp : kp) + (tok0 + (size_t)t * H) * D)[w];
             }
         }
-        if (tid < CT) {
-            const int t = T - 1 - (ch * CT + tid);
+        if (tid < 16) {
+            const int t = 16 * m + tid;
             ram = -1; rgt = 0.f;
-            if (t >= 0) { ram = a.am[tok0 + (size_t)t * H]; rgt = a.gate[tok0 + (size_t)t * H]; }
+            if (m >= 0 && t < T) { ram = a.am[tok0 + (size_t)t * H]; rgt = a.gate[tok0 + (size_t)t * H]; }
         }
     };
     auto store_chunk = [&](int buf) {
-        uint4* dst = reinterpret_cast<uint4*>(&s_tok[buf][0][0][0]);
 #pragma unroll
-        for (int m = 0; m < UPT; m++) {
-            const int u = tid + 512 * m;
-            if (u < NU) dst[u] = rq[m];
+        for (int u2 = 0; u2 < UPT; u2++) {
+            const int u = tid + 512 * u2;
+            if (u < NU) {
+                const int i = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
+                stage_store(&s_tok[buf][i][arr][w * EPU], rq[u2], BF);
+            }
         }
-        if (tid < CT) { s_am[buf][tid] = ram; s_g[buf][tid] = rgt; }
+        if (tid < 16) { s_am[buf][tid] = ram; s_g[buf][tid] = rgt; }
     };
 
-    float K[EPL], V[EPL], dK[EPL], dV[EPL], pk[EPL], pv[EPL];
+    float K[EPL], V[EPL], dK[EPL], dV[EPL], pk1[EPL], pv1[EPL], pk2[EPL], pv2[EPL];
     ld_slice<EPL>(K, a.kfin + ((size_t)bh * N + n) * D, c);
     ld_slice<EPL>(V, a.vfin + ((size_t)bh * N + n) * D, c);
 #pragma unroll
-    for (int e = 0; e < EPL; e++) { dK[e] = 0.f; dV[e] = 0.f; }
+    for (int e = 0; e < EPL; e++) { dK[e] = 0.f; dV[e] = 0.f; pk2[e] = 0.f; pv2[e] = 0.f; }
+    float cp = 0.f;                                      // this lane's share of <K, dK> + <V, dV>
     const size_t sbstride = (size_t)H * N * D;
     const float* dkb0 = a.dkbuf + ((size_t)b * a.NB * H + h) * N * D + (size_t)n * D;
     const float* dvb0 = a.dvbuf + ((size_t)b * a.NB * H + h) * N * D + (size_t)n * D;
-    {   // prefetch the gradient of the last emitted block
-        const int blk = (T - 1) / G;
-        ld_slice<EPL>(pk, dkb0 + (size_t)blk * sbstride, c);
-        ld_slice<EPL>(pv, dvb0 + (size_t)blk * sbstride, c);
+    int nxt = (T - 1) / G;                               // next block whose gradient enters (reverse order)
+    ld_slice_nt<EPL>(pk1, dkb0 + (size_t)nxt * sbstride, c);
+    ld_slice_nt<EPL>(pv1, dvb0 + (size_t)nxt * sbstride, c);
+    if (nxt >= 1) {
+        ld_slice_nt<EPL>(pk2, dkb0 + (size_t)(nxt - 1) * sbstride, c);
+        ld_slice_nt<EPL>(pv2, dvb0 + (size_t)(nxt - 1) * sbstride, c);
     }
-    float dnk = 0.f;
-    load_chunk(0);
+    int tb = nxt * G;                                    // the step at which block `nxt` enters
+    const int nblk = (T + 15) / 16;
+    load_chunk(nblk - 1);
     store_chunk(0);
     __syncthreads();
-    load_chunk(1);
-    int j = 0, buf = 0;
-    for (int s = 0; s < T; s++) {
-        const int t = T - 1 - s;
-        float kt[EPL], vt[EPL];
-        ld_slice<EPL>(kt, &s_tok[buf][j][0][0], c);
-        ld_slice<EPL>(vt, &s_tok[buf][j][1][0], c);
-        const bool hit = live && (s_am[buf][j] == n);
-        const float g = s_g[buf][j];
-        const size_t ix = tok0 + (size_t)t * H;
-        if (hit) {                                          // undo: the row before this step's write
-            ld_slice<EPL>(K, a.kold + ix * D, c);
-            ld_slice<EPL>(V, a.vold + ix * D, c);
-        }
-        float p = 0.f;
+    load_chunk(nblk - 2);
+    int buf = 0;
+    for (int m = nblk - 1; m >= 0; m--) {
+        const int i_hi = min(15, T - 1 - 16 * m);
+        for (int i = 15; i > i_hi; i--) s_part[rg][i][c] = 0.f;
+        for (int i = i_hi; i >= 0; i--) {
+            const int t = 16 * m + i;
+            const bool hit = live && (s_am[buf][i] == n);
+            if (hit) {                                      // undo: the row before this step's write
+                const size_t ix = tok0 + (size_t)t * H;
+                ld_slice<EPL>(K, a.kold + ix * D, c);
+                ld_slice<EPL>(V, a.vold + ix * D, c);
+                cp = 0.f;
 #pragma unroll
-        for (int e = 0; e < EPL; e++) p = fmaf(kt[e] - K[e], dK[e], p);
+                for (int e = 0; e < EPL; e++) cp = fmaf(K[e], dK[e], fmaf(V[e], dV[e], cp));
+            }
+            float p = -cp;
+            const float* kt = &s_tok[buf][i][0][0];
+            const float* vt = &s_tok[buf][i][1][0];
 #pragma unroll
-        for (int e = 0; e < EPL; e++) p = fmaf(vt[e] - V[e], dV[e], p);
-        p = rowsum16(p);
-        if ((t & 15) == c) dnk = p;
-        if ((t & 15) == 0 && live) {
-            const int tt = t + c;
-            if (tt < T) a.dn[((size_t)bh * N + n) * T + tt] = dnk;
-        }
-        if (hit) {
-            const float omw = 1.f - g;
-            float x[EPL], y[EPL];
+            for (int jj = 0; jj < EPL / 4; jj++) {
+                const float4 k4 = *reinterpret_cast<const float4*>(kt + 4 * c + 64 * jj);
+                const float4 v4 = *reinterpret_cast<const float4*>(vt + 4 * c + 64 * jj);
+                p = fmaf(k4.x, dK[4 * jj + 0], p); p = fmaf(k4.y, dK[4 * jj + 1], p);
+                p = fmaf(k4.z, dK[4 * jj + 2], p); p = fmaf(k4.w, dK[4 * jj + 3], p);
+                p = fmaf(v4.x, dV[4 * jj + 0], p); p = fmaf(v4.y, dV[4 * jj + 1], p);
+                p = fmaf(v4.z, dV[4 * jj + 2], p); p = fmaf(v4.w, dV[4 * jj + 3], p);
+            }
+            s_part[rg][i][c] = p;
+            if (hit) {
+                const size_t ix = tok0 + (size_t)t * H;
+                const float g = s_g[buf][i], omw = 1.f - g;
+                float x[EPL], y[EPL];
 #pragma unroll
-            for (int e = 0; e < EPL; e++) { x[e] = g * dK[e]; y[e] = g * dV[e]; dK[e] *= omw; dV[e] *= omw; }
-            st_slice<EPL>(dkp + ix * D, x, c);
-            st_slice<EPL>(dvp + ix * D, y, c);
-        }
-        if (t % G == 0) {                                   // the copy emitted at t is the pre-write state
+                for (int e = 0; e < EPL; e++) { x[e] = g * dK[e]; y[e] = g * dV[e]; dK[e] *= omw; dV[e] *= omw; }
+                cp *= omw;
+                st_slice<EPL>(dkp + ix * D, x, c);
+                st_slice<EPL>(dvp + ix * D, y, c);
+            }
+            if (t == tb) {                                  // the copy emitted at t is the pre-write state
 #pragma unroll
-            for (int e = 0; e < EPL; e++) { dK[e] += pk[e]; dV[e] += pv[e]; }
-            const int blk = t / G - 1;
-            if (blk >= 0) {
-                ld_slice<EPL>(pk, dkb0 + (size_t)blk * sbstride, c);
-                ld_slice<EPL>(pv, dvb0 + (size_t)blk * sbstride, c);
+                for (int e = 0; e < EPL; e++) {
+                    dK[e] += pk1[e];
+                    dV[e] += pv1[e];
+                    cp = fmaf(K[e], pk1[e], fmaf(V[e], pv1[e], cp));
+                    pk1[e] = pk2[e];
+                    pv1[e] = pv2[e];
+                }
+                nxt -= 1;
+                tb -= G;
+                if (nxt >= 1) {
+                    ld_slice_nt<EPL>(pk2, dkb0 + (size_t)(nxt - 1) * sbstride, c);
+                    ld_slice_nt<EPL>(pv2, dvb0 + (size_t)(nxt - 1) * sbstride, c);
+                }
             }
         }
-        if (j == CT - 1) {
+        // lane c sums the row group's 16 partials of step 16m + c (same wave wrote them: wave barrier only)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float dnv = 0.f;
+#pragma unroll
+        for (int l = 0; l < 16; l++) dnv += s_part[rg][c][l];
+        if (live && 16 * m + c < T) a.dn[((size_t)bh * N + n) * T + 16 * m + c] = dnv;
+        if (m > 0) {
             store_chunk(buf ^ 1);
-            load_chunk(s / CT + 2);
+            load_chunk(m - 2);
         }
         __syncthreads();
-        if (++j == CT) { j = 0; buf ^= 1; }
+        buf ^= 1;
     }
 }
 
@@ -470,55 +629,62 @@ struct ChainBwdArgs {
     int T, H, N; float eps; int frt, occb;
 };
 
-// OCCB (occ_bin) is a template flag here: with it the occupancy enters only through [o >= eps], so the
-// kernel keeps one taken-bit per row instead of o and the (identically zero) occupancy adjoint dO.
-template <int D, int RPT, typename TI, bool OCCB>
+// OCCB (occ_bin) is a template flag: with it the occupancy enters only through [o >= eps] and its
+// adjoint dO is identically zero, so the kernel carries no dO.
+template <int D, int P, typename TI, bool OCCB>
 CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
-    constexpr int CT = RPT >= 12 ? 8 : SLOT_CT;                         // fewer staging registers at N > 128
+    constexpr int CT = P >= 16 ? 4 : SLOT_CT;           // fewer staging registers at N > 96
     constexpr int EPL = D / 16;
-    constexpr int RUQ = D * (int)sizeof(TI) / 16, RUK = D / 4;
+    constexpr int EPU = 16 / (int)sizeof(TI);
+    constexpr int RUQ = D / EPU, RUK = D / 4;
     constexpr int NUQ = CT * RUQ, NU = NUQ + CT * RUK;
-    constexpr int UPT = (NU + 255) / 256;
-    constexpr int NMAX = 16 * RPT;
-    constexpr int DPT = (CT * NMAX + 255) / 256;
+    constexpr int UPT = (NU + CHAIN_THREADS - 1) / CHAIN_THREADS;
+    constexpr int NMAX = 4 * CHAIN_WAVES * P;
+    constexpr int DPT = (CT * NMAX + CHAIN_THREADS - 1) / CHAIN_THREADS;
     constexpr int EPW = D / 64;                          // q elements per lane in the dq finaliser
-    __shared__ __align__(16) TI s_q[2][CT][D];
+    constexpr bool BF = sizeof(TI) == 2;
+    __shared__ __align__(16) float s_q[2][CT][D];
     __shared__ __align__(16) float s_ko[2][CT][D];
     __shared__ float s_dn[2][CT][NMAX];
     __shared__ float s_g[2][CT], s_fr[2][CT], s_oo[2][CT];
     __shared__ int s_am[2][CT];
-    __shared__ float s_st[2][4][8];
-    __shared__ float s_pq[2][4][D];
-    __shared__ float s_pfr[2][4];
+    __shared__ __align__(16) float s_st[2][CHAIN_WAVES][8];
+    __shared__ float s_pq[2][CHAIN_WAVES][D];
+    __shared__ float s_pfr[2][CHAIN_WAVES];
     __shared__ float s_qn[2][2];
-    __shared__ float s_fin[2][4];
+    __shared__ float s_fin[2][CHAIN_WAVES];
+    __shared__ __align__(16) float s_cf[NMAX];
 
     const int T = a.T, H = a.H, N = a.N;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
-    const int tid = threadIdx.x, rg = tid >> 4, c = tid & 15, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = tid & 15;
+    const ChainRows<P> R(tid);
     const TI* __restrict__ qp = (const TI*)a.q;
     const size_t tok0 = (size_t)b * T * H + h;
     const float temp = a.temp[0];
     const float fr_s = a.frt ? 0.f : a.fr[0];
     const float eps = a.eps;
     const bool frt = a.frt != 0;
+    const bool valid_me = R.n_me < N;
 
-    float K[RPT][EPL], o[RPT], kinv[RPT], dO[RPT];
-    u32 tk = 0;                                          // OCCB: bit i = row slice i is taken (o >= eps)
+    float K[P][EPL];
+    float o_me = 0.f, dO_me = 0.f, kinv_me;
+    {
+        float x[P];
 #pragma unroll
-    for (int i = 0; i < RPT; i++) {
-        const int n = rg + 16 * i;
-        o[i] = 0.f; dO[i] = 0.f;
+        for (int j = 0; j < P; j++) {
+            const int n = R.row(j);
 #pragma unroll
-        for (int e = 0; e < EPL; e++) K[i][e] = 0.f;
-        if (n < N) {
-            ld_slice<EPL>(K[i], a.kfin + ((size_t)bh * N + n) * D, c);
-            o[i] = a.ofin[(size_t)bh * N + n];
-            if (o[i] >= eps) tk |= 1u << i;
+            for (int e = 0; e < EPL; e++) K[j][e] = 0.f;
+            if (n < N) ld_slice<EPL>(K[j], a.kfin + ((size_t)bh * N + n) * D, c);
+            float kk = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) kk = fmaf(K[j][e], K[j][e], kk);
+            x[j] = kk;
         }
-        kinv[i] = norm_inv<EPL>(K[i]);
+        kinv_me = rsq_clamped(rs_reduce<P>(x, c));
+        if (valid_me) o_me = a.ofin[(size_t)bh * N + R.n_me];
     }
-    auto taken_of = [&](int i) -> bool { if constexpr (OCCB) return (tk >> i) & 1u; else return o[i] >= eps; };
 
     uint4 rq[UPT];
     float rdn[DPT];
@@ -526,7 +692,7 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
     auto load_chunk = [&](int ch) {
 #pragma unroll
         for (int m = 0; m < UPT; m++) {
-            const int u = tid + 256 * m;
+            const int u = tid + CHAIN_THREADS * m;
             rq[m] = make_uint4(0u, 0u, 0u, 0u);
             if (u < NUQ) {
                 const int jj = u / RUQ, w = u % RUQ, t = T - 1 - (ch * CT + jj);
@@ -538,7 +704,7 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
         }
 #pragma unroll
         for (int m = 0; m < DPT; m++) {
-            const int u = tid + 256 * m;
+            const int u = tid + CHAIN_THREADS * m;
             rdn[m] = 0.f;
             if (u < CT * N) {
                 const int nn = u / CT, jj = u % CT, t = T - 1 - (ch * CT + jj);
@@ -557,17 +723,18 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
         }
     };
     auto store_chunk = [&](int buf) {
-        uint4* dq_ = reinterpret_cast<uint4*>(&s_q[buf][0][0]);
-        uint4* dk_ = reinterpret_cast<uint4*>(&s_ko[buf][0][0]);
 #pragma unroll
         for (int m = 0; m < UPT; m++) {
-            const int u = tid + 256 * m;
-            if (u < NUQ) dq_[u] = rq[m];
-            else if (u < NU) dk_[u - NUQ] = rq[m];
+            const int u = tid + CHAIN_THREADS * m;
+            if (u < NUQ) stage_store(&s_q[buf][u / RUQ][(u % RUQ) * EPU], rq[m], BF);
+            else if (u < NU) {
+                const int u2 = u - NUQ;
+                stage_store(&s_ko[buf][u2 / RUK][(u2 % RUK) * 4], rq[m], false);
+            }
         }
 #pragma unroll
         for (int m = 0; m < DPT; m++) {
-            const int u = tid + 256 * m;
+            const int u = tid + CHAIN_THREADS * m;
             if (u < CT * N) s_dn[buf][u % CT][u / CT] = rdn[m];
         }
         if (tid < 4 * CT) {
@@ -578,28 +745,52 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
             else s_oo[buf][jj] = rs;
         }
     };
+    auto dot_me = [&](const float* qv) -> float {
+        float x[P];
+#pragma unroll
+        for (int jr = 0; jr < P; jr++) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) d = fmaf(K[jr][e], qv[e], d);
+            x[jr] = d;
+        }
+        return rs_reduce<P>(x, c);
+    };
+    auto qsq_of = [&](const float* qv) -> float {
+        float qq = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) qq = fmaf(qv[e], qv[e], qq);
+        return rowsum16(qq);
+    };
     // dq (and per-token dfr) of processed step sp, by one wave, from the per-wave partials of that step
     auto finalize = [&](int sp) {
         const int pp = sp & 1, bp = (sp / CT) & 1, jp = sp % CT, tp = T - 1 - sp;
-        const float qn = s_qn[pp][0], qi = s_qn[pp][1];
+        const float qq = s_qn[pp][0], qi = s_qn[pp][1];
         float dqn[EPW], qh[EPW];
         float pr = 0.f;
 #pragma unroll
         for (int m = 0; m < EPW; m++) {
             const int e = lane + 64 * m;
-            dqn[m] = temp * ((s_pq[pp][0][e] + s_pq[pp][1][e]) + (s_pq[pp][2][e] + s_pq[pp][3][e]));
-            qh[m] = ld1<TI>(&s_q[bp][jp][e]) * qi;
+            float acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < CHAIN_WAVES; w++) acc += s_pq[pp][w][e];
+            dqn[m] = temp * acc;
+            qh[m] = s_q[bp][jp][e] * qi;
             pr = fmaf(dqn[m], qh[m], pr);
         }
         pr = wavesum(pr);
         TI* dqp = (TI*)a.dq + (tok0 + (size_t)tp * H) * D;
 #pragma unroll
         for (int m = 0; m < EPW; m++) {
-            const float r = qn < 1e-6f ? qi * dqn[m] : qi * (dqn[m] - qh[m] * pr);
+            const float r = qq < 1e-12f ? qi * dqn[m] : qi * (dqn[m] - qh[m] * pr);   // |q| < 1e-6: no projection
             st1<TI>(dqp + lane + 64 * m, r);
         }
-        if (frt && lane == 0)
-            a.dfr[tok0 + (size_t)tp * H] = (s_pfr[pp][0] + s_pfr[pp][1]) + (s_pfr[pp][2] + s_pfr[pp][3]);
+        if (frt && lane == 0) {
+            float f = 0.f;
+#pragma unroll
+            for (int w = 0; w < CHAIN_WAVES; w++) f += s_pfr[pp][w];
+            a.dfr[tok0 + (size_t)tp * H] = f;
+        }
     };
 
     float dtemp_acc = 0.f, dfr_acc = 0.f;
@@ -607,141 +798,183 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
     store_chunk(0);
     __syncthreads();
     load_chunk(1);
-    int par = 0, j = 0, buf = 0;
+    float qv[EPL];
+    ld_slice<EPL>(qv, &s_q[0][0][0], c);
+    float qq = qsq_of(qv);
+    float dme = dot_me(qv);                              // <K_me, q_t> with the keys before this step's undo
+    int par = 0, j = 0, buf = 0, fin_wave = 0;
     for (int s = 0; s < T; s++) {
         const int t = T - 1 - s;
-        const int amv = s_am[buf][j];
+        const int amv = __builtin_amdgcn_readfirstlane(s_am[buf][j]);
         const float g = s_g[buf][j];
         const float frv = frt ? s_fr[buf][j] : fr_s;
-        // undo this step's write: the written row goes back to its logged pre-write key and occupancy
+        const float omw = 1.f - g;
+        // undo this step's write: the written row goes back to its logged pre-write key and occupancy,
+        // and only that row's dot product with q_t is recomputed
+        if (amv >= R.rowbase && amv < R.rowbase + P) {
+            const int sl = amv & (P - 1);
+            float kv[EPL];
+            ld_slice<EPL>(kv, &s_ko[buf][j][0], c);
+            float part = 0.f, pd = 0.f;
 #pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int n = rg + 16 * i;
-            if (n == amv) {
-                ld_slice<EPL>(K[i], &s_ko[buf][j][0], c);
-                const float oo = s_oo[buf][j];
-                if constexpr (OCCB) tk = (tk & ~(1u << i)) | ((oo >= eps ? 1u : 0u) << i);
-                else o[i] = oo;
-                kinv[i] = norm_inv<EPL>(K[i]);
+            for (int jr = 0; jr < P; jr++) {
+                if (jr == sl) {
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) {
+                        K[jr][e] = kv[e];
+                        part = fmaf(kv[e], kv[e], part);
+                        pd = fmaf(kv[e], qv[e], pd);
+                    }
+                }
+            }
+            const float kk = rowsum16(part);
+            const float kd = rowsum16(pd);
+            if (R.n_me == amv) {
+                o_me = s_oo[buf][j];
+                kinv_me = rsq_clamped(kk);
+                dme = kd;
             }
         }
-        float qv[EPL];
-        ld_slice<EPL>(qv, &s_q[buf][j][0], c);
-        float qq = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; e++) qq = fmaf(qv[e], qv[e], qq);
-        qq = rowsum16(qq);
-        const float qnorm = sqrtf(qq), qinv = 1.f / fmaxf(qnorm, 1e-6f);
-
-        float cs[RPT], dw[RPT], ex[RPT];
-        float mloc = -INFINITY;
-        int ei = SLOT_BIGI;
-        float ez = 0.f, ed = 0.f;
-#pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int n = rg + 16 * i;
-            float d = 0.f;
-#pragma unroll
-            for (int e = 0; e < EPL; e++) d = fmaf(K[i][e], qv[e], d);
-            d = rowsum16(d);
-            cs[i] = (d * kinv[i]) * qinv;
-            const bool taken = taken_of(i);
-            float z;
-            if constexpr (OCCB) {
-                z = temp * cs[i] - (taken ? frv : 0.f);
-                dw[i] = n < N ? s_dn[buf][j][n] : 0.f;
-            } else {
-                z = temp * cs[i] - frv * o[i];
-                dw[i] = (n < N ? s_dn[buf][j][n] : 0.f) + (1.f - o[i]) * dO[i];
-            }
-            ex[i] = z;
-            if (n < N && taken) mloc = fmaxf(mloc, z);
-            if (n < N && !taken && n < ei) { ei = n; ez = z; ed = dw[i]; }
+        const float qinv = rsq_clamped(qq);
+        const float cs = (dme * kinv_me) * qinv;         // cosine of this lane's row
+        const bool taken = valid_me && o_me >= eps;
+        float z, dw;
+        if constexpr (OCCB) {
+            z = temp * cs - (taken ? frv : 0.f);
+            dw = valid_me ? s_dn[buf][j][R.n_me] : 0.f;
+        } else {
+            z = temp * cs - frv * o_me;
+            dw = (valid_me ? s_dn[buf][j][R.n_me] : 0.f) + (1.f - o_me) * dO_me;
         }
-        float S = 0.f, SD = 0.f;
-#pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int n = rg + 16 * i;
-            const bool taken = n < N && taken_of(i);
-            ex[i] = taken ? expf(ex[i] - mloc) : 0.f;
-            S += ex[i];
-            SD = fmaf(ex[i], dw[i], SD);
-        }
-        {
-            float M = -INFINITY, SS = 0.f, SSD = 0.f, EZ = 0.f, ED = 0.f;
-            int EI = SLOT_BIGI;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                smerge(M, SS, SSD, readlanef(mloc, 16 * r), readlanef(S, 16 * r), readlanef(SD, 16 * r));
-                const int e2 = __builtin_amdgcn_readlane(ei, 16 * r);
-                if (e2 < EI) { EI = e2; EZ = readlanef(ez, 16 * r); ED = readlanef(ed, 16 * r); }
+        {   // this wave's softmax partials over occupied rows (each row counted at its primary lane), and
+            // its lowest free row with that row's z and dw
+            const float zo = taken ? z : -INFINITY;
+            const float wm = wavemax(zo);
+            const float e = (taken && R.prim) ? __expf(z - wm) : 0.f;
+            const float S = wavesum(e), SD = wavesum(e * dw);
+            const u64 mf = __ballot(valid_me && !taken);
+            int fo = -1;
+            float fz = 0.f, fd = 0.f;
+            if (mf) {
+                const int lf = __builtin_ctzll(mf);
+                fo = row_of_lane<P>(wave, lf);
+                fz = readlanef(z, lf);
+                fd = readlanef(dw, lf);
             }
             if (lane == 0) {
-                s_st[par][wave][0] = M; s_st[par][wave][1] = SS; s_st[par][wave][2] = SSD;
-                s_st[par][wave][3] = __int_as_float(EI); s_st[par][wave][4] = EZ; s_st[par][wave][5] = ED;
+                *reinterpret_cast<float4*>(&s_st[par][wave][0]) = make_float4(wm, S, SD, __int_as_float(fo));
+                *reinterpret_cast<float2*>(&s_st[par][wave][4]) = make_float2(fz, fd);
             }
         }
-        if (j == CT - 1) {
+        // next step's query and its dot products with the current keys (its undo corrects one row)
+        float qqn = 0.f, dnext = 0.f;
+        float qvn[EPL];
+        if (s + 1 < T) {
+            const int jn = j + 1 == CT ? 0 : j + 1, bn = j + 1 == CT ? (buf ^ 1) : buf;
+            ld_slice<EPL>(qvn, &s_q[bn][jn][0], c);
+            qqn = qsq_of(qvn);
+            dnext = dot_me(qvn);
+        }
+        if (j == CT - 2) {
             store_chunk(buf ^ 1);
             load_chunk(s / CT + 2);
         }
         __syncthreads();
-        if (s > 0 && wave == ((s - 1) & 3)) finalize(s - 1);
-        float M = -INFINITY, SS = 0.f, SSD = 0.f, EZ = 0.f, ED = 0.f;
-        int EI = SLOT_BIGI;
+        if (s > 0 && wave == fin_wave) finalize(s - 1);
+        if (s > 0 && ++fin_wave == CHAIN_WAVES) fin_wave = 0;
+        float4 st0[CHAIN_WAVES];
+        float2 st1[CHAIN_WAVES];
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
-            smerge(M, SS, SSD, s_st[par][w][0], s_st[par][w][1], s_st[par][w][2]);
-            const int e2 = __float_as_int(s_st[par][w][3]);
-            if (e2 < EI) { EI = e2; EZ = s_st[par][w][4]; ED = s_st[par][w][5]; }
+        for (int w = 0; w < CHAIN_WAVES; w++) {
+            st0[w] = *reinterpret_cast<const float4*>(&s_st[par][w][0]);
+            st1[w] = *reinterpret_cast<const float2*>(&s_st[par][w][4]);
         }
-        if (EI != SLOT_BIGI) smerge(M, SS, SSD, EZ, 1.f, ED);   // the first free row competes too
-        const float sa = g * SSD / SS;                          // sum_n asoft_n * g * dw_n
-        const float sloc = mloc == -INFINITY ? 0.f : expf(mloc - M) / SS;
-        const float afree = EI != SLOT_BIGI ? expf(EZ - M) / SS : 0.f;   // soft address of the first free row
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < CHAIN_WAVES; w++) M = fmaxf(M, st0[w].x);
+        float FZ = 0.f, FD = 0.f;
+        int FO = -1;
+#pragma unroll
+        for (int w = 0; w < CHAIN_WAVES; w++) {
+            const int f2 = __float_as_int(st0[w].w);
+            const bool tf = f2 >= 0 && FO < 0;
+            FO = tf ? f2 : FO;
+            FZ = tf ? st1[w].x : FZ;
+            FD = tf ? st1[w].y : FD;
+        }
+        if (FO >= 0) M = fmaxf(M, FZ);                       // the first free row competes too
+        float SS = 0.f, SSD = 0.f;
+#pragma unroll
+        for (int w = 0; w < CHAIN_WAVES; w++) {
+            const float sc = st0[w].x == -INFINITY ? 0.f : __expf(st0[w].x - M);
+            SS = fmaf(st0[w].y, sc, SS);
+            SSD = fmaf(st0[w].z, sc, SSD);
+        }
+        if (FO >= 0) {
+            const float ef = __expf(FZ - M);
+            SS += ef;
+            SSD = fmaf(ef, FD, SSD);
+        }
+        const float sa = g * SSD / SS;                       // sum_n asoft_n * g * dw_n
+        const bool elig = taken || (valid_me && R.n_me == FO);
+        const float as = elig ? __expf(z - M) / SS : 0.f;
+        const float dz = as * (g * dw - sa);
+        const size_t ix = tok0 + (size_t)t * H;
+        if (R.n_me == amv && R.prim) a.dg[ix] = dw;
+        float frp = 0.f;
+        if (R.prim) {
+            dtemp_acc = fmaf(dz, cs, dtemp_acc);
+            if constexpr (OCCB) frp = taken ? -dz : 0.f;
+            else frp = -o_me * dz;
+        }
+        if constexpr (!OCCB) dO_me = (R.n_me == amv ? omw : 1.f) * dO_me - frv * dz;
+        // dqn partial: sum over this row group's rows of dz kinv K_n, then over the wave's 4 row groups.
+        // Each row's coefficient goes through LDS to the 16 lanes holding that row (same wave: a wave
+        // barrier orders the write and the reads).
+        if (R.prim) s_cf[R.n_me] = dz * kinv_me;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float cf[P];
+#pragma unroll
+        for (int jr = 0; jr < P; jr++) cf[jr] = s_cf[R.rowbase + jr];
         float pq[EPL];
 #pragma unroll
         for (int e = 0; e < EPL; e++) pq[e] = 0.f;
-        float frp = 0.f;
-        const float omw = 1.f - g;
 #pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int n = rg + 16 * i;
-            const bool taken = n < N && taken_of(i);
-            const bool first_free = n == EI;
-            const float as = taken ? ex[i] * sloc : (first_free ? afree : 0.f);
-            const float dz = (taken || first_free) ? as * (g * dw[i] - sa) : 0.f;
-            if (n == amv && c == 0) a.dg[tok0 + (size_t)t * H] = dw[i];
-            dtemp_acc = fmaf(dz, cs[i], dtemp_acc);
-            if constexpr (OCCB) frp -= taken ? dz : 0.f;
-            else frp = fmaf(-o[i], dz, frp);
-            const float cf = dz * kinv[i];
+        for (int jr = 0; jr < P; jr++) {
 #pragma unroll
-            for (int e = 0; e < EPL; e++) pq[e] = fmaf(cf, K[i][e], pq[e]);
-            if constexpr (!OCCB) dO[i] = (n == amv ? omw : 1.f) * dO[i] - frv * dz;
+            for (int e = 0; e < EPL; e++) pq[e] = fmaf(cf[jr], K[jr][e], pq[e]);
         }
 #pragma unroll
         for (int e = 0; e < EPL; e++) pq[e] = sum4rows(pq[e]);
-        frp = sum4rows(frp);
+        frp = wavesum(frp);
         if (lane < 16) {
 #pragma unroll
             for (int jj = 0; jj < EPL / 4; jj++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) s_pq[par][wave][4 * c + 64 * jj + r] = pq[4 * jj + r];
+                *reinterpret_cast<float4*>(&s_pq[par][wave][4 * c + 64 * jj]) =
+                    make_float4(pq[4 * jj], pq[4 * jj + 1], pq[4 * jj + 2], pq[4 * jj + 3]);
         }
         if (lane == 0) { s_pfr[par][wave] = frp; dfr_acc += frp; }
-        if (tid == 0) { s_qn[par][0] = qnorm; s_qn[par][1] = qinv; }
+        if (tid == 0) { s_qn[par][0] = qq; s_qn[par][1] = qinv; }
         par ^= 1;
         if (++j == CT) { j = 0; buf ^= 1; }
+#pragma unroll
+        for (int e = 0; e < EPL; e++) qv[e] = qvn[e];
+        qq = qqn;
+        dme = dnext;
     }
     __syncthreads();
-    if (wave == ((T - 1) & 3)) finalize(T - 1);
-    dtemp_acc = sum4rows(dtemp_acc);
+    if (wave == fin_wave) finalize(T - 1);
+    dtemp_acc = wavesum(dtemp_acc);
     if (lane == 0) { s_fin[0][wave] = dtemp_acc; s_fin[1][wave] = dfr_acc; }
     __syncthreads();
     if (tid == 0) {
-        a.part[2 * (size_t)bh + 0] = (s_fin[0][0] + s_fin[0][1]) + (s_fin[0][2] + s_fin[0][3]);
-        a.part[2 * (size_t)bh + 1] = (s_fin[1][0] + s_fin[1][1]) + (s_fin[1][2] + s_fin[1][3]);
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int w = 0; w < CHAIN_WAVES; w++) { s0 += s_fin[0][w]; s1 += s_fin[1][w]; }
+        a.part[2 * (size_t)bh + 0] = s0;
+        a.part[2 * (size_t)bh + 1] = s1;
     }
 }
 
@@ -764,22 +997,20 @@ __global__ __launch_bounds__(256) void reduce_parts(const float* __restrict__ pa
 // ===================================================================================== host dispatch
 template <int D, typename TI>
 hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
-    const int rpt_need = (a.N + 15) / 16;
-    dim3 grid(B * a.H), block(256);
-#define SLOT_CF(R) if (rpt_need <= R) { hipLaunchKernelGGL((chain_fwd<D, R, TI>), grid, block, 0, st, a); return hipGetLastError(); }
-    SLOT_CF(2) SLOT_CF(4) SLOT_CF(6) SLOT_CF(8) SLOT_CF(12)
+    dim3 grid(B * a.H), block(CHAIN_THREADS);
+#define SLOT_CF(PP) if (a.N <= 4 * CHAIN_WAVES * PP) { hipLaunchKernelGGL((chain_fwd<D, PP, TI>), grid, block, 0, st, a); return hipGetLastError(); }
+    SLOT_CF(1) SLOT_CF(2) SLOT_CF(4) SLOT_CF(8) SLOT_CF(16)
 #undef SLOT_CF
     return hipErrorInvalidValue;
 }
 template <int D, typename TI>
 hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
-    const int rpt_need = (a.N + 15) / 16;
-    dim3 grid(B * a.H), block(256);
-#define SLOT_CB(R) if (rpt_need <= R) { \
-        if (a.occb) hipLaunchKernelGGL((chain_bwd<D, R, TI, true>), grid, block, 0, st, a); \
-        else hipLaunchKernelGGL((chain_bwd<D, R, TI, false>), grid, block, 0, st, a); \
+    dim3 grid(B * a.H), block(CHAIN_THREADS);
+#define SLOT_CB(PP) if (a.N <= 4 * CHAIN_WAVES * PP) { \
+        if (a.occb) hipLaunchKernelGGL((chain_bwd<D, PP, TI, true>), grid, block, 0, st, a); \
+        else hipLaunchKernelGGL((chain_bwd<D, PP, TI, false>), grid, block, 0, st, a); \
         return hipGetLastError(); }
-    SLOT_CB(2) SLOT_CB(4) SLOT_CB(6) SLOT_CB(8) SLOT_CB(12)
+    SLOT_CB(1) SLOT_CB(2) SLOT_CB(4) SLOT_CB(8) SLOT_CB(16)
 #undef SLOT_CB
     return hipErrorInvalidValue;
 }
@@ -886,8 +1117,8 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
         return fail(SLOTSCAN_ERR_ALIGN, "slotscan_fwd: row buffers must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     const int NB = (int)((T + G - 1) / G);
-    ChainFwdArgs ca{q, k, gate, fr, temp, k0, o0, kbuf, am, kold, oold, kfin, ofin,
-                    (int)T, (int)H, (int)N, (int)G, NB, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0};
+    ChainFwdArgs ca{q, k, gate, fr, temp, k0, o0, am, kold, oold, kfin, ofin,
+                    (int)T, (int)H, (int)N, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0};
     hipError_t e;
     {
         slotprof::Scope sc(SLOTSCAN_K_CHAIN_FWD, st);
@@ -895,7 +1126,7 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
         else e = dtype == SLOTSCAN_BF16 ? launch_chain_fwd<64, bf16_t>(ca, (int)B, st) : launch_chain_fwd<64, float>(ca, (int)B, st);
     }
     if (e != hipSuccess) return hip_fail(e, "chain_fwd launch");
-    RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB};
+    RowsFwdArgs ra{k, v, gate, am, k0, v0, kbuf, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB};
     dim3 grid((unsigned)(B * H), (unsigned)((N + 31) / 32)), block(512);
     {
         slotprof::Scope sc(SLOTSCAN_K_ROWS_FWD, st);
