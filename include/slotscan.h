@@ -16,7 +16,8 @@
  *     (slotkern_kvg.py:258-259).  Final state kfin, vfin (B*H, N, D) and ofin (B*H, N) fp32.
  *   - Undo log: am (B, T, H) int32 = the written row; kold, vold (B, T, H, D) fp32 and oold (B, T, H) fp32 =
  *     that row's key, value and occupancy BEFORE the write (the reference's saved tensors,
- *     slotkern_cuda.py:502-504, 510).
+ *     slotkern_cuda.py:502-504, 510); cslog (B*H, T, N) fp32 = the cosine of every row with q_t as the
+ *     forward computed it, so the backward rebuilds the forward's soft address without recomputing scores.
  *   - Return value: 0 on success, else one of the SLOTSCAN_ERR_* codes; slotscan_last_error() then holds a
  *     message (per calling thread).
  *   - Semantics: hard address, detached address gradient (slotkern_cuda.py:536-543); hard_gate is applied by
@@ -51,7 +52,7 @@ int slotscan_max_slots(int64_t D);
 /* Forward scan.  Replaces _KVScanC.forward's two launches (slotkern_cuda.py:484-512).
  *   k0, v0, o0   optional carried state (B*H, N, D) / (B*H, N); NULL = the all-zero, all-free start
  *                (the reference always starts from zero, slotkern_cuda.py:83-87, 190-192)
- *   kold, vold, oold  the undo log; all NULL for a forward that will not be differentiated
+ *   kold, vold, oold, cslog  the undo log; all NULL for a forward that will not be differentiated
  *   am, kfin, vfin, ofin  always written (am drives the value replay; the final state is the carry out). */
 int slotscan_fwd(const void* k, const void* q, const void* v, int dtype,
                  const float* gate, const float* fr, int fr_per_token, const float* temp,
@@ -59,7 +60,7 @@ int slotscan_fwd(const void* k, const void* q, const void* v, int dtype,
                  float eps, int occ_bin,
                  const float* k0, const float* v0, const float* o0,
                  float* kbuf, float* vbuf, int32_t* am,
-                 float* kold, float* vold, float* oold,
+                 float* kold, float* vold, float* oold, float* cslog,
                  float* kfin, float* vfin, float* ofin, void* stream);
 
 /* Bytes of device workspace slotscan_bwd needs: the row adjoint Dn (B*H, N, T) fp32 plus (B*H, 2) fp32
@@ -77,7 +78,7 @@ int slotscan_bwd(const void* k, const void* q, const void* v, int dtype,
                  int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
                  float eps, int occ_bin,
                  const int32_t* am, const float* kold, const float* vold, const float* oold,
-                 const float* kfin, const float* vfin, const float* ofin,
+                 const float* cslog, const float* kfin, const float* vfin, const float* ofin,
                  const float* dkbuf, const float* dvbuf, void* workspace,
                  void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
                  void* stream);

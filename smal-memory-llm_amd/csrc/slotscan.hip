@@ -181,12 +181,13 @@ template <int P> __device__ __forceinline__ int row_of_lane(int wave, int lane) 
 struct ChainFwdArgs {
     const void* q; const void* k; const float* gate; const float* fr; const float* temp;
     const float* k0; const float* o0;
-    int32_t* am; float* kold; float* oold; float* kfin; float* ofin;
-    int T, H, N; float eps; int frt, occb;
+    float* kbuf; int32_t* am; float* kold; float* oold; float* cslog; float* kfin; float* ofin;
+    int T, H, N, G, NB; float eps; int frt, occb;
 };
 
 template <int D, int P, typename TI>
 CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
+    constexpr int CT = (sizeof(TI) == 4 && P >= 16) ? 8 : SLOT_CT;   // fewer staging registers for fp32 tokens
     constexpr int EPL = D / 16;
     constexpr int EPU = 16 / (int)sizeof(TI);          // token elements per uint4
     constexpr int RU = D / EPU;                         // uint4 per token row
@@ -197,13 +198,15 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
     __shared__ float s_g[2][CT], s_fr[2][CT];
     __shared__ uint4 s_red[2][CHAIN_WAVES];
 
-    const int T = a.T, H = a.H, N = a.N;
+    const int T = a.T, H = a.H, N = a.N, G = a.G;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = tid & 15;
     const ChainRows<P> R(tid);
     const TI* __restrict__ qp = (const TI*)a.q;
     const TI* __restrict__ kp = (const TI*)a.k;
     const size_t tok0 = (size_t)b * T * H + h;          // token (b, t, h) = tok0 + t * H
+    float* kb = a.kbuf + ((size_t)b * a.NB * H + h) * N * D;   // key snapshot of block 0 of this chain
+    const size_t sstride = (size_t)H * N * D;
 
     float K[P][EPL];
     float o_me = 0.f, kinv_me;
@@ -288,11 +291,13 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
     ld_slice<EPL>(qv, &s_tok[0][0][0][0], c);
     float qinv = qinv_of(qv);
     float dme = dot_me(qv);                             // <K_me, q_t> for the current keys
-    int par = 0, j = 0, buf = 0;
+    int par = 0, j = 0, buf = 0, gc = 0;
     for (int t = 0; t < T; t++) {
         const float g = s_g[buf][j];
         const float frv = frt ? s_fr[buf][j] : fr_s;
-        const float s = temp * ((dme * kinv_me) * qinv);
+        const float cs = (dme * kinv_me) * qinv;         // cosine of this lane's row with q_t
+        const float s = temp * cs;
+        if (a.cslog && R.prim && valid_me) a.cslog[((size_t)bh * T + t) * N + R.n_me] = cs;
         const bool taken = o_me >= eps;
         const float occ = occb ? (taken ? 1.f : 0.f) : o_me;
         const float z = s - frv * occ;
@@ -329,6 +334,15 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
         uint4 r[CHAIN_WAVES];
 #pragma unroll
         for (int w = 0; w < CHAIN_WAVES; w++) r[w] = s_red[par][w];
+        if (gc == 0) {                                      // the PRE-write key state of block t / G:
+#pragma unroll
+            for (int jr = 0; jr < P; jr++) {                // every row group stores whole 512-byte rows
+                const int n = R.row(jr);
+                if (n < N) st_slice_nt<EPL>(kb + (size_t)n * D, K[jr], c);
+            }
+            kb += sstride;
+        }
+        if (++gc == G) gc = 0;
         // waves in order = rows in order: strict '>' keeps the lowest row on ties
         float bz = -INFINITY, fz = 0.f;
         int bo = -1, fo = -1;
@@ -388,14 +402,13 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
 
 // =========================================================================================== rows_fwd
 struct RowsFwdArgs {
-    const void* k; const void* v; const float* gate; const int32_t* am; const float* k0; const float* v0;
-    float* kbuf; float* vbuf; float* vold; float* vfin;
+    const void* v; const float* gate; const int32_t* am; const float* v0;
+    float* vbuf; float* vold; float* vfin;
     int T, H, N, G, NB;
 };
 
-// 512 lanes = 32 rows of one chain per workgroup; grid (B*H, ceil(N/32)).  Replays every row's key and
-// value from the address log (the same blend as the chain, so the keys match its state bitwise) and emits
-// both snapshots with full-row non-temporal stores.
+// 512 lanes = 32 rows of one chain per workgroup; grid (B*H, ceil(N/32)).  Replays every row's value from
+// the address log and emits the value snapshots with full-row non-temporal stores.
 template <int D, typename TI>
 ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     constexpr int EPL = D / 16;
@@ -407,17 +420,13 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     const int tid = threadIdx.x, rg = tid >> 4, c = tid & 15;
     const int n = blockIdx.y * 32 + rg;
     const bool live = n < N;
-    const TI* __restrict__ kp = (const TI*)a.k;
     const TI* __restrict__ vp = (const TI*)a.v;
     const size_t tok0 = (size_t)b * T * H + h;
-    float K[EPL], V[EPL];
+    float V[EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; e++) { K[e] = 0.f; V[e] = 0.f; }
-    if (live && a.k0) ld_slice<EPL>(K, a.k0 + ((size_t)bh * N + n) * D, c);
+    for (int e = 0; e < EPL; e++) V[e] = 0.f;
     if (live && a.v0) ld_slice<EPL>(V, a.v0 + ((size_t)bh * N + n) * D, c);
-    const size_t roff = ((size_t)b * a.NB * H + h) * N * D + (size_t)(live ? n : 0) * D;
-    float* kb = a.kbuf + roff;
-    float* vb = a.vbuf + roff;
+    float* vb = a.vbuf + ((size_t)b * a.NB * H + h) * N * D + (size_t)(live ? n : 0) * D;
     const size_t sstride = (size_t)H * N * D;
     int gc = 0;
     for (int t0 = 0; t0 < T; t0 += TC) {
@@ -432,21 +441,18 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
         if (!live) continue;
         for (int jt = 0; jt < tn; jt++) {
             if (gc == 0) {
-                st_slice_nt<EPL>(kb, K, c);
                 st_slice_nt<EPL>(vb, V, c);
-                kb += sstride;
                 vb += sstride;
             }
             if (++gc == G) gc = 0;
             if (s_am[jt] == n) {
                 const size_t ix = tok0 + (size_t)(t0 + jt) * H;
                 const float g = s_g[jt], omw = 1.f - g;
-                float kk[EPL], vv[EPL];
-                ld_slice<EPL>(kk, kp + ix * D, c);
+                float vv[EPL];
                 ld_slice<EPL>(vv, vp + ix * D, c);
                 if (a.vold) st_slice<EPL>(a.vold + ix * D, V, c);
 #pragma unroll
-                for (int e = 0; e < EPL; e++) { K[e] = blend(K[e], kk[e], g, omw); V[e] = blend(V[e], vv[e], g, omw); }
+                for (int e = 0; e < EPL; e++) V[e] = blend(V[e], vv[e], g, omw);
             }
         }
     }
@@ -623,14 +629,16 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
 // =========================================================================================== chain_bwd
 struct ChainBwdArgs {
     const void* q; const float* gate; const float* fr; const float* temp;
-    const int32_t* am; const float* kold; const float* oold; const float* kfin; const float* ofin;
+    const int32_t* am; const float* kold; const float* oold; const float* cslog; const float* kfin; const float* ofin;
     const float* dn;                                     // (B*H, N, T)
     void* dq; float* dg; float* dfr; float* part;        // part (B*H, 2): dtemp and scalar-dfr partials
     int T, H, N; float eps; int frt, occb;
 };
 
 // OCCB (occ_bin) is a template flag: with it the occupancy enters only through [o >= eps] and its
-// adjoint dO is identically zero, so the kernel carries no dO.
+// adjoint dO is identically zero, so the kernel carries no dO.  The scores are not recomputed: the
+// forward logged every row's cosine with q_t (cslog), so the backward rebuilds exactly the forward's
+// soft address and keeps the keys only for the query gradient dq = sum_n dz_n kinv_n K_n.
 template <int D, int P, typename TI, bool OCCB>
 CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
     constexpr int CT = P >= 16 ? 4 : SLOT_CT;           // fewer staging registers at N > 96
@@ -646,12 +654,12 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
     __shared__ __align__(16) float s_q[2][CT][D];
     __shared__ __align__(16) float s_ko[2][CT][D];
     __shared__ float s_dn[2][CT][NMAX];
+    __shared__ float s_cs[2][CT][NMAX];
     __shared__ float s_g[2][CT], s_fr[2][CT], s_oo[2][CT];
     __shared__ int s_am[2][CT];
     __shared__ __align__(16) float s_st[2][CHAIN_WAVES][8];
     __shared__ float s_pq[2][CHAIN_WAVES][D];
     __shared__ float s_pfr[2][CHAIN_WAVES];
-    __shared__ float s_qn[2][2];
     __shared__ float s_fin[2][CHAIN_WAVES];
     __shared__ __align__(16) float s_cf[NMAX];
 
@@ -687,7 +695,7 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
     }
 
     uint4 rq[UPT];
-    float rdn[DPT];
+    float rdn[DPT], rcs[DPT];
     float rs = 0.f;
     auto load_chunk = [&](int ch) {
 #pragma unroll
@@ -706,9 +714,12 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
         for (int m = 0; m < DPT; m++) {
             const int u = tid + CHAIN_THREADS * m;
             rdn[m] = 0.f;
+            rcs[m] = 0.f;
             if (u < CT * N) {
-                const int nn = u / CT, jj = u % CT, t = T - 1 - (ch * CT + jj);
-                if (t >= 0) rdn[m] = a.dn[((size_t)bh * N + nn) * T + t];
+                int nn = u / CT, jj = u % CT, t = T - 1 - (ch * CT + jj);
+                if (t >= 0) rdn[m] = a.dn[((size_t)bh * N + nn) * T + t];          // Dn is (N, T) per chain
+                jj = u / N; nn = u % N; t = T - 1 - (ch * CT + jj);
+                if (t >= 0) rcs[m] = a.cslog[((size_t)bh * T + t) * N + nn];       // the cosines are (T, N)
             }
         }
         if (tid < 4 * CT) {
@@ -735,7 +746,10 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 #pragma unroll
         for (int m = 0; m < DPT; m++) {
             const int u = tid + CHAIN_THREADS * m;
-            if (u < CT * N) s_dn[buf][u % CT][u / CT] = rdn[m];
+            if (u < CT * N) {
+                s_dn[buf][u % CT][u / CT] = rdn[m];
+                s_cs[buf][u / N][u % N] = rcs[m];
+            }
         }
         if (tid < 4 * CT) {
             const int jj = tid & (CT - 1), kind = tid / CT;
@@ -745,29 +759,11 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
             else s_oo[buf][jj] = rs;
         }
     };
-    auto dot_me = [&](const float* qv) -> float {
-        float x[P];
-#pragma unroll
-        for (int jr = 0; jr < P; jr++) {
-            float d = 0.f;
-#pragma unroll
-            for (int e = 0; e < EPL; e++) d = fmaf(K[jr][e], qv[e], d);
-            x[jr] = d;
-        }
-        return rs_reduce<P>(x, c);
-    };
-    auto qsq_of = [&](const float* qv) -> float {
-        float qq = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; e++) qq = fmaf(qv[e], qv[e], qq);
-        return rowsum16(qq);
-    };
     // dq (and per-token dfr) of processed step sp, by one wave, from the per-wave partials of that step
     auto finalize = [&](int sp) {
         const int pp = sp & 1, bp = (sp / CT) & 1, jp = sp % CT, tp = T - 1 - sp;
-        const float qq = s_qn[pp][0], qi = s_qn[pp][1];
-        float dqn[EPW], qh[EPW];
-        float pr = 0.f;
+        float dqn[EPW], qe[EPW];
+        float pr = 0.f, qq = 0.f;
 #pragma unroll
         for (int m = 0; m < EPW; m++) {
             const int e = lane + 64 * m;
@@ -775,14 +771,17 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 #pragma unroll
             for (int w = 0; w < CHAIN_WAVES; w++) acc += s_pq[pp][w][e];
             dqn[m] = temp * acc;
-            qh[m] = s_q[bp][jp][e] * qi;
-            pr = fmaf(dqn[m], qh[m], pr);
+            qe[m] = s_q[bp][jp][e];
+            pr = fmaf(dqn[m], qe[m], pr);
+            qq = fmaf(qe[m], qe[m], qq);
         }
-        pr = wavesum(pr);
+        qq = wavesum(qq);
+        const float qi = rsq_clamped(qq);
+        pr = wavesum(pr) * qi;                            // <qhat, dqn>
         TI* dqp = (TI*)a.dq + (tok0 + (size_t)tp * H) * D;
 #pragma unroll
         for (int m = 0; m < EPW; m++) {
-            const float r = qq < 1e-12f ? qi * dqn[m] : qi * (dqn[m] - qh[m] * pr);   // |q| < 1e-6: no projection
+            const float r = qq < 1e-12f ? qi * dqn[m] : qi * (dqn[m] - (qe[m] * qi) * pr);   // |q| < 1e-6: no projection
             st1<TI>(dqp + lane + 64 * m, r);
         }
         if (frt && lane == 0) {
@@ -798,10 +797,6 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
     store_chunk(0);
     __syncthreads();
     load_chunk(1);
-    float qv[EPL];
-    ld_slice<EPL>(qv, &s_q[0][0][0], c);
-    float qq = qsq_of(qv);
-    float dme = dot_me(qv);                              // <K_me, q_t> with the keys before this step's undo
     int par = 0, j = 0, buf = 0, fin_wave = 0;
     for (int s = 0; s < T; s++) {
         const int t = T - 1 - s;
@@ -809,34 +804,26 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
         const float g = s_g[buf][j];
         const float frv = frt ? s_fr[buf][j] : fr_s;
         const float omw = 1.f - g;
-        // undo this step's write: the written row goes back to its logged pre-write key and occupancy,
-        // and only that row's dot product with q_t is recomputed
+        // undo this step's write: the written row goes back to its logged pre-write key and occupancy
         if (amv >= R.rowbase && amv < R.rowbase + P) {
             const int sl = amv & (P - 1);
             float kv[EPL];
             ld_slice<EPL>(kv, &s_ko[buf][j][0], c);
-            float part = 0.f, pd = 0.f;
+            float part = 0.f;
 #pragma unroll
             for (int jr = 0; jr < P; jr++) {
                 if (jr == sl) {
 #pragma unroll
-                    for (int e = 0; e < EPL; e++) {
-                        K[jr][e] = kv[e];
-                        part = fmaf(kv[e], kv[e], part);
-                        pd = fmaf(kv[e], qv[e], pd);
-                    }
+                    for (int e = 0; e < EPL; e++) { K[jr][e] = kv[e]; part = fmaf(kv[e], kv[e], part); }
                 }
             }
             const float kk = rowsum16(part);
-            const float kd = rowsum16(pd);
             if (R.n_me == amv) {
                 o_me = s_oo[buf][j];
                 kinv_me = rsq_clamped(kk);
-                dme = kd;
             }
         }
-        const float qinv = rsq_clamped(qq);
-        const float cs = (dme * kinv_me) * qinv;         // cosine of this lane's row
+        const float cs = valid_me ? s_cs[buf][j][R.n_me] : 0.f;   // the forward's cosine of this row
         const bool taken = valid_me && o_me >= eps;
         float z, dw;
         if constexpr (OCCB) {
@@ -865,15 +852,6 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
                 *reinterpret_cast<float4*>(&s_st[par][wave][0]) = make_float4(wm, S, SD, __int_as_float(fo));
                 *reinterpret_cast<float2*>(&s_st[par][wave][4]) = make_float2(fz, fd);
             }
-        }
-        // next step's query and its dot products with the current keys (its undo corrects one row)
-        float qqn = 0.f, dnext = 0.f;
-        float qvn[EPL];
-        if (s + 1 < T) {
-            const int jn = j + 1 == CT ? 0 : j + 1, bn = j + 1 == CT ? (buf ^ 1) : buf;
-            ld_slice<EPL>(qvn, &s_q[bn][jn][0], c);
-            qqn = qsq_of(qvn);
-            dnext = dot_me(qvn);
         }
         if (j == CT - 2) {
             store_chunk(buf ^ 1);
@@ -956,13 +934,8 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
                     make_float4(pq[4 * jj], pq[4 * jj + 1], pq[4 * jj + 2], pq[4 * jj + 3]);
         }
         if (lane == 0) { s_pfr[par][wave] = frp; dfr_acc += frp; }
-        if (tid == 0) { s_qn[par][0] = qq; s_qn[par][1] = qinv; }
         par ^= 1;
         if (++j == CT) { j = 0; buf ^= 1; }
-#pragma unroll
-        for (int e = 0; e < EPL; e++) qv[e] = qvn[e];
-        qq = qqn;
-        dme = dnext;
     }
     __syncthreads();
     if (wave == fin_wave) finalize(T - 1);
@@ -1105,20 +1078,21 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
                             float eps, int occ_bin,
                             const float* k0, const float* v0, const float* o0,
                             float* kbuf, float* vbuf, int32_t* am,
-                            float* kold, float* vold, float* oold,
+                            float* kold, float* vold, float* oold, float* cslog,
                             float* kfin, float* vfin, float* ofin, void* stream) {
     if (int r = check_common(B, T, H, N, D, G, dtype)) return r;
     if (!k || !q || !v || !gate || !fr || !temp || !kbuf || !vbuf || !am || !kfin || !vfin || !ofin)
         return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd: a required pointer is NULL");
-    if ((kold == nullptr) != (oold == nullptr) || (kold == nullptr) != (vold == nullptr))
-        return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd: kold, vold and oold must be all set or all NULL");
+    if ((kold == nullptr) != (oold == nullptr) || (kold == nullptr) != (vold == nullptr) ||
+        (kold == nullptr) != (cslog == nullptr))
+        return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd: kold, vold, oold and cslog must be all set or all NULL");
     if (!al16(k) || !al16(q) || !al16(v) || !al16(kbuf) || !al16(vbuf) || !al16(kfin) || !al16(vfin) ||
         (kold && (!al16(kold) || !al16(vold))) || (k0 && !al16(k0)) || (v0 && !al16(v0)))
         return fail(SLOTSCAN_ERR_ALIGN, "slotscan_fwd: row buffers must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     const int NB = (int)((T + G - 1) / G);
-    ChainFwdArgs ca{q, k, gate, fr, temp, k0, o0, am, kold, oold, kfin, ofin,
-                    (int)T, (int)H, (int)N, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0};
+    ChainFwdArgs ca{q, k, gate, fr, temp, k0, o0, kbuf, am, kold, oold, cslog, kfin, ofin,
+                    (int)T, (int)H, (int)N, (int)G, NB, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0};
     hipError_t e;
     {
         slotprof::Scope sc(SLOTSCAN_K_CHAIN_FWD, st);
@@ -1126,7 +1100,7 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
         else e = dtype == SLOTSCAN_BF16 ? launch_chain_fwd<64, bf16_t>(ca, (int)B, st) : launch_chain_fwd<64, float>(ca, (int)B, st);
     }
     if (e != hipSuccess) return hip_fail(e, "chain_fwd launch");
-    RowsFwdArgs ra{k, v, gate, am, k0, v0, kbuf, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB};
+    RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB};
     dim3 grid((unsigned)(B * H), (unsigned)((N + 31) / 32)), block(512);
     {
         slotprof::Scope sc(SLOTSCAN_K_ROWS_FWD, st);
@@ -1154,12 +1128,12 @@ extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dty
                             int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
                             float eps, int occ_bin,
                             const int32_t* am, const float* kold, const float* vold, const float* oold,
-                            const float* kfin, const float* vfin, const float* ofin,
+                            const float* cslog, const float* kfin, const float* vfin, const float* ofin,
                             const float* dkbuf, const float* dvbuf, void* workspace,
                             void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
                             void* stream) {
     if (int r = check_common(B, T, H, N, D, G, dtype)) return r;
-    if (!k || !q || !v || !gate || !fr || !temp || !am || !kold || !vold || !oold || !kfin || !vfin || !ofin ||
+    if (!k || !q || !v || !gate || !fr || !temp || !am || !kold || !vold || !oold || !cslog || !kfin || !vfin || !ofin ||
         !dkbuf || !dvbuf || !workspace || !dk || !dq || !dv || !dgate || !dfr || !dtemp)
         return fail(SLOTSCAN_ERR_NULL, "slotscan_bwd: a required pointer is NULL");
     if (!al16(k) || !al16(q) || !al16(v) || !al16(kold) || !al16(vold) || !al16(kfin) || !al16(vfin) ||
@@ -1186,7 +1160,7 @@ extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dty
         e = hipGetLastError();
     }
     if (e != hipSuccess) return hip_fail(e, "rows_bwd launch");
-    ChainBwdArgs ca{q, gate, fr, temp, am, kold, oold, kfin, ofin, dn, dq, dgate, dfr, part,
+    ChainBwdArgs ca{q, gate, fr, temp, am, kold, oold, cslog, kfin, ofin, dn, dq, dgate, dfr, part,
                     (int)T, (int)H, (int)N, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0};
     {
         slotprof::Scope sc(SLOTSCAN_K_CHAIN_BWD, st);

@@ -70,9 +70,9 @@ def _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, state=Non
     e = lambda *s, dtype=f32: torch.empty(*s, device=dev, dtype=dtype)
     kbuf, vbuf = e(B, NB, H, N, D), e(B, NB, H, N, D)
     am = e(B, T, H, dtype=torch.int32)
-    kold = vold = oold = None
+    kold = vold = oold = cslog = None
     if logs:
-        kold, vold, oold = e(B, T, H, D), e(B, T, H, D), e(B, T, H)
+        kold, vold, oold, cslog = e(B, T, H, D), e(B, T, H, D), e(B, T, H), e(B * H, T, N)
     kfin, vfin, ofin = e(B * H, N, D), e(B * H, N, D), e(B * H, N)
     k0 = v0 = o0 = None
     if state is not None:
@@ -82,10 +82,10 @@ def _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, state=Non
     rc = L.lib().slotscan_fwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
                               int(frt), L.ptr(temp_), B, T, H, N, D, G, float(eps), int(bool(occ_bin)),
                               L.ptr(k0), L.ptr(v0), L.ptr(o0), L.ptr(kbuf), L.ptr(vbuf), L.ptr(am),
-                              L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(kfin), L.ptr(vfin), L.ptr(ofin),
-                              L.stream_of(dev))
+                              L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(cslog), L.ptr(kfin), L.ptr(vfin),
+                              L.ptr(ofin), L.stream_of(dev))
     L.check(rc, "slotscan_fwd")
-    return kbuf, vbuf, am, kold, vold, oold, kfin, vfin, ofin
+    return kbuf, vbuf, am, kold, vold, oold, cslog, kfin, vfin, ofin
 
 
 class _KVScanHip(torch.autograd.Function):
@@ -96,16 +96,16 @@ class _KVScanHip(torch.autograd.Function):
             raise ValueError("the HIP scan needs DK == DV")
         dt, k_, q_, v_, g, fr_, frt, temp_ = _prep(k, q, v, gate, fr, temp, hard_gate)
         logs = any(ctx.needs_input_grad[:6])
-        kbuf, vbuf, am, kold, vold, oold, kfin, vfin, ofin = _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps,
-                                                                  occ_bin, dt, logs)
+        kbuf, vbuf, am, kold, vold, oold, cslog, kfin, vfin, ofin = _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G,
+                                                                         eps, occ_bin, dt, logs)
         if logs:
-            ctx.save_for_backward(k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, kfin, vfin, ofin)
+            ctx.save_for_backward(k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, cslog, kfin, vfin, ofin)
         ctx.meta = (int(N), int(G), frt, float(eps), bool(occ_bin), dt, tuple(fr.shape), torch.is_tensor(temp))
         return kbuf, vbuf
 
     @staticmethod
     def backward(ctx, dkbuf, dvbuf):
-        k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, kfin, vfin, ofin = ctx.saved_tensors
+        k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, cslog, kfin, vfin, ofin = ctx.saved_tensors
         N, G, frt, eps, occ_bin, dt, fr_shape, temp_is_tensor = ctx.meta
         B, T, H, D = k_.shape
         NB = (T + G - 1) // G
@@ -121,8 +121,8 @@ class _KVScanHip(torch.autograd.Function):
         dtemp = torch.empty(1, device=dev, dtype=f32)
         rc = L.lib().slotscan_bwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
                                   int(frt), L.ptr(temp_), B, T, H, N, D, G, float(eps), int(occ_bin),
-                                  L.ptr(am), L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(kfin), L.ptr(vfin),
-                                  L.ptr(ofin), L.ptr(dkbuf), L.ptr(dvbuf), L.ptr(ws),
+                                  L.ptr(am), L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(cslog), L.ptr(kfin),
+                                  L.ptr(vfin), L.ptr(ofin), L.ptr(dkbuf), L.ptr(dvbuf), L.ptr(ws),
                                   L.ptr(dk), L.ptr(dq), L.ptr(dv), L.ptr(dg), L.ptr(dfr), L.ptr(dtemp),
                                   L.stream_of(dev))
         L.check(rc, "slotscan_bwd")
@@ -180,6 +180,6 @@ def kv_scan_stream(k, v, gate, fr, N, temp, G=8, hard_gate=False, eps=1e-4, q=No
         raise NotImplementedError(why)
     qq = k if q is None else q
     dt, k_, q_, v_, g, fr_, frt, temp_ = _prep(k, qq, v, gate, fr, temp, hard_gate)
-    kbuf, vbuf, _am, _ko, _vo, _oo, kfin, vfin, ofin = _fwd(k_, q_, v_, g, fr_, frt, temp_, int(N), int(G), eps,
-                                                            occ_bin, dt, logs=False, state=state)
+    kbuf, vbuf, _am, _ko, _vo, _oo, _cs, kfin, vfin, ofin = _fwd(k_, q_, v_, g, fr_, frt, temp_, int(N), int(G),
+                                                                 eps, occ_bin, dt, logs=False, state=state)
     return kbuf, vbuf, (kfin, vfin, ofin)

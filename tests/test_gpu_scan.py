@@ -49,7 +49,7 @@ def run_gpu(k, q, v, g, fr, N, G, occb, hardg, wk, wv, temp=TEMP, eps=1e-4):
     torch.cuda.synchronize()
     grads = dict(dk=kk.grad, dv=vv.grad, dgate=gg.grad, dfr=ff.grad, dtemp=tp.grad,
                  dq=None if qq is None else qq.grad)
-    return kb.detach(), vb.detach(), out[2], out[8], out[0], out[1], grads
+    return kb.detach(), vb.detach(), out[2], out[9], out[0], out[1], grads
 
 
 def oracle(k, q, v, g, fr, N, G, occb, hardg, am_gpu, wk, wv, temp=TEMP, eps=1e-4):

@@ -47,7 +47,7 @@ def test_workspace_size():
 def _fwd_call(**over):
     a = dict(k=1 << 20, q=1 << 20, v=1 << 20, dtype=0, gate=1 << 20, fr=1 << 20, frt=1, temp=1 << 20,
              B=1, T=8, H=1, N=16, D=64, G=8, eps=1e-4, occ=1, k0=None, v0=None, o0=None,
-             kbuf=1 << 20, vbuf=1 << 20, am=1 << 20, kold=None, vold=None, oold=None,
+             kbuf=1 << 20, vbuf=1 << 20, am=1 << 20, kold=None, vold=None, oold=None, cslog=None,
              kfin=1 << 20, vfin=1 << 20, ofin=1 << 20)
     a.update(over)
     vp = lambda x: None if x is None else ctypes.c_void_p(x)
@@ -55,7 +55,7 @@ def _fwd_call(**over):
                                 a["frt"], vp(a["temp"]), a["B"], a["T"], a["H"], a["N"], a["D"], a["G"],
                                 a["eps"], a["occ"], vp(a["k0"]), vp(a["v0"]), vp(a["o0"]), vp(a["kbuf"]),
                                 vp(a["vbuf"]), vp(a["am"]), vp(a["kold"]), vp(a["vold"]), vp(a["oold"]),
-                                vp(a["kfin"]), vp(a["vfin"]), vp(a["ofin"]), None)
+                                vp(a["cslog"]), vp(a["kfin"]), vp(a["vfin"]), vp(a["ofin"]), None)
 
 
 @pytest.mark.parametrize("over,code", [
