@@ -30,12 +30,14 @@
 // <K_n, q_t> are finished with a DPP REDUCE-SCATTER instead of a 16-lane all-reduce, after which each
 // lane holds the complete dot product of ONE row: all per-row scalar work (score, occupancy, softmax,
 // adjoint) is done once per row instead of 16 times.  Rows increase with the lane index, so the argmax
-// tie rule (lowest index) is a ballot plus a find-first-set.  The 3 waves meet in one ping-pong LDS slot: ONE workgroup barrier per step.  A barrier
-// every step makes the step time the per-SIMD sum of issued instructions, so the design minimises
-// per-wave work: the next step's dot products are computed before the barrier with the current keys and
-// only the one rewritten row is corrected afterwards; row norms use v_rsq; the key snapshots are not
-// written by the chain at all (the row replay emits them, perfectly coalesced).  Token inputs (q, k, gate,
-// fr; in the backward also the undo log and Dn) are staged in LDS as fp32 in double-buffered chunks.
+// tie rule (lowest index) is a ballot plus a find-first-set.  The 3 waves meet in one ping-pong LDS
+// slot: ONE workgroup barrier per step.  A barrier every step makes the step time the per-SIMD sum of
+// issued instructions, so the design minimises per-wave work: the next step's dot products are computed
+// before the barrier with the current keys and only the one rewritten row is corrected afterwards; row
+// norms use v_rsq; the key snapshot slab is written every G steps as 256-byte contiguous runs, and the
+// cosines of every step go to a log so the backward chain never recomputes a dot product for its scores.
+// Token inputs (q, k, gate, fr; in the backward also the undo log, Dn and the cosine log) are staged in
+// LDS as fp32 in double-buffered chunks.
 #include "slot_common.h"
 
 using namespace slot;
