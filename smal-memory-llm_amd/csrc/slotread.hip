@@ -1,0 +1,713 @@
+// Cosine slot read with per-token sharpness, for MI355X (gfx950), as bf16 MFMA contractions.
+//
+// Semantics (reference: /root/reference/gqa25/memlm_sh.py:362-397).  The G tokens of block j share the
+// block's PRE-write copy (kbuf_j, vbuf_j); every token has NQ unit read queries.  For query m of block j:
+//   raw_n = bf16(<q_m, K_n>)                 the bf16 einsum's output rounding    (memlm_sh.py:383)
+//   sc_n  = raw_n * kinv_n * scale_m         kinv, exp(log_rsel), exp(C tanh(s/C)) (memlm_sh.py:383-393)
+//   a     = softmax over valid n; no valid row -> a = 0 (masked_fill + nan_to_num, memlm_sh.py:394)
+//   rd_m  = bf16(sum_n bf16(a_n) V_n)        att.to(bf16) then the bf16 einsum    (memlm_sh.py:395)
+//
+// gfx950 mapping.  One workgroup = 4 waves per (b, j, h) block and a range of up to MC query rows.  The
+// slots are SPLIT across the waves (wave w owns the 16-row key tiles w*TPW .. w*TPW+TPW-1, TPW <= 3 for
+// N <= 192), so a wave's share of the keys and values is loaded ONCE into VGPRs as MFMA operands and then
+// reused for every 16-query tile of the range:
+//   scores   S^T (16 slots x 16 queries) = K_tile Q^T   v_mfma_f32_16x16x32_bf16, K as the A operand
+//            (lane row = slot), Q as the B operand (lane column = query), D/32 k-steps;
+//   softmax  the D layout of S^T puts one query column in every lane (4 slots per lane per tile), so the
+//            max / sum over slots is 4*TPW values per lane, a cross-row permlane reduction and one LDS
+//            exchange between the 4 waves;
+//   output   O^T (16 dims x 16 queries) = V^T P^T       v_mfma_f32_16x16x16_bf16: the B operand (P^T,
+//            lane column = query, 4 slots per lane) is EXACTLY the D layout of the score tile, so the
+//            probabilities never move; V^T is the A operand, built once from LDS-staged value rows;
+//   reduce   the 4 waves' partial O (their slot ranges) are summed in a fixed order through LDS and
+//            written as bf16, 16 contiguous bytes per lane, in token-major order.
+// Three workgroup barriers per 16-query tile; no atomics, so the result is bitwise reproducible.
+#include "slot_common.h"
+#include "slotscan.h"
+#include "slotread.h"
+#include "slot_host.h"
+
+using namespace slot;
+using slothost::fail;
+using slothost::hip_fail;
+using slothost::al16;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define READ_WAVES 4
+#define READ_THREADS (64 * READ_WAVES)
+#define READ_TPW 3                       // 16-slot tiles per wave at most: 4 x 3 x 16 = 192 slots
+
+namespace {
+
+__device__ __forceinline__ f32x4 mfma_k32(const uint4& a, const uint4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_k16(const uint2& a, const uint2& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                     0, 0, 0);
+}
+__device__ __forceinline__ float bf16r(float x) { return bf2f(f2bf(x)); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// max over the 4 row groups of a wave (lanes c, c+16, c+32, c+48); same permlane pattern as sum4rows
+__device__ __forceinline__ float max4rows(float v) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    float s = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// order LDS writes of this wave before later LDS reads by other lanes of the same wave
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+struct ReadFwdArgs {
+    const bf16_t* q;
+    const bf16_t* kb;
+    const bf16_t* vb;
+    const float* kinv;
+    const uint8_t* valid;
+    const float* scale;
+    bf16_t* rd;
+    int T, H, NQ, N, G, NB, MC;   // MC: query rows per workgroup (multiple of 16)
+};
+
+template <int D>
+struct ReadSmem {
+    static constexpr int VST = D + 8;   // staged value row stride (bf16): rows 4 apart land 16 banks apart
+    static constexpr int OST = D + 4;   // output-partial row stride (floats)
+    static constexpr int VBYTES = READ_WAVES * READ_TPW * 16 * VST * 2;
+    static constexpr int OBYTES = READ_WAVES * 16 * OST * 4;
+    static constexpr int BIG = VBYTES > OBYTES ? VBYTES : OBYTES;
+};
+
+template <int D>
+__global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
+    constexpr int KK = D / 32;
+    constexpr int DT = D / 16;
+    constexpr int VST = ReadSmem<D>::VST;
+    constexpr int OST = ReadSmem<D>::OST;
+    __shared__ __align__(16) unsigned char s_big[ReadSmem<D>::BIG];   // staged values, then output partials
+    __shared__ float s_max[READ_WAVES][16];
+    __shared__ float s_sum[READ_WAVES][16];
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int slab = blockIdx.x;                                // (b * NB + j) * H + h: the kbuf slab
+    const int h = slab % a.H;
+    const int j = (slab / a.H) % a.NB;
+    const int b = slab / (a.H * a.NB);
+    const int t0 = j * a.G;
+    const int Mblk = min(a.G, a.T - t0) * a.NQ;
+    const int mlo = blockIdx.y * a.MC;
+    const int mhi = min(Mblk, mlo + a.MC);
+    if (mlo >= mhi) return;                                     // uniform over the workgroup
+
+    const int N = a.N;
+    const int NT16 = (N + 15) >> 4;
+    const int TPW = (NT16 + READ_WAVES - 1) / READ_WAVES;
+    const bf16_t* Kb = a.kb + (size_t)slab * N * D;
+    const bf16_t* Vb = a.vb + (size_t)slab * N * D;
+    const float* KI = a.kinv + (size_t)slab * N;
+    const uint8_t* VA = a.valid + (size_t)slab * N;
+
+    // ---- this wave's keys (A operand of the score product), kinv and validity, values (A of the output)
+    uint4 kf[READ_TPW][KK];
+    float kv[READ_TPW][4];
+    uint32_t vmask = 0;
+#pragma unroll
+    for (int u = 0; u < READ_TPW; u++) {
+        const int nt = w * TPW + u;
+        const bool tile = u < TPW && nt < NT16;
+        const int nr = nt * 16 + c;                              // A-operand row of this lane
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++)
+            kf[u][kk] = (tile && nr < N) ? *reinterpret_cast<const uint4*>(Kb + (size_t)nr * D + kk * 32 + 8 * g)
+                                         : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = nt * 16 + 4 * g + i;                     // D-layout row of item i
+            const bool ok = tile && n < N && VA[n] != 0;
+            kv[u][i] = ok ? KI[n] : 0.f;
+            vmask |= (ok ? 1u : 0u) << (u * 4 + i);
+        }
+    }
+    bf16_t* sV = reinterpret_cast<bf16_t*>(s_big) + w * (READ_TPW * 16 * VST);
+    {
+        const int nbase = w * TPW * 16;
+        const int rows = TPW * 16;
+        for (int e = lane; e < rows * (D / 8); e += 64) {
+            const int r = e / (D / 8), cc = e % (D / 8);
+            const int n = nbase + r;
+            uint4 x = n < N ? *reinterpret_cast<const uint4*>(Vb + (size_t)n * D + cc * 8) : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4*>(sV + r * VST + cc * 8) = x;
+        }
+    }
+    wave_lds_sync();
+    uint2 vf[READ_TPW][DT];                                      // V^T tile: row = dim 16dt + c, k = slot 4g + i
+#pragma unroll
+    for (int u = 0; u < READ_TPW; u++)
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            if (u < TPW) {
+                const bf16_t* p = sV + (u * 16 + 4 * g) * VST + dt * 16 + c;
+                vf[u][dt].x = (uint32_t)p[0] | ((uint32_t)p[VST] << 16);
+                vf[u][dt].y = (uint32_t)p[2 * VST] | ((uint32_t)p[3 * VST] << 16);
+            } else {
+                vf[u][dt] = make_uint2(0, 0);
+            }
+        }
+
+    float* sO = reinterpret_cast<float*>(s_big);
+    const bf16_t* qbase = a.q;
+    for (int m0 = mlo; m0 < mhi; m0 += 16) {
+        // ---- queries of this tile: B operand, lane column = query m0 + c
+        const int m = m0 + c;
+        const bool mok = m < mhi;
+        size_t qrow = 0;
+        if (mok) qrow = (((size_t)b * a.T + t0 + m / a.NQ) * a.H + h) * a.NQ + (m % a.NQ);
+        uint4 qf[KK];
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++)
+            qf[kk] = mok ? *reinterpret_cast<const uint4*>(qbase + qrow * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
+        const float scl = mok ? a.scale[qrow] : 0.f;
+
+        f32x4 acc[READ_TPW];
+#pragma unroll
+        for (int u = 0; u < READ_TPW; u++) {
+            acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (u < TPW && w * TPW + u < NT16) {
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) acc[u] = mfma_k32(kf[u][kk], qf[kk], acc[u]);
+            }
+        }
+        // ---- masked softmax over the slots of this lane's query column
+        float sc[READ_TPW][4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < READ_TPW; u++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float s = bf16r(acc[u][i]) * kv[u][i] * scl;
+                sc[u][i] = s;
+                if ((vmask >> (u * 4 + i)) & 1u) mx = fmaxf(mx, s);
+            }
+        mx = max4rows(mx);
+        if (g == 0) s_max[w][c] = mx;
+        __syncthreads();
+        const float M = fmaxf(fmaxf(s_max[0][c], s_max[1][c]), fmaxf(s_max[2][c], s_max[3][c]));
+        float sum = 0.f;
+#pragma unroll
+        for (int u = 0; u < READ_TPW; u++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float e = ((vmask >> (u * 4 + i)) & 1u) ? __expf(sc[u][i] - M) : 0.f;
+                sc[u][i] = e;
+                sum += e;
+            }
+        sum = sum4rows(sum);
+        if (g == 0) s_sum[w][c] = sum;
+        __syncthreads();
+        const float S = ((s_sum[0][c] + s_sum[1][c]) + s_sum[2][c]) + s_sum[3][c];
+        const float inv = S > 0.f ? 1.f / S : 0.f;
+        uint2 pf[READ_TPW];
+#pragma unroll
+        for (int u = 0; u < READ_TPW; u++) {
+            pf[u].x = pack2(sc[u][0] * inv, sc[u][1] * inv);
+            pf[u].y = pack2(sc[u][2] * inv, sc[u][3] * inv);
+        }
+        // ---- O^T partial over this wave's slots
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < READ_TPW; u++)
+                if (u < TPW && w * TPW + u < NT16) o = mfma_k16(vf[u][dt], pf[u], o);
+            *reinterpret_cast<f32x4*>(sO + (w * 16 + c) * OST + dt * 16 + 4 * g) = o;
+        }
+        __syncthreads();
+        // ---- fixed-order sum of the 4 partials, bf16, token-major store
+        {
+            constexpr int EPT = D / 16;
+            const int mr = threadIdx.x >> 4, dc = (threadIdx.x & 15) * EPT;
+            const int mm = m0 + mr;
+            if (mm < mhi) {
+                float r[EPT];
+#pragma unroll
+                for (int e = 0; e < EPT; e++) r[e] = sO[mr * OST + dc + e];
+#pragma unroll
+                for (int ww = 1; ww < READ_WAVES; ww++)
+#pragma unroll
+                    for (int e = 0; e < EPT; e++) r[e] += sO[(ww * 16 + mr) * OST + dc + e];
+                const size_t orow = (((size_t)b * a.T + t0 + mm / a.NQ) * a.H + h) * a.NQ + (mm % a.NQ);
+                bf16_t* dst = a.rd + orow * D + dc;
+                if constexpr (EPT == 8) {
+                    uint4 x;
+                    x.x = pack2(r[0], r[1]); x.y = pack2(r[2], r[3]); x.z = pack2(r[4], r[5]); x.w = pack2(r[6], r[7]);
+                    *reinterpret_cast<uint4*>(dst) = x;
+                } else {
+                    uint2 x;
+                    x.x = pack2(r[0], r[1]); x.y = pack2(r[2], r[3]);
+                    *reinterpret_cast<uint2*>(dst) = x;
+                }
+            }
+        }
+    }
+}
+
+
+// ---------------------------------------------------------------------------------------------- backward
+// Adjoint of read_fwd, the straight derivative of the reference's ops (memlm_sh.py:383-395) with the same
+// bf16 roundings autograd makes there: d(att_bf16) = bf16(dO V^T), the softmax adjoint in fp32 from the fp32
+// probabilities, d raw = bf16(dsc * kinv * scale) (the .float() of a bf16 einsum casts its gradient back),
+// and bf16 outputs of the three gradient contractions.
+//   S     (16 queries x 16 slots) = Q K^T        16x16x32, Q tile from LDS as A, K rows from L2 as B;
+//         queries are the ROWS here, so the softmax max / sums over slots are DPP row reductions
+//   datt  = bf16(dO V^T)                         16x16x32, same shapes
+//   dK^T  (16 dims x 16 slots) = Q^T draw        16x16x16: the B operand is exactly the D layout of draw
+//   dV^T  = dO^T P                               16x16x16: the B operand is exactly the D layout of P
+//   dQ^T  (16 dims x 16 queries) = K^T draw^T    16x16x16, partial over the wave's slots, fixed-order sum
+// The transposed operands (Q^T, dO^T, K^T) are gathered as 16-bit elements from LDS or L2; draw^T goes
+// through a per-wave LDS tile.  ACC = the block has more than one 16-query tile, so dK, dV accumulate in
+// registers across tiles; otherwise every output tile is finished by one MFMA and stored at once.
+struct ReadBwdArgs {
+    const bf16_t* q;
+    const bf16_t* kb;
+    const bf16_t* vb;
+    const float* kinv;
+    const uint8_t* valid;
+    const float* scale;
+    const bf16_t* drd;
+    bf16_t* dq;
+    bf16_t* dkb;
+    bf16_t* dvb;
+    float* dkinv;
+    float* dscale;
+    int T, H, NQ, N, G, NB;
+};
+
+template <int D>
+struct ReadBwdSmem {
+    static constexpr int TST = D + 8;               // Q / dO tile row stride (bf16)
+    static constexpr int RST = READ_TPW * 16 + 8;   // draw^T tile row stride (bf16)
+    static constexpr int OST = D + 4;               // dQ partial row stride (floats)
+};
+
+__device__ __forceinline__ uint2 gather4(const bf16_t* p, int stride) {
+    uint2 r;
+    r.x = (uint32_t)p[0] | ((uint32_t)p[stride] << 16);
+    r.y = (uint32_t)p[2 * stride] | ((uint32_t)p[3 * stride] << 16);
+    return r;
+}
+
+template <int D, bool ACC>
+__global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
+    constexpr int KK = D / 32;
+    constexpr int DT = D / 16;
+    constexpr int TST = ReadBwdSmem<D>::TST;
+    constexpr int RST = ReadBwdSmem<D>::RST;
+    constexpr int OST = ReadBwdSmem<D>::OST;
+    __shared__ __align__(16) bf16_t s_q[16 * TST];
+    __shared__ __align__(16) bf16_t s_do[16 * TST];
+    __shared__ __align__(16) bf16_t s_dr[READ_WAVES][16 * RST];
+    __shared__ __align__(16) float s_part[READ_WAVES * 16 * OST];
+    __shared__ float s_scl[16];
+    __shared__ float s_red[3][READ_WAVES][16];
+    __shared__ float s_dsc[READ_WAVES][16];
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int slab = blockIdx.x;
+    const int h = slab % a.H;
+    const int j = (slab / a.H) % a.NB;
+    const int b = slab / (a.H * a.NB);
+    const int t0 = j * a.G;
+    const int Mblk = min(a.G, a.T - t0) * a.NQ;
+    const int N = a.N;
+    const int NT16 = (N + 15) >> 4;
+    const int TPW = (NT16 + READ_WAVES - 1) / READ_WAVES;
+    const bf16_t* Kb = a.kb + (size_t)slab * N * D;
+    const bf16_t* Vb = a.vb + (size_t)slab * N * D;
+    const float* KI = a.kinv + (size_t)slab * N;
+    const uint8_t* VA = a.valid + (size_t)slab * N;
+    bf16_t* dKb = a.dkb + (size_t)slab * N * D;
+    bf16_t* dVb = a.dvb + (size_t)slab * N * D;
+
+    // this lane's slot column in the S layout: n = 16 nt + c
+    float kvc[READ_TPW];
+    uint32_t vmask = 0;
+    bool tile[READ_TPW];
+#pragma unroll
+    for (int u = 0; u < READ_TPW; u++) {
+        const int nt = w * TPW + u;
+        tile[u] = u < TPW && nt < NT16;
+        const int n = nt * 16 + c;
+        const bool ok = tile[u] && n < N && VA[n] != 0;
+        kvc[u] = ok ? KI[n] : 0.f;
+        vmask |= (ok ? 1u : 0u) << u;
+    }
+    float dkinv_acc[READ_TPW] = {};
+    f32x4 acc_dk[ACC ? READ_TPW : 1][ACC ? DT : 1];
+    f32x4 acc_dv[ACC ? READ_TPW : 1][ACC ? DT : 1];
+    if constexpr (ACC) {
+#pragma unroll
+        for (int u = 0; u < READ_TPW; u++)
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) { acc_dk[u][dt] = f32x4{0.f, 0.f, 0.f, 0.f}; acc_dv[u][dt] = f32x4{0.f, 0.f, 0.f, 0.f}; }
+    }
+
+    for (int m0 = 0; m0 < Mblk; m0 += 16) {
+        // ---- (a) the 16-query tile of Q and dO, and the multipliers, into LDS
+        for (int e = threadIdx.x; e < 16 * (D / 8); e += READ_THREADS) {
+            const int r = e / (D / 8), cc = e % (D / 8);
+            const int m = m0 + r;
+            uint4 xq = make_uint4(0, 0, 0, 0), xd = make_uint4(0, 0, 0, 0);
+            if (m < Mblk) {
+                const size_t row = (((size_t)b * a.T + t0 + m / a.NQ) * a.H + h) * a.NQ + (m % a.NQ);
+                xq = *reinterpret_cast<const uint4*>(a.q + row * D + cc * 8);
+                xd = *reinterpret_cast<const uint4*>(a.drd + row * D + cc * 8);
+            }
+            *reinterpret_cast<uint4*>(s_q + r * TST + cc * 8) = xq;
+            *reinterpret_cast<uint4*>(s_do + r * TST + cc * 8) = xd;
+        }
+        if (threadIdx.x < 16) {
+            const int m = m0 + threadIdx.x;
+            float sv = 0.f;
+            if (m < Mblk) sv = a.scale[(((size_t)b * a.T + t0 + m / a.NQ) * a.H + h) * a.NQ + (m % a.NQ)];
+            s_scl[threadIdx.x] = sv;
+        }
+        __syncthreads();
+        float scl[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) scl[i] = s_scl[4 * g + i];
+
+        // ---- (b) scores S = Q K^T and datt = dO V^T, D layout: rows m = 4g + i, column n = 16 nt + c
+        f32x4 sacc[READ_TPW], dacc[READ_TPW];
+        {
+            uint4 qa[KK], da[KK];
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+                qa[kk] = *reinterpret_cast<const uint4*>(s_q + c * TST + kk * 32 + 8 * g);
+                da[kk] = *reinterpret_cast<const uint4*>(s_do + c * TST + kk * 32 + 8 * g);
+            }
+#pragma unroll
+            for (int u = 0; u < READ_TPW; u++) {
+                sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+                dacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (tile[u]) {
+                    const int n = (w * TPW + u) * 16 + c;
+                    const bool in = n < N;
+#pragma unroll
+                    for (int kk = 0; kk < KK; kk++) {
+                        const uint4 kbv = in ? *reinterpret_cast<const uint4*>(Kb + (size_t)n * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
+                        const uint4 vbv = in ? *reinterpret_cast<const uint4*>(Vb + (size_t)n * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
+                        sacc[u] = mfma_k32(qa[kk], kbv, sacc[u]);
+                        dacc[u] = mfma_k32(da[kk], vbv, dacc[u]);
+                    }
+                }
+            }
+        }
+        // ---- (c) softmax statistics per query row over all slots (DPP rows, then the 4 waves)
+        float raw[READ_TPW][4], sc[READ_TPW][4];
+        float mx[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            mx[i] = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < READ_TPW; u++) {
+                raw[u][i] = bf16r(sacc[u][i]);
+                sc[u][i] = raw[u][i] * kvc[u] * scl[i];
+                if ((vmask >> u) & 1u) mx[i] = fmaxf(mx[i], sc[u][i]);
+            }
+            mx[i] = rowmax16(mx[i]);
+        }
+        if (c == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_red[0][w][4 * g + i] = mx[i];
+        }
+        __syncthreads();
+        float inv[4];
+        {
+            float sm[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 4 * g + i;
+                const float M = fmaxf(fmaxf(s_red[0][0][m], s_red[0][1][m]), fmaxf(s_red[0][2][m], s_red[0][3][m]));
+                sm[i] = 0.f;
+#pragma unroll
+                for (int u = 0; u < READ_TPW; u++) {
+                    const float e = ((vmask >> u) & 1u) ? __expf(sc[u][i] - M) : 0.f;
+                    sc[u][i] = e;
+                    sm[i] += e;
+                }
+                sm[i] = rowsum16(sm[i]);
+            }
+            if (c == 0) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) s_red[1][w][4 * g + i] = sm[i];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 4 * g + i;
+                const float S = ((s_red[1][0][m] + s_red[1][1][m]) + s_red[1][2][m]) + s_red[1][3][m];
+                inv[i] = S > 0.f ? 1.f / S : 0.f;
+            }
+        }
+        // att (fp32) in sc, datt = bf16(dO V^T), delta = sum_n att * datt
+        float dat[READ_TPW][4];
+        {
+            float dl[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                dl[i] = 0.f;
+#pragma unroll
+                for (int u = 0; u < READ_TPW; u++) {
+                    sc[u][i] *= inv[i];
+                    dat[u][i] = bf16r(dacc[u][i]);
+                    dl[i] += sc[u][i] * dat[u][i];
+                }
+                dl[i] = rowsum16(dl[i]);
+            }
+            if (c == 0) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) s_red[2][w][4 * g + i] = dl[i];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 4 * g + i;
+                const float delta = ((s_red[2][0][m] + s_red[2][1][m]) + s_red[2][2][m]) + s_red[2][3][m];
+#pragma unroll
+                for (int u = 0; u < READ_TPW; u++) dat[u][i] = sc[u][i] * (dat[u][i] - delta);   // dsc
+            }
+        }
+        // draw = bf16(dsc * kinv * scale), P = bf16(att); dkinv / dscale partials
+        uint2 drB[READ_TPW], pB[READ_TPW];
+        float dsl[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < READ_TPW; u++) {
+            float dr[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float dsc = dat[u][i];
+                dr[i] = dsc * kvc[u] * scl[i];
+                dkinv_acc[u] += dsc * raw[u][i] * scl[i];
+                dsl[i] += dsc * raw[u][i] * kvc[u];
+            }
+            drB[u].x = pack2(dr[0], dr[1]);
+            drB[u].y = pack2(dr[2], dr[3]);
+            pB[u].x = pack2(sc[u][0], sc[u][1]);
+            pB[u].y = pack2(sc[u][2], sc[u][3]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) dsl[i] = rowsum16(dsl[i]);
+        if (c == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_dsc[w][4 * g + i] = dsl[i];
+        }
+        // ---- (d) dK^T = Q^T draw and dV^T = dO^T P, per (slot tile, dim tile)
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const uint2 qT = gather4(s_q + (4 * g) * TST + dt * 16 + c, TST);    // A: row dim 16dt + c, k = query 4g + i
+            const uint2 dT = gather4(s_do + (4 * g) * TST + dt * 16 + c, TST);
+#pragma unroll
+            for (int u = 0; u < READ_TPW; u++) {
+                if (!tile[u]) continue;
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (ACC) {
+                    acc_dk[u][dt] = mfma_k16(qT, drB[u], acc_dk[u][dt]);
+                    acc_dv[u][dt] = mfma_k16(dT, pB[u], acc_dv[u][dt]);
+                } else {
+                    const f32x4 gk = mfma_k16(qT, drB[u], z);
+                    const f32x4 gv = mfma_k16(dT, pB[u], z);
+                    // D layout: row dim 16dt + 4g + i, column slot 16 nt + c -> 4 consecutive dims of one slot
+                    const int n = (w * TPW + u) * 16 + c;
+                    if (n < N) {
+                        uint2 xk, xv;
+                        xk.x = pack2(gk[0], gk[1]); xk.y = pack2(gk[2], gk[3]);
+                        xv.x = pack2(gv[0], gv[1]); xv.y = pack2(gv[2], gv[3]);
+                        *reinterpret_cast<uint2*>(dKb + (size_t)n * D + dt * 16 + 4 * g) = xk;
+                        *reinterpret_cast<uint2*>(dVb + (size_t)n * D + dt * 16 + 4 * g) = xv;
+                    }
+                }
+            }
+        }
+        // ---- (e) dQ^T partial = K^T draw^T over this wave's slots
+        bf16_t* dr_t = s_dr[w];
+#pragma unroll
+        for (int u = 0; u < READ_TPW; u++) {                 // draw tile [query m][slot], row = m
+            const uint32_t v2[2] = {drB[u].x, drB[u].y};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                dr_t[(4 * g + i) * RST + u * 16 + c] = (bf16_t)(v2[i >> 1] >> (16 * (i & 1)));
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < READ_TPW; u++) {
+                if (!tile[u]) continue;
+                const int nb = (w * TPW + u) * 16 + 4 * g;       // A: row dim 16dt + c, k = slot nb + i
+                uint2 kT = make_uint2(0, 0);
+                if (nb + 3 < N) {
+                    kT = gather4(Kb + (size_t)nb * D + dt * 16 + c, D);
+                } else {
+                    uint32_t e4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) e4[i] = nb + i < N ? Kb[(size_t)(nb + i) * D + dt * 16 + c] : 0u;
+                    kT.x = e4[0] | (e4[1] << 16);
+                    kT.y = e4[2] | (e4[3] << 16);
+                }
+                const uint2 drT = *reinterpret_cast<const uint2*>(dr_t + c * RST + u * 16 + 4 * g);   // B: k = slot, column m = c
+                o = mfma_k16(kT, drT, o);
+            }
+            *reinterpret_cast<f32x4*>(s_part + (w * 16 + c) * OST + dt * 16 + 4 * g) = o;
+        }
+        __syncthreads();
+        {
+            constexpr int EPT = D / 16;
+            const int mr = threadIdx.x >> 4, dc = (threadIdx.x & 15) * EPT;
+            const int mm = m0 + mr;
+            if (mm < Mblk) {
+                float r[EPT];
+#pragma unroll
+                for (int e = 0; e < EPT; e++) r[e] = s_part[mr * OST + dc + e];
+#pragma unroll
+                for (int ww = 1; ww < READ_WAVES; ww++)
+#pragma unroll
+                    for (int e = 0; e < EPT; e++) r[e] += s_part[(ww * 16 + mr) * OST + dc + e];
+                const size_t row = (((size_t)b * a.T + t0 + mm / a.NQ) * a.H + h) * a.NQ + (mm % a.NQ);
+                bf16_t* dst = a.dq + row * D + dc;
+                if constexpr (EPT == 8) {
+                    uint4 x;
+                    x.x = pack2(r[0], r[1]); x.y = pack2(r[2], r[3]); x.z = pack2(r[4], r[5]); x.w = pack2(r[6], r[7]);
+                    *reinterpret_cast<uint4*>(dst) = x;
+                } else {
+                    uint2 x;
+                    x.x = pack2(r[0], r[1]); x.y = pack2(r[2], r[3]);
+                    *reinterpret_cast<uint2*>(dst) = x;
+                }
+                if ((threadIdx.x & 15) == 0)
+                    a.dscale[row] = ((s_dsc[0][mr] + s_dsc[1][mr]) + s_dsc[2][mr]) + s_dsc[3][mr];
+            }
+        }
+    }
+    // ---- dkinv per slot: this lane's column, summed over the 4 query row groups
+#pragma unroll
+    for (int u = 0; u < READ_TPW; u++) {
+        const float v = sum4rows(dkinv_acc[u]);
+        const int n = (w * TPW + u) * 16 + c;
+        if (tile[u] && g == 0 && n < N) a.dkinv[(size_t)slab * N + n] = v;
+    }
+    if constexpr (ACC) {
+#pragma unroll
+        for (int u = 0; u < READ_TPW; u++) {
+            const int n = (w * TPW + u) * 16 + c;
+            if (!tile[u] || n >= N) continue;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                uint2 xk, xv;
+                xk.x = pack2(acc_dk[u][dt][0], acc_dk[u][dt][1]); xk.y = pack2(acc_dk[u][dt][2], acc_dk[u][dt][3]);
+                xv.x = pack2(acc_dv[u][dt][0], acc_dv[u][dt][1]); xv.y = pack2(acc_dv[u][dt][2], acc_dv[u][dt][3]);
+                *reinterpret_cast<uint2*>(dKb + (size_t)n * D + dt * 16 + 4 * g) = xk;
+                *reinterpret_cast<uint2*>(dVb + (size_t)n * D + dt * 16 + 4 * g) = xv;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+// ======================================================================================== C-ABI
+
+static int check_read(int64_t B, int64_t T, int64_t H, int64_t NQ, int64_t N, int64_t D, int64_t G) {
+    if (B < 1 || T < 1 || H < 1 || NQ < 1 || N < 1 || G < 1)
+        return fail(SLOTSCAN_ERR_SHAPE, "slotread: B, T, H, NQ, N and G must be >= 1");
+    if (D != 64 && D != 128) return fail(SLOTSCAN_ERR_SHAPE, "slotread: D must be 64 or 128");
+    if (N > READ_WAVES * READ_TPW * 16) return fail(SLOTSCAN_ERR_SHAPE, "slotread: N must be <= 192");
+    const int64_t NB = (T + G - 1) / G;
+    if (B * NB * H > 0x7fffffffLL || G * NQ > 0x7fffffffLL)
+        return fail(SLOTSCAN_ERR_SHAPE, "slotread: B*NB*H and G*NQ must fit in int32");
+    return 0;
+}
+
+// query rows per workgroup: enough workgroups to fill 256 CUs a few times over, at least one 16-row tile
+static int read_rows_per_wg(int64_t slabs, int64_t Mfull) {
+    const int64_t tiles = (Mfull + 15) / 16;
+    int64_t split = (768 + slabs - 1) / slabs;
+    if (split > tiles) split = tiles;
+    if (split < 1) split = 1;
+    const int64_t per = (tiles + split - 1) / split;
+    return (int)(per * 16);
+}
+
+extern "C" int slotread_fwd(const void* q, const void* kbuf, const void* vbuf, const float* kinv,
+                            const uint8_t* valid, const float* scale, int64_t B, int64_t T, int64_t H, int64_t NQ,
+                            int64_t N, int64_t D, int64_t G, void* rd, void* stream) {
+    if (int r = check_read(B, T, H, NQ, N, D, G)) return r;
+    if (!q || !kbuf || !vbuf || !kinv || !valid || !scale || !rd)
+        return fail(SLOTSCAN_ERR_NULL, "slotread_fwd: a required pointer is NULL");
+    if (!al16(q) || !al16(kbuf) || !al16(vbuf) || !al16(rd))
+        return fail(SLOTSCAN_ERR_ALIGN, "slotread_fwd: q, kbuf, vbuf and rd must be 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t NB = (T + G - 1) / G;
+    const int64_t slabs = B * NB * H;
+    const int MC = read_rows_per_wg(slabs, G * NQ);
+    const int64_t ysplit = (G * NQ + MC - 1) / MC;
+    ReadFwdArgs ra{(const bf16_t*)q, (const bf16_t*)kbuf, (const bf16_t*)vbuf, kinv, valid, scale, (bf16_t*)rd,
+                   (int)T, (int)H, (int)NQ, (int)N, (int)G, (int)NB, MC};
+    dim3 grid((unsigned)slabs, (unsigned)ysplit), block(READ_THREADS);
+    hipError_t e;
+    {
+        slothost::Scope sc(SLOTSCAN_K_READ_FWD, st);
+        if (D == 128) hipLaunchKernelGGL(read_fwd<128>, grid, block, 0, st, ra);
+        else hipLaunchKernelGGL(read_fwd<64>, grid, block, 0, st, ra);
+        e = hipGetLastError();
+    }
+    if (e != hipSuccess) return hip_fail(e, "read_fwd launch");
+    return 0;
+}
+
+extern "C" int slotread_bwd(const void* q, const void* kbuf, const void* vbuf, const float* kinv,
+                            const uint8_t* valid, const float* scale, const void* drd, int64_t B, int64_t T,
+                            int64_t H, int64_t NQ, int64_t N, int64_t D, int64_t G, void* dq, void* dkbuf,
+                            void* dvbuf, float* dkinv, float* dscale, void* stream) {
+    if (int r = check_read(B, T, H, NQ, N, D, G)) return r;
+    if (!q || !kbuf || !vbuf || !kinv || !valid || !scale || !drd || !dq || !dkbuf || !dvbuf || !dkinv || !dscale)
+        return fail(SLOTSCAN_ERR_NULL, "slotread_bwd: a required pointer is NULL");
+    if (!al16(q) || !al16(kbuf) || !al16(vbuf) || !al16(drd) || !al16(dq) || ((uintptr_t)dkbuf & 7u) ||
+        ((uintptr_t)dvbuf & 7u))
+        return fail(SLOTSCAN_ERR_ALIGN, "slotread_bwd: q, kbuf, vbuf, drd, dq must be 16-byte aligned (dkbuf, dvbuf 8)");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t NB = (T + G - 1) / G;
+    ReadBwdArgs ra{(const bf16_t*)q, (const bf16_t*)kbuf, (const bf16_t*)vbuf, kinv, valid, scale,
+                   (const bf16_t*)drd, (bf16_t*)dq, (bf16_t*)dkbuf, (bf16_t*)dvbuf, dkinv, dscale,
+                   (int)T, (int)H, (int)NQ, (int)N, (int)G, (int)NB};
+    dim3 grid((unsigned)(B * NB * H)), block(READ_THREADS);
+    const bool acc = G * NQ > 16;
+    hipError_t e;
+    {
+        slothost::Scope sc(SLOTSCAN_K_READ_BWD, st);
+        if (D == 128) {
+            if (acc) hipLaunchKernelGGL((read_bwd<128, true>), grid, block, 0, st, ra);
+            else hipLaunchKernelGGL((read_bwd<128, false>), grid, block, 0, st, ra);
+        } else {
+            if (acc) hipLaunchKernelGGL((read_bwd<64, true>), grid, block, 0, st, ra);
+            else hipLaunchKernelGGL((read_bwd<64, false>), grid, block, 0, st, ra);
+        }
+        e = hipGetLastError();
+    }
+    if (e != hipSuccess) return hip_fail(e, "read_bwd launch");
+    return 0;
+}

@@ -994,6 +994,7 @@ hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
 
 // ======================================================================================== C-ABI
 #include "slotscan.h"
+#include "slot_host.h"
 #include <mutex>
 #include <vector>
 
@@ -1011,24 +1012,37 @@ hipEvent_t get() {
     if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
 }
-struct Scope {
-    int kid; hipStream_t st; hipEvent_t a = nullptr;
-    Scope(int k, hipStream_t s) : kid(k), st(s) {
-        if (!on) return;
-        std::lock_guard<std::mutex> g(mu);
-        a = get();
-        if (a) hipEventRecord(a, st);
-    }
-    ~Scope() {
-        if (!a) return;
-        std::lock_guard<std::mutex> g(mu);
-        hipEvent_t b = get();
-        if (!b) return;
-        hipEventRecord(b, st);
-        recs.push_back({kid, a, b});
-    }
-};
 }  // namespace slotprof
+
+namespace slothost {
+Scope::Scope(int k, hipStream_t s) : kid(k), st(s) {
+    if (!slotprof::on) return;
+    std::lock_guard<std::mutex> g(slotprof::mu);
+    a = slotprof::get();
+    if (a) hipEventRecord(a, st);
+}
+Scope::~Scope() {
+    if (!a) return;
+    std::lock_guard<std::mutex> g(slotprof::mu);
+    hipEvent_t b = slotprof::get();
+    if (!b) return;
+    hipEventRecord(b, st);
+    slotprof::recs.push_back({kid, a, b});
+}
+
+static thread_local char g_err[512];
+int fail(int code, const char* msg) {
+    snprintf(g_err, sizeof g_err, "%s", msg);
+    return code;
+}
+int hip_fail(hipError_t e, const char* where) {
+    snprintf(g_err, sizeof g_err, "%s: %s", where, hipGetErrorString(e));
+    return SLOTSCAN_ERR_HIP;
+}
+}  // namespace slothost
+using slothost::fail;
+using slothost::hip_fail;
+using slothost::al16;
 
 extern "C" int slotscan_profile(int enable) {
     std::lock_guard<std::mutex> g(slotprof::mu);
@@ -1051,17 +1065,7 @@ extern "C" int slotscan_profile_read(double* total_ms, int64_t* count, int nk) {
     return rc;
 }
 
-static thread_local char g_err[512];
-static int fail(int code, const char* msg) {
-    snprintf(g_err, sizeof g_err, "%s", msg);
-    return code;
-}
-static int hip_fail(hipError_t e, const char* where) {
-    snprintf(g_err, sizeof g_err, "%s: %s", where, hipGetErrorString(e));
-    return SLOTSCAN_ERR_HIP;
-}
-
-extern "C" const char* slotscan_last_error(void) { return g_err; }
+extern "C" const char* slotscan_last_error(void) { return slothost::g_err; }
 extern "C" int slotscan_max_slots(int64_t D) { (void)D; return SLOTSCAN_MAX_SLOTS; }
 
 static int check_common(int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G, int dtype) {
@@ -1072,7 +1076,6 @@ static int check_common(int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, i
     if (B * H > 0x7fffffffLL || T > 0x7fffffffLL) return fail(SLOTSCAN_ERR_SHAPE, "B*H and T must fit in int32");
     return 0;
 }
-static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dtype,
                             const float* gate, const float* fr, int fr_per_token, const float* temp,
@@ -1097,7 +1100,7 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
                     (int)T, (int)H, (int)N, (int)G, NB, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0};
     hipError_t e;
     {
-        slotprof::Scope sc(SLOTSCAN_K_CHAIN_FWD, st);
+        slothost::Scope sc(SLOTSCAN_K_CHAIN_FWD, st);
         if (D == 128) e = dtype == SLOTSCAN_BF16 ? launch_chain_fwd<128, bf16_t>(ca, (int)B, st) : launch_chain_fwd<128, float>(ca, (int)B, st);
         else e = dtype == SLOTSCAN_BF16 ? launch_chain_fwd<64, bf16_t>(ca, (int)B, st) : launch_chain_fwd<64, float>(ca, (int)B, st);
     }
@@ -1105,7 +1108,7 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
     RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB};
     dim3 grid((unsigned)(B * H), (unsigned)((N + 31) / 32)), block(512);
     {
-        slotprof::Scope sc(SLOTSCAN_K_ROWS_FWD, st);
+        slothost::Scope sc(SLOTSCAN_K_ROWS_FWD, st);
         if (D == 128) {
             if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_fwd<128, bf16_t>), grid, block, 0, st, ra);
             else hipLaunchKernelGGL((rows_fwd<128, float>), grid, block, 0, st, ra);
@@ -1151,7 +1154,7 @@ extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dty
     dim3 grid((unsigned)(B * H), (unsigned)((N + 31) / 32)), block(512);
     hipError_t e;
     {
-        slotprof::Scope sc(SLOTSCAN_K_ROWS_BWD, st);
+        slothost::Scope sc(SLOTSCAN_K_ROWS_BWD, st);
         if (D == 128) {
             if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_bwd<128, bf16_t>), grid, block, 0, st, ra);
             else hipLaunchKernelGGL((rows_bwd<128, float>), grid, block, 0, st, ra);
@@ -1165,13 +1168,13 @@ extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dty
     ChainBwdArgs ca{q, gate, fr, temp, am, kold, oold, cslog, kfin, ofin, dn, dq, dgate, dfr, part,
                     (int)T, (int)H, (int)N, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0};
     {
-        slotprof::Scope sc(SLOTSCAN_K_CHAIN_BWD, st);
+        slothost::Scope sc(SLOTSCAN_K_CHAIN_BWD, st);
         if (D == 128) e = dtype == SLOTSCAN_BF16 ? launch_chain_bwd<128, bf16_t>(ca, (int)B, st) : launch_chain_bwd<128, float>(ca, (int)B, st);
         else e = dtype == SLOTSCAN_BF16 ? launch_chain_bwd<64, bf16_t>(ca, (int)B, st) : launch_chain_bwd<64, float>(ca, (int)B, st);
     }
     if (e != hipSuccess) return hip_fail(e, "chain_bwd launch");
     {
-        slotprof::Scope sc(SLOTSCAN_K_REDUCE, st);
+        slothost::Scope sc(SLOTSCAN_K_REDUCE, st);
         hipLaunchKernelGGL(reduce_parts, dim3(1), dim3(256), 0, st, part, (int)(B * H), dtemp,
                            fr_per_token ? (float*)nullptr : dfr);
         e = hipGetLastError();

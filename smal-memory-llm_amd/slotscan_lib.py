@@ -1,4 +1,4 @@
-"""ctypes binding of libslotscan.so (declarations: include/slotscan.h).
+"""ctypes binding of libslotscan.so (declarations: include/slotscan.h, include/slotread.h).
 
 torch is imported BEFORE the library is opened: libslotscan.so needs libamdhip64.so.7 by SONAME, and with
 torch loaded first the dynamic loader binds it to torch's own HIP runtime, so the streams and device
@@ -34,6 +34,9 @@ SIGNATURES = {
                             _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "slotread_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "slotread_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _vp, _vp, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None
