@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Slot-scan fwd+bwd throughput on one MI355X (BASELINE metric, config 2).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config3]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config3*|config4]
 
 One step = one hard-address slot scan forward (kv_scan_c) plus its backward (torch.autograd.grad of the two
 snapshot outputs against fixed upstream gradients) over one synthetic batch already resident in HBM:
@@ -9,6 +9,9 @@ B=64, T=1024 (65,536 tokens), H=6 heads, N=192 slots, DK=DV=128, G=8, temp=16, p
 hard, detached address (the reference's training setting, run_sh25.sh:213, 222-224).  k, q, v are bf16
 N(0,1) with k and q L2-normalised, gate = sigmoid(N(0,1.5)) bf16, fr ~ U[0,2) bf16, upstream gradients
 N(0,1) drawn in bf16 and passed as fp32 -- all drawn on the GPU from a seeded generator (seed 1).
+
+--workload config4 measures the read instead: one step = the 6 independent reader-layer reads of the frozen
+store, forward only, with the read kernel's HBM and MFMA fractions.
 
 Prints ONE JSON line.  `value` is tokens/s over the K timed steps; `roofline` is the dominant kernel's
 algorithmic HBM bytes per launch over its average launch time, measured with HIP events recorded inside the
@@ -29,10 +32,18 @@ for _p in (ROOT, PKG):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 
 WORKLOADS = {
-    "config2": dict(B=64, T=1024, H=6, N=192, D=128, G=8),
-    "config3": dict(B=64, T=1024, H=6, N=96, D=128, G=8),
+    "config2": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8),
+    "config3": dict(kind="scan", B=64, T=1024, H=6, N=96, D=128, G=8),
+    "config3_t512": dict(kind="scan", B=128, T=512, H=6, N=96, D=128, G=8),
+    "config3_t256": dict(kind="scan", B=256, T=256, H=6, N=96, D=128, G=8),
+    "config3_t128": dict(kind="scan", B=512, T=128, H=6, N=96, D=128, G=8),
+    # frozen-store read fan-out: 6 reader layers, one block (NB = 1: G = T), one query per head and token
+    "config4": dict(kind="read", B=64, T=1024, H=6, N=192, D=128, G=1024, NQ=1, layers=6),
+    # one reader layer of training at the config-2 memory: G = 8 tokens per block, NQ = 2, forward + backward
+    "read_train": dict(kind="read", B=64, T=1024, H=6, N=192, D=128, G=8, NQ=2, layers=1, backward=True),
 }
 
 
@@ -52,6 +63,24 @@ def algorithmic_bytes(B, T, H, N, D, G):
     }
     step = (3 * row + 2 * tok * 2 + 2 * snap) + (2 * snap + 3 * row + 2 * tok * 2 + 3 * row + 2 * tok * 2)
     return per_kernel, step
+
+
+def read_algorithmic(B, T, H, N, D, NQ, layers, NB=1):
+    """Per-launch (one reader layer) algorithmic bytes and MFMA flops of the forward read: q and rd bf16, the
+    sharpness multiplier as the bf16 value the model holds, one pass over the bf16 copies (NB blocks) and
+    their kinv / valid."""
+    tok = B * T * H * NQ
+    by = tok * (2 * D + 2 * D + 2) + 2 * B * NB * H * N * D * 2 + (B * NB * H * N * 5 if NB > 1 else 0)
+    fl = 2 * 2 * tok * N * D
+    return by, fl
+
+
+def read_bwd_algorithmic(B, T, H, N, D, NQ, NB):
+    """Backward read: q, drd, the two copies, kinv / valid and the multiplier in; dq, dkbuf, dvbuf bf16 and
+    dkinv, dscale out."""
+    tok = B * T * H * NQ
+    cp = B * NB * H * N * D * 2
+    return tok * (2 * D + 2 * D + 2) + 2 * cp + B * NB * H * N * 5 + tok * 2 * D + 2 * cp + B * NB * H * N * 4 + tok * 4
 
 
 def measured_traffic(workload):
@@ -93,6 +122,105 @@ def cpu_baseline(W, seed=1, Bs=12):
                        f"fwd+bwd, {dt:.1f} s", seconds=round(dt, 2))
 
 
+def cpu_baseline_read(W, seed=3, Bs=32):
+    """The numpy oracle read (oracle/read_oracle.py, fp64 einsums with the bf16 roundings), one reader layer
+    on a B-slice of the workload."""
+    import numpy as np
+    from oracle import read_oracle as RO
+    T, H, N, D, NQ = W["T"], W["H"], W["N"], W["D"], W["NQ"]
+    rng = np.random.default_rng(seed)
+    unit = lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True)
+    K = unit(rng.standard_normal((Bs, 1, H, N, D)))
+    V = rng.standard_normal((Bs, 1, H, N, D))
+    q = unit(rng.standard_normal((Bs, 1, H, T * NQ, D)))
+    sc = np.log1p(np.exp(rng.standard_normal((Bs, 1, H, T * NQ)))) + 1.0
+    kinv = np.ones((Bs, 1, H, N))
+    valid = np.ones((Bs, 1, H, N), bool)
+    t0 = time.perf_counter()
+    RO.read_forward(q, K, V, kinv, valid, sc, bf16=True)
+    dt = time.perf_counter() - t0
+    return dict(value=round(Bs * T / dt, 1), unit="tokens/s (one reader layer)", cores=1, kind="port",
+                sample=f"B={Bs} slice, one reader layer (T={T}, H={H}, N={N}, D={D}), numpy oracle read, {dt:.2f} s",
+                seconds=round(dt, 2))
+
+
+def bench_read(args, W):
+    import torch
+    import slotread_hip as RH
+    import slotscan_lib as L
+
+    B, T, H, N, D, G, NQ, layers = (W[x] for x in ("B", "T", "H", "N", "D", "G", "NQ", "layers"))
+    NB = (T + G - 1) // G
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=gen)
+    unit = lambda x: x / x.norm(dim=-1, keepdim=True)
+    K = unit(rn(B, NB, H, N, D)).to(torch.bfloat16)
+    V = rn(B, NB, H, N, D).to(torch.bfloat16)
+    kinv = torch.ones(B, NB, H, N, device=dev)
+    valid = torch.ones(B, NB, H, N, device=dev, dtype=torch.bool)
+    qs = [unit(rn(B, T, H, NQ, D)).to(torch.bfloat16) for _ in range(layers)]
+    scs = [torch.nn.functional.softplus(rn(B, T, H, NQ)) + 1.0 for _ in range(layers)]
+    bwd = W.get("backward", False)
+    if bwd:
+        K.requires_grad_()
+        V.requires_grad_()
+        for x in qs + scs:
+            x.requires_grad_()
+        drd = rn(B, T, H, NQ, D).to(torch.bfloat16)
+
+    def step():
+        if bwd:
+            rd = RH.slot_read(qs[0], K, V, kinv, valid, scs[0], G)
+            return torch.autograd.grad(rd, (qs[0], K, V, scs[0]), drd)
+        with torch.no_grad():
+            return [RH.slot_read(qs[i], K, V, kinv, valid, scs[i], G) for i in range(layers)]
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    L.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    L.profile(False)
+    prof = L.profile_read()
+    ms = (t1 - t0) * 1e3 / args.steps
+    tot, cnt = prof["read_fwd"]
+    kms = tot / cnt
+    by, fl = read_algorithmic(B, T, H, N, D, NQ, layers, NB)
+    ach = by / (kms * 1e-3) / 1e9
+    out = {
+        "metric": "slot-read fan-out tokens/s (6 reader layers, frozen store B64 H6 S192 d128, forward)",
+        "value": round(B * T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded GPU generator, seed 3)",
+        "config": {"workload": args.workload, "B": B, "T": T, "H": H, "N": N, "D": D, "NQ": NQ, "G": G,
+                   "layers": layers, "tokens_per_step": B * T},
+        "roofline": {"bound": "hbm", "kernel": "read_fwd", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic(args.workload).get("read_fwd"),
+                     "algorithmic_bytes_per_launch": by, "avg_launch_ms": round(kms, 4),
+                     "mfma_tflops": round(fl / (kms * 1e-3) / 1e12, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                     "mfma_frac": round(fl / (kms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "kernels_ms": {n: round(x / c, 4) for n, (x, c) in prof.items()},
+    }
+    if bwd:
+        bt, bc = prof["read_bwd"]
+        bby = read_bwd_algorithmic(B, T, H, N, D, NQ, NB)
+        out["metric"] = "slot-read fwd+bwd tokens/s (one reader layer, training shape G8 NQ2, B64 H6 S192 d128)"
+        out["read_bwd_roofline"] = {"achieved": round(bby / (bt / bc * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBPS,
+                                    "unit": "GB/s", "frac": round(bby / (bt / bc * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                                    "algorithmic_bytes_per_launch": bby, "avg_launch_ms": round(bt / bc, 4)}
+    if not args.no_cpu and not bwd:
+        out["cpu_baseline"] = cpu_baseline_read(W)
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,11 +238,14 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    W = WORKLOADS[args.workload]
+    if W["kind"] == "read":
+        return bench_read(args, W)
+
     import torch
     import slotkern_hip as KH
     import slotscan_lib as L
 
-    W = WORKLOADS[args.workload]
     B, T, H, N, D, G = (W[x] for x in ("B", "T", "H", "N", "D", "G"))
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(1)

@@ -13,13 +13,19 @@ typedef uint16_t bf16_t;
 
 __device__ __forceinline__ float bf2f(bf16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
-// float -> bfloat16, round to nearest even, NaN kept quiet (same rounding as torch's .to(torch.bfloat16))
-__device__ __forceinline__ bf16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (bf16_t)(u >> 16);
+// float -> bfloat16, round to nearest even (torch's .to(torch.bfloat16) rounding); gfx950 converts in
+// hardware (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
+// two floats -> packed bfloat16 pair (lo in bits 0-15), one v_cvt_pk_bf16_f32
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+// float rounded to the nearest bfloat16, returned as float
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float((uint32_t)f2bf(x) << 16); }
 
 // ---- 4-element vector access in the input / output element type --------------------------------------
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -31,8 +37,8 @@ __device__ __forceinline__ float4 ld4(const bf16_t* p) {
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 __device__ __forceinline__ void st4(bf16_t* p, float4 v) {
     uint2 r;
-    r.x = (uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16);
-    r.y = (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16);
+    r.x = pack_bf16x2(v.x, v.y);
+    r.y = pack_bf16x2(v.z, v.w);
     *reinterpret_cast<uint2*>(p) = r;
 }
 // streaming (write-once) store of a float4: non-temporal, so the snapshot stream does not evict the

@@ -50,10 +50,9 @@ __device__ __forceinline__ f32x4 mfma_k16(const uint2& a, const uint2& b, f32x4 
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
                                                      0, 0, 0);
 }
-__device__ __forceinline__ float bf16r(float x) { return bf2f(f2bf(x)); }
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-}
+__device__ __forceinline__ float bf16r(float x) { return bf16_round(x); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
+#define LOG2E_F 1.4426950408889634f
 
 // max over the 4 row groups of a wave (lanes c, c+16, c+32, c+48); same permlane pattern as sum4rows
 __device__ __forceinline__ float max4rows(float v) {
@@ -130,26 +129,41 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
         const bool tile = u < TPW && nt < NT16;
         const int nr = nt * 16 + c;                              // A-operand row of this lane
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++)
-            kf[u][kk] = (tile && nr < N) ? *reinterpret_cast<const uint4*>(Kb + (size_t)nr * D + kk * 32 + 8 * g)
-                                         : make_uint4(0, 0, 0, 0);
+        for (int kk = 0; kk < KK; kk++) {                        // clamped address, then select: no branch
+            const uint4 x = *reinterpret_cast<const uint4*>(Kb + (size_t)min(nr, N - 1) * D + kk * 32 + 8 * g);
+            kf[u][kk] = (tile && nr < N) ? x : make_uint4(0, 0, 0, 0);
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+            // both loads issued unconditionally (in range): no load waits on another's result
             const int n = nt * 16 + 4 * g + i;                     // D-layout row of item i
-            const bool ok = tile && n < N && VA[n] != 0;
-            kv[u][i] = ok ? KI[n] : 0.f;
+            const bool in = tile && n < N;
+            const uint8_t va = in ? VA[n] : (uint8_t)0;
+            const float ki = in ? KI[n] : 0.f;
+            const bool ok = va != 0;
+            kv[u][i] = ok ? ki : 0.f;
             vmask |= (ok ? 1u : 0u) << (u * 4 + i);
         }
     }
     bf16_t* sV = reinterpret_cast<bf16_t*>(s_big) + w * (READ_TPW * 16 * VST);
     {
+        // fixed trip count, fully unrolled: all of this wave's value loads are in flight together
+        constexpr int CH = READ_TPW * 16 * (D / 8) / 64;            // 16-byte chunks per lane
         const int nbase = w * TPW * 16;
         const int rows = TPW * 16;
-        for (int e = lane; e < rows * (D / 8); e += 64) {
+        uint4 x[CH];
+#pragma unroll
+        for (int it = 0; it < CH; it++) {
+            const int e = lane + 64 * it;
             const int r = e / (D / 8), cc = e % (D / 8);
             const int n = nbase + r;
-            uint4 x = n < N ? *reinterpret_cast<const uint4*>(Vb + (size_t)n * D + cc * 8) : make_uint4(0, 0, 0, 0);
-            *reinterpret_cast<uint4*>(sV + r * VST + cc * 8) = x;
+            x[it] = (r < rows && n < N) ? *reinterpret_cast<const uint4*>(Vb + (size_t)n * D + cc * 8) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int it = 0; it < CH; it++) {
+            const int e = lane + 64 * it;
+            const int r = e / (D / 8), cc = e % (D / 8);
+            *reinterpret_cast<uint4*>(sV + r * VST + cc * 8) = x[it];
         }
     }
     wave_lds_sync();
@@ -157,18 +171,13 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
 #pragma unroll
     for (int u = 0; u < READ_TPW; u++)
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            if (u < TPW) {
-                const bf16_t* p = sV + (u * 16 + 4 * g) * VST + dt * 16 + c;
-                vf[u][dt].x = (uint32_t)p[0] | ((uint32_t)p[VST] << 16);
-                vf[u][dt].y = (uint32_t)p[2 * VST] | ((uint32_t)p[3 * VST] << 16);
-            } else {
-                vf[u][dt] = make_uint2(0, 0);
-            }
+        for (int dt = 0; dt < DT; dt++) {                       // rows past this wave's tiles are zero
+            const bf16_t* p = sV + (u * 16 + 4 * g) * VST + dt * 16 + c;
+            vf[u][dt].x = (uint32_t)p[0] | ((uint32_t)p[VST] << 16);
+            vf[u][dt].y = (uint32_t)p[2 * VST] | ((uint32_t)p[3 * VST] << 16);
         }
 
     float* sO = reinterpret_cast<float*>(s_big);
-    const bf16_t* qbase = a.q;
     for (int m0 = mlo; m0 < mhi; m0 += 16) {
         // ---- queries of this tile: B operand, lane column = query m0 + c
         const int m = m0 + c;
@@ -178,17 +187,15 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
         uint4 qf[KK];
 #pragma unroll
         for (int kk = 0; kk < KK; kk++)
-            qf[kk] = mok ? *reinterpret_cast<const uint4*>(qbase + qrow * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
+            qf[kk] = mok ? *reinterpret_cast<const uint4*>(a.q + qrow * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
         const float scl = mok ? a.scale[qrow] : 0.f;
 
         f32x4 acc[READ_TPW];
 #pragma unroll
         for (int u = 0; u < READ_TPW; u++) {
             acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (u < TPW && w * TPW + u < NT16) {
 #pragma unroll
-                for (int kk = 0; kk < KK; kk++) acc[u] = mfma_k32(kf[u][kk], qf[kk], acc[u]);
-            }
+            for (int kk = 0; kk < KK; kk++) acc[u] = mfma_k32(kf[u][kk], qf[kk], acc[u]);   // zero keys past N
         }
         // ---- masked softmax over the slots of this lane's query column
         float sc[READ_TPW][4];
@@ -231,7 +238,7 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
             f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < READ_TPW; u++)
-                if (u < TPW && w * TPW + u < NT16) o = mfma_k16(vf[u][dt], pf[u], o);
+                o = mfma_k16(vf[u][dt], pf[u], o);
             *reinterpret_cast<f32x4*>(sO + (w * 16 + c) * OST + dt * 16 + 4 * g) = o;
         }
         __syncthreads();
@@ -264,6 +271,223 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
     }
 }
 
+
+// ------------------------------------------------------------------------------------ wide query blocks
+// Blocks with many queries (the frozen-store fan-out: one block of T*NQ queries per head) invert the split:
+// the workgroup stages the block's keys (row-major) and values (TRANSPOSED, slot-contiguous) in LDS once,
+// and each of its 8 waves owns whole 16-query tiles against ALL slots, so the softmax is wave-local (no
+// workgroup barrier after staging).  Per tile and wave:
+//   S^T = K Q^T     12 x D/32 MFMA 16x16x32, A = key rows from LDS (16 B per lane), B = queries from HBM
+//                   (loaded one tile ahead);
+//   softmax         48 scores per lane (its query column), cross-row permlane max / sum;
+//   O^T = V^T P^T   D/16 x 6 MFMA 16x16x32: B = the probabilities straight from the score tiles (slots
+//                   4g+i of tile 2c and 16+4g+i of tile 2c+1 as the 8 k-slots of lane group g), A = the
+//                   same 8 slots of one value dimension, two 8-byte reads from the transposed LDS copy;
+//   store           4 consecutive dims of one query per lane and tile (8 bytes), token-major.
+#define WIDE_WAVES 8
+#define WIDE_THREADS (64 * WIDE_WAVES)
+#define WIDE_NP 192                              // staged slots (N rounded up to 32, at most 192)
+
+template <int D>
+struct WideSmem {
+    static constexpr int KST = D + 8;            // key row stride (bf16)
+    static constexpr int VTS = WIDE_NP + 8;      // transposed value row stride (bf16)
+};
+
+template <int D>
+__global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
+    constexpr int KK = D / 32;
+    constexpr int DT = D / 16;
+    constexpr int KST = WideSmem<D>::KST;
+    constexpr int VTS = WideSmem<D>::VTS;
+    __shared__ __align__(16) bf16_t sK[WIDE_NP * KST];
+    __shared__ __align__(16) bf16_t sVt[D * VTS];
+    __shared__ __align__(16) float sKV[WIDE_NP];          // kinv of a valid slot, 0 otherwise
+    __shared__ __align__(16) float sMK[WIDE_NP];          // 0 for a valid slot, -inf otherwise
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int slab = blockIdx.x;
+    const int h = slab % a.H;
+    const int j = (slab / a.H) % a.NB;
+    const int b = slab / (a.H * a.NB);
+    const int t0 = j * a.G;
+    const int Mblk = min(a.G, a.T - t0) * a.NQ;
+    const int mlo = blockIdx.y * a.MC;
+    const int mhi = min(Mblk, mlo + a.MC);
+    if (mlo >= mhi) return;
+    const int N = a.N;
+    const bf16_t* Kb = a.kb + (size_t)slab * N * D;
+    const bf16_t* Vb = a.vb + (size_t)slab * N * D;
+
+    // ---- stage keys, transposed values and kinv/valid (rows >= N are zero / invalid)
+    {
+        constexpr int KCH = WIDE_NP * (D / 8) / WIDE_THREADS;           // 16-byte key chunks per thread
+        static_assert(KCH * WIDE_THREADS == WIDE_NP * (D / 8), "key staging must cover every chunk");
+        uint4 xk[KCH];
+#pragma unroll
+        for (int it = 0; it < KCH; it++) {
+            const int e = threadIdx.x + WIDE_THREADS * it;
+            const int n = e / (D / 8), cc = e % (D / 8);
+            xk[it] = n < N ? *reinterpret_cast<const uint4*>(Kb + (size_t)n * D + cc * 8) : make_uint4(0, 0, 0, 0);
+        }
+        // row pairs x 8-dim chunks per thread; the row pair varies fastest across lanes so that the
+        // transposed 4-byte LDS writes of a wave land in consecutive banks
+        constexpr int VTOT = (WIDE_NP / 2) * (D / 8);
+        constexpr int VCH = (VTOT + WIDE_THREADS - 1) / WIDE_THREADS;
+        uint4 v0[VCH], v1[VCH];
+#pragma unroll
+        for (int it = 0; it < VCH; it++) {
+            const int e = min(threadIdx.x + WIDE_THREADS * it, VTOT - 1);
+            const int p = e % (WIDE_NP / 2), cc = e / (WIDE_NP / 2);
+            const int n = 2 * p;
+            v0[it] = n < N ? *reinterpret_cast<const uint4*>(Vb + (size_t)n * D + cc * 8) : make_uint4(0, 0, 0, 0);
+            v1[it] = n + 1 < N ? *reinterpret_cast<const uint4*>(Vb + (size_t)(n + 1) * D + cc * 8) : make_uint4(0, 0, 0, 0);
+        }
+        if (threadIdx.x < WIDE_NP) {
+            const int n = threadIdx.x;
+            const int nc = min(n, N - 1);
+            const uint8_t va = a.valid[(size_t)slab * N + nc];
+            const float ki = a.kinv[(size_t)slab * N + nc];
+            const bool ok = n < N && va != 0;
+            sKV[n] = ok ? ki : 0.f;
+            sMK[n] = ok ? 0.f : -INFINITY;
+        }
+#pragma unroll
+        for (int it = 0; it < KCH; it++) {
+            const int e = threadIdx.x + WIDE_THREADS * it;
+            const int n = e / (D / 8), cc = e % (D / 8);
+            *reinterpret_cast<uint4*>(sK + n * KST + cc * 8) = xk[it];
+        }
+#pragma unroll
+        for (int it = 0; it < VCH; it++) {
+            const int e = threadIdx.x + WIDE_THREADS * it;
+            if (e >= VTOT) break;
+            const int p = e % (WIDE_NP / 2), cc = e / (WIDE_NP / 2);
+            const uint32_t a0[4] = {v0[it].x, v0[it].y, v0[it].z, v0[it].w};
+            const uint32_t a1[4] = {v1[it].x, v1[it].y, v1[it].z, v1[it].w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {                 // dims 8cc + 2q, 8cc + 2q + 1: slots (2p, 2p+1) packed
+                const uint32_t lo = (a0[q] & 0xffffu) | (a1[q] << 16);
+                const uint32_t hi = (a0[q] >> 16) | (a1[q] & 0xffff0000u);
+                *reinterpret_cast<uint32_t*>(sVt + (8 * cc + 2 * q) * VTS + 2 * p) = lo;
+                *reinterpret_cast<uint32_t*>(sVt + (8 * cc + 2 * q + 1) * VTS + 2 * p) = hi;
+            }
+        }
+    }
+    __syncthreads();
+
+    auto load_q = [&](int m0, uint4* qf, float& scl) {
+        const int m = m0 + c;
+        const bool mok = m < mhi;
+        size_t qrow = 0;
+        if (mok) qrow = (((size_t)b * a.T + t0 + m / a.NQ) * a.H + h) * a.NQ + (m % a.NQ);
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++)
+            qf[kk] = mok ? *reinterpret_cast<const uint4*>(a.q + qrow * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
+        scl = mok ? a.scale[qrow] : 0.f;
+    };
+    int m0 = mlo + 16 * w;
+    uint4 qn[KK];
+    float scn = 0.f;
+    if (m0 < mhi) load_q(m0, qn, scn);
+    for (; m0 < mhi; m0 += 16 * WIDE_WAVES) {
+        // an opaque zero offset for the LDS operand reads: keeps the compiler from hoisting all 96 invariant
+        // key / value fragments out of the loop (they would need 384 registers)
+        int lo0 = 0;
+        asm volatile("" : "+v"(lo0));
+        uint4 qf[KK];
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) qf[kk] = qn[kk];
+        const float scl = scn;
+        if (m0 + 16 * WIDE_WAVES < mhi) load_q(m0 + 16 * WIDE_WAVES, qn, scn);
+
+        // ---- scores S^T for all slot tiles: lane column = query m0 + c, items = slots 16nt + 4g + i
+        // k-step outer, slot tile inner: 12 independent accumulation chains keep the MFMA pipe full
+        f32x4 acc[WIDE_NP / 16];
+#pragma unroll
+        for (int nt = 0; nt < WIDE_NP / 16; nt++) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ng = 0; ng < WIDE_NP / 64; ng++) {               // 3 groups of 4 slot tiles
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+                for (int nt = 4 * ng; nt < 4 * ng + 4; nt++) {
+                    // all 192 staged slots, branch-free: rows >= N are zero and marked invalid
+                    const uint4 ka = *reinterpret_cast<const uint4*>(sK + lo0 + (nt * 16 + c) * KST + kk * 32 + 8 * g);
+                    acc[nt] = mfma_k32(ka, qf[kk], acc[nt]);
+                }
+            __builtin_amdgcn_sched_barrier(0);                    // bound the operand prefetch window
+        }
+        // scores in the log2 domain, u = raw * kinv * scale * log2(e) (+ -inf for an invalid slot), so that
+        // exp(s - max s) = exp2(u - max u): 9 VALU operations per score
+        float sc[WIDE_NP / 16][4];
+        float mx = -INFINITY;
+        const float scl2 = scl * LOG2E_F;
+#pragma unroll
+        for (int nt = 0; nt < WIDE_NP / 16; nt++) {
+            const float4 kv = *reinterpret_cast<const float4*>(sKV + lo0 + nt * 16 + 4 * g);
+            const float4 mk = *reinterpret_cast<const float4*>(sMK + lo0 + nt * 16 + 4 * g);
+            const float kvs[4] = {kv.x, kv.y, kv.z, kv.w};
+            const float mks[4] = {mk.x, mk.y, mk.z, mk.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float u = fmaf(bf16r(acc[nt][i]) * kvs[i], scl2, mks[i]);
+                sc[nt][i] = u;
+                mx = fmaxf(mx, u);
+            }
+        }
+        mx = max4rows(mx);
+        const float mxs = mx == -INFINITY ? 0.f : mx;              // no valid slot: every term is exp2(-inf) = 0
+        float sum = 0.f;
+#pragma unroll
+        for (int nt = 0; nt < WIDE_NP / 16; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float e = exp2f(sc[nt][i] - mxs);
+                sc[nt][i] = e;
+                sum += e;
+            }
+        sum = sum4rows(sum);
+        const float inv = sum > 0.f ? 1.f / sum : 0.f;
+        uint4 pB[WIDE_NP / 32];
+#pragma unroll
+        for (int cc = 0; cc < WIDE_NP / 32; cc++) {
+            pB[cc].x = pack2(sc[2 * cc][0] * inv, sc[2 * cc][1] * inv);
+            pB[cc].y = pack2(sc[2 * cc][2] * inv, sc[2 * cc][3] * inv);
+            pB[cc].z = pack2(sc[2 * cc + 1][0] * inv, sc[2 * cc + 1][1] * inv);
+            pB[cc].w = pack2(sc[2 * cc + 1][2] * inv, sc[2 * cc + 1][3] * inv);
+        }
+        // ---- O^T = V^T P^T, one 16-dim tile at a time, stored as 4 dims x 1 query per lane
+        const int m = m0 + c;
+        const bool mok = m < mhi;
+        bf16_t* dst = nullptr;
+        if (mok) dst = a.rd + ((((size_t)b * a.T + t0 + m / a.NQ) * a.H + h) * a.NQ + (m % a.NQ)) * D;
+        f32x4 o[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < WIDE_NP / 32; cc++) {
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const bf16_t* vr = sVt + lo0 + (dt * 16 + c) * VTS + cc * 32 + 4 * g;
+                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+                o[dt] = mfma_k32(make_uint4(lo.x, lo.y, hi.x, hi.y), pB[cc], o[dt]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (mok) {
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                uint2 x;
+                x.x = pack2(o[dt][0], o[dt][1]);
+                x.y = pack2(o[dt][2], o[dt][3]);
+                *reinterpret_cast<uint2*>(dst + dt * 16 + 4 * g) = x;
+            }
+        }
+    }
+}
 
 // ---------------------------------------------------------------------------------------------- backward
 // Adjoint of read_fwd, the straight derivative of the reference's ops (memlm_sh.py:383-395) with the same
@@ -351,8 +575,11 @@ __global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
         const int nt = w * TPW + u;
         tile[u] = u < TPW && nt < NT16;
         const int n = nt * 16 + c;
-        const bool ok = tile[u] && n < N && VA[n] != 0;
-        kvc[u] = ok ? KI[n] : 0.f;
+        const bool in = tile[u] && n < N;
+        const uint8_t va = in ? VA[n] : (uint8_t)0;
+        const float ki = in ? KI[n] : 0.f;
+        const bool ok = va != 0;
+        kvc[u] = ok ? ki : 0.f;
         vmask |= (ok ? 1u : 0u) << u;
     }
     float dkinv_acc[READ_TPW] = {};
@@ -403,16 +630,15 @@ __global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
             for (int u = 0; u < READ_TPW; u++) {
                 sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
                 dacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-                if (tile[u]) {
-                    const int n = (w * TPW + u) * 16 + c;
-                    const bool in = n < N;
+                const int n = (w * TPW + u) * 16 + c;
+                const bool in = tile[u] && n < N;
+                const size_t nc = (size_t)min(n, N - 1) * D;          // clamped address, then select
 #pragma unroll
-                    for (int kk = 0; kk < KK; kk++) {
-                        const uint4 kbv = in ? *reinterpret_cast<const uint4*>(Kb + (size_t)n * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
-                        const uint4 vbv = in ? *reinterpret_cast<const uint4*>(Vb + (size_t)n * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
-                        sacc[u] = mfma_k32(qa[kk], kbv, sacc[u]);
-                        dacc[u] = mfma_k32(da[kk], vbv, dacc[u]);
-                    }
+                for (int kk = 0; kk < KK; kk++) {
+                    const uint4 kx = *reinterpret_cast<const uint4*>(Kb + nc + kk * 32 + 8 * g);
+                    const uint4 vx = *reinterpret_cast<const uint4*>(Vb + nc + kk * 32 + 8 * g);
+                    sacc[u] = mfma_k32(qa[kk], in ? kx : make_uint4(0, 0, 0, 0), sacc[u]);
+                    dacc[u] = mfma_k32(da[kk], in ? vx : make_uint4(0, 0, 0, 0), dacc[u]);
                 }
             }
         }
@@ -521,8 +747,7 @@ __global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
             const uint2 qT = gather4(s_q + (4 * g) * TST + dt * 16 + c, TST);    // A: row dim 16dt + c, k = query 4g + i
             const uint2 dT = gather4(s_do + (4 * g) * TST + dt * 16 + c, TST);
 #pragma unroll
-            for (int u = 0; u < READ_TPW; u++) {
-                if (!tile[u]) continue;
+            for (int u = 0; u < READ_TPW; u++) {                // tiles past N carry zero draw and P
                 const f32x4 z = {0.f, 0.f, 0.f, 0.f};
                 if constexpr (ACC) {
                     acc_dk[u][dt] = mfma_k16(qT, drB[u], acc_dk[u][dt]);
@@ -532,7 +757,7 @@ __global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
                     const f32x4 gv = mfma_k16(dT, pB[u], z);
                     // D layout: row dim 16dt + 4g + i, column slot 16 nt + c -> 4 consecutive dims of one slot
                     const int n = (w * TPW + u) * 16 + c;
-                    if (n < N) {
+                    if (tile[u] && n < N) {
                         uint2 xk, xv;
                         xk.x = pack2(gk[0], gk[1]); xk.y = pack2(gk[2], gk[3]);
                         xv.x = pack2(gv[0], gv[1]); xv.y = pack2(gv[2], gv[3]);
@@ -557,18 +782,16 @@ __global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
             f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < READ_TPW; u++) {
-                if (!tile[u]) continue;
                 const int nb = (w * TPW + u) * 16 + 4 * g;       // A: row dim 16dt + c, k = slot nb + i
-                uint2 kT = make_uint2(0, 0);
-                if (nb + 3 < N) {
-                    kT = gather4(Kb + (size_t)nb * D + dt * 16 + c, D);
-                } else {
-                    uint32_t e4[4];
+                uint32_t e4[4];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) e4[i] = nb + i < N ? Kb[(size_t)(nb + i) * D + dt * 16 + c] : 0u;
-                    kT.x = e4[0] | (e4[1] << 16);
-                    kT.y = e4[2] | (e4[3] << 16);
+                for (int i = 0; i < 4; i++) {                     // clamped address, then select
+                    const uint32_t x = Kb[(size_t)min(nb + i, N - 1) * D + dt * 16 + c];
+                    e4[i] = (tile[u] && nb + i < N) ? x : 0u;
                 }
+                uint2 kT;
+                kT.x = e4[0] | (e4[1] << 16);
+                kT.y = e4[2] | (e4[3] << 16);
                 const uint2 drT = *reinterpret_cast<const uint2*>(dr_t + c * RST + u * 16 + 4 * g);   // B: k = slot, column m = c
                 o = mfma_k16(kT, drT, o);
             }
@@ -643,9 +866,18 @@ static int check_read(int64_t B, int64_t T, int64_t H, int64_t NQ, int64_t N, in
 }
 
 // query rows per workgroup: enough workgroups to fill 256 CUs a few times over, at least one 16-row tile
+#ifndef READ_TARGET_WGS
+#define READ_TARGET_WGS 768
+#endif
+#ifndef READ_WIDE_TARGET_WGS
+#define READ_WIDE_TARGET_WGS 512
+#endif
+#ifndef READ_WIDE_MIN_M
+#define READ_WIDE_MIN_M 256                      // queries per block from which the wide kernel is used
+#endif
 static int read_rows_per_wg(int64_t slabs, int64_t Mfull) {
     const int64_t tiles = (Mfull + 15) / 16;
-    int64_t split = (768 + slabs - 1) / slabs;
+    int64_t split = (READ_TARGET_WGS + slabs - 1) / slabs;
     if (split > tiles) split = tiles;
     if (split < 1) split = 1;
     const int64_t per = (tiles + split - 1) / split;
@@ -671,8 +903,20 @@ extern "C" int slotread_fwd(const void* q, const void* kbuf, const void* vbuf, c
     hipError_t e;
     {
         slothost::Scope sc(SLOTSCAN_K_READ_FWD, st);
-        if (D == 128) hipLaunchKernelGGL(read_fwd<128>, grid, block, 0, st, ra);
-        else hipLaunchKernelGGL(read_fwd<64>, grid, block, 0, st, ra);
+        if (G * NQ >= READ_WIDE_MIN_M) {
+            // many queries per block: each workgroup takes a range of whole 16-query tiles for its 8 waves
+            const int64_t tiles = (G * NQ + 15) / 16;
+            int64_t split = (READ_WIDE_TARGET_WGS + slabs - 1) / slabs;
+            if (split > (tiles + WIDE_WAVES - 1) / WIDE_WAVES) split = (tiles + WIDE_WAVES - 1) / WIDE_WAVES;
+            if (split < 1) split = 1;
+            ra.MC = (int)(((tiles + split - 1) / split) * 16);
+            dim3 wgrid((unsigned)slabs, (unsigned)((G * NQ + ra.MC - 1) / ra.MC)), wblock(WIDE_THREADS);
+            if (D == 128) hipLaunchKernelGGL(read_fwd_wide<128>, wgrid, wblock, 0, st, ra);
+            else hipLaunchKernelGGL(read_fwd_wide<64>, wgrid, wblock, 0, st, ra);
+        } else {
+            if (D == 128) hipLaunchKernelGGL(read_fwd<128>, grid, block, 0, st, ra);
+            else hipLaunchKernelGGL(read_fwd<64>, grid, block, 0, st, ra);
+        }
         e = hipGetLastError();
     }
     if (e != hipSuccess) return hip_fail(e, "read_fwd launch");

@@ -98,6 +98,8 @@ READ_CASES = [  # B, T, H, NQ, N, D, G
     (2, 256, 2, 1, 192, 128, 256),   # frozen store (config 4 shape per head): one block, 16 query tiles
     (1, 1024, 1, 1, 192, 128, 1024), # one slab split over many workgroups
     (1, 37, 3, 3, 17, 64, 5),        # odd everything
+    (2, 300, 2, 1, 40, 64, 300),     # wide-block kernel: partial slot chunk, ragged last query tile
+    (1, 200, 3, 2, 96, 128, 256),    # wide-block kernel with NQ=2 and a partial block (T < G)
 ]
 
 
