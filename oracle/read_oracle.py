@@ -16,8 +16,9 @@ is rounded to bf16 before the value contraction.
 naive_block_read is the reference's own per-token check of the strided read (gqa25/test_sh.py:77-86,
 kvu/test_rs.py:102-112): every token t reads the copy taken at the start of its block, t // G.
 
-fq restates the midrise storage quantiser _fq (memlm_sh.py:221-229) in float32 arithmetic, and
-quantize_mem restates _quantize_mem (memlm_sh.py:231-234).
+fq restates the midrise storage quantiser _fq (memlm_sh.py:221-228) in float32 arithmetic, fq_ste its
+straight-through return value (memlm_sh.py:229), and quantize_mem restates _quantize_mem
+(memlm_sh.py:231-234).
 
 Pinning (tests/test_oracle_read.py): read_forward against naive_block_read (a per-token loop with its
 own indexing), against the textbook identity for one valid row (att = 1 there), all-invalid blocks read
@@ -115,10 +116,18 @@ def fq(x, bits, group):
     return val.reshape(sh), code.astype(np.int8).reshape(sh), s[..., 0]
 
 
+def fq_ste(x, bits, group):
+    """What _fq RETURNS for a float32 x (memlm_sh.py:229): x + (q - x), each operation rounded to float32 --
+    the straight-through expression's forward value, which equals q except where q - x is inexact."""
+    x = np.asarray(x, np.float32)
+    q, _, _ = fq(x, bits, group)
+    return (x + (q - x).astype(np.float32)).astype(np.float32)
+
+
 def quantize_mem(kbuf, buf, bits, group):
     """_quantize_mem (memlm_sh.py:231-234): (kq, vq, kinv, valid) from the float32 copies."""
-    kq, _, _ = fq(kbuf, bits, group)
-    vq, _, _ = fq(buf, bits, group)
+    kq = fq_ste(kbuf, bits, group)
+    vq = fq_ste(buf, bits, group)
     nsq = (kq.astype(np.float32) ** 2).sum(-1, dtype=np.float32)
     kinv = (1.0 / np.sqrt(np.maximum(nsq, np.float32(1e-12)))).astype(np.float32)
     return kq, vq, kinv, nsq > 1e-12

@@ -1,4 +1,4 @@
-"""ctypes binding of libslotscan.so (declarations: include/slotscan.h, include/slotread.h).
+"""ctypes binding of libslotscan.so (declarations: include/slotscan.h, slotread.h, slotmem.h).
 
 torch is imported BEFORE the library is opened: libslotscan.so needs libamdhip64.so.7 by SONAME, and with
 torch loaded first the dynamic loader binds it to torch's own HIP runtime, so the streams and device
@@ -37,6 +37,9 @@ SIGNATURES = {
     "slotread_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "slotread_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _vp, _vp, _vp, _vp, _vp, _vp]),
+    "slotmem_epilogue_fwd": (_i32, [_vp, _vp, _i64, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "slotmem_epilogue_bwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i64, _i32, _vp, _vp, _vp]),
+    "slotmem_codes": (_i32, [_vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp]),
 }
 
 _lib = None
@@ -81,7 +84,8 @@ def dtype_code(dt):
     raise TypeError(f"token dtype {dt} is not supported by the HIP kernels (float32 or bfloat16)")
 
 
-KERNEL_NAMES = ("chain_fwd", "rows_fwd", "rows_bwd", "chain_bwd", "reduce_parts", "read_fwd", "read_bwd", "spare")
+KERNEL_NAMES = ("chain_fwd", "rows_fwd", "rows_bwd", "chain_bwd", "reduce_parts", "read_fwd", "read_bwd", "mem_fwd",
+                "mem_bwd", "spare")
 
 
 def profile(enable):

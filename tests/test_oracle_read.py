@@ -131,3 +131,35 @@ def test_fq_matches_torch_statement():
     qq = (torch.floor(xg / s).clamp(-4, 3) + 0.5) * s
     qq = torch.where(a > 0, qq, torch.zeros_like(qq)).reshape(4, 3, 128)
     np.testing.assert_array_equal(RO.fq(x, 3, 16)[0], qq.numpy())
+
+
+def test_fq_ste_and_quantize_mem_match_torch_statement():
+    """_fq's return value x + (q - x) (memlm_sh.py:229) and _quantize_mem (:231-234) in torch float32 give the
+    oracle's values bit for bit (kinv to rsqrt's last bit)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(11)
+    k = (rng.standard_normal((3, 4, 64)) * 2).astype(np.float32)
+    v = rng.standard_normal((3, 4, 64)).astype(np.float32)
+    k[0, 1] = 0.0
+    k[1, 2, :5] = 1e-9                                       # tiny entries: q - x inexact cases
+    kt, vt = torch.tensor(k), torch.tensor(v)
+
+    def fq(x, bits, group):
+        sh = x.shape
+        xg = x.float().reshape(*sh[:-1], sh[-1] // group, group)
+        a = xg.abs().amax(-1, keepdim=True)
+        half = 2 ** (bits - 1)
+        s = (a / half).clamp_min(1e-30)
+        q = ((torch.floor(xg / s).clamp(-half, half - 1) + 0.5) * s)
+        q = torch.where(a > 0, q, torch.zeros_like(q)).reshape(sh)
+        return x + (q.to(x.dtype) - x).detach()
+
+    for bits, group in ((3, 16), (8, 64), (2, 4)):
+        np.testing.assert_array_equal(RO.fq_ste(k, bits, group), fq(kt, bits, group).numpy())
+        kq = fq(kt, bits, group)
+        nsq = kq.float().pow(2).sum(-1)
+        okq, ovq, oki, ova = RO.quantize_mem(k, v, bits, group)
+        np.testing.assert_array_equal(okq, kq.numpy())
+        np.testing.assert_array_equal(ovq, fq(vt, bits, group).numpy())
+        np.testing.assert_array_equal(ova, (nsq > 1e-12).numpy())
+        np.testing.assert_allclose(oki, torch.rsqrt(nsq.clamp_min(1e-12)).numpy(), rtol=1e-6)
