@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Slot-scan fwd+bwd throughput on one MI355X (BASELINE metric, config 2).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config3*|config4]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config3*|config4|config5]
 
 One step = one hard-address slot scan forward (kv_scan_c) plus its backward (torch.autograd.grad of the two
 snapshot outputs against fixed upstream gradients) over one synthetic batch already resident in HBM:
@@ -42,6 +42,8 @@ WORKLOADS = {
     "config3_t128": dict(kind="scan", B=512, T=128, H=6, N=96, D=128, G=8),
     # frozen-store read fan-out: 6 reader layers, one block (NB = 1: G = T), one query per head and token
     "config4": dict(kind="read", B=64, T=1024, H=6, N=192, D=128, G=1024, NQ=1, layers=6),
+    # long-context streaming: 128 chunks of 1024 tokens, state carried, int8 + per-row fp32 scale emission
+    "config5": dict(kind="stream", B=8, T=131072, H=6, N=192, D=128, G=8, chunk=1024),
     # one reader layer of training at the config-2 memory: G = 8 tokens per block, NQ = 2, forward + backward
     "read_train": dict(kind="read", B=64, T=1024, H=6, N=192, D=128, G=8, NQ=2, layers=1, backward=True),
 }
@@ -144,6 +146,80 @@ def cpu_baseline_read(W, seed=3, Bs=32):
                 seconds=round(dt, 2))
 
 
+def bench_stream(args, W):
+    """Config 5: forward-only streaming scan, 1024-token chunks with the slot state carried, every chunk's
+    snapshot copies emitted as int8 codes + one fp32 scale per row (the storage quantiser, bits 8, group D).
+    The emission of chunk c runs on a second stream while chunk c+1 scans: the scan keeps only B*H = 48
+    workgroups busy, so the quantiser passes fill otherwise idle CUs.  One step = the whole T-token stream."""
+    import torch
+    import slotkern_hip as KH
+    import slotmem_hip as MH
+    import slotscan_lib as L
+
+    B, T, H, N, D, G, C = (W[x] for x in ("B", "T", "H", "N", "D", "G", "chunk"))
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(4)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=gen)
+    unit = lambda x: x / x.norm(dim=-1, keepdim=True)
+    k = unit(rn(B, T, H, D)).to(torch.bfloat16)
+    q = unit(rn(B, T, H, D)).to(torch.bfloat16)
+    v = rn(B, T, H, D).to(torch.bfloat16)
+    gate = torch.sigmoid(rn(B, T, H) * 1.5).to(torch.bfloat16)
+    fr = (torch.rand(B, T, H, device=dev, generator=gen) * 2).to(torch.bfloat16)
+    side = torch.cuda.Stream(device=dev)                  # default priority
+    main = torch.cuda.current_stream(dev)
+
+    def stream_pass():
+        st = None
+        pending = None
+        for t0 in range(0, T, C):
+            sl = slice(t0, t0 + C)
+            kb, vb, st = KH.kv_scan_stream(k[:, sl], v[:, sl], gate[:, sl], fr[:, sl], N, 16.0, G=G, q=q[:, sl],
+                                           occ_bin=True, state=st)
+            ev = torch.cuda.Event()
+            ev.record(main)
+            side.wait_event(ev)
+            with torch.cuda.stream(side):
+                kb.record_stream(side)
+                vb.record_stream(side)
+                pending = (MH.fq_codes(kb, 8, D), MH.fq_codes(vb, 8, D))
+            del kb, vb
+        main.wait_stream(side)
+        return st, pending
+
+    for _ in range(args.warmup):
+        stream_pass()
+    torch.cuda.synchronize()
+    L.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        stream_pass()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    L.profile(False)
+    prof = L.profile_read()
+    ms = (t1 - t0) * 1e3 / args.steps
+    tok = B * T
+    NBc = (C + G - 1) // G
+    per_tok = 3 * H * D * 2 + 2 * H * 2 + 2 * H * N * (D + 4) // G      # inputs + int8 emission with row scales
+    by = tok * per_tok
+    out = {
+        "metric": "streaming slot-scan forward tokens/s (config 5: B8 T131072 H6 S192 d128, int8 + row-scale emission)",
+        "value": round(tok / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 state, bf16 tokens, int8 emission",
+        "data": "synthetic (seeded GPU generator, seed 4)",
+        "config": {"workload": args.workload, "B": B, "T": T, "H": H, "N": N, "D": D, "G": G, "chunk": C,
+                   "chunks": T // C, "snapshots_per_chunk": NBc, "tokens_per_step": tok},
+        "step_roofline": {"algorithmic_bytes": by, "achieved": round(by / (ms * 1e-3) / 1e9, 1),
+                          "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                          "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
+        "kernels_ms": {n: round(x / c, 4) for n, (x, c) in prof.items()},
+        "kernels_total_ms": {n: round(x / args.steps, 3) for n, (x, c) in prof.items()},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def bench_read(args, W):
     import torch
     import slotread_hip as RH
@@ -241,6 +317,8 @@ def main():
     W = WORKLOADS[args.workload]
     if W["kind"] == "read":
         return bench_read(args, W)
+    if W["kind"] == "stream":
+        return bench_stream(args, W)
 
     import torch
     import slotkern_hip as KH

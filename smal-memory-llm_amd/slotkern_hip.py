@@ -27,6 +27,7 @@ setting (run_sh25.sh:213, 222-223) and exactly the mode the reference's CUDA ker
 """
 import torch
 
+import slotmem_hip as MH
 import slotscan_lib as L
 
 _SUPPORTED_D = (64, 128)
@@ -183,3 +184,15 @@ def kv_scan_stream(k, v, gate, fr, N, temp, G=8, hard_gate=False, eps=1e-4, q=No
     kbuf, vbuf, _am, _ko, _vo, _oo, _cs, kfin, vfin, ofin = _fwd(k_, q_, v_, g, fr_, frt, temp_, int(N), int(G),
                                                                  eps, occ_bin, dt, logs=False, state=state)
     return kbuf, vbuf, (kfin, vfin, ofin)
+
+
+@torch.no_grad()
+def kv_scan_stream_q(k, v, gate, fr, N, temp, G=8, hard_gate=False, eps=1e-4, q=None, occ_bin=False, state=None,
+                     bits=8, group=None):
+    """kv_scan_stream with the emitted copies in the storage quantiser's integer form (memlm_sh.py:221-228):
+    returns ((kcodes, kscales), (vcodes, vscales), state_out), codes int8 (B, NB, H, N, D) and fp32 scales
+    (B, NB, H, N, D // group).  bits = 8 with group = D (the default) is one fp32 absmax scale per row."""
+    kbuf, vbuf, st = kv_scan_stream(k, v, gate, fr, N, temp, G=G, hard_gate=hard_gate, eps=eps, q=q,
+                                    occ_bin=occ_bin, state=state)
+    grp = k.shape[-1] if group is None else int(group)
+    return MH.fq_codes(kbuf, bits, grp), MH.fq_codes(vbuf, bits, grp), st

@@ -188,3 +188,27 @@ def test_unsupported_modes_raise():
         KH.kv_scan(k, v, g, fr, 16, TEMP, hard=True, detach_addr=True, occ_bin=True)
     with pytest.raises(NotImplementedError):
         KH.kv_scan_c(k, v, g, fr, 400, TEMP, G=8, hard=True, detach_addr=True, q=q)
+
+
+def test_stream_quantised_emission_equals_quantised_one_shot():
+    """Config 5's emission: chunked scan with int8 + per-row scale copies == the one-shot scan's copies
+    quantised the same way (bitwise), and the codes decode to the storage quantiser's value."""
+    import slotmem_hip as MH
+    B, T, H, N, D, G = 2, 192, 2, 64, 128, 8
+    k, q, v, g, fr = scan_inputs(B, T, H, D, 23)
+    c = lambda x: x.to(DEV)
+    kb1, vb1, _ = KH.kv_scan_stream(c(k), c(v), c(g), c(fr), N, TEMP, G=G, q=c(q), occ_bin=True)
+    kc1, vc1 = MH.fq_codes(kb1, 8, D), MH.fq_codes(vb1, 8, D)
+    st = None
+    parts = []
+    for t0 in range(0, T, 64):
+        sl = slice(t0, t0 + 64)
+        kq, vq, st = KH.kv_scan_stream_q(c(k[:, sl]), c(v[:, sl]), c(g[:, sl]), c(fr[:, sl]), N, TEMP, G=G,
+                                         q=c(q[:, sl]), occ_bin=True, state=st)
+        parts.append((kq, vq))
+    for i, (a, b) in enumerate(((kc1, [p[0] for p in parts]), (vc1, [p[1] for p in parts]))):
+        assert torch.equal(torch.cat([x[0] for x in b], 1), a[0]), i
+        assert torch.equal(torch.cat([x[1] for x in b], 1), a[1]), i
+    dec = MH.fq_decode(kc1[0], kc1[1], D).cpu().numpy()
+    from oracle import read_oracle as RO
+    np.testing.assert_array_equal(dec, RO.fq(kb1.cpu().numpy(), 8, D)[0])
