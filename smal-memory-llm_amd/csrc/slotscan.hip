@@ -953,6 +953,431 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
     }
 }
 
+// ====================================================================================== chain_bwd_w
+// Windowed address backward for the occ_bin mode.  With occupancy entering only through [o >= eps], the
+// adjoint of step t needs no carry from step t + 1: given the replayed occupancy at t, the logged cosines
+// and Dn, every step's softmax adjoint is independent.  The chain is therefore processed in windows of
+// WIN = 16 steps (reverse order), by four waves:
+//   replay   every lane replays the occupancy of its slot rows (n = lane + 64 j) backwards through the
+//            window, recording taken_n(t);
+//   softmax  wave w owns steps 4w .. 4w+3 of the window: the whole masked softmax adjoint of a step (max,
+//            sum e, sum e dw over every row, the lowest free row) is a wave reduction, no cross-wave merge;
+//            W[t][n] = temp dz_n(t) goes to LDS;
+//   dq       wave w owns dims [w D/4, (w+1) D/4): dqn[t][d] = sum_n W[t][n] Kh_n(t)[d] as fp32 MFMA over
+//            the window, with Kh = K / max(|K|, 1e-6) the normalised keys (the reference's order: normalise,
+//            then contract, slotkern_kvt.py:86-90), held in registers in the MFMA B-operand layout as the
+//            keys AFTER the window's writes (Kh_end); the rows the window rewrote are corrected exactly with
+//            the undo deltas d_s = Kh(kold_s) - Kh_{a_s}(after write s), Kh_n(t) = Kh_end_n + sum over
+//            s >= t with a_s = n of d_s, as a second small MFMA (16 x 16 x DW).  Every term is bounded by
+//            |dz| (|Kh| <= 1): an empty row has Kh = 0, never K * 1e6;
+//   undo     every wave restores its dims of each rewritten row from kold (the next window's Kh_end);
+//   dq       the clamped-normalisation Jacobian of q needs <dqn, q> over all of D: one LDS exchange.
+// B-operand layout (v_mfma_f32_16x16x4f32, B[k][j] at lane 16k + j): lane l of wave w holds
+//   Kh[row 4*kk + (l >> 4)][dim w*DW + 16*nb + (l & 15)] = Kv[nb][kk >> 4][kk & 15],  kk < 16*RPL, nb < DW/16.
+// Kv is an array of 16-float register vectors, so the undo can address row kk with a uniform dynamic index
+// (M0-relative moves, s_set_gpr_idx) instead of branching over every possible row.
+// A operand: lane l holds W[step l & 15][row 4*kk + (l >> 4)]; result lane l, register r:
+//   dqn[step 4*(l >> 4) + r][dim w*DW + 16*nb + (l & 15)].
+#define WIN 16
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int D, int RPL, typename TI>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2)))
+void chain_bwd_w(ChainBwdArgs a) {
+    constexpr int NT = 256;                             // 4 waves
+    constexpr int NR = 64 * RPL;                        // slot-row capacity
+    constexpr int KK = NR / 4;                          // MFMA k-steps over the rows
+    constexpr int DW = D / 4;                           // dims per wave
+    constexpr int NBW = DW / 16;                        // MFMA column blocks per wave
+    constexpr int NCH = KK / 16;                        // 16-row-group chunks of a key column block
+    constexpr int SWS = NR + 4;                         // W row stride (conflict-free A-operand reads)
+    constexpr int UKO = (WIN * D / 4 + NT - 1) / NT;    // uint4 per lane: a window's kold rows (fp32)
+    constexpr int EPU = 16 / (int)sizeof(TI);
+    constexpr int UQ = (WIN * D / EPU + NT - 1) / NT;   // uint4 per lane: a window's queries
+    constexpr int UCS = (WIN * NR + NT - 1) / NT;       // floats per lane: a window's cosines
+    constexpr int UDN = (NR * WIN + NT - 1) / NT;       // floats per lane: a window's Dn
+    constexpr bool BF = sizeof(TI) == 2;
+    __shared__ __align__(16) float s_ko[WIN][D];
+    __shared__ __align__(16) float s_q[WIN][D];
+    __shared__ float s_cs[WIN * NR];                    // row stride N
+    __shared__ float s_dn[NR][WIN + 1];
+    __shared__ float s_W[WIN][SWS];
+    __shared__ __align__(16) float s_delta[WIN][D];
+    __shared__ int s_am[WIN];
+    __shared__ float s_g[WIN], s_fr[WIN], s_oo[WIN];
+    __shared__ float2 s_proj[4][WIN];
+    __shared__ float s_fin[2][4];
+
+    const int T = a.T, H = a.H, N = a.N;
+    const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, grp = lane >> 4;
+    const TI* __restrict__ qp = (const TI*)a.q;
+    const size_t tok0 = (size_t)b * T * H + h;
+    const float temp = a.temp[0];
+    const float fr_s = a.frt ? 0.f : a.fr[0];
+    const float eps = a.eps;
+    const bool frt = a.frt != 0;
+    const int d0 = wave * DW;                           // this wave's first dim
+
+    // ---- Kh_end (the final keys, normalised) into the B-operand layout; full-row norms through LDS
+    f32x16 Kv[NBW][NCH];
+#define KREG(kk, nb) Kv[nb][(kk) >> 4][(kk) & 15]
+    {
+        float* s_nrm = &s_W[0][0];                      // [4][NR] scratch before the first window
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) {
+            const int row = 4 * kk + grp;
+            float ss = 0.f;
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++) {
+                const float x = row < N ? a.kfin[((size_t)bh * N + row) * D + d0 + 16 * nb + c] : 0.f;
+                KREG(kk, nb) = x;
+                ss = fmaf(x, x, ss);
+            }
+            ss = rowsum16(ss);
+            if (c == 0) s_nrm[wave * NR + row] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) {
+            const int row = 4 * kk + grp;
+            const float ki = rsq_clamped(((s_nrm[row] + s_nrm[NR + row]) + s_nrm[2 * NR + row]) + s_nrm[3 * NR + row]);
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++) KREG(kk, nb) *= ki;
+        }
+    }
+    float o_me[RPL];
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+        const int n = lane + 64 * j;
+        o_me[j] = n < N ? a.ofin[(size_t)bh * N + n] : 0.f;
+    }
+
+    // ---- window prefetch into registers.  Every load is a uniform (scalar) base plus ONE 32-bit per-lane
+    // offset computed once, so the prefetch costs no per-load address registers.
+    const int nwin = (T + WIN - 1) / WIN;
+    float ncs[UCS], ndn[UDN];
+    uint4 nko[UKO], nq[UQ];
+    float nsc = 0.f;
+    const unsigned off_dn = (unsigned)(tid / WIN) * (unsigned)T + (unsigned)(tid % WIN);
+    constexpr int KR = NT / (D / 4);                     // kold rows per 256-lane pass
+    constexpr int QR = NT / (D / EPU);                   // query rows per pass
+    const unsigned off_ko = (unsigned)(tid / (D / 4)) * (unsigned)(H * D) + 4u * (unsigned)(tid % (D / 4));
+    const unsigned off_q = (unsigned)(tid / (D / EPU)) * (unsigned)(H * D) + (unsigned)EPU * (unsigned)(tid % (D / EPU));
+    auto load_win = [&](int m) {
+        const int t0 = m * WIN, nt = min(WIN, T - t0);
+        const float* csb = a.cslog + ((size_t)bh * T + t0) * N;          // (nt, N) contiguous
+        const int ncsv = nt * N;
+#pragma unroll
+        for (int u2 = 0; u2 < UCS; u2++) {
+            const float* bp = csb + NT * u2;
+            ncs[u2] = (tid + NT * u2 < ncsv) ? bp[(unsigned)tid] : 0.f;
+        }
+        const float* dnb = a.dn + (size_t)bh * N * T + t0;               // row n at + n * T
+#pragma unroll
+        for (int u2 = 0; u2 < UDN; u2++) {
+            const float* bp = dnb + (size_t)(NT / WIN) * u2 * T;
+            const int nn = tid / WIN + (NT / WIN) * u2;
+            ndn[u2] = (tid % WIN < nt && nn < N) ? bp[off_dn] : 0.f;
+        }
+        const float* kob = a.kold + (tok0 + (size_t)t0 * H) * D;
+#pragma unroll
+        for (int u2 = 0; u2 < UKO; u2++) {
+            const float* bp = kob + (size_t)KR * u2 * H * D;
+            const int i = tid / (D / 4) + KR * u2;
+            nko[u2] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < nt) nko[u2] = *reinterpret_cast<const uint4*>(bp + off_ko);
+        }
+        const TI* qb = qp + (tok0 + (size_t)t0 * H) * D;
+#pragma unroll
+        for (int u2 = 0; u2 < UQ; u2++) {
+            const TI* bp = qb + (size_t)QR * u2 * H * D;
+            const int i = tid / (D / EPU) + QR * u2;
+            nq[u2] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < nt) nq[u2] = *reinterpret_cast<const uint4*>(bp + off_q);
+        }
+        if (tid < 4 * WIN) {
+            const int kind = tid / WIN, i = tid % WIN;
+            nsc = kind == 0 ? __int_as_float(-1) : 0.f;
+            if (i < nt) {
+                const size_t ix = tok0 + (size_t)(t0 + i) * H;
+                nsc = kind == 0 ? __int_as_float(a.am[ix]) : kind == 1 ? a.gate[ix]
+                    : kind == 2 ? (frt ? a.fr[ix] : 0.f) : a.oold[ix];
+            }
+        }
+    };
+
+    float dtemp_acc = 0.f, dfr_acc = 0.f;
+    load_win(nwin - 1);
+    for (int m = nwin - 1; m >= 0; m--) {
+        const int t0 = m * WIN, nt = min(WIN, T - t0);
+        // S1: publish the prefetched window into LDS
+#pragma unroll
+        for (int u2 = 0; u2 < UCS; u2++) {
+            const int u = tid + NT * u2;
+            if (u < WIN * NR) s_cs[u] = ncs[u2];
+        }
+#pragma unroll
+        for (int u2 = 0; u2 < UDN; u2++) {
+            const int u = tid + NT * u2;
+            if (u < NR * WIN) s_dn[u / WIN][u % WIN] = ndn[u2];
+        }
+#pragma unroll
+        for (int u2 = 0; u2 < UKO; u2++) {
+            const int u = tid + NT * u2;
+            if (u < WIN * D / 4) *reinterpret_cast<uint4*>(&s_ko[u / (D / 4)][(u % (D / 4)) * 4]) = nko[u2];
+        }
+#pragma unroll
+        for (int u2 = 0; u2 < UQ; u2++) {
+            const int u = tid + NT * u2;
+            if (u < WIN * D / EPU) stage_store(&s_q[u / (D / EPU)][(u % (D / EPU)) * EPU], nq[u2], BF);
+        }
+        if (tid < 4 * WIN) {
+            const int kind = tid / WIN, i = tid % WIN;
+            if (kind == 0) s_am[i] = __float_as_int(nsc);
+            else if (kind == 1) s_g[i] = nsc;
+            else if (kind == 2) s_fr[i] = nsc;
+            else s_oo[i] = nsc;
+        }
+        __syncthreads();                                                      // B1
+        // S2: |kold_i|^2 of the window's rows (every wave): lane = (row c, quarter grp)
+        float knrm;
+        {
+            float ss = 0.f;
+#pragma unroll
+            for (int u = 0; u < D / 16; u++) {
+                const float4 x = *reinterpret_cast<const float4*>(&s_ko[c][grp * (D / 4) + 4 * u]);
+                ss = fmaf(x.x, x.x, ss); ss = fmaf(x.y, x.y, ss); ss = fmaf(x.z, x.z, ss); ss = fmaf(x.w, x.w, ss);
+            }
+            knrm = sum4rows(ss);                         // lane l: |kold_{l & 15}|^2
+        }
+        // S3: replay the occupancy of this lane's rows backwards through the window: taken_n(t)
+        int amw[WIN];
+        float oow[WIN];
+#pragma unroll
+        for (int u = 0; u < WIN / 4; u++) {
+            const int4 a4 = *reinterpret_cast<const int4*>(&s_am[4 * u]);
+            const float4 o4 = *reinterpret_cast<const float4*>(&s_oo[4 * u]);
+            amw[4 * u] = a4.x; amw[4 * u + 1] = a4.y; amw[4 * u + 2] = a4.z; amw[4 * u + 3] = a4.w;
+            oow[4 * u] = o4.x; oow[4 * u + 1] = o4.y; oow[4 * u + 2] = o4.z; oow[4 * u + 3] = o4.w;
+        }
+        u32 tk[RPL];
+#pragma unroll
+        for (int j = 0; j < RPL; j++) tk[j] = 0;
+#pragma unroll
+        for (int i = WIN - 1; i >= 0; i--) {
+#pragma unroll
+            for (int j = 0; j < RPL; j++) {
+                const int n = lane + 64 * j;
+                if (n == amw[i]) o_me[j] = oow[i];
+                if (n < N && o_me[j] >= eps) tk[j] |= 1u << i;
+            }
+        }
+        // S4: the softmax adjoint of this wave's steps, over every row.  With a_n = e_n / SS over the eligible
+        // rows, sum over taken rows of dz_n = (g * SSD_taken - sa * SS_taken) / SS, so dfr needs no extra
+        // reduction.
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++) {
+            const int i = 4 * wave + ii;
+            if (i < nt) {
+                const int ai = s_am[i];
+                const float g = s_g[i];
+                const float frv = frt ? s_fr[i] : fr_s;
+                float cs[RPL], dw[RPL], z[RPL];
+                float lm = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < RPL; j++) {
+                    const int n = lane + 64 * j;
+                    const bool tj = (tk[j] >> i) & 1u;
+                    cs[j] = n < N ? s_cs[i * N + n] : 0.f;
+                    dw[j] = s_dn[n][i];
+                    z[j] = temp * cs[j] - (tj ? frv : 0.f);
+                    lm = fmaxf(lm, tj ? z[j] : -INFINITY);
+                }
+                const float wm = wavemax(lm);
+                float ls = 0.f, lsd = 0.f;
+#pragma unroll
+                for (int j = 0; j < RPL; j++) {
+                    const bool tj = (tk[j] >> i) & 1u;
+                    const float e = tj ? __expf(z[j] - wm) : 0.f;
+                    ls += e;
+                    lsd = fmaf(e, dw[j], lsd);
+                }
+                const float S = wavesum(ls), SD = wavesum(lsd);
+                int FO = -1;
+                float FZ = 0.f, FD = 0.f;
+#pragma unroll
+                for (int j = 0; j < RPL; j++) {            // the lowest free row (rows grow with j, lane)
+                    const bool tj = (tk[j] >> i) & 1u;
+                    const u64 mf = __ballot(lane + 64 * j < N && !tj);
+                    if (FO < 0 && mf) {
+                        const int lf = __builtin_ctzll(mf);
+                        FO = 64 * j + lf;
+                        FZ = readlanef(z[j], lf);
+                        FD = readlanef(dw[j], lf);
+                    }
+                }
+                float M = wm;
+                if (FO >= 0) M = fmaxf(M, FZ);             // the first free row competes too
+                const float sc = wm == -INFINITY ? 0.f : __expf(wm - M);
+                const float SSt = S * sc, SSDt = SD * sc;
+                float SS = SSt, SSD = SSDt;
+                if (FO >= 0) {
+                    const float ef = __expf(FZ - M);
+                    SS += ef;
+                    SSD = fmaf(ef, FD, SSD);
+                }
+                const float rss = 1.f / SS, sa = g * SSD / SS;
+#pragma unroll
+                for (int j = 0; j < RPL; j++) {
+                    const int n = lane + 64 * j;
+                    const bool tj = (tk[j] >> i) & 1u;
+                    const bool elig = tj || (n < N && n == FO);
+                    const float as = elig ? __expf(z[j] - M) * rss : 0.f;
+                    const float dz = as * (g * dw[j] - sa);
+                    dtemp_acc = fmaf(dz, cs[j], dtemp_acc);
+                    if (n < N && n == ai) a.dg[tok0 + (size_t)(t0 + i) * H] = dw[j];
+                    s_W[i][n] = temp * dz;
+                }
+                const float dfri = -(g * SSDt - sa * SSt) * rss;
+                if (lane == 0) {
+                    if (frt) a.dfr[tok0 + (size_t)(t0 + i) * H] = dfri;
+                    else dfr_acc += dfri;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < RPL; j++) s_W[i][lane + 64 * j] = 0.f;
+            }
+        }
+        __syncthreads();                                                      // B2
+        // S5: prefetch the next (earlier) window while the matrix cores run
+        if (m > 0) load_win(m - 1);
+        // S6: dqn over every row for this wave's dims, with the window-end keys
+        f32x4 acc[NBW];
+#pragma unroll
+        for (int nb = 0; nb < NBW; nb++) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) {
+            const float av = s_W[c][4 * kk + grp];
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, KREG(kk, nb), acc[nb], 0, 0, 0);
+        }
+        // S7: undo the window's writes (reverse order) in this wave's dims, logging
+        //     d_s = Kh(kold_s) - Kh_{a_s}(after write s).  First every event's Kh(kold_s) in place (this wave's
+        //     dims of s_ko: no other wave reads them after B2), then one short dependent step per event.
+#pragma unroll
+        for (int i = 0; i < WIN; i++) {
+            const float ki = rsq_clamped(readlanef(knrm, i));
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++) s_ko[i][d0 + 16 * nb + c] *= ki;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        {
+            int i = nt - 1;
+            int ar = amw[WIN - 1];
+#pragma unroll
+            for (int u = 0; u < WIN - 1; u++) if (nt - 1 == u) ar = amw[u];
+            float x[NBW];
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++) x[nb] = s_ko[i][d0 + 16 * nb + c];
+#pragma unroll 1
+            for (; i >= 0; i--) {
+                const int arn = i > 0 ? s_am[i - 1] : 0;     // next event, loaded ahead
+                float xn[NBW];
+#pragma unroll
+                for (int nb = 0; nb < NBW; nb++) xn[nb] = i > 0 ? s_ko[i - 1][d0 + 16 * nb + c] : 0.f;
+                const int kk = __builtin_amdgcn_readfirstlane(ar) >> 2;
+                const int ch = kk >> 4, e = kk & 15;
+                const bool mine = grp == (ar & 3);
+                float dd[NBW];
+#pragma unroll
+                for (int cc = 0; cc < NCH; cc++) {
+                    if (ch == cc) {
+#pragma unroll
+                        for (int nb = 0; nb < NBW; nb++) {
+                            const float old = Kv[nb][cc][e];
+                            dd[nb] = x[nb] - old;
+                            Kv[nb][cc][e] = mine ? x[nb] : old;
+                        }
+                    }
+                }
+                if (mine) {
+#pragma unroll
+                    for (int nb = 0; nb < NBW; nb++) s_delta[i][d0 + 16 * nb + c] = dd[nb];
+                }
+                ar = arn;
+#pragma unroll
+                for (int nb = 0; nb < NBW; nb++) x[nb] = xn[nb];
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // S8: the rewritten rows' correction, sum_{s >= t} W[t][a_s] d_s, as a 16 x 16 x DW MFMA
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            const int s = 4 * kc + grp;
+            const bool ok = s < nt;
+            const float av = (ok && s >= c) ? s_W[c][s_am[s]] : 0.f;
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++) {
+                const float bv = ok ? s_delta[s][d0 + 16 * nb + c] : 0.f;
+                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[nb], 0, 0, 0);
+            }
+        }
+        // S9: <dqn, q> and |q|^2 over this wave's dims for the 4 steps of this lane
+        float qv[4][NBW];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int st = 4 * grp + r;
+            float p = 0.f, qq = 0.f;
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++) {
+                qv[r][nb] = s_q[st][d0 + 16 * nb + c];
+                p = fmaf(acc[nb][r], qv[r][nb], p);
+                qq = fmaf(qv[r][nb], qv[r][nb], qq);
+            }
+            p = rowsum16(p);
+            qq = rowsum16(qq);
+            if (c == 0) s_proj[wave][st] = make_float2(p, qq);
+        }
+        __syncthreads();                                                      // B3
+        // S10: dq = qinv (dqn - qhat <qhat, dqn>)  (qinv dqn where |q| < 1e-6)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int st = 4 * grp + r;
+            if (st < nt) {
+                float P = 0.f, QQ = 0.f;
+#pragma unroll
+                for (int w = 0; w < 4; w++) { const float2 x = s_proj[w][st]; P += x.x; QQ += x.y; }
+                const float qi = rsq_clamped(QQ);
+                const float pr = P * qi;
+                TI* dqp = (TI*)a.dq + (tok0 + (size_t)(t0 + st) * H) * D + d0 + c;
+#pragma unroll
+                for (int nb = 0; nb < NBW; nb++) {
+                    const float dqn = acc[nb][r];
+                    const float rr = QQ < 1e-12f ? qi * dqn : qi * (dqn - (qv[r][nb] * qi) * pr);
+                    st1<TI>(dqp + 16 * nb, rr);
+                }
+            }
+        }
+        __syncthreads();                                                      // B4
+    }
+#undef KREG
+    dtemp_acc = wavesum(dtemp_acc);
+    dfr_acc = wavesum(dfr_acc);
+    if (lane == 0) { s_fin[0][wave] = dtemp_acc; s_fin[1][wave] = dfr_acc; }
+    __syncthreads();
+    if (tid == 0) {
+        const float s0 = ((s_fin[0][0] + s_fin[0][1]) + s_fin[0][2]) + s_fin[0][3];
+        const float s1 = ((s_fin[1][0] + s_fin[1][1]) + s_fin[1][2]) + s_fin[1][3];
+        a.part[2 * (size_t)bh + 0] = s0;
+        a.part[2 * (size_t)bh + 1] = s1;
+    }
+}
+
 // fixed-order sum of the per-chain partials: dtemp = sum_bh part[bh][0]; scalar dfr = sum_bh part[bh][1]
 __global__ __launch_bounds__(256) void reduce_parts(const float* __restrict__ part, int nbh, float* dtemp,
                                                     float* dfr) {
@@ -980,6 +1405,14 @@ hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
 }
 template <int D, typename TI>
 hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
+    if (a.occb) {                                        // windowed kernel, four waves
+        dim3 grid(B * a.H), block(256);
+        if (a.N <= 64) hipLaunchKernelGGL((chain_bwd_w<D, 1, TI>), grid, block, 0, st, a);
+        else if (a.N <= 128) hipLaunchKernelGGL((chain_bwd_w<D, 2, TI>), grid, block, 0, st, a);
+        else if (a.N <= 192) hipLaunchKernelGGL((chain_bwd_w<D, 3, TI>), grid, block, 0, st, a);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     dim3 grid(B * a.H), block(CHAIN_THREADS);
 #define SLOT_CB(PP) if (a.N <= 4 * CHAIN_WAVES * PP) { \
         if (a.occb) hipLaunchKernelGGL((chain_bwd<D, PP, TI, true>), grid, block, 0, st, a); \

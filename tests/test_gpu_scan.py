@@ -107,6 +107,7 @@ CASES = [  # B, T, H, N, D, G, frt, occb, sep_q, hardg
     (2, 128, 1, 64, 64, 8, True, True, True, False),        # config 1
     (2, 256, 2, 192, 128, 8, True, True, True, False),      # config 2 shape per chain
     (2, 256, 2, 96, 128, 8, True, True, True, False),       # config 3 (encoder memory) shape per chain
+    (2, 200, 2, 128, 128, 8, True, True, True, False),      # three 48-row waves in the windowed backward
     (2, 250, 3, 192, 64, 8, True, True, True, False),       # T % G != 0
     (1, 300, 4, 40, 64, 16, False, False, False, False),    # scalar fr, no occ_bin, q = k
     (1, 300, 4, 40, 64, 7, False, True, True, True),        # G = 7, hard gate
