@@ -2,6 +2,7 @@
 // optional per-kernel HIP-event timing (implemented once, in slotscan.hip).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stdint.h>
 
 namespace slothost {
 
@@ -21,5 +22,10 @@ struct Scope {
 };
 
 inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// The library's second stream on the current device (non-blocking, default priority) and a pool of
+// timing-free events, for fork/join pipelines inside one entry point.  Created on first use per device and
+// kept until the process ends.  Returns 0, or SLOTSCAN_ERR_HIP with the message set.
+int side_stream(hipStream_t* side, hipEvent_t** ev, int nev);
 
 }  // namespace slothost

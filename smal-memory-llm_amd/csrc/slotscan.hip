@@ -185,6 +185,7 @@ struct ChainFwdArgs {
     const float* k0; const float* o0;
     float* kbuf; int32_t* am; float* kold; float* oold; float* cslog; float* kfin; float* ofin;
     int T, H, N, G, NB; float eps; int frt, occb;
+    int ts, te;                                          // steps [ts, te) of the T-long sequence; ts % G == 0
 };
 
 template <int D, int P, typename TI>
@@ -200,14 +201,14 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
     __shared__ float s_g[2][CT], s_fr[2][CT];
     __shared__ uint4 s_red[2][CHAIN_WAVES];
 
-    const int T = a.T, H = a.H, N = a.N, G = a.G;
+    const int T = a.T, H = a.H, N = a.N, G = a.G, ts = a.ts, te = a.te;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = tid & 15;
     const ChainRows<P> R(tid);
     const TI* __restrict__ qp = (const TI*)a.q;
     const TI* __restrict__ kp = (const TI*)a.k;
     const size_t tok0 = (size_t)b * T * H + h;          // token (b, t, h) = tok0 + t * H
-    float* kb = a.kbuf + ((size_t)b * a.NB * H + h) * N * D;   // key snapshot of block 0 of this chain
+    float* kb = a.kbuf + (((size_t)b * a.NB + ts / G) * H + h) * N * D;   // key snapshot of block ts / G
     const size_t sstride = (size_t)H * N * D;
 
     float K[P][EPL];
@@ -238,14 +239,14 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
             rq[m] = make_uint4(0u, 0u, 0u, 0u);
             if (u < NU) {
                 const int j = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
-                const int t = ch * CT + j;
-                if (t < T) rq[m] = reinterpret_cast<const uint4*>((arr ? kp : qp) + (tok0 + (size_t)t * H) * D)[w];
+                const int t = ts + ch * CT + j;
+                if (t < te) rq[m] = reinterpret_cast<const uint4*>((arr ? kp : qp) + (tok0 + (size_t)t * H) * D)[w];
             }
         }
         if (tid < 2 * CT) {
-            const int t = ch * CT + (tid & (CT - 1));
+            const int t = ts + ch * CT + (tid & (CT - 1));
             rs = 0.f;
-            if (t < T) rs = (tid < CT) ? a.gate[tok0 + (size_t)t * H] : (a.frt ? a.fr[tok0 + (size_t)t * H] : 0.f);
+            if (t < te) rs = (tid < CT) ? a.gate[tok0 + (size_t)t * H] : (a.frt ? a.fr[tok0 + (size_t)t * H] : 0.f);
         }
     };
     auto store_chunk = [&](int buf) {
@@ -294,7 +295,7 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
     float qinv = qinv_of(qv);
     float dme = dot_me(qv);                             // <K_me, q_t> for the current keys
     int par = 0, j = 0, buf = 0, gc = 0;
-    for (int t = 0; t < T; t++) {
+    for (int t = ts; t < te; t++) {
         const float g = s_g[buf][j];
         const float frv = frt ? s_fr[buf][j] : fr_s;
         const float cs = (dme * kinv_me) * qinv;         // cosine of this lane's row with q_t
@@ -322,7 +323,7 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
         // next step's query, its norm and its dot products with the CURRENT keys; after the write below
         // only the rewritten row's dot is recomputed
         float qinv_n = 0.f, dnext = 0.f;
-        if (t + 1 < T) {
+        if (t + 1 < te) {
             const int jn = j + 1 == CT ? 0 : j + 1, bn = j + 1 == CT ? (buf ^ 1) : buf;
             ld_slice<EPL>(qv, &s_tok[bn][jn][0][0], c);
             qinv_n = qinv_of(qv);
@@ -330,7 +331,7 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
         }
         if (j == CT - 2) {                                  // refill: chunk t/CT+1 -> LDS, fetch t/CT+2
             store_chunk(buf ^ 1);
-            load_chunk(t / CT + 2);
+            load_chunk((t - ts) / CT + 2);
         }
         __syncthreads();
         uint4 r[CHAIN_WAVES];
@@ -407,6 +408,7 @@ struct RowsFwdArgs {
     const void* v; const float* gate; const int32_t* am; const float* v0;
     float* vbuf; float* vold; float* vfin;
     int T, H, N, G, NB;
+    int ts, te;                                          // steps [ts, te); ts % G == 0
 };
 
 // 512 lanes = 32 rows of one chain per workgroup; grid (B*H, ceil(N/32)).  Replays every row's value from
@@ -428,11 +430,11 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
 #pragma unroll
     for (int e = 0; e < EPL; e++) V[e] = 0.f;
     if (live && a.v0) ld_slice<EPL>(V, a.v0 + ((size_t)bh * N + n) * D, c);
-    float* vb = a.vbuf + ((size_t)b * a.NB * H + h) * N * D + (size_t)(live ? n : 0) * D;
+    float* vb = a.vbuf + (((size_t)b * a.NB + a.ts / G) * H + h) * N * D + (size_t)(live ? n : 0) * D;
     const size_t sstride = (size_t)H * N * D;
     int gc = 0;
-    for (int t0 = 0; t0 < T; t0 += TC) {
-        const int tn = min(TC, T - t0);
+    for (int t0 = a.ts; t0 < a.te; t0 += TC) {
+        const int tn = min(TC, a.te - t0);
         __syncthreads();
         for (int u = tid; u < tn; u += 512) {
             const size_t ix = tok0 + (size_t)(t0 + u) * H;
@@ -1428,6 +1430,7 @@ hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
 // ======================================================================================== C-ABI
 #include "slotscan.h"
 #include "slot_host.h"
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -1461,6 +1464,30 @@ Scope::~Scope() {
     if (!b) return;
     hipEventRecord(b, st);
     slotprof::recs.push_back({kid, a, b});
+}
+
+static std::mutex side_mu;
+struct SideRes { hipStream_t s = nullptr; std::vector<hipEvent_t> ev; };
+static SideRes side_res[64];
+int side_stream(hipStream_t* side, hipEvent_t** ev, int nev) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(SLOTSCAN_ERR_HIP, "device id out of range");
+    std::lock_guard<std::mutex> g(side_mu);
+    SideRes& r = side_res[dev];
+    if (!r.s && (e = hipStreamCreateWithFlags(&r.s, hipStreamNonBlocking)) != hipSuccess) {
+        r.s = nullptr;
+        return hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    while ((int)r.ev.size() < nev) {
+        hipEvent_t x = nullptr;
+        if ((e = hipEventCreateWithFlags(&x, hipEventDisableTiming)) != hipSuccess) return hip_fail(e, "hipEventCreate");
+        r.ev.push_back(x);
+    }
+    *side = r.s;
+    *ev = r.ev.data();
+    return 0;
 }
 
 static thread_local char g_err[512];
@@ -1530,28 +1557,53 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
     hipStream_t st = (hipStream_t)stream;
     const int NB = (int)((T + G - 1) / G);
     ChainFwdArgs ca{q, k, gate, fr, temp, k0, o0, kbuf, am, kold, oold, cslog, kfin, ofin,
-                    (int)T, (int)H, (int)N, (int)G, NB, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0};
-    hipError_t e;
-    {
-        slothost::Scope sc(SLOTSCAN_K_CHAIN_FWD, st);
-        if (D == 128) e = dtype == SLOTSCAN_BF16 ? launch_chain_fwd<128, bf16_t>(ca, (int)B, st) : launch_chain_fwd<128, float>(ca, (int)B, st);
-        else e = dtype == SLOTSCAN_BF16 ? launch_chain_fwd<64, bf16_t>(ca, (int)B, st) : launch_chain_fwd<64, float>(ca, (int)B, st);
-    }
-    if (e != hipSuccess) return hip_fail(e, "chain_fwd launch");
-    RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB};
+                    (int)T, (int)H, (int)N, (int)G, NB, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0, 0, (int)T};
+    RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB, 0, (int)T};
+    // Long sequences run as a two-stream pipeline over step chunks of a multiple of G: the key chain of
+    // chunk c + 1 (latency-bound, caller's stream) overlaps the value replay of chunk c (HBM-bound, the
+    // library's side stream).  Both kernels carry their state through kfin / ofin and vfin in place
+    // (every element is read at a chunk's start and written at its end by the same lane).
+    const int64_t len = T >= 512 ? ((std::max<int64_t>(128, T / 8) + G - 1) / G) * G : T;
+    const int nch = (int)((T + len - 1) / len);
+    hipStream_t side = nullptr;
+    hipEvent_t* ev = nullptr;
+    if (nch > 1)
+        if (int r = slothost::side_stream(&side, &ev, nch + 1)) return r;
     dim3 grid((unsigned)(B * H), (unsigned)((N + 31) / 32)), block(512);
-    {
-        slothost::Scope sc(SLOTSCAN_K_ROWS_FWD, st);
-        if (D == 128) {
-            if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_fwd<128, bf16_t>), grid, block, 0, st, ra);
-            else hipLaunchKernelGGL((rows_fwd<128, float>), grid, block, 0, st, ra);
-        } else {
-            if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_fwd<64, bf16_t>), grid, block, 0, st, ra);
-            else hipLaunchKernelGGL((rows_fwd<64, float>), grid, block, 0, st, ra);
+    hipError_t e;
+    for (int c = 0; c < nch; c++) {
+        ca.ts = ra.ts = (int)(c * len);
+        ca.te = ra.te = (int)std::min<int64_t>(T, (c + 1) * len);
+        if (c > 0) { ca.k0 = kfin; ca.o0 = ofin; ra.v0 = vfin; }
+        {
+            slothost::Scope sc(SLOTSCAN_K_CHAIN_FWD, st);
+            if (D == 128) e = dtype == SLOTSCAN_BF16 ? launch_chain_fwd<128, bf16_t>(ca, (int)B, st) : launch_chain_fwd<128, float>(ca, (int)B, st);
+            else e = dtype == SLOTSCAN_BF16 ? launch_chain_fwd<64, bf16_t>(ca, (int)B, st) : launch_chain_fwd<64, float>(ca, (int)B, st);
         }
-        e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(e, "chain_fwd launch");
+        hipStream_t rs = st;
+        if (nch > 1) {
+            if ((e = hipEventRecord(ev[c], st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+            if ((e = hipStreamWaitEvent(side, ev[c], 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+            rs = side;
+        }
+        {
+            slothost::Scope sc(SLOTSCAN_K_ROWS_FWD, rs);
+            if (D == 128) {
+                if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_fwd<128, bf16_t>), grid, block, 0, rs, ra);
+                else hipLaunchKernelGGL((rows_fwd<128, float>), grid, block, 0, rs, ra);
+            } else {
+                if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_fwd<64, bf16_t>), grid, block, 0, rs, ra);
+                else hipLaunchKernelGGL((rows_fwd<64, float>), grid, block, 0, rs, ra);
+            }
+            e = hipGetLastError();
+        }
+        if (e != hipSuccess) return hip_fail(e, "rows_fwd launch");
     }
-    if (e != hipSuccess) return hip_fail(e, "rows_fwd launch");
+    if (nch > 1) {                                       // join: the caller's stream sees every chunk
+        if ((e = hipEventRecord(ev[nch], side)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+        if ((e = hipStreamWaitEvent(st, ev[nch], 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+    }
     return 0;
 }
 

@@ -113,6 +113,8 @@ CASES = [  # B, T, H, N, D, G, frt, occb, sep_q, hardg
     (1, 300, 4, 40, 64, 7, False, True, True, True),        # G = 7, hard gate
     (1, 300, 3, 50, 128, 8, False, False, True, False),
     (1, 5, 2, 20, 64, 8, True, True, True, False),          # T < G
+    (1, 600, 2, 96, 64, 8, True, True, True, False),        # T >= 512: chunked two-stream forward
+    (1, 520, 2, 64, 64, 7, False, False, True, False),      # chunked forward, G = 7, no occ_bin
 ]
 
 
