@@ -489,7 +489,7 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
     constexpr int UPT = (NU + 511) / 512;
     constexpr bool BF = sizeof(TI) == 2;
     __shared__ __align__(16) float s_tok[2][16][2][D];
-    __shared__ int s_am[2][16];
+    __shared__ __align__(16) int s_am[2][16];
     __shared__ float s_g[2][16];
     __shared__ __align__(16) float s_part[32][16][17];   // [row group][step][lane], padded
 
@@ -562,9 +562,17 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
     for (int m = nblk - 1; m >= 0; m--) {
         const int i_hi = min(15, T - 1 - 16 * m);
         for (int i = 15; i > i_hi; i--) s_part[rg][i][c] = 0.f;
+        u32 hm = 0;                                      // steps of this chunk that wrote this row
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int4 a4 = *reinterpret_cast<const int4*>(&s_am[buf][4 * u]);
+            hm |= (a4.x == n ? 1u : 0u) << (4 * u) | (a4.y == n ? 2u : 0u) << (4 * u)
+                | (a4.z == n ? 4u : 0u) << (4 * u) | (a4.w == n ? 8u : 0u) << (4 * u);
+        }
+        if (!live) hm = 0;
         for (int i = i_hi; i >= 0; i--) {
             const int t = 16 * m + i;
-            const bool hit = live && (s_am[buf][i] == n);
+            const bool hit = (hm >> i) & 1u;
             if (hit) {                                      // undo: the row before this step's write
                 const size_t ix = tok0 + (size_t)t * H;
                 ld_slice<EPL>(K, a.kold + ix * D, c);
