@@ -967,13 +967,14 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 // Windowed address backward for the occ_bin mode.  With occupancy entering only through [o >= eps], the
 // adjoint of step t needs no carry from step t + 1: given the replayed occupancy at t, the logged cosines
 // and Dn, every step's softmax adjoint is independent.  The chain is therefore processed in windows of
-// WIN = 16 steps (reverse order), by four waves:
+// WIN = 16 steps (reverse order), by NW = 4 or 8 waves:
 //   replay   every lane replays the occupancy of its slot rows (n = lane + 64 j) backwards through the
 //            window, recording taken_n(t);
-//   softmax  wave w owns steps 4w .. 4w+3 of the window: the whole masked softmax adjoint of a step (max,
+//   softmax  wave w owns steps SPW w .. SPW w + SPW - 1 of the window (SPW = 16 / NW): the whole masked
+//            softmax adjoint of a step (max,
 //            sum e, sum e dw over every row, the lowest free row) is a wave reduction, no cross-wave merge;
 //            W[t][n] = temp dz_n(t) goes to LDS;
-//   dq       wave w owns dims [w D/4, (w+1) D/4): dqn[t][d] = sum_n W[t][n] Kh_n(t)[d] as fp32 MFMA over
+//   dq       wave w owns dims [w DW, (w+1) DW), DW = D / NW: dqn[t][d] = sum_n W[t][n] Kh_n(t)[d] as fp32 MFMA over
 //            the window, with Kh = K / max(|K|, 1e-6) the normalised keys (the reference's order: normalise,
 //            then contract, slotkern_kvt.py:86-90), held in registers in the MFMA B-operand layout as the
 //            keys AFTER the window's writes (Kh_end); the rows the window rewrote are corrected exactly with
@@ -983,21 +984,24 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 //   undo     every wave restores its dims of each rewritten row from kold (the next window's Kh_end);
 //   dq       the clamped-normalisation Jacobian of q needs <dqn, q> over all of D: one LDS exchange.
 // B-operand layout (v_mfma_f32_16x16x4f32, B[k][j] at lane 16k + j): lane l of wave w holds
-//   Kh[row 4*kk + (l >> 4)][dim w*DW + 16*nb + (l & 15)] = Kv[nb][kk >> 4][kk & 15],  kk < 16*RPL, nb < DW/16.
+//   Kh[row kk + KK*(l >> 4)][dim w*DW + 16*nb + (l & 15)] = Kv[nb][kk >> 4][kk & 15],  kk < KK = 16*RPL,
+// nb < DW/16 (k-step kk contracts rows kk, KK + kk, 2 KK + kk, 3 KK + kk, so four consecutive k-steps of a
+// lane's A operand are one 16-byte LDS read).
 // Kv is an array of 16-float register vectors, so the undo can address row kk with a uniform dynamic index
 // (M0-relative moves, s_set_gpr_idx) instead of branching over every possible row.
-// A operand: lane l holds W[step l & 15][row 4*kk + (l >> 4)]; result lane l, register r:
+// A operand: lane l holds W[step l & 15][row kk + KK*(l >> 4)]; result lane l, register r:
 //   dqn[step 4*(l >> 4) + r][dim w*DW + 16*nb + (l & 15)].
 #define WIN 16
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int D, int RPL, typename TI>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2)))
+template <int D, int RPL, int NW, typename TI>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(NW == 8 ? 4 : 2)))
 void chain_bwd_w(ChainBwdArgs a) {
-    constexpr int NT = 256;                             // 4 waves
+    constexpr int NT = 64 * NW;
+    constexpr int SPW = WIN / NW;                       // window steps per wave in the softmax phase
     constexpr int NR = 64 * RPL;                        // slot-row capacity
     constexpr int KK = NR / 4;                          // MFMA k-steps over the rows
-    constexpr int DW = D / 4;                           // dims per wave
+    constexpr int DW = D / NW;                          // dims per wave
     constexpr int NBW = DW / 16;                        // MFMA column blocks per wave
     constexpr int NCH = KK / 16;                        // 16-row-group chunks of a key column block
     constexpr int SWS = NR + 4;                         // W row stride (conflict-free A-operand reads)
@@ -1015,8 +1019,8 @@ void chain_bwd_w(ChainBwdArgs a) {
     __shared__ __align__(16) float s_delta[WIN][D];
     __shared__ int s_am[WIN];
     __shared__ float s_g[WIN], s_fr[WIN], s_oo[WIN];
-    __shared__ float2 s_proj[4][WIN];
-    __shared__ float s_fin[2][4];
+    __shared__ float2 s_proj[NW][WIN];
+    __shared__ float s_fin[2][NW];
 
     const int T = a.T, H = a.H, N = a.N;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
@@ -1033,10 +1037,10 @@ void chain_bwd_w(ChainBwdArgs a) {
     f32x16 Kv[NBW][NCH];
 #define KREG(kk, nb) Kv[nb][(kk) >> 4][(kk) & 15]
     {
-        float* s_nrm = &s_W[0][0];                      // [4][NR] scratch before the first window
+        float* s_nrm = &s_W[0][0];                      // [NW][NR] scratch before the first window
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) {
-            const int row = 4 * kk + grp;
+            const int row = kk + KK * grp;
             float ss = 0.f;
 #pragma unroll
             for (int nb = 0; nb < NBW; nb++) {
@@ -1050,8 +1054,11 @@ void chain_bwd_w(ChainBwdArgs a) {
         __syncthreads();
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) {
-            const int row = 4 * kk + grp;
-            const float ki = rsq_clamped(((s_nrm[row] + s_nrm[NR + row]) + s_nrm[2 * NR + row]) + s_nrm[3 * NR + row]);
+            const int row = kk + KK * grp;
+            float nsq = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) nsq += s_nrm[w * NR + row];
+            const float ki = rsq_clamped(nsq);
 #pragma unroll
             for (int nb = 0; nb < NBW; nb++) KREG(kk, nb) *= ki;
         }
@@ -1187,9 +1194,10 @@ void chain_bwd_w(ChainBwdArgs a) {
         // rows, sum over taken rows of dz_n = (g * SSD_taken - sa * SS_taken) / SS, so dfr needs no extra
         // reduction.
 #pragma unroll
-        for (int ii = 0; ii < 4; ii++) {
-            const int i = 4 * wave + ii;
-            if (i < nt) {
+        for (int ii = 0; ii < SPW; ii++) {
+            const int i = SPW * wave + ii;
+            {                                            // steps past nt hold zeros: W = 0, no stores
+                const bool live_i = i < nt;
                 const int ai = s_am[i];
                 const float g = s_g[i];
                 const float frv = frt ? s_fr[i] : fr_s;
@@ -1237,7 +1245,7 @@ void chain_bwd_w(ChainBwdArgs a) {
                     SS += ef;
                     SSD = fmaf(ef, FD, SSD);
                 }
-                const float rss = 1.f / SS, sa = g * SSD / SS;
+                const float rss = live_i ? __builtin_amdgcn_rcpf(SS) : 0.f, sa = (g * SSD) * rss;
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
                     const int n = lane + 64 * j;
@@ -1246,17 +1254,14 @@ void chain_bwd_w(ChainBwdArgs a) {
                     const float as = elig ? __expf(z[j] - M) * rss : 0.f;
                     const float dz = as * (g * dw[j] - sa);
                     dtemp_acc = fmaf(dz, cs[j], dtemp_acc);
-                    if (n < N && n == ai) a.dg[tok0 + (size_t)(t0 + i) * H] = dw[j];
+                    if (live_i && n < N && n == ai) a.dg[tok0 + (size_t)(t0 + i) * H] = dw[j];
                     s_W[i][n] = temp * dz;
                 }
-                const float dfri = -(g * SSDt - sa * SSt) * rss;
+                const float dfri = live_i ? -(g * SSDt - sa * SSt) * rss : 0.f;
                 if (lane == 0) {
-                    if (frt) a.dfr[tok0 + (size_t)(t0 + i) * H] = dfri;
+                    if (frt) { if (live_i) a.dfr[tok0 + (size_t)(t0 + i) * H] = dfri; }
                     else dfr_acc += dfri;
                 }
-            } else {
-#pragma unroll
-                for (int j = 0; j < RPL; j++) s_W[i][lane + 64 * j] = 0.f;
             }
         }
         __syncthreads();                                                      // B2
@@ -1267,10 +1272,16 @@ void chain_bwd_w(ChainBwdArgs a) {
 #pragma unroll
         for (int nb = 0; nb < NBW; nb++) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            const float av = s_W[c][4 * kk + grp];
+        for (int k4 = 0; k4 < KK / 4; k4++) {
+            const float4 av = *reinterpret_cast<const float4*>(&s_W[c][KK * grp + 4 * k4]);
 #pragma unroll
-            for (int nb = 0; nb < NBW; nb++) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, KREG(kk, nb), acc[nb], 0, 0, 0);
+            for (int nb = 0; nb < NBW; nb++) {
+                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, KREG(4 * k4 + 0, nb), acc[nb], 0, 0, 0);
+                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, KREG(4 * k4 + 1, nb), acc[nb], 0, 0, 0);
+                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, KREG(4 * k4 + 2, nb), acc[nb], 0, 0, 0);
+                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, KREG(4 * k4 + 3, nb), acc[nb], 0, 0, 0);
+            }
+            if ((k4 & 1) == 1) __builtin_amdgcn_sched_barrier(0);
         }
         // S7: undo the window's writes (reverse order) in this wave's dims, logging
         //     d_s = Kh(kold_s) - Kh_{a_s}(after write s).  First every event's Kh(kold_s) in place (this wave's
@@ -1284,23 +1295,17 @@ void chain_bwd_w(ChainBwdArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        {
-            int i = nt - 1;
-            int ar = amw[WIN - 1];
+        const int am_l = s_am[lane & (WIN - 1)];         // lane i (< 16) holds the row written at window step i
 #pragma unroll
-            for (int u = 0; u < WIN - 1; u++) if (nt - 1 == u) ar = amw[u];
-            float x[NBW];
+        for (int i = WIN - 1; i >= 0; i--) {             // program order keeps repeated rows sequential
+            if (i < nt) {
+                const int ar = __builtin_amdgcn_readlane(am_l, i);
+                float x[NBW];
 #pragma unroll
-            for (int nb = 0; nb < NBW; nb++) x[nb] = s_ko[i][d0 + 16 * nb + c];
-#pragma unroll 1
-            for (; i >= 0; i--) {
-                const int arn = i > 0 ? s_am[i - 1] : 0;     // next event, loaded ahead
-                float xn[NBW];
-#pragma unroll
-                for (int nb = 0; nb < NBW; nb++) xn[nb] = i > 0 ? s_ko[i - 1][d0 + 16 * nb + c] : 0.f;
-                const int kk = __builtin_amdgcn_readfirstlane(ar) >> 2;
+                for (int nb = 0; nb < NBW; nb++) x[nb] = s_ko[i][d0 + 16 * nb + c];
+                const int ag = ar / KK, kk = ar - KK * ag;
                 const int ch = kk >> 4, e = kk & 15;
-                const bool mine = grp == (ar & 3);
+                const bool mine = grp == ag;
                 float dd[NBW];
 #pragma unroll
                 for (int cc = 0; cc < NCH; cc++) {
@@ -1317,9 +1322,6 @@ void chain_bwd_w(ChainBwdArgs a) {
 #pragma unroll
                     for (int nb = 0; nb < NBW; nb++) s_delta[i][d0 + 16 * nb + c] = dd[nb];
                 }
-                ar = arn;
-#pragma unroll
-                for (int nb = 0; nb < NBW; nb++) x[nb] = xn[nb];
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1361,7 +1363,7 @@ void chain_bwd_w(ChainBwdArgs a) {
             if (st < nt) {
                 float P = 0.f, QQ = 0.f;
 #pragma unroll
-                for (int w = 0; w < 4; w++) { const float2 x = s_proj[w][st]; P += x.x; QQ += x.y; }
+                for (int w = 0; w < NW; w++) { const float2 x = s_proj[w][st]; P += x.x; QQ += x.y; }
                 const float qi = rsq_clamped(QQ);
                 const float pr = P * qi;
                 TI* dqp = (TI*)a.dq + (tok0 + (size_t)(t0 + st) * H) * D + d0 + c;
@@ -1381,8 +1383,9 @@ void chain_bwd_w(ChainBwdArgs a) {
     if (lane == 0) { s_fin[0][wave] = dtemp_acc; s_fin[1][wave] = dfr_acc; }
     __syncthreads();
     if (tid == 0) {
-        const float s0 = ((s_fin[0][0] + s_fin[0][1]) + s_fin[0][2]) + s_fin[0][3];
-        const float s1 = ((s_fin[1][0] + s_fin[1][1]) + s_fin[1][2]) + s_fin[1][3];
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) { s0 += s_fin[0][w]; s1 += s_fin[1][w]; }
         a.part[2 * (size_t)bh + 0] = s0;
         a.part[2 * (size_t)bh + 1] = s1;
     }
@@ -1416,10 +1419,11 @@ hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
 template <int D, typename TI>
 hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
     if (a.occb) {                                        // windowed kernel, four waves
-        dim3 grid(B * a.H), block(256);
-        if (a.N <= 64) hipLaunchKernelGGL((chain_bwd_w<D, 1, TI>), grid, block, 0, st, a);
-        else if (a.N <= 128) hipLaunchKernelGGL((chain_bwd_w<D, 2, TI>), grid, block, 0, st, a);
-        else if (a.N <= 192) hipLaunchKernelGGL((chain_bwd_w<D, 3, TI>), grid, block, 0, st, a);
+        constexpr int NW = 4;
+        dim3 grid(B * a.H), block(64 * NW);
+        if (a.N <= 64) hipLaunchKernelGGL((chain_bwd_w<D, 1, NW, TI>), grid, block, 0, st, a);
+        else if (a.N <= 128) hipLaunchKernelGGL((chain_bwd_w<D, 2, NW, TI>), grid, block, 0, st, a);
+        else if (a.N <= 192) hipLaunchKernelGGL((chain_bwd_w<D, 3, NW, TI>), grid, block, 0, st, a);
         else return hipErrorInvalidValue;
         return hipGetLastError();
     }
