@@ -188,14 +188,20 @@ struct ChainFwdArgs {
     int ts, te;                                          // steps [ts, te) of the T-long sequence; ts % G == 0
 };
 
+// Three compute waves run the chain; a fourth, producer wave does every token load (q, k, gate, fr into the
+// double-buffered LDS staging) and joins the per-step barrier.  The compute waves then issue only stores
+// to global memory and never wait on the vector-memory counter, which on gfx9 also counts stores: a
+// refill in a compute wave would wait for its own snapshot and log stores to reach memory.
+#define FWD_THREADS (CHAIN_THREADS + 64)
 template <int D, int P, typename TI>
-CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
+__global__ __attribute__((amdgpu_flat_work_group_size(FWD_THREADS, FWD_THREADS), amdgpu_waves_per_eu(2)))
+void chain_fwd(ChainFwdArgs a) {
     constexpr int CT = (sizeof(TI) == 4 && P >= 16) ? 8 : SLOT_CT;   // fewer staging registers for fp32 tokens
     constexpr int EPL = D / 16;
     constexpr int EPU = 16 / (int)sizeof(TI);          // token elements per uint4
     constexpr int RU = D / EPU;                         // uint4 per token row
     constexpr int NU = CT * 2 * RU;                     // uint4 per staged chunk: (q row, k row) per token
-    constexpr int UPT = (NU + CHAIN_THREADS - 1) / CHAIN_THREADS;
+    constexpr int UPT = (NU + 63) / 64;                // per producer lane
     constexpr bool BF = sizeof(TI) == 2;
     __shared__ __align__(16) float s_tok[2][CT][2][D];
     __shared__ float s_g[2][CT], s_fr[2][CT];
@@ -210,6 +216,54 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
     const size_t tok0 = (size_t)b * T * H + h;          // token (b, t, h) = tok0 + t * H
     float* kb = a.kbuf + (((size_t)b * a.NB + ts / G) * H + h) * N * D;   // key snapshot of block ts / G
     const size_t sstride = (size_t)H * N * D;
+
+    if (wave == CHAIN_WAVES) {                          // the producer wave
+        uint4 rq[UPT];
+        float rs = 0.f;
+        auto load_chunk = [&](int ch) {
+#pragma unroll
+            for (int m = 0; m < UPT; m++) {
+                const int u = lane + 64 * m;
+                rq[m] = make_uint4(0u, 0u, 0u, 0u);
+                if (u < NU) {
+                    const int j = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
+                    const int t = ts + ch * CT + j;
+                    if (t < te) rq[m] = reinterpret_cast<const uint4*>((arr ? kp : qp) + (tok0 + (size_t)t * H) * D)[w];
+                }
+            }
+            if (lane < 2 * CT) {
+                const int t = ts + ch * CT + (lane & (CT - 1));
+                rs = 0.f;
+                if (t < te) rs = (lane < CT) ? a.gate[tok0 + (size_t)t * H] : (a.frt ? a.fr[tok0 + (size_t)t * H] : 0.f);
+            }
+        };
+        auto store_chunk = [&](int bf) {
+#pragma unroll
+            for (int m = 0; m < UPT; m++) {
+                const int u = lane + 64 * m;
+                if (u < NU) {
+                    const int j = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
+                    stage_store(&s_tok[bf][j][arr][w * EPU], rq[m], BF);
+                }
+            }
+            if (lane < CT) s_g[bf][lane] = rs;
+            else if (lane < 2 * CT) s_fr[bf][lane - CT] = rs;
+        };
+        load_chunk(0);
+        store_chunk(0);
+        __syncthreads();
+        load_chunk(1);
+        int j = 0, buf = 0;
+        for (int t = ts; t < te; t++) {
+            if (j == CT - 2) {                           // refill: chunk (t-ts)/CT+1 -> LDS, fetch +2
+                store_chunk(buf ^ 1);
+                load_chunk((t - ts) / CT + 2);
+            }
+            __syncthreads();
+            if (++j == CT) { j = 0; buf ^= 1; }
+        }
+        return;
+    }
 
     float K[P][EPL];
     float o_me = 0.f, kinv_me;
@@ -230,37 +284,6 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
         if (a.o0 && R.n_me < N) o_me = a.o0[(size_t)bh * N + R.n_me];
     }
 
-    uint4 rq[UPT];
-    float rs = 0.f;
-    auto load_chunk = [&](int ch) {
-#pragma unroll
-        for (int m = 0; m < UPT; m++) {
-            const int u = tid + CHAIN_THREADS * m;
-            rq[m] = make_uint4(0u, 0u, 0u, 0u);
-            if (u < NU) {
-                const int j = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
-                const int t = ts + ch * CT + j;
-                if (t < te) rq[m] = reinterpret_cast<const uint4*>((arr ? kp : qp) + (tok0 + (size_t)t * H) * D)[w];
-            }
-        }
-        if (tid < 2 * CT) {
-            const int t = ts + ch * CT + (tid & (CT - 1));
-            rs = 0.f;
-            if (t < te) rs = (tid < CT) ? a.gate[tok0 + (size_t)t * H] : (a.frt ? a.fr[tok0 + (size_t)t * H] : 0.f);
-        }
-    };
-    auto store_chunk = [&](int buf) {
-#pragma unroll
-        for (int m = 0; m < UPT; m++) {
-            const int u = tid + CHAIN_THREADS * m;
-            if (u < NU) {
-                const int j = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
-                stage_store(&s_tok[buf][j][arr][w * EPU], rq[m], BF);
-            }
-        }
-        if (tid < CT) s_g[buf][tid] = rs;
-        else if (tid < 2 * CT) s_fr[buf][tid - CT] = rs;
-    };
     // this lane's row dotted with a query slice, completed by the reduce-scatter
     auto dot_me = [&](const float* qv) -> float {
         float x[P];
@@ -286,10 +309,7 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
     const bool occb = a.occb != 0, frt = a.frt != 0;
     const bool valid_me = R.n_me < N;
 
-    load_chunk(0);
-    store_chunk(0);
-    __syncthreads();
-    load_chunk(1);
+    __syncthreads();                                    // the producer staged the first chunk
     float qv[EPL];
     ld_slice<EPL>(qv, &s_tok[0][0][0][0], c);
     float qinv = qinv_of(qv);
@@ -328,10 +348,6 @@ CHAIN_ATTR void chain_fwd(ChainFwdArgs a) {
             ld_slice<EPL>(qv, &s_tok[bn][jn][0][0], c);
             qinv_n = qinv_of(qv);
             dnext = dot_me(qv);
-        }
-        if (j == CT - 2) {                                  // refill: chunk t/CT+1 -> LDS, fetch t/CT+2
-            store_chunk(buf ^ 1);
-            load_chunk((t - ts) / CT + 2);
         }
         __syncthreads();
         uint4 r[CHAIN_WAVES];
@@ -412,12 +428,15 @@ struct RowsFwdArgs {
 };
 
 // 512 lanes = 32 rows of one chain per workgroup; grid (B*H, ceil(N/32)).  Replays every row's value from
-// the address log and emits the value snapshots with full-row non-temporal stores.
+// the address log and emits the value snapshots with full-row non-temporal stores.  A row changes only at
+// its own writes, so the replay visits events, not steps: per 16-step piece of the staged address log a
+// lane forms the mask of steps that wrote its row (4 LDS reads) and, with the piece's G-aligned snapshot
+// steps, walks the set bits in step order (snapshot first: it is the PRE-write state).
 template <int D, typename TI>
 ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     constexpr int EPL = D / 16;
     constexpr int TC = 2048;
-    __shared__ int s_am[TC];
+    __shared__ __align__(16) int s_am[TC];
     __shared__ float s_g[TC];
     const int T = a.T, H = a.H, N = a.N, G = a.G;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
@@ -432,7 +451,6 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     if (live && a.v0) ld_slice<EPL>(V, a.v0 + ((size_t)bh * N + n) * D, c);
     float* vb = a.vbuf + (((size_t)b * a.NB + a.ts / G) * H + h) * N * D + (size_t)(live ? n : 0) * D;
     const size_t sstride = (size_t)H * N * D;
-    int gc = 0;
     for (int t0 = a.ts; t0 < a.te; t0 += TC) {
         const int tn = min(TC, a.te - t0);
         __syncthreads();
@@ -441,22 +459,37 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
             s_am[u] = a.am[ix];
             s_g[u] = a.gate[ix];
         }
+        for (int u = tn + tid; u < ((tn + 15) & ~15); u += 512) s_am[u] = -1;
         __syncthreads();
         if (!live) continue;
-        for (int jt = 0; jt < tn; jt++) {
-            if (gc == 0) {
-                st_slice_nt<EPL>(vb, V, c);
-                vb += sstride;
-            }
-            if (++gc == G) gc = 0;
-            if (s_am[jt] == n) {
-                const size_t ix = tok0 + (size_t)(t0 + jt) * H;
-                const float g = s_g[jt], omw = 1.f - g;
-                float vv[EPL];
-                ld_slice<EPL>(vv, vp + ix * D, c);
-                if (a.vold) st_slice<EPL>(a.vold + ix * D, V, c);
+        for (int j0 = 0; j0 < tn; j0 += 16) {
+            u32 hm = 0;
 #pragma unroll
-                for (int e = 0; e < EPL; e++) V[e] = blend(V[e], vv[e], g, omw);
+            for (int u = 0; u < 4; u++) {
+                const int4 a4 = *reinterpret_cast<const int4*>(&s_am[j0 + 4 * u]);
+                hm |= ((a4.x == n ? 1u : 0u) | (a4.y == n ? 2u : 0u) | (a4.z == n ? 4u : 0u) | (a4.w == n ? 8u : 0u)) << (4 * u);
+            }
+            const int len = min(16, tn - j0);
+            const int ph = (t0 + j0 - a.ts) % G;          // steps since the last snapshot (ts % G == 0)
+            u32 sm = 0;
+            for (int i = ph == 0 ? 0 : G - ph; i < len; i += G) sm |= 1u << i;
+            u32 ev = hm | sm;
+            while (ev) {
+                const int i = __builtin_ctz(ev);
+                ev &= ev - 1;
+                if ((sm >> i) & 1u) {
+                    st_slice_nt<EPL>(vb, V, c);
+                    vb += sstride;
+                }
+                if ((hm >> i) & 1u) {
+                    const size_t ix = tok0 + (size_t)(t0 + j0 + i) * H;
+                    const float g = s_g[j0 + i], omw = 1.f - g;
+                    float vv[EPL];
+                    ld_slice<EPL>(vv, vp + ix * D, c);
+                    if (a.vold) st_slice<EPL>(a.vold + ix * D, V, c);
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) V[e] = blend(V[e], vv[e], g, omw);
+                }
             }
         }
     }
@@ -1410,7 +1443,7 @@ __global__ __launch_bounds__(256) void reduce_parts(const float* __restrict__ pa
 // ===================================================================================== host dispatch
 template <int D, typename TI>
 hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
-    dim3 grid(B * a.H), block(CHAIN_THREADS);
+    dim3 grid(B * a.H), block(FWD_THREADS);
 #define SLOT_CF(PP) if (a.N <= 4 * CHAIN_WAVES * PP) { hipLaunchKernelGGL((chain_fwd<D, PP, TI>), grid, block, 0, st, a); return hipGetLastError(); }
     SLOT_CF(1) SLOT_CF(2) SLOT_CF(4) SLOT_CF(8) SLOT_CF(16)
 #undef SLOT_CF
