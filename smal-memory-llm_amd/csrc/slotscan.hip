@@ -44,6 +44,7 @@ using namespace slot;
 typedef uint64_t u64;
 typedef uint32_t u32;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define SLOT_CT 16          // tokens per staged chunk
 #define CHAIN_WAVES 3
@@ -188,34 +189,88 @@ struct ChainFwdArgs {
     int ts, te;                                          // steps [ts, te) of the T-long sequence; ts % G == 0
 };
 
-// Three compute waves run the chain; a fourth, producer wave does every token load (q, k, gate, fr into the
-// double-buffered LDS staging) and joins the per-step barrier.  The compute waves then issue only stores
-// to global memory and never wait on the vector-memory counter, which on gfx9 also counts stores: a
-// refill in a compute wave would wait for its own snapshot and log stores to reach memory.
+// Wave-local LDS ordering: lanes of one wave exchange data through LDS (DS instructions of a wave execute
+// in order; the fences keep the compiler from moving the accesses across).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Row-slice stores at a scalar base plus a 32-bit lane byte offset (the saddr form: no per-row 64-bit
+// address registers)
+template <int EPL, bool NT>
+__device__ __forceinline__ void st_slice_at(float* base, u32 boff, const float* s) {
+    char* p = reinterpret_cast<char*>(base) + boff;
+#pragma unroll
+    for (int jj = 0; jj < EPL / 4; jj++) {
+        f32x4 v = {s[4 * jj], s[4 * jj + 1], s[4 * jj + 2], s[4 * jj + 3]};
+        if (NT) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p + 256 * jj));
+        else *reinterpret_cast<f32x4*>(p + 256 * jj) = v;
+    }
+}
+
+// Wave max of an ordered key (fkey), at every lane: integer max needs no NaN canonicalisation, so each
+// DPP stage is one v_max_u32 with a DPP source.
+__device__ __forceinline__ u32 wavemax_key(u32 v) {
+    v = max(v, dppu<SLOT_DPP_XOR1>(v));
+    v = max(v, dppu<SLOT_DPP_XOR2>(v));
+    v = max(v, dppu<SLOT_DPP_HMIR>(v));
+    v = max(v, dppu<SLOT_DPP_MIR>(v));
+    auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max(p[0], p[1]);
+    auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max(r[0], r[1]);
+}
+
+// The sequential key chain, windowed over the staged 16-step chunks.
+//
+// Three compute waves hold the keys in registers (row layout of ChainRows; the P row slots of a lane are
+// P-wide vectors, one per element, so the written row -- a wave-uniform slot -- is addressed with an
+// M0-relative move instead of a branch).  A fourth, producer wave stages the tokens of the next chunk in
+// LDS, and with one MFMA pass per chunk computes the chunk's Gram block E[s][u] = <k_s, q_u> and the
+// query norms.  The producer does every global load, so the compute waves never wait on the
+// vector-memory counter, which on gfx9 also counts their snapshot and log stores.
+//
+// At the start of a window every compute wave computes the dot products of ALL its rows with the 16
+// queries of the window, S[n][u] = <K_n, q_u>, as fp32 MFMA (v_mfma_f32_16x16x4f32): the keys go through
+// a wave-private LDS tile into the B-operand layout, 16 rows at a time.  Inside the window a step writes
+// one row a; its dot products with the window's later queries follow exactly from linearity,
+//     <(1-g) K_a + g k_t, q_u> = (1-g) <K_a, q_u> + g E[t][u],
+// which the owner lane applies to its row's scores (rounded once per term, re-derived from the keys at
+// the next window).  The row norm of the written row is recomputed from its new elements.  The per-step
+// work left is the score, the argmax, and the one-row update.
 #define FWD_THREADS (CHAIN_THREADS + 64)
 template <int D, int P, typename TI>
 __global__ __attribute__((amdgpu_flat_work_group_size(FWD_THREADS, FWD_THREADS), amdgpu_waves_per_eu(2)))
 void chain_fwd(ChainFwdArgs a) {
-    constexpr int CT = (sizeof(TI) == 4 && P >= 16) ? 8 : SLOT_CT;   // fewer staging registers for fp32 tokens
     constexpr int EPL = D / 16;
+    constexpr int DP = D + 4;                           // padded LDS row: 16 rows at stride DP hit 16 bank groups
     constexpr int EPU = 16 / (int)sizeof(TI);          // token elements per uint4
     constexpr int RU = D / EPU;                         // uint4 per token row
     constexpr int NU = CT * 2 * RU;                     // uint4 per staged chunk: (q row, k row) per token
     constexpr int UPT = (NU + 63) / 64;                // per producer lane
     constexpr bool BF = sizeof(TI) == 2;
-    __shared__ __align__(16) float s_tok[2][CT][2][D];
-    __shared__ float s_g[2][CT], s_fr[2][CT];
+    constexpr int WR = 4 * P;                           // rows per compute wave
+    constexpr int NT = WR >= 16 ? WR / 16 : 1;          // 16-row MFMA tiles per wave
+    constexpr int KL = D / 4;                           // MFMA operand dims per lane group
+    constexpr int SS = CT + 4;                          // padded row of the per-wave score table
+    constexpr int KT = (16 * DP > WR * SS) ? 16 * DP : WR * SS;
+    typedef float rowv __attribute__((ext_vector_type(P)));
+    __shared__ __align__(16) float s_q[2][CT][DP];
+    __shared__ __align__(16) float s_k[2][CT][DP];
+    __shared__ __align__(16) float s_E[2][CT][CT];
+    __shared__ float s_qi[2][CT], s_g[2][CT], s_fr[2][CT];
+    __shared__ __align__(16) float s_kt[CHAIN_WAVES][KT];
     __shared__ uint4 s_red[2][CHAIN_WAVES];
 
     const int T = a.T, H = a.H, N = a.N, G = a.G, ts = a.ts, te = a.te;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = tid & 15;
-    const ChainRows<P> R(tid);
+    const int m16 = lane & 15, ag = lane >> 4;          // MFMA operand position: row / column m16, k group ag
     const TI* __restrict__ qp = (const TI*)a.q;
     const TI* __restrict__ kp = (const TI*)a.k;
     const size_t tok0 = (size_t)b * T * H + h;          // token (b, t, h) = tok0 + t * H
-    float* kb = a.kbuf + (((size_t)b * a.NB + ts / G) * H + h) * N * D;   // key snapshot of block ts / G
-    const size_t sstride = (size_t)H * N * D;
 
     if (wave == CHAIN_WAVES) {                          // the producer wave
         uint4 rq[UPT];
@@ -243,20 +298,49 @@ void chain_fwd(ChainFwdArgs a) {
                 const int u = lane + 64 * m;
                 if (u < NU) {
                     const int j = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
-                    stage_store(&s_tok[bf][j][arr][w * EPU], rq[m], BF);
+                    stage_store(arr ? &s_k[bf][j][w * EPU] : &s_q[bf][j][w * EPU], rq[m], BF);
                 }
             }
             if (lane < CT) s_g[bf][lane] = rs;
             else if (lane < 2 * CT) s_fr[bf][lane - CT] = rs;
         };
+        // E[s][u] = <k_s, q_u> (A = key tokens, B = query tokens; lane l, reg r -> E[4 ag + r][m16]) and
+        // 1 / max(|q_u|, 1e-6) (four lanes per query, dims split in quarters)
+        auto gram = [&](int bf) {
+            wave_lds_sync();
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i4 = 0; i4 < KL / 4; i4++) {
+                const float4 ka = ld4(&s_k[bf][m16][ag * KL + 4 * i4]);
+                const float4 qb = ld4(&s_q[bf][m16][ag * KL + 4 * i4]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.x, qb.x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.y, qb.y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.z, qb.z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.w, qb.w, acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) s_E[bf][4 * ag + r][m16] = acc[r];
+            const int u = lane >> 2, p4 = lane & 3;
+            float qq = 0.f;
+#pragma unroll
+            for (int i4 = 0; i4 < D / 16; i4++) {
+                const float4 x = ld4(&s_q[bf][u][p4 * (D / 4) + 4 * i4]);
+                qq = fmaf(x.x, x.x, qq); qq = fmaf(x.y, x.y, qq); qq = fmaf(x.z, x.z, qq); qq = fmaf(x.w, x.w, qq);
+            }
+            qq += dppf<SLOT_DPP_XOR1>(qq);
+            qq += dppf<SLOT_DPP_XOR2>(qq);
+            if (p4 == 0) s_qi[bf][u] = rsq_clamped(qq);
+        };
         load_chunk(0);
         store_chunk(0);
+        gram(0);
         __syncthreads();
         load_chunk(1);
         int j = 0, buf = 0;
         for (int t = ts; t < te; t++) {
-            if (j == CT - 2) {                           // refill: chunk (t-ts)/CT+1 -> LDS, fetch +2
-                store_chunk(buf ^ 1);
+            if (j == CT - 3) store_chunk(buf ^ 1);      // chunk +1 -> the other buffer (read from the next window)
+            else if (j == CT - 2) {
+                gram(buf ^ 1);
                 load_chunk((t - ts) / CT + 2);
             }
             __syncthreads();
@@ -265,42 +349,31 @@ void chain_fwd(ChainFwdArgs a) {
         return;
     }
 
-    float K[P][EPL];
+    const ChainRows<P> R(tid);
+    float* kb = a.kbuf + (((size_t)b * a.NB + ts / G) * H + h) * N * D;   // key snapshot of block ts / G
+    const size_t sstride = (size_t)H * N * D;
+    rowv Kv[EPL];                                       // Kv[e][j]: element e of this lane's slice of row j
     float o_me = 0.f, kinv_me;
     {
         float x[P];
 #pragma unroll
         for (int j = 0; j < P; j++) {
             const int n = R.row(j);
+            float row[EPL];
 #pragma unroll
-            for (int e = 0; e < EPL; e++) K[j][e] = 0.f;
-            if (a.k0 && n < N) ld_slice<EPL>(K[j], a.k0 + ((size_t)bh * N + n) * D, c);
+            for (int e = 0; e < EPL; e++) row[e] = 0.f;
+            if (a.k0 && n < N) ld_slice<EPL>(row, a.k0 + ((size_t)bh * N + n) * D, c);
             float kk = 0.f;
 #pragma unroll
-            for (int e = 0; e < EPL; e++) kk = fmaf(K[j][e], K[j][e], kk);
+            for (int e = 0; e < EPL; e++) { Kv[e][j] = row[e]; kk = fmaf(row[e], row[e], kk); }
             x[j] = kk;
         }
         kinv_me = rsq_clamped(rs_reduce<P>(x, c));
         if (a.o0 && R.n_me < N) o_me = a.o0[(size_t)bh * N + R.n_me];
     }
-
-    // this lane's row dotted with a query slice, completed by the reduce-scatter
-    auto dot_me = [&](const float* qv) -> float {
-        float x[P];
+    auto row_of = [&](int j, float* row) {
 #pragma unroll
-        for (int jr = 0; jr < P; jr++) {
-            float d = 0.f;
-#pragma unroll
-            for (int e = 0; e < EPL; e++) d = fmaf(K[jr][e], qv[e], d);
-            x[jr] = d;
-        }
-        return rs_reduce<P>(x, c);
-    };
-    auto qinv_of = [&](const float* qv) -> float {
-        float qq = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; e++) qq = fmaf(qv[e], qv[e], qq);
-        return rsq_clamped(rowsum16(qq));
+        for (int e = 0; e < EPL; e++) row[e] = Kv[e][j];
     };
 
     const float temp = a.temp[0];
@@ -308,113 +381,151 @@ void chain_fwd(ChainFwdArgs a) {
     const float eps = a.eps;
     const bool occb = a.occb != 0, frt = a.frt != 0;
     const bool valid_me = R.n_me < N;
+    const u32 roff = (u32)((R.rowbase * D + 4 * c) * 4);  // byte offset of this lane's slice of row rowbase
+    const int nvalid = min(max(N - R.rowbase, 0), P);    // rows of this row group below N
+    const int nl_me = (lane >> 4) * P + (c >> RS<P>::SH);  // this lane's row, wave-local
+    float* kt = &s_kt[wave][0];
 
     __syncthreads();                                    // the producer staged the first chunk
-    float qv[EPL];
-    ld_slice<EPL>(qv, &s_tok[0][0][0][0], c);
-    float qinv = qinv_of(qv);
-    float dme = dot_me(qv);                             // <K_me, q_t> for the current keys
-    int par = 0, j = 0, buf = 0, gc = 0;
-    for (int t = ts; t < te; t++) {
-        const float g = s_g[buf][j];
-        const float frv = frt ? s_fr[buf][j] : fr_s;
-        const float cs = (dme * kinv_me) * qinv;         // cosine of this lane's row with q_t
-        const float s = temp * cs;
-        if (a.cslog && R.prim && valid_me) a.cslog[((size_t)bh * T + t) * N + R.n_me] = cs;
-        const bool taken = o_me >= eps;
-        const float occ = occb ? (taken ? 1.f : 0.f) : o_me;
-        const float z = s - frv * occ;
-        {   // this wave's candidates: best occupied (z, lowest row) and lowest free row; mo and mf are
-            // wave-uniform, so the readlane runs outside divergent code
-            const float zo = (valid_me && taken) ? z : -INFINITY;
-            const float wm = wavemax(zo);
-            const u64 mo = __ballot(valid_me && taken && zo == wm);
-            const u64 mf = __ballot(valid_me && !taken);
+    int par = 0, gc = 0;
+    for (int w0 = ts; w0 < te; w0 += CT) {
+        const int buf = ((w0 - ts) / CT) & 1;
+        f32x16 Sr;                                      // <K_me, q_{w0+u}>
+        {   // window GEMM: S^T = Q K^T, 16 rows per tile; lane l, reg r -> S[16 tau + m16][4 ag + r]
+            f32x4 acc[NT];
+#pragma unroll
+            for (int tau = 0; tau < NT; tau++) {
+                // P divides 16, so a row group's rows lie in one tile: (lane >> 4) * P / 16
+                if (WR <= 16 || (lane >> 4) * P / 16 == tau) {
+#pragma unroll
+                    for (int jr = 0; jr < P; jr++) {
+                        float row[EPL];
+                        row_of(jr, row);
+                        st_slice<EPL>(kt + ((lane >> 4) * P + jr - 16 * tau) * DP, row, c);
+                    }
+                }
+                wave_lds_sync();
+                acc[tau] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i4 = 0; i4 < KL / 4; i4++) {
+                    const float4 qa = ld4(&s_q[buf][m16][ag * KL + 4 * i4]);
+                    const float4 kb4 = ld4(kt + m16 * DP + ag * KL + 4 * i4);
+                    acc[tau] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.x, kb4.x, acc[tau], 0, 0, 0);
+                    acc[tau] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.y, kb4.y, acc[tau], 0, 0, 0);
+                    acc[tau] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.z, kb4.z, acc[tau], 0, 0, 0);
+                    acc[tau] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.w, kb4.w, acc[tau], 0, 0, 0);
+                }
+                wave_lds_sync();
+            }
+#pragma unroll
+            for (int tau = 0; tau < NT; tau++)
+                if (16 * tau + m16 < WR) *reinterpret_cast<f32x4*>(kt + (16 * tau + m16) * SS + 4 * ag) = acc[tau];
+            wave_lds_sync();
+#pragma unroll
+            for (int q4 = 0; q4 < CT / 4; q4++) {
+                const float4 v = ld4(kt + nl_me * SS + 4 * q4);
+                Sr[4 * q4 + 0] = v.x; Sr[4 * q4 + 1] = v.y; Sr[4 * q4 + 2] = v.z; Sr[4 * q4 + 3] = v.w;
+            }
+            wave_lds_sync();
+        }
+#pragma unroll 1
+        for (int j = 0; j < CT; j++) {                  // rolled: the step's score is one M0-relative move
+            const int t = w0 + j;
+            if (t >= te) break;
+            const float g = s_g[buf][j];
+            const float frv = frt ? s_fr[buf][j] : fr_s;
+            const float cs = (Sr[j] * kinv_me) * s_qi[buf][j];   // cosine of this lane's row with q_t
+            const float s = temp * cs;
+            if (a.cslog && R.prim && valid_me) a.cslog[((size_t)bh * T + t) * N + R.n_me] = cs;
+            const bool taken = o_me >= eps;
+            const float occ = occb ? (taken ? 1.f : 0.f) : o_me;
+            const float z = s - frv * occ;
+            {   // this wave's candidates: best occupied (z, lowest row) and lowest free row; the ballots are
+                // wave-uniform, so the readlane runs outside divergent code
+                const u32 zk = (valid_me && taken) ? fkey(z) : 0u;
+                const u32 wm = wavemax_key(zk);
+                const u64 mo = __ballot(valid_me && taken && zk == wm);
+                const u64 mf = __ballot(valid_me && !taken);
+                int bo = -1, fo = -1;
+                u32 fz = 0u;
+                if (mo) bo = row_of_lane<P>(wave, __builtin_ctzll(mo));
+                if (mf) {
+                    const int lf = __builtin_ctzll(mf);
+                    fo = row_of_lane<P>(wave, lf);
+                    fz = (u32)__builtin_amdgcn_readlane((int)fkey(z), lf);
+                }
+                if (lane == 0) s_red[par][wave] = make_uint4(wm, (u32)bo, (u32)fo, fz);
+            }
+            float kv[EPL];                                  // the key token, for the write below
+            ld_slice<EPL>(kv, &s_k[buf][j][0], c);
+            __syncthreads();
+            uint4 r[CHAIN_WAVES];
+#pragma unroll
+            for (int w = 0; w < CHAIN_WAVES; w++) r[w] = s_red[par][w];
+            if (gc == 0) {                                  // the PRE-write key state of block t / G:
+                u32 ro = roff;                              // every row group stores whole 512-byte rows
+                int nvv = nvalid;
+                asm volatile("" : "+v"(ro), "+v"(nvv));     // per-snapshot offsets, not 16 live registers
+#pragma unroll
+                for (int jr = 0; jr < P; jr++) {
+                    float row[EPL];
+                    row_of(jr, row);
+                    if (jr < nvv) st_slice_at<EPL, true>(kb, ro + (u32)(jr * D * 4), row);
+                }
+                kb += sstride;
+            }
+            if (++gc == G) gc = 0;
+            // waves in order = rows in order: strict '>' keeps the lowest row on ties
+            u32 bz = 0u, fz = 0u;
             int bo = -1, fo = -1;
-            float fz = 0.f;
-            if (mo) bo = row_of_lane<P>(wave, __builtin_ctzll(mo));
-            if (mf) {
-                const int lf = __builtin_ctzll(mf);
-                fo = row_of_lane<P>(wave, lf);
-                fz = readlanef(z, lf);
+#pragma unroll
+            for (int w = 0; w < CHAIN_WAVES; w++) {
+                const int o2 = (int)r[w].y, f2 = (int)r[w].z;
+                const bool tk = o2 >= 0 && (bo < 0 || r[w].x > bz);
+                bz = tk ? r[w].x : bz;
+                bo = tk ? o2 : bo;
+                const bool tf = f2 >= 0 && fo < 0;
+                fo = tf ? f2 : fo;
+                fz = tf ? r[w].w : fz;
             }
-            if (lane == 0) s_red[par][wave] = make_uint4(__float_as_uint(wm), (u32)bo, (u32)fo, __float_as_uint(fz));
-        }
-        // next step's query, its norm and its dot products with the CURRENT keys; after the write below
-        // only the rewritten row's dot is recomputed
-        float qinv_n = 0.f, dnext = 0.f;
-        if (t + 1 < te) {
-            const int jn = j + 1 == CT ? 0 : j + 1, bn = j + 1 == CT ? (buf ^ 1) : buf;
-            ld_slice<EPL>(qv, &s_tok[bn][jn][0][0], c);
-            qinv_n = qinv_of(qv);
-            dnext = dot_me(qv);
-        }
-        __syncthreads();
-        uint4 r[CHAIN_WAVES];
+            par ^= 1;
+            const int amv = __builtin_amdgcn_readfirstlane((fo >= 0 && (bo < 0 || fz > bz || (fz == bz && fo < bo))) ? fo : bo);
+            const size_t ix = tok0 + (size_t)t * H;
+            if (tid == 0) a.am[ix] = amv;
+            if (amv >= R.rowbase && amv < R.rowbase + P) {  // this row group holds the written row
+                const int sl = amv & (P - 1);               // its register slot: the same in every lane
+                const float omw = 1.f - g;
+                float old[EPL], part = 0.f;
 #pragma unroll
-        for (int w = 0; w < CHAIN_WAVES; w++) r[w] = s_red[par][w];
-        if (gc == 0) {                                      // the PRE-write key state of block t / G:
+                for (int e = 0; e < EPL; e++) {
+                    old[e] = Kv[e][sl];
+                    const float nv = blend(old[e], kv[e], g, omw);
+                    Kv[e][sl] = nv;
+                    part = fmaf(nv, nv, part);
+                }
+                if (a.kold) st_slice<EPL>(a.kold + ix * D, old, c);
+                const float kk = rowsum16(part);
+                if (R.n_me == amv) {
+                    if (a.oold && R.prim) a.oold[ix] = o_me;
+                    o_me = omw * o_me + g;
+                    kinv_me = rsq_clamped(kk);
+                    // all 16 entries: those at or before step j are never read again in this window
+                    const f32x4* er = reinterpret_cast<const f32x4*>(&s_E[buf][j][0]);
 #pragma unroll
-            for (int jr = 0; jr < P; jr++) {                // every row group stores whole 512-byte rows
-                const int n = R.row(jr);
-                if (n < N) st_slice_nt<EPL>(kb + (size_t)n * D, K[jr], c);
-            }
-            kb += sstride;
-        }
-        if (++gc == G) gc = 0;
-        // waves in order = rows in order: strict '>' keeps the lowest row on ties
-        float bz = -INFINITY, fz = 0.f;
-        int bo = -1, fo = -1;
+                    for (int q4 = 0; q4 < CT / 4; q4++) {
+                        const f32x4 e4 = er[q4];
 #pragma unroll
-        for (int w = 0; w < CHAIN_WAVES; w++) {
-            const float z2 = __uint_as_float(r[w].x);
-            const int o2 = (int)r[w].y, f2 = (int)r[w].z;
-            const bool tk = o2 >= 0 && (bo < 0 || z2 > bz);
-            bz = tk ? z2 : bz;
-            bo = tk ? o2 : bo;
-            const bool tf = f2 >= 0 && fo < 0;
-            fo = tf ? f2 : fo;
-            fz = tf ? __uint_as_float(r[w].w) : fz;
-        }
-        par ^= 1;
-        const int amv = __builtin_amdgcn_readfirstlane((fo >= 0 && (bo < 0 || fz > bz || (fz == bz && fo < bo))) ? fo : bo);
-        const size_t ix = tok0 + (size_t)t * H;
-        if (tid == 0) a.am[ix] = amv;
-        if (amv >= R.rowbase && amv < R.rowbase + P) {      // this row group holds the written row
-            const int sl = amv & (P - 1);                   // its register slot: the same in every lane
-            const float omw = 1.f - g;
-            float kv[EPL];
-            ld_slice<EPL>(kv, &s_tok[buf][j][1][0], c);
-            float part = 0.f, pd = 0.f;
-#pragma unroll
-            for (int jr = 0; jr < P; jr++) {
-                if (jr == sl) {
-                    if (a.kold) st_slice<EPL>(a.kold + ix * D, K[jr], c);
-#pragma unroll
-                    for (int e = 0; e < EPL; e++) {
-                        K[jr][e] = blend(K[jr][e], kv[e], g, omw);
-                        part = fmaf(K[jr][e], K[jr][e], part);
-                        pd = fmaf(K[jr][e], qv[e], pd);
+                        for (int x = 0; x < 4; x++) Sr[4 * q4 + x] = fmaf(omw, Sr[4 * q4 + x], g * e4[x]);
                     }
                 }
             }
-            const float kk = rowsum16(part);
-            const float kd = rowsum16(pd);
-            if (R.n_me == amv) {
-                if (a.oold && R.prim) a.oold[ix] = o_me;
-                o_me = omw * o_me + g;
-                kinv_me = rsq_clamped(kk);
-                dnext = kd;
-            }
         }
-        dme = dnext;
-        qinv = qinv_n;
-        if (++j == CT) { j = 0; buf ^= 1; }
     }
 #pragma unroll
     for (int jr = 0; jr < P; jr++) {
-        const int n = R.row(jr);
-        if (n < N) st_slice<EPL>(a.kfin + ((size_t)bh * N + n) * D, K[jr], c);
+        float row[EPL];
+        row_of(jr, row);
+        if (jr < nvalid) st_slice_at<EPL, false>(a.kfin + (size_t)bh * N * D, roff + (u32)(jr * D * 4), row);
     }
     if (valid_me && R.prim) a.ofin[(size_t)bh * N + R.n_me] = o_me;
 }
@@ -1025,7 +1136,6 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 // A operand: lane l holds W[step l & 15][row kk + KK*(l >> 4)]; result lane l, register r:
 //   dqn[step 4*(l >> 4) + r][dim w*DW + 16*nb + (l & 15)].
 #define WIN 16
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 template <int D, int RPL, int NW, typename TI>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(NW == 8 ? 4 : 2)))
