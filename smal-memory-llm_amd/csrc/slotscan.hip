@@ -624,7 +624,11 @@ struct RowsBwdArgs {
 // Dn (B*H, N, T), 64 contiguous bytes per row.  The upstream snapshot gradient is prefetched two blocks
 // ahead.  The step loop is not unrolled, which keeps the rare write/boundary paths from multiplying
 // register copies.
-template <int D, typename TI>
+// An empty asm whose output `o` (a load offset) depends on the register set's last uses: loads addressed
+// with `o` cannot be scheduled before those uses, so they can reuse the set's registers.
+#define RB_AFTER(o) { if constexpr (EPL == 8) asm volatile("" : "+v"(o) : "v"(cp), "v"(dK[0]), "v"(dK[1]), "v"(dK[2]), "v"(dK[3]), "v"(dK[4]), "v"(dK[5]), "v"(dK[6]), "v"(dK[7]), "v"(dV[0]), "v"(dV[1]), "v"(dV[2]), "v"(dV[3]), "v"(dV[4]), "v"(dV[5]), "v"(dV[6]), "v"(dV[7])); \
+    else asm volatile("" : "+v"(o) : "v"(cp), "v"(dK[0]), "v"(dK[1]), "v"(dK[2]), "v"(dK[3]), "v"(dV[0]), "v"(dV[1]), "v"(dV[2]), "v"(dV[3])); }
+template <int D, typename TI, bool G8>
 ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
     constexpr int EPL = D / 16;
     constexpr int EPU = 16 / (int)sizeof(TI);
@@ -703,9 +707,61 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
     __syncthreads();
     load_chunk(nblk - 2);
     int buf = 0;
+    // one reverse step of this row: undo at a write, the Dn partial, the write's token gradients
+    auto step = [&](int i, int t, u32 hm) {
+        const bool hit = (hm >> i) & 1u;
+        if (hit) {                                      // undo: the row before this step's write
+            const size_t ix = tok0 + (size_t)t * H;
+            ld_slice<EPL>(K, a.kold + ix * D, c);
+            ld_slice<EPL>(V, a.vold + ix * D, c);
+            cp = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) cp = fmaf(K[e], dK[e], fmaf(V[e], dV[e], cp));
+        }
+        float p = -cp;
+        const float* kt = &s_tok[buf][i][0][0];
+        const float* vt = &s_tok[buf][i][1][0];
+#pragma unroll
+        for (int jj = 0; jj < EPL / 4; jj++) {
+            const float4 k4 = *reinterpret_cast<const float4*>(kt + 4 * c + 64 * jj);
+            const float4 v4 = *reinterpret_cast<const float4*>(vt + 4 * c + 64 * jj);
+            p = fmaf(k4.x, dK[4 * jj + 0], p); p = fmaf(k4.y, dK[4 * jj + 1], p);
+            p = fmaf(k4.z, dK[4 * jj + 2], p); p = fmaf(k4.w, dK[4 * jj + 3], p);
+            p = fmaf(v4.x, dV[4 * jj + 0], p); p = fmaf(v4.y, dV[4 * jj + 1], p);
+            p = fmaf(v4.z, dV[4 * jj + 2], p); p = fmaf(v4.w, dV[4 * jj + 3], p);
+        }
+        s_part[rg][i][c] = p;
+        if (hit) {
+            const size_t ix = tok0 + (size_t)t * H;
+            const float g = s_g[buf][i], omw = 1.f - g;
+            float x[EPL], y[EPL];
+#pragma unroll
+            for (int e = 0; e < EPL; e++) { x[e] = g * dK[e]; y[e] = g * dV[e]; dK[e] *= omw; dV[e] *= omw; }
+            cp *= omw;
+            st_slice<EPL>(dkp + ix * D, x, c);
+            st_slice<EPL>(dvp + ix * D, y, c);
+        }
+    };
+    // the gradient of the snapshot emitted at a block boundary enters (it is the pre-write state)
+    auto enter = [&](const float* pk, const float* pv) {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            dK[e] += pk[e];
+            dV[e] += pv[e];
+            cp = fmaf(K[e], pk[e], fmaf(V[e], pv[e], cp));
+        }
+    };
+    // lane c sums the row group's 16 partials of step 16m + c (same wave wrote them: wave barrier only)
+    auto emit_dn = [&](int m) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float dnv = 0.f;
+#pragma unroll
+        for (int l = 0; l < 16; l++) dnv += s_part[rg][c][l];
+        if (live && 16 * m + c < T) a.dn[((size_t)bh * N + n) * T + 16 * m + c] = dnv;
+    };
     for (int m = nblk - 1; m >= 0; m--) {
-        const int i_hi = min(15, T - 1 - 16 * m);
-        for (int i = 15; i > i_hi; i--) s_part[rg][i][c] = 0.f;
         u32 hm = 0;                                      // steps of this chunk that wrote this row
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -714,68 +770,57 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
                 | (a4.z == n ? 4u : 0u) << (4 * u) | (a4.w == n ? 8u : 0u) << (4 * u);
         }
         if (!live) hm = 0;
-        for (int i = i_hi; i >= 0; i--) {
-            const int t = 16 * m + i;
-            const bool hit = (hm >> i) & 1u;
-            if (hit) {                                      // undo: the row before this step's write
-                const size_t ix = tok0 + (size_t)t * H;
-                ld_slice<EPL>(K, a.kold + ix * D, c);
-                ld_slice<EPL>(V, a.vold + ix * D, c);
-                cp = 0.f;
-#pragma unroll
-                for (int e = 0; e < EPL; e++) cp = fmaf(K[e], dK[e], fmaf(V[e], dV[e], cp));
+        if (G8) {
+            // G == 8, T % 16 == 0: boundaries at i = 8 (block 2m + 1, register set 1) and i = 0 (block 2m,
+            // set 2).  Each set is reloaded in place with the block two boundaries ahead; the load offset
+            // passes through an empty asm that takes the set's last uses as inputs, so the loads issue after
+            // them into the same registers, and the first wait on them comes 8 to 16 steps later.
+#pragma unroll 1
+            for (int i = 15; i >= 9; i--) step(i, 16 * m + i, hm);
+            step(8, 16 * m + 8, hm);
+            enter(pk1, pv1);
+            {
+                u32 o = (u32)max(2 * m - 1, 0) * (u32)(sbstride * sizeof(float));
+                RB_AFTER(o)
+                ld_slice_nt<EPL>(pk1, (const float*)((const char*)dkb0 + o), c);
+                ld_slice_nt<EPL>(pv1, (const float*)((const char*)dvb0 + o), c);
             }
-            float p = -cp;
-            const float* kt = &s_tok[buf][i][0][0];
-            const float* vt = &s_tok[buf][i][1][0];
-#pragma unroll
-            for (int jj = 0; jj < EPL / 4; jj++) {
-                const float4 k4 = *reinterpret_cast<const float4*>(kt + 4 * c + 64 * jj);
-                const float4 v4 = *reinterpret_cast<const float4*>(vt + 4 * c + 64 * jj);
-                p = fmaf(k4.x, dK[4 * jj + 0], p); p = fmaf(k4.y, dK[4 * jj + 1], p);
-                p = fmaf(k4.z, dK[4 * jj + 2], p); p = fmaf(k4.w, dK[4 * jj + 3], p);
-                p = fmaf(v4.x, dV[4 * jj + 0], p); p = fmaf(v4.y, dV[4 * jj + 1], p);
-                p = fmaf(v4.z, dV[4 * jj + 2], p); p = fmaf(v4.w, dV[4 * jj + 3], p);
+#pragma unroll 1
+            for (int i = 7; i >= 1; i--) step(i, 16 * m + i, hm);
+            if (m > 0) store_chunk(buf ^ 1);            // before the set-2 reload, whose loads it would wait on
+            step(0, 16 * m, hm);
+            enter(pk2, pv2);
+            {
+                u32 o = (u32)max(2 * m - 2, 0) * (u32)(sbstride * sizeof(float));
+                RB_AFTER(o)
+                ld_slice_nt<EPL>(pk2, (const float*)((const char*)dkb0 + o), c);
+                ld_slice_nt<EPL>(pv2, (const float*)((const char*)dvb0 + o), c);
             }
-            s_part[rg][i][c] = p;
-            if (hit) {
-                const size_t ix = tok0 + (size_t)t * H;
-                const float g = s_g[buf][i], omw = 1.f - g;
-                float x[EPL], y[EPL];
+            emit_dn(m);
+            if (m > 0) load_chunk(m - 2);
+        } else {
+            const int i_hi = min(15, T - 1 - 16 * m);
+            for (int i = 15; i > i_hi; i--) s_part[rg][i][c] = 0.f;
+            for (int i = i_hi; i >= 0; i--) {
+                const int t = 16 * m + i;
+                step(i, t, hm);
+                if (t == tb) {
+                    enter(pk1, pv1);
 #pragma unroll
-                for (int e = 0; e < EPL; e++) { x[e] = g * dK[e]; y[e] = g * dV[e]; dK[e] *= omw; dV[e] *= omw; }
-                cp *= omw;
-                st_slice<EPL>(dkp + ix * D, x, c);
-                st_slice<EPL>(dvp + ix * D, y, c);
-            }
-            if (t == tb) {                                  // the copy emitted at t is the pre-write state
-#pragma unroll
-                for (int e = 0; e < EPL; e++) {
-                    dK[e] += pk1[e];
-                    dV[e] += pv1[e];
-                    cp = fmaf(K[e], pk1[e], fmaf(V[e], pv1[e], cp));
-                    pk1[e] = pk2[e];
-                    pv1[e] = pv2[e];
-                }
-                nxt -= 1;
-                tb -= G;
-                if (nxt >= 1) {
-                    ld_slice_nt<EPL>(pk2, dkb0 + (size_t)(nxt - 1) * sbstride, c);
-                    ld_slice_nt<EPL>(pv2, dvb0 + (size_t)(nxt - 1) * sbstride, c);
+                    for (int e = 0; e < EPL; e++) { pk1[e] = pk2[e]; pv1[e] = pv2[e]; }
+                    nxt -= 1;
+                    tb -= G;
+                    if (nxt >= 1) {
+                        ld_slice_nt<EPL>(pk2, dkb0 + (size_t)(nxt - 1) * sbstride, c);
+                        ld_slice_nt<EPL>(pv2, dvb0 + (size_t)(nxt - 1) * sbstride, c);
+                    }
                 }
             }
-        }
-        // lane c sums the row group's 16 partials of step 16m + c (same wave wrote them: wave barrier only)
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float dnv = 0.f;
-#pragma unroll
-        for (int l = 0; l < 16; l++) dnv += s_part[rg][c][l];
-        if (live && 16 * m + c < T) a.dn[((size_t)bh * N + n) * T + 16 * m + c] = dnv;
-        if (m > 0) {
-            store_chunk(buf ^ 1);
-            load_chunk(m - 2);
+            emit_dn(m);
+            if (m > 0) {
+                store_chunk(buf ^ 1);
+                load_chunk(m - 2);
+            }
         }
         __syncthreads();
         buf ^= 1;
@@ -1795,13 +1840,15 @@ extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dty
     hipError_t e;
     {
         slothost::Scope sc(SLOTSCAN_K_ROWS_BWD, st);
+        const bool g8 = G == 8 && T % 16 == 0;          // two boundaries per chunk at fixed positions
+#define SLOT_RB(DD, TT) { if (g8) hipLaunchKernelGGL((rows_bwd<DD, TT, true>), grid, block, 0, st, ra); \
+                          else hipLaunchKernelGGL((rows_bwd<DD, TT, false>), grid, block, 0, st, ra); }
         if (D == 128) {
-            if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_bwd<128, bf16_t>), grid, block, 0, st, ra);
-            else hipLaunchKernelGGL((rows_bwd<128, float>), grid, block, 0, st, ra);
+            if (dtype == SLOTSCAN_BF16) SLOT_RB(128, bf16_t) else SLOT_RB(128, float)
         } else {
-            if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_bwd<64, bf16_t>), grid, block, 0, st, ra);
-            else hipLaunchKernelGGL((rows_bwd<64, float>), grid, block, 0, st, ra);
+            if (dtype == SLOTSCAN_BF16) SLOT_RB(64, bf16_t) else SLOT_RB(64, float)
         }
+#undef SLOT_RB
         e = hipGetLastError();
     }
     if (e != hipSuccess) return hip_fail(e, "rows_bwd launch");
