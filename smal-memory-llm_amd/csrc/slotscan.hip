@@ -1271,35 +1271,41 @@ void chain_bwd_w(ChainBwdArgs a) {
     const unsigned off_q = (unsigned)(tid / (D / EPU)) * (unsigned)(H * D) + (unsigned)EPU * (unsigned)(tid % (D / EPU));
     auto load_win = [&](int m) {
         const int t0 = m * WIN, nt = min(WIN, T - t0);
-        const float* csb = a.cslog + ((size_t)bh * T + t0) * N;          // (nt, N) contiguous
+        // byte offsets re-derived per window through an empty asm: the loads keep the scalar-base +
+        // 32-bit-offset form instead of 64-bit per-lane addresses hoisted out of the loop (which spill,
+        // and whose reloads would wait on this prefetch: scratch loads share the vector-memory counter)
+        u32 b_tid = 4u * (u32)tid, b_dn = 4u * off_dn, b_ko = 4u * off_ko, b_q = (u32)sizeof(TI) * off_q;
+        int tl = tid;                                    // bounds indices from a fresh copy, likewise
+        asm volatile("" : "+v"(b_tid), "+v"(b_dn), "+v"(b_ko), "+v"(b_q), "+v"(tl));
+        const char* csb = (const char*)(a.cslog + ((size_t)bh * T + t0) * N);   // (nt, N) contiguous
         const int ncsv = nt * N;
 #pragma unroll
         for (int u2 = 0; u2 < UCS; u2++) {
-            const float* bp = csb + NT * u2;
-            ncs[u2] = (tid + NT * u2 < ncsv) ? bp[(unsigned)tid] : 0.f;
+            const char* bp = csb + (size_t)NT * u2 * sizeof(float);
+            ncs[u2] = (tl + NT * u2 < ncsv) ? *reinterpret_cast<const float*>(bp + b_tid) : 0.f;
         }
-        const float* dnb = a.dn + (size_t)bh * N * T + t0;               // row n at + n * T
+        const char* dnb = (const char*)(a.dn + (size_t)bh * N * T + t0);      // row n at + n * T
 #pragma unroll
         for (int u2 = 0; u2 < UDN; u2++) {
-            const float* bp = dnb + (size_t)(NT / WIN) * u2 * T;
-            const int nn = tid / WIN + (NT / WIN) * u2;
-            ndn[u2] = (tid % WIN < nt && nn < N) ? bp[off_dn] : 0.f;
+            const char* bp = dnb + (size_t)(NT / WIN) * u2 * T * sizeof(float);
+            const int nn = tl / WIN + (NT / WIN) * u2;
+            ndn[u2] = (tl % WIN < nt && nn < N) ? *reinterpret_cast<const float*>(bp + b_dn) : 0.f;
         }
-        const float* kob = a.kold + (tok0 + (size_t)t0 * H) * D;
+        const char* kob = (const char*)(a.kold + (tok0 + (size_t)t0 * H) * D);
 #pragma unroll
         for (int u2 = 0; u2 < UKO; u2++) {
-            const float* bp = kob + (size_t)KR * u2 * H * D;
-            const int i = tid / (D / 4) + KR * u2;
+            const char* bp = kob + (size_t)KR * u2 * H * D * sizeof(float);
+            const int i = tl / (D / 4) + KR * u2;
             nko[u2] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < nt) nko[u2] = *reinterpret_cast<const uint4*>(bp + off_ko);
+            if (i < nt) nko[u2] = *reinterpret_cast<const uint4*>(bp + b_ko);
         }
-        const TI* qb = qp + (tok0 + (size_t)t0 * H) * D;
+        const char* qb = (const char*)(qp + (tok0 + (size_t)t0 * H) * D);
 #pragma unroll
         for (int u2 = 0; u2 < UQ; u2++) {
-            const TI* bp = qb + (size_t)QR * u2 * H * D;
-            const int i = tid / (D / EPU) + QR * u2;
+            const char* bp = qb + (size_t)QR * u2 * H * D * sizeof(TI);
+            const int i = tl / (D / EPU) + QR * u2;
             nq[u2] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < nt) nq[u2] = *reinterpret_cast<const uint4*>(bp + off_q);
+            if (i < nt) nq[u2] = *reinterpret_cast<const uint4*>(bp + b_q);
         }
         if (tid < 4 * WIN) {
             const int kind = tid / WIN, i = tid % WIN;
