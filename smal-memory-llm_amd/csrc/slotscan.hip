@@ -628,6 +628,28 @@ struct RowsBwdArgs {
 // with `o` cannot be scheduled before those uses, so they can reuse the set's registers.
 #define RB_AFTER(o) { if constexpr (EPL == 8) asm volatile("" : "+v"(o) : "v"(cp), "v"(dK[0]), "v"(dK[1]), "v"(dK[2]), "v"(dK[3]), "v"(dK[4]), "v"(dK[5]), "v"(dK[6]), "v"(dK[7]), "v"(dV[0]), "v"(dV[1]), "v"(dV[2]), "v"(dV[3]), "v"(dV[4]), "v"(dV[5]), "v"(dV[6]), "v"(dV[7])); \
     else asm volatile("" : "+v"(o) : "v"(cp), "v"(dK[0]), "v"(dK[1]), "v"(dK[2]), "v"(dK[3]), "v"(dV[0]), "v"(dV[1]), "v"(dV[2]), "v"(dV[3])); }
+// Loads the compiler does not track (it inserts no wait of its own for them).  The consumer waits with an
+// explicit vmcnt whose asm operands are the destinations, so no use can be scheduled before the wait; "+v"
+// keeps each destination in place, so no copy of a value that has not arrived can be made.  Used where the
+// compiler's own bookkeeping would otherwise wait with vmcnt(0) on loads issued a moment earlier.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void ldg_untracked_nt(f32x4& d, const void* p) {
+    asm volatile("global_load_dwordx4 %0, %1, off nt" : "+v"(d) : "v"(p));
+}
+__device__ __forceinline__ void ldg_untracked(u32x4& d, const void* p) {
+    asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(d) : "v"(p));
+}
+__device__ __forceinline__ void ldg_untracked(float& d, const void* p) {
+    asm volatile("global_load_dword %0, %1, off" : "+v"(d) : "v"(p));
+}
+template <int N4> __device__ __forceinline__ void vm_wait(f32x4* a, f32x4* b);
+template <> __device__ __forceinline__ void vm_wait<1>(f32x4* a, f32x4* b) {     // the 2 youngest may fly
+    asm volatile("s_waitcnt vmcnt(2)" : "+v"(a[0]), "+v"(b[0]));
+}
+template <> __device__ __forceinline__ void vm_wait<2>(f32x4* a, f32x4* b) {     // the 4 youngest may fly
+    asm volatile("s_waitcnt vmcnt(4)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
+}
+
 template <int D, typename TI, bool G8>
 ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
     constexpr int EPL = D / 16;
@@ -653,57 +675,94 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
     TI* __restrict__ dvp = (TI*)a.dv;
     const size_t tok0 = (size_t)b * T * H + h;
 
-    uint4 rq[UPT];
-    int ram = -1;
+    u32x4 rq[UPT];
+    float ram = __int_as_float(-1);                     // the address, as bits
     float rgt = 0.f;
     auto load_chunk = [&](int m) {                      // chunk m: t in [16m, 16m + 16)
 #pragma unroll
         for (int u2 = 0; u2 < UPT; u2++) {
             const int u = tid + 512 * u2;
-            rq[u2] = make_uint4(0u, 0u, 0u, 0u);
+            rq[u2] = u32x4{0u, 0u, 0u, 0u};
             if (u < NU && m >= 0) {
                 const int i = u / (2 * RU), arr = (u / RU) & 1, w = u % RU, t = 16 * m + i;
-                if (t < T) rq[u2] = reinterpret_cast<const uint4*>((arr ? vp : kp) + (tok0 + (size_t)t * H) * D)[w];
+                if (t < T) {
+                    const u32x4* src = reinterpret_cast<const u32x4*>((arr ? vp : kp) + (tok0 + (size_t)t * H) * D) + w;
+                    if constexpr (G8) ldg_untracked(rq[u2], src); else rq[u2] = *src;
+                }
             }
         }
         if (tid < 16) {
             const int t = 16 * m + tid;
-            ram = -1; rgt = 0.f;
-            if (m >= 0 && t < T) { ram = a.am[tok0 + (size_t)t * H]; rgt = a.gate[tok0 + (size_t)t * H]; }
+            ram = __int_as_float(-1); rgt = 0.f;
+            if (m >= 0 && t < T) {
+                const size_t ix = tok0 + (size_t)t * H;
+                if constexpr (G8) { ldg_untracked(ram, a.am + ix); ldg_untracked(rgt, a.gate + ix); }
+                else { ram = __int_as_float(a.am[ix]); rgt = a.gate[ix]; }
+            }
         }
     };
-    auto store_chunk = [&](int buf) {
+    // `fly`: the vector-memory operations that may still be in flight, all issued after the tokens (the
+    // G8 path's untracked token loads; the general path's loads are tracked by the compiler)
+    auto store_chunk = [&](int buf, auto fly) {
+        if constexpr (G8) {
+#define RB_TOKWAIT(S) { if constexpr (UPT == 1) asm volatile(S : "+v"(rq[0]), "+v"(ram), "+v"(rgt)); \
+                        else asm volatile(S : "+v"(rq[0]), "+v"(rq[1]), "+v"(ram), "+v"(rgt)); }
+            if constexpr (decltype(fly)::value == 0) RB_TOKWAIT("s_waitcnt vmcnt(0)")
+            else if constexpr (decltype(fly)::value == 2) RB_TOKWAIT("s_waitcnt vmcnt(2)")
+            else RB_TOKWAIT("s_waitcnt vmcnt(4)")
+#undef RB_TOKWAIT
+        }
 #pragma unroll
         for (int u2 = 0; u2 < UPT; u2++) {
             const int u = tid + 512 * u2;
             if (u < NU) {
                 const int i = u / (2 * RU), arr = (u / RU) & 1, w = u % RU;
-                stage_store(&s_tok[buf][i][arr][w * EPU], rq[u2], BF);
+                const uint4 r4 = make_uint4(rq[u2].x, rq[u2].y, rq[u2].z, rq[u2].w);
+                stage_store(&s_tok[buf][i][arr][w * EPU], r4, BF);
             }
         }
-        if (tid < 16) { s_am[buf][tid] = ram; s_g[buf][tid] = rgt; }
+        if (tid < 16) { s_am[buf][tid] = __float_as_int(ram); s_g[buf][tid] = rgt; }
     };
 
+    constexpr int NQ = EPL / 4;                          // 16-byte pieces of a row slice
     float K[EPL], V[EPL], dK[EPL], dV[EPL], pk1[EPL], pv1[EPL], pk2[EPL], pv2[EPL];
+    f32x4 gk1[NQ], gv1[NQ], gk2[NQ], gv2[NQ];           // the G8 path's two untracked gradient sets
     ld_slice<EPL>(K, a.kfin + ((size_t)bh * N + n) * D, c);
     ld_slice<EPL>(V, a.vfin + ((size_t)bh * N + n) * D, c);
 #pragma unroll
     for (int e = 0; e < EPL; e++) { dK[e] = 0.f; dV[e] = 0.f; pk2[e] = 0.f; pv2[e] = 0.f; }
+#pragma unroll
+    for (int q = 0; q < NQ; q++) { gk1[q] = gv1[q] = gk2[q] = gv2[q] = f32x4{0.f, 0.f, 0.f, 0.f}; }
     float cp = 0.f;                                      // this lane's share of <K, dK> + <V, dV>
     const size_t sbstride = (size_t)H * N * D;
     const float* dkb0 = a.dkbuf + ((size_t)b * a.NB * H + h) * N * D + (size_t)n * D;
     const float* dvb0 = a.dvbuf + ((size_t)b * a.NB * H + h) * N * D + (size_t)n * D;
+    // the G8 path's reload of a gradient set with block `blk` (clamped), untracked; the offset passes
+    // through an empty asm that takes the set's last uses as inputs, so the loads issue after them
+    auto reload = [&](f32x4* gk, f32x4* gv, int blk) {
+        u32 o = (u32)max(blk, 0) * (u32)(sbstride * sizeof(float)) + 16u * (u32)c;
+        RB_AFTER(o)
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            ldg_untracked_nt(gk[q], (const char*)dkb0 + o + 256 * q);
+            ldg_untracked_nt(gv[q], (const char*)dvb0 + o + 256 * q);
+        }
+    };
     int nxt = (T - 1) / G;                               // next block whose gradient enters (reverse order)
-    ld_slice_nt<EPL>(pk1, dkb0 + (size_t)nxt * sbstride, c);
-    ld_slice_nt<EPL>(pv1, dvb0 + (size_t)nxt * sbstride, c);
-    if (nxt >= 1) {
-        ld_slice_nt<EPL>(pk2, dkb0 + (size_t)(nxt - 1) * sbstride, c);
-        ld_slice_nt<EPL>(pv2, dvb0 + (size_t)(nxt - 1) * sbstride, c);
+    if constexpr (G8) {
+        reload(gk1, gv1, nxt);                           // set 2 is refilled during the first chunk
+    } else {
+        ld_slice_nt<EPL>(pk1, dkb0 + (size_t)nxt * sbstride, c);
+        ld_slice_nt<EPL>(pv1, dvb0 + (size_t)nxt * sbstride, c);
+        if (nxt >= 1) {
+            ld_slice_nt<EPL>(pk2, dkb0 + (size_t)(nxt - 1) * sbstride, c);
+            ld_slice_nt<EPL>(pv2, dvb0 + (size_t)(nxt - 1) * sbstride, c);
+        }
     }
     int tb = nxt * G;                                    // the step at which block `nxt` enters
     const int nblk = (T + 15) / 16;
     load_chunk(nblk - 1);
-    store_chunk(0);
+    store_chunk(0, std::integral_constant<int, 0>());
     __syncthreads();
     load_chunk(nblk - 2);
     int buf = 0;
@@ -712,8 +771,24 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
         const bool hit = (hm >> i) & 1u;
         if (hit) {                                      // undo: the row before this step's write
             const size_t ix = tok0 + (size_t)t * H;
-            ld_slice<EPL>(K, a.kold + ix * D, c);
-            ld_slice<EPL>(V, a.vold + ix * D, c);
+            if constexpr (G8) {                         // untracked, so no tracked load stays pending
+                f32x4 k4[NQ], v4[NQ];
+#pragma unroll
+                for (int q = 0; q < NQ; q++) {
+                    k4[q] = v4[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    ldg_untracked_nt(k4[q], a.kold + ix * D + 4 * c + 64 * q);
+                    ldg_untracked_nt(v4[q], a.vold + ix * D + 4 * c + 64 * q);
+                }
+                if constexpr (NQ == 2) asm volatile("s_waitcnt vmcnt(0)" : "+v"(k4[0]), "+v"(k4[1]), "+v"(v4[0]), "+v"(v4[1]));
+                else asm volatile("s_waitcnt vmcnt(0)" : "+v"(k4[0]), "+v"(v4[0]));
+#pragma unroll
+                for (int q = 0; q < NQ; q++)
+#pragma unroll
+                    for (int x = 0; x < 4; x++) { K[4 * q + x] = k4[q][x]; V[4 * q + x] = v4[q][x]; }
+            } else {
+                ld_slice<EPL>(K, a.kold + ix * D, c);
+                ld_slice<EPL>(V, a.vold + ix * D, c);
+            }
             cp = 0.f;
 #pragma unroll
             for (int e = 0; e < EPL; e++) cp = fmaf(K[e], dK[e], fmaf(V[e], dV[e], cp));
@@ -752,6 +827,10 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
         }
     };
     // lane c sums the row group's 16 partials of step 16m + c (same wave wrote them: wave barrier only)
+    // A row's Dn slice of one chunk is 64 bytes, half a 128-byte line; the odd chunk's value is held until
+    // the even chunk below it is done, and both halves of the line are stored together (written a chunk
+    // apart, the halves reached HBM as separate partial-line writes).
+    float dn_hold = 0.f;
     auto emit_dn = [&](int m) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -759,7 +838,13 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
         float dnv = 0.f;
 #pragma unroll
         for (int l = 0; l < 16; l++) dnv += s_part[rg][c][l];
-        if (live && 16 * m + c < T) a.dn[((size_t)bh * N + n) * T + 16 * m + c] = dnv;
+        float* drow = a.dn + ((size_t)bh * N + n) * T;
+        if (m & 1) {
+            dn_hold = dnv;                              // chunk m - 1 always follows
+        } else {
+            if (live && 16 * m + c < T) __builtin_nontemporal_store(dnv, drow + 16 * m + c);
+            if (live && m + 1 < nblk && 16 * (m + 1) + c < T) __builtin_nontemporal_store(dn_hold, drow + 16 * (m + 1) + c);
+        }
     };
     for (int m = nblk - 1; m >= 0; m--) {
         u32 hm = 0;                                      // steps of this chunk that wrote this row
@@ -770,32 +855,37 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
                 | (a4.z == n ? 4u : 0u) << (4 * u) | (a4.w == n ? 8u : 0u) << (4 * u);
         }
         if (!live) hm = 0;
-        if (G8) {
-            // G == 8, T % 16 == 0: boundaries at i = 8 (block 2m + 1, register set 1) and i = 0 (block 2m,
-            // set 2).  Each set is reloaded in place with the block two boundaries ahead; the load offset
-            // passes through an empty asm that takes the set's last uses as inputs, so the loads issue after
-            // them into the same registers, and the first wait on them comes 8 to 16 steps later.
+        if constexpr (G8) {
+            // G == 8, T % 16 == 0: boundaries at i = 8 (block 2m + 1, set 1) and i = 0 (block 2m, set 2).
+            // Each set is refilled untracked and in place, ONE load per step so the vector-memory queue
+            // never fills: set 2 (block 2m) during steps 15..12 of this chunk, set 1 (block 2m - 1, used by
+            // the next chunk) during steps 7..4 after its use at i = 8.  Every wait is explicit; at each one
+            // the NS = 2 NQ loads of the latest refill are younger than the data it needs:
+            //   set 1 at i = 8       (refilled in the previous chunk; younger: this chunk's set-2 loads),
+            //   tokens before i = 0  (loaded at the previous chunk's end; younger: both refills),
+            //   set 2 after i = 0    (refilled at steps 15..12; younger: the set-1 loads of steps 7..4).
+            // A write adds younger operations, which only makes a wait stricter.
+            using FLY = std::integral_constant<int, 2 * NQ>;
+            auto refill = [&](f32x4* gk, f32x4* gv, int blk, int q) {     // load q of a set's 2 NQ
+                const u32 o = (u32)max(blk, 0) * (u32)(sbstride * sizeof(float)) + 16u * (u32)c;
+                if (q < NQ) ldg_untracked_nt(gk[q], (const char*)dkb0 + o + 256 * q);
+                else ldg_untracked_nt(gv[q - NQ], (const char*)dvb0 + o + 256 * (q - NQ));
+            };
+#pragma unroll
+            for (int i = 15; i >= 16 - 2 * NQ; i--) { step(i, 16 * m + i, hm); refill(gk2, gv2, 2 * m, 15 - i); }
 #pragma unroll 1
-            for (int i = 15; i >= 9; i--) step(i, 16 * m + i, hm);
+            for (int i = 15 - 2 * NQ; i >= 9; i--) step(i, 16 * m + i, hm);
             step(8, 16 * m + 8, hm);
-            enter(pk1, pv1);
-            {
-                u32 o = (u32)max(2 * m - 1, 0) * (u32)(sbstride * sizeof(float));
-                RB_AFTER(o)
-                ld_slice_nt<EPL>(pk1, (const float*)((const char*)dkb0 + o), c);
-                ld_slice_nt<EPL>(pv1, (const float*)((const char*)dvb0 + o), c);
-            }
+            vm_wait<NQ>(gk1, gv1);
+            enter(reinterpret_cast<const float*>(gk1), reinterpret_cast<const float*>(gv1));
+#pragma unroll
+            for (int i = 7; i >= 8 - 2 * NQ; i--) { step(i, 16 * m + i, hm); refill(gk1, gv1, 2 * m - 1, 7 - i); }
 #pragma unroll 1
-            for (int i = 7; i >= 1; i--) step(i, 16 * m + i, hm);
-            if (m > 0) store_chunk(buf ^ 1);            // before the set-2 reload, whose loads it would wait on
+            for (int i = 7 - 2 * NQ; i >= 1; i--) step(i, 16 * m + i, hm);
+            if (m > 0) store_chunk(buf ^ 1, FLY());
             step(0, 16 * m, hm);
-            enter(pk2, pv2);
-            {
-                u32 o = (u32)max(2 * m - 2, 0) * (u32)(sbstride * sizeof(float));
-                RB_AFTER(o)
-                ld_slice_nt<EPL>(pk2, (const float*)((const char*)dkb0 + o), c);
-                ld_slice_nt<EPL>(pv2, (const float*)((const char*)dvb0 + o), c);
-            }
+            vm_wait<NQ>(gk2, gv2);
+            enter(reinterpret_cast<const float*>(gk2), reinterpret_cast<const float*>(gv2));
             emit_dn(m);
             if (m > 0) load_chunk(m - 2);
         } else {
@@ -818,13 +908,14 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
             }
             emit_dn(m);
             if (m > 0) {
-                store_chunk(buf ^ 1);
+                store_chunk(buf ^ 1, std::integral_constant<int, 0>());
                 load_chunk(m - 2);
             }
         }
         __syncthreads();
         buf ^= 1;
     }
+    if constexpr (G8) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last reloads are never consumed
 }
 
 // =========================================================================================== chain_bwd
