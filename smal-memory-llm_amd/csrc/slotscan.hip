@@ -878,8 +878,10 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
             step(8, 16 * m + 8, hm);
             vm_wait<NQ>(gk1, gv1);
             enter(reinterpret_cast<const float*>(gk1), reinterpret_cast<const float*>(gv1));
+            // (no set-1 refill in the last chunk: nothing would wait for it, and a load still in flight when
+            // the loop ends would land in registers the code after the loop may be given)
 #pragma unroll
-            for (int i = 7; i >= 8 - 2 * NQ; i--) { step(i, 16 * m + i, hm); refill(gk1, gv1, 2 * m - 1, 7 - i); }
+            for (int i = 7; i >= 8 - 2 * NQ; i--) { step(i, 16 * m + i, hm); if (m > 0) refill(gk1, gv1, 2 * m - 1, 7 - i); }
 #pragma unroll 1
             for (int i = 7 - 2 * NQ; i >= 1; i--) step(i, 16 * m + i, hm);
             if (m > 0) store_chunk(buf ^ 1, FLY());
@@ -915,7 +917,7 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
         __syncthreads();
         buf ^= 1;
     }
-    if constexpr (G8) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last reloads are never consumed
+    if constexpr (G8) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no untracked load is left in flight; belt and braces
 }
 
 // =========================================================================================== chain_bwd
