@@ -161,6 +161,49 @@ __device__ __forceinline__ float wavemax(float v) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// K independent wave reductions in lockstep: the same trees as wavemax / wavesum, stage by stage over the
+// K values, so the DPP and permlane latencies of different values overlap.
+template <int K> __device__ __forceinline__ void wavemax_k(float* v) {
+#pragma unroll
+    for (int k = 0; k < K; k++) v[k] = fmaxf(v[k], dppf<SLOT_DPP_XOR1>(v[k]));
+#pragma unroll
+    for (int k = 0; k < K; k++) v[k] = fmaxf(v[k], dppf<SLOT_DPP_XOR2>(v[k]));
+#pragma unroll
+    for (int k = 0; k < K; k++) v[k] = fmaxf(v[k], dppf<SLOT_DPP_HMIR>(v[k]));
+#pragma unroll
+    for (int k = 0; k < K; k++) v[k] = fmaxf(v[k], dppf<SLOT_DPP_MIR>(v[k]));
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k]), false, false);
+        v[k] = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k]), false, false);
+        v[k] = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+}
+template <int K> __device__ __forceinline__ void wavesum_k(float* v) {
+#pragma unroll
+    for (int k = 0; k < K; k++) v[k] += dppf<SLOT_DPP_XOR1>(v[k]);
+#pragma unroll
+    for (int k = 0; k < K; k++) v[k] += dppf<SLOT_DPP_XOR2>(v[k]);
+#pragma unroll
+    for (int k = 0; k < K; k++) v[k] += dppf<SLOT_DPP_HMIR>(v[k]);
+#pragma unroll
+    for (int k = 0; k < K; k++) v[k] += dppf<SLOT_DPP_MIR>(v[k]);
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k]), false, false);
+        v[k] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k]), false, false);
+        v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+
 // Row layout of a chain workgroup.  Lane `lane` of wave `w`: row group r = lane >> 4, c = lane & 15;
 // register slot j holds row rowbase + j (the same order in every lane); after a reduce-scatter the lane
 // owns row rowbase + (c >> SH).  Rows therefore increase with the lane index, and the lowest lane of each
@@ -546,7 +589,7 @@ struct RowsFwdArgs {
 template <int D, typename TI>
 ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     constexpr int EPL = D / 16;
-    constexpr int TC = 2048;
+    constexpr int TC = 256;                              // staged steps: 2 KB of LDS, so the replay blocks fit beside two chain blocks on a CU
     __shared__ __align__(16) int s_am[TC];
     __shared__ float s_g[TC];
     const int T = a.T, H = a.H, N = a.N, G = a.G;
@@ -1280,6 +1323,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_
 void chain_bwd_w(ChainBwdArgs a) {
     constexpr int NT = 64 * NW;
     constexpr int SPW = WIN / NW;                       // window steps per wave in the softmax phase
+    constexpr int GS = RPL >= 3 ? 1 : SPW;              // of which processed in lockstep
     constexpr int NR = 64 * RPL;                        // slot-row capacity
     constexpr int KK = NR / 4;                          // MFMA k-steps over the rows
     constexpr int DW = D / NW;                          // dims per wave
@@ -1480,75 +1524,109 @@ void chain_bwd_w(ChainBwdArgs a) {
         // S4: the softmax adjoint of this wave's steps, over every row.  With a_n = e_n / SS over the eligible
         // rows, sum over taken rows of dz_n = (g * SSD_taken - sa * SS_taken) / SS, so dfr needs no extra
         // reduction.
+        // the SPW steps of this wave in lockstep groups of GS: one interleaved wave max and one interleaved
+        // wave sum per group, branch-free free-row search; the per-step stores are gathered to lanes
+        // 0 .. SPW-1 at the end.  z is recomputed from the cosine where needed (fewer live registers).
+        float dgv[SPW], dfv[SPW];
+        bool livev[SPW];
 #pragma unroll
-        for (int ii = 0; ii < SPW; ii++) {
-            const int i = SPW * wave + ii;
-            {                                            // steps past nt hold zeros: W = 0, no stores
-                const bool live_i = i < nt;
-                const int ai = s_am[i];
-                const float g = s_g[i];
-                const float frv = frt ? s_fr[i] : fr_s;
-                float cs[RPL], dw[RPL], z[RPL];
-                float lm = -INFINITY;
+        for (int i0 = 0; i0 < SPW; i0 += GS) {
+            int ai[GS];
+            float g[GS], frv[GS], lm[GS], cs[GS][RPL], dw[GS][RPL];
+#pragma unroll
+            for (int ii = 0; ii < GS; ii++) {                 // steps past nt hold zeros: W = 0, no stores
+                const int i = SPW * wave + i0 + ii;
+                livev[i0 + ii] = i < nt;
+                ai[ii] = s_am[i];
+                g[ii] = s_g[i];
+                frv[ii] = frt ? s_fr[i] : fr_s;
+                lm[ii] = -INFINITY;
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
                     const int n = lane + 64 * j;
                     const bool tj = (tk[j] >> i) & 1u;
-                    cs[j] = n < N ? s_cs[i * N + n] : 0.f;
-                    dw[j] = s_dn[n][i];
-                    z[j] = temp * cs[j] - (tj ? frv : 0.f);
-                    lm = fmaxf(lm, tj ? z[j] : -INFINITY);
+                    cs[ii][j] = n < N ? s_cs[i * N + n] : 0.f;
+                    dw[ii][j] = s_dn[n][i];
+                    const float z = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
+                    lm[ii] = fmaxf(lm[ii], tj ? z : -INFINITY);
                 }
-                const float wm = wavemax(lm);
-                float ls = 0.f, lsd = 0.f;
+            }
+            wavemax_k<GS>(lm);                                 // lm[ii] = the wave max over taken rows
+            float ls[2 * GS];                                  // [ii]: sum e, [GS + ii]: sum e * dw
+#pragma unroll
+            for (int ii = 0; ii < GS; ii++) {
+                const int i = SPW * wave + i0 + ii;
+                float s0 = 0.f, s1 = 0.f;
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
                     const bool tj = (tk[j] >> i) & 1u;
-                    const float e = tj ? __expf(z[j] - wm) : 0.f;
-                    ls += e;
-                    lsd = fmaf(e, dw[j], lsd);
+                    const float z = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
+                    const float e = tj ? __expf(z - lm[ii]) : 0.f;
+                    s0 += e;
+                    s1 = fmaf(e, dw[ii][j], s1);
                 }
-                const float S = wavesum(ls), SD = wavesum(lsd);
+                ls[ii] = s0;
+                ls[GS + ii] = s1;
+            }
+            wavesum_k<2 * GS>(ls);
+#pragma unroll
+            for (int ii = 0; ii < GS; ii++) {
+                const int i = SPW * wave + i0 + ii;
+                // the lowest free row (rows grow with j, then lane): scan j downwards with selects
                 int FO = -1;
                 float FZ = 0.f, FD = 0.f;
 #pragma unroll
-                for (int j = 0; j < RPL; j++) {            // the lowest free row (rows grow with j, lane)
+                for (int j = RPL - 1; j >= 0; j--) {
                     const bool tj = (tk[j] >> i) & 1u;
                     const u64 mf = __ballot(lane + 64 * j < N && !tj);
-                    if (FO < 0 && mf) {
-                        const int lf = __builtin_ctzll(mf);
-                        FO = 64 * j + lf;
-                        FZ = readlanef(z[j], lf);
-                        FD = readlanef(dw[j], lf);
-                    }
+                    const int lf = (int)__builtin_ctzll(mf | (1ull << 63));
+                    const float zj = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
+                    const float zf = readlanef(zj, lf), df = readlanef(dw[ii][j], lf);
+                    FO = mf ? 64 * j + lf : FO;
+                    FZ = mf ? zf : FZ;
+                    FD = mf ? df : FD;
                 }
-                float M = wm;
-                if (FO >= 0) M = fmaxf(M, FZ);             // the first free row competes too
+                const float wm = lm[ii];
+                const float M = FO >= 0 ? fmaxf(wm, FZ) : wm;       // the first free row competes too
                 const float sc = wm == -INFINITY ? 0.f : __expf(wm - M);
-                const float SSt = S * sc, SSDt = SD * sc;
-                float SS = SSt, SSD = SSDt;
-                if (FO >= 0) {
-                    const float ef = __expf(FZ - M);
-                    SS += ef;
-                    SSD = fmaf(ef, FD, SSD);
-                }
-                const float rss = live_i ? __builtin_amdgcn_rcpf(SS) : 0.f, sa = (g * SSD) * rss;
+                const float SSt = ls[ii] * sc, SSDt = ls[GS + ii] * sc;
+                const float ef = FO >= 0 ? __expf(FZ - M) : 0.f;
+                const float SS = FO >= 0 ? SSt + ef : SSt;
+                const float SSD = FO >= 0 ? fmaf(ef, FD, SSDt) : SSDt;
+                const float rss = livev[i0 + ii] ? __builtin_amdgcn_rcpf(SS) : 0.f, sa = (g[ii] * SSD) * rss;
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
                     const int n = lane + 64 * j;
                     const bool tj = (tk[j] >> i) & 1u;
                     const bool elig = tj || (n < N && n == FO);
-                    const float as = elig ? __expf(z[j] - M) * rss : 0.f;
-                    const float dz = as * (g * dw[j] - sa);
-                    dtemp_acc = fmaf(dz, cs[j], dtemp_acc);
-                    if (live_i && n < N && n == ai) a.dg[tok0 + (size_t)(t0 + i) * H] = dw[j];
+                    const float z = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
+                    const float as = elig ? __expf(z - M) * rss : 0.f;
+                    const float dz = as * (g[ii] * dw[ii][j] - sa);
+                    dtemp_acc = fmaf(dz, cs[ii][j], dtemp_acc);
                     s_W[i][n] = temp * dz;
                 }
-                const float dfri = live_i ? -(g * SSDt - sa * SSt) * rss : 0.f;
-                if (lane == 0) {
-                    if (frt) { if (live_i) a.dfr[tok0 + (size_t)(t0 + i) * H] = dfri; }
-                    else dfr_acc += dfri;
-                }
+                // dgate of the written row: its Dn entry, read from the lane that holds it
+                const int aj = ai[ii] >> 6, al = ai[ii] & 63;
+                float dsel = dw[ii][0];
+#pragma unroll
+                for (int j = 1; j < RPL; j++) dsel = aj == j ? dw[ii][j] : dsel;
+                dgv[i0 + ii] = readlanef(dsel, al);
+                dfv[i0 + ii] = livev[i0 + ii] ? -(g[ii] * SSDt - sa * SSt) * rss : 0.f;
+            }
+        }
+        if (!frt) {
+#pragma unroll
+            for (int ii = 0; ii < SPW; ii++) if (lane == 0) dfr_acc += dfv[ii];
+        }
+        if (lane < SPW) {                                      // lane ii stores step SPW * wave + ii
+            float dgl = dgv[0], dfl = dfv[0];
+            bool lv = livev[0];
+#pragma unroll
+            for (int ii = 1; ii < SPW; ii++) { dgl = lane == ii ? dgv[ii] : dgl; dfl = lane == ii ? dfv[ii] : dfl; lv = lane == ii ? livev[ii] : lv; }
+            if (lv) {
+                const size_t ix = tok0 + (size_t)(t0 + SPW * wave + lane) * H;
+                a.dg[ix] = dgl;
+                if (frt) a.dfr[ix] = dfl;
             }
         }
         __syncthreads();                                                      // B2
