@@ -83,6 +83,40 @@ int slotscan_bwd(const void* k, const void* q, const void* v, int dtype,
                  void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
                  void* stream);
 
+/* Forward scan with the writer epilogue fused in.  Replaces kv_scan_g followed by the full-precision epilogue
+ * of the writer layer (memlm_sh.py:453-456 then :473-475):
+ *     nsq = kbuf.pow(2).sum(-1);  mem = (kbuf.to(bf16), vbuf.to(bf16), rsqrt(nsq.clamp_min(1e-12)), nsq > 1e-12)
+ * The fp32 snapshots are never stored: the chain kernel emits each key snapshot row as bf16 together with
+ * its kinv and valid, and the value replay emits each value snapshot row as bf16.
+ *   kb, vb   (B, ceil(T/G), H, N, D) bf16 (uint16 bit patterns)
+ *   kinv     (B, ceil(T/G), H, N) fp32;  valid  (B, ceil(T/G), H, N) uint8 (0 / 1)
+ * Every other argument is as in slotscan_fwd.  Applies where the epilogue follows the scan directly: not
+ * with the value renormalisation (memlm_sh.py:464-465) or the storage quantiser (memlm_sh.py:468-471). */
+int slotscan_fwd_mem(const void* k, const void* q, const void* v, int dtype,
+                     const float* gate, const float* fr, int fr_per_token, const float* temp,
+                     int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                     float eps, int occ_bin,
+                     const float* k0, const float* v0, const float* o0,
+                     void* kb, void* vb, float* kinv, uint8_t* valid, int32_t* am,
+                     float* kold, float* vold, float* oold, float* cslog,
+                     float* kfin, float* vfin, float* ofin, void* stream);
+
+/* Backward of slotscan_fwd_mem: the autograd of the epilogue's expressions (memlm_sh.py:473-475) folded
+ * into the row adjoint.  The snapshot gradients it forms from its inputs are
+ *     dkbuf = dkb + 2 K dnsq,  dnsq = -0.5 kinv^3 dkinv where nsq >= 1e-12 (else 0);  dvbuf = dvb
+ * with K the snapshot the replay restores, and from there it is slotscan_bwd.
+ *   dkb, dvb  gradients of kb, vb: (B, ceil(T/G), H, N, D) bf16;  dkinv  (B, ceil(T/G), H, N) fp32
+ * Every other argument is as in slotscan_bwd (the same workspace size). */
+int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
+                     const float* gate, const float* fr, int fr_per_token, const float* temp,
+                     int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                     float eps, int occ_bin,
+                     const int32_t* am, const float* kold, const float* vold, const float* oold,
+                     const float* cslog, const float* kfin, const float* vfin, const float* ofin,
+                     const void* dkb, const void* dvb, const float* dkinv, void* workspace,
+                     void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
+                     void* stream);
+
 /* Per-kernel timing (the reference's kvu/prof_cuda.py:9-20 wraps each compiled kernel's launch in CUDA
  * events; this is the same facility inside the library).  While enabled, every kernel launch is bracketed
  * by two hipEvents recorded on its stream.  slotscan_profile_read waits for the recorded events, writes

@@ -230,6 +230,8 @@ struct ChainFwdArgs {
     float* kbuf; int32_t* am; float* kold; float* oold; float* cslog; float* kfin; float* ofin;
     int T, H, N, G, NB; float eps; int frt, occb;
     int ts, te;                                          // steps [ts, te) of the T-long sequence; ts % G == 0
+    // the writer-epilogue emission (all NULL: fp32 kbuf): bf16 key copies, kinv and valid per snapshot row
+    bf16_t* kbm; float* kinvm; uint8_t* validm;
 };
 
 // Wave-local LDS ordering: lanes of one wave exchange data through LDS (DS instructions of a wave execute
@@ -250,6 +252,18 @@ __device__ __forceinline__ void st_slice_at(float* base, u32 boff, const float* 
         f32x4 v = {s[4 * jj], s[4 * jj + 1], s[4 * jj + 2], s[4 * jj + 3]};
         if (NT) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p + 256 * jj));
         else *reinterpret_cast<f32x4*>(p + 256 * jj) = v;
+    }
+}
+
+// The same slice as bf16 (the writer epilogue's cast, round to nearest even): 8 bytes per 4 elements
+template <int EPL>
+__device__ __forceinline__ void st_slice_bf_at(bf16_t* base, u32 boff, const float* s) {
+    char* p = reinterpret_cast<char*>(base) + boff;
+#pragma unroll
+    for (int jj = 0; jj < EPL / 4; jj++) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 r = {pack_bf16x2(s[4 * jj], s[4 * jj + 1]), pack_bf16x2(s[4 * jj + 2], s[4 * jj + 3])};
+        __builtin_nontemporal_store(r, reinterpret_cast<u32x2*>(p + 128 * jj));
     }
 }
 
@@ -284,7 +298,7 @@ __device__ __forceinline__ u32 wavemax_key(u32 v) {
 // the next window).  The row norm of the written row is recomputed from its new elements.  The per-step
 // work left is the score, the argmax, and the one-row update.
 #define FWD_THREADS (CHAIN_THREADS + 64)
-template <int D, int P, typename TI>
+template <int D, int P, typename TI, bool MB>
 __global__ __attribute__((amdgpu_flat_work_group_size(FWD_THREADS, FWD_THREADS), amdgpu_waves_per_eu(2)))
 void chain_fwd(ChainFwdArgs a) {
     constexpr int EPL = D / 16;
@@ -393,10 +407,15 @@ void chain_fwd(ChainFwdArgs a) {
     }
 
     const ChainRows<P> R(tid);
-    float* kb = a.kbuf + (((size_t)b * a.NB + ts / G) * H + h) * N * D;   // key snapshot of block ts / G
     const size_t sstride = (size_t)H * N * D;
+    const size_t snap0 = ((size_t)b * a.NB + ts / G) * H + h;           // (b, ts / G, h): snapshot of block ts / G
+    float* kb = MB ? nullptr : a.kbuf + snap0 * N * D;
+    bf16_t* kbm = MB ? a.kbm + snap0 * N * D : nullptr;
+    float* kinvm = MB ? a.kinvm + snap0 * N : nullptr;
+    uint8_t* validm = MB ? a.validm + snap0 * N : nullptr;
     rowv Kv[EPL];                                       // Kv[e][j]: element e of this lane's slice of row j
     float o_me = 0.f, kinv_me;
+    bool vld_me;                                        // |K_me|^2 > 1e-12 (the epilogue's `valid`)
     {
         float x[P];
 #pragma unroll
@@ -411,7 +430,9 @@ void chain_fwd(ChainFwdArgs a) {
             for (int e = 0; e < EPL; e++) { Kv[e][j] = row[e]; kk = fmaf(row[e], row[e], kk); }
             x[j] = kk;
         }
-        kinv_me = rsq_clamped(rs_reduce<P>(x, c));
+        const float nsq0 = rs_reduce<P>(x, c);
+        kinv_me = rsq_clamped(nsq0);
+        vld_me = nsq0 > 1e-12f;
         if (a.o0 && R.n_me < N) o_me = a.o0[(size_t)bh * N + R.n_me];
     }
     auto row_of = [&](int j, float* row) {
@@ -506,16 +527,32 @@ void chain_fwd(ChainFwdArgs a) {
 #pragma unroll
             for (int w = 0; w < CHAIN_WAVES; w++) r[w] = s_red[par][w];
             if (gc == 0) {                                  // the PRE-write key state of block t / G:
-                u32 ro = roff;                              // every row group stores whole 512-byte rows
+                u32 ro = roff;                              // every row group stores whole rows
                 int nvv = nvalid;
                 asm volatile("" : "+v"(ro), "+v"(nvv));     // per-snapshot offsets, not 16 live registers
+                if constexpr (MB) {                         // the writer epilogue: bf16 copy, kinv, valid
 #pragma unroll
-                for (int jr = 0; jr < P; jr++) {
-                    float row[EPL];
-                    row_of(jr, row);
-                    if (jr < nvv) st_slice_at<EPL, true>(kb, ro + (u32)(jr * D * 4), row);
+                    for (int jr = 0; jr < P; jr++) {
+                        float row[EPL];
+                        row_of(jr, row);
+                        if (jr < nvv) st_slice_bf_at<EPL>(kbm, (ro >> 1) + (u32)(jr * D * 2), row);
+                    }
+                    if (R.prim && valid_me) {
+                        kinvm[R.n_me] = kinv_me;
+                        validm[R.n_me] = vld_me ? 1 : 0;
+                    }
+                    kbm += sstride;
+                    kinvm += (size_t)H * N;
+                    validm += (size_t)H * N;
+                } else {
+#pragma unroll
+                    for (int jr = 0; jr < P; jr++) {
+                        float row[EPL];
+                        row_of(jr, row);
+                        if (jr < nvv) st_slice_at<EPL, true>(kb, ro + (u32)(jr * D * 4), row);
+                    }
+                    kb += sstride;
                 }
-                kb += sstride;
             }
             if (++gc == G) gc = 0;
             // waves in order = rows in order: strict '>' keeps the lowest row on ties
@@ -552,6 +589,7 @@ void chain_fwd(ChainFwdArgs a) {
                     if (a.oold && R.prim) a.oold[ix] = o_me;
                     o_me = omw * o_me + g;
                     kinv_me = rsq_clamped(kk);
+                    vld_me = kk > 1e-12f;
                     // all 16 entries: those at or before step j are never read again in this window
                     const f32x4* er = reinterpret_cast<const f32x4*>(&s_E[buf][j][0]);
 #pragma unroll
@@ -579,6 +617,7 @@ struct RowsFwdArgs {
     float* vbuf; float* vold; float* vfin;
     int T, H, N, G, NB;
     int ts, te;                                          // steps [ts, te); ts % G == 0
+    bf16_t* vbm;                                         // the writer-epilogue emission (NULL: fp32 vbuf)
 };
 
 // 512 lanes = 32 rows of one chain per workgroup; grid (B*H, ceil(N/32)).  Replays every row's value from
@@ -586,7 +625,7 @@ struct RowsFwdArgs {
 // its own writes, so the replay visits events, not steps: per 16-step piece of the staged address log a
 // lane forms the mask of steps that wrote its row (4 LDS reads) and, with the piece's G-aligned snapshot
 // steps, walks the set bits in step order (snapshot first: it is the PRE-write state).
-template <int D, typename TI>
+template <int D, typename TI, bool MB>
 ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     constexpr int EPL = D / 16;
     constexpr int TC = 256;                              // staged steps: 2 KB of LDS, so the replay blocks fit beside two chain blocks on a CU
@@ -603,7 +642,9 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
 #pragma unroll
     for (int e = 0; e < EPL; e++) V[e] = 0.f;
     if (live && a.v0) ld_slice<EPL>(V, a.v0 + ((size_t)bh * N + n) * D, c);
-    float* vb = a.vbuf + (((size_t)b * a.NB + a.ts / G) * H + h) * N * D + (size_t)(live ? n : 0) * D;
+    const size_t vrow0 = (((size_t)b * a.NB + a.ts / G) * H + h) * N * D + (size_t)(live ? n : 0) * D;
+    float* vb = MB ? nullptr : a.vbuf + vrow0;
+    bf16_t* vbh = MB ? a.vbm + vrow0 : nullptr;
     const size_t sstride = (size_t)H * N * D;
     for (int t0 = a.ts; t0 < a.te; t0 += TC) {
         const int tn = min(TC, a.te - t0);
@@ -632,8 +673,8 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
                 const int i = __builtin_ctz(ev);
                 ev &= ev - 1;
                 if ((sm >> i) & 1u) {
-                    st_slice_nt<EPL>(vb, V, c);
-                    vb += sstride;
+                    if constexpr (MB) { st_slice_bf_at<EPL>(vbh, 8u * (u32)c, V); vbh += sstride; }
+                    else { st_slice_nt<EPL>(vb, V, c); vb += sstride; }
                 }
                 if ((hm >> i) & 1u) {
                     const size_t ix = tok0 + (size_t)(t0 + j0 + i) * H;
@@ -657,6 +698,8 @@ struct RowsBwdArgs {
     const float* dkbuf; const float* dvbuf;
     void* dk; void* dv; float* dn;
     int T, H, N, G, NB;
+    // the writer-epilogue contract upstream (rows_bwd<..., MB = true>): the bf16 copies' gradients and dkinv
+    const bf16_t* dkbm; const bf16_t* dvbm; const float* dkinvm;
 };
 
 // 512 lanes = 32 rows per workgroup, grid (B*H, ceil(N/32)); reverse in t, in 16-step chunks aligned to
@@ -685,16 +728,33 @@ __device__ __forceinline__ void ldg_untracked(u32x4& d, const void* p) {
 __device__ __forceinline__ void ldg_untracked(float& d, const void* p) {
     asm volatile("global_load_dword %0, %1, off" : "+v"(d) : "v"(p));
 }
-template <int N4> __device__ __forceinline__ void vm_wait(f32x4* a, f32x4* b);
-template <> __device__ __forceinline__ void vm_wait<1>(f32x4* a, f32x4* b) {     // the 2 youngest may fly
-    asm volatile("s_waitcnt vmcnt(2)" : "+v"(a[0]), "+v"(b[0]));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void ldg_untracked_nt(u32x2& d, const void* p) {
+    asm volatile("global_load_dwordx2 %0, %1, off nt" : "+v"(d) : "v"(p));
 }
-template <> __device__ __forceinline__ void vm_wait<2>(f32x4* a, f32x4* b) {     // the 4 youngest may fly
-    asm volatile("s_waitcnt vmcnt(4)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
+__device__ __forceinline__ void ldg_untracked_nt(float& d, const void* p) {
+    asm volatile("global_load_dword %0, %1, off nt" : "+v"(d) : "v"(p));
+}
+// Waits for a gradient set.  `all`: wait for every load (the last chunk, where fewer younger operations
+// than the count may have been issued, so the counted wait would not cover the set).
+// the MB set of D = 128: K and V bf16 slices (2 x 8 bytes each) and dkinv; the 5 youngest may fly
+__device__ __forceinline__ void vm_wait_mb(u32x2* k, u32x2* v, float& ki, bool all) {
+    if (all) asm volatile("s_waitcnt vmcnt(0)" : "+v"(k[0]), "+v"(k[1]), "+v"(v[0]), "+v"(v[1]), "+v"(ki));
+    else asm volatile("s_waitcnt vmcnt(5)" : "+v"(k[0]), "+v"(k[1]), "+v"(v[0]), "+v"(v[1]), "+v"(ki));
+}
+template <int N4> __device__ __forceinline__ void vm_wait(f32x4* a, f32x4* b, bool all);
+template <> __device__ __forceinline__ void vm_wait<1>(f32x4* a, f32x4* b, bool all) {     // the 2 youngest may fly
+    if (all) asm volatile("s_waitcnt vmcnt(0)" : "+v"(a[0]), "+v"(b[0]));
+    else asm volatile("s_waitcnt vmcnt(2)" : "+v"(a[0]), "+v"(b[0]));
+}
+template <> __device__ __forceinline__ void vm_wait<2>(f32x4* a, f32x4* b, bool all) {     // the 4 youngest may fly
+    if (all) asm volatile("s_waitcnt vmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
+    else asm volatile("s_waitcnt vmcnt(4)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
 }
 
-template <int D, typename TI, bool G8>
+template <int D, typename TI, bool G8, bool MB>
 ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
+    static_assert(!(G8 && MB) || D == 128, "the untracked MB path is built for D = 128");
     constexpr int EPL = D / 16;
     constexpr int EPU = 16 / (int)sizeof(TI);
     constexpr int RU = D / EPU;
@@ -752,6 +812,7 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
                         else asm volatile(S : "+v"(rq[0]), "+v"(rq[1]), "+v"(ram), "+v"(rgt)); }
             if constexpr (decltype(fly)::value == 0) RB_TOKWAIT("s_waitcnt vmcnt(0)")
             else if constexpr (decltype(fly)::value == 2) RB_TOKWAIT("s_waitcnt vmcnt(2)")
+            else if constexpr (decltype(fly)::value == 5) RB_TOKWAIT("s_waitcnt vmcnt(5)")
             else RB_TOKWAIT("s_waitcnt vmcnt(4)")
 #undef RB_TOKWAIT
         }
@@ -770,16 +831,33 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
     constexpr int NQ = EPL / 4;                          // 16-byte pieces of a row slice
     float K[EPL], V[EPL], dK[EPL], dV[EPL], pk1[EPL], pv1[EPL], pk2[EPL], pv2[EPL];
     f32x4 gk1[NQ], gv1[NQ], gk2[NQ], gv2[NQ];           // the G8 path's two untracked gradient sets
+    u32x2 hk1[NQ], hv1[NQ], hk2[NQ], hv2[NQ];           // ... in the MB contract: bf16 slices (8 bytes each)
+    float hi1 = 0.f, hi2 = 0.f, pki1 = 0.f, pki2 = 0.f;  // dkinv of a set / of the general path's blocks
     ld_slice<EPL>(K, a.kfin + ((size_t)bh * N + n) * D, c);
     ld_slice<EPL>(V, a.vfin + ((size_t)bh * N + n) * D, c);
 #pragma unroll
     for (int e = 0; e < EPL; e++) { dK[e] = 0.f; dV[e] = 0.f; pk2[e] = 0.f; pv2[e] = 0.f; }
 #pragma unroll
-    for (int q = 0; q < NQ; q++) { gk1[q] = gv1[q] = gk2[q] = gv2[q] = f32x4{0.f, 0.f, 0.f, 0.f}; }
+    for (int q = 0; q < NQ; q++) {
+        gk1[q] = gv1[q] = gk2[q] = gv2[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        hk1[q] = hv1[q] = hk2[q] = hv2[q] = u32x2{0u, 0u};
+    }
     float cp = 0.f;                                      // this lane's share of <K, dK> + <V, dV>
     const size_t sbstride = (size_t)H * N * D;
     const float* dkb0 = a.dkbuf + ((size_t)b * a.NB * H + h) * N * D + (size_t)n * D;
     const float* dvb0 = a.dvbuf + ((size_t)b * a.NB * H + h) * N * D + (size_t)n * D;
+    // MB: the bf16 gradients of the writer epilogue's copies and dkinv, same (b, nb, h, n) order
+    const size_t kistride = (size_t)H * N;
+    const bf16_t* dkh0 = MB ? a.dkbm + ((size_t)b * a.NB * H + h) * N * D + (size_t)n * D : nullptr;
+    const bf16_t* dvh0 = MB ? a.dvbm + ((size_t)b * a.NB * H + h) * N * D + (size_t)n * D : nullptr;
+    const float* dki0 = MB ? a.dkinvm + ((size_t)b * a.NB * H + h) * N + n : nullptr;
+    // MB, the G8 path: load q of a set's 2 NQ + 1 (K slice pieces, V slice pieces, dkinv), untracked
+    auto refill_mb = [&](u32x2* hk, u32x2* hv, float& hki, int blk, int q) {
+        const u32 o = (u32)max(blk, 0) * (u32)(sbstride * sizeof(bf16_t)) + 8u * (u32)c;
+        if (q < NQ) ldg_untracked_nt(hk[q], (const char*)dkh0 + o + 128 * q);
+        else if (q < 2 * NQ) ldg_untracked_nt(hv[q - NQ], (const char*)dvh0 + o + 128 * (q - NQ));
+        else ldg_untracked_nt(hki, dki0 + (size_t)max(blk, 0) * kistride);
+    };
     // the G8 path's reload of a gradient set with block `blk` (clamped), untracked; the offset passes
     // through an empty asm that takes the set's last uses as inputs, so the loads issue after them
     auto reload = [&](f32x4* gk, f32x4* gv, int blk) {
@@ -792,8 +870,20 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
         }
     };
     int nxt = (T - 1) / G;                               // next block whose gradient enters (reverse order)
-    if constexpr (G8) {
+    if constexpr (G8 && MB) {
+#pragma unroll
+        for (int q = 0; q < 2 * NQ + 1; q++) refill_mb(hk1, hv1, hi1, nxt, q);   // set 2: the first chunk
+    } else if constexpr (G8) {
         reload(gk1, gv1, nxt);                           // set 2 is refilled during the first chunk
+    } else if constexpr (MB) {
+        ld_slice<EPL>(pk1, dkh0 + (size_t)nxt * sbstride, c);
+        ld_slice<EPL>(pv1, dvh0 + (size_t)nxt * sbstride, c);
+        pki1 = dki0[(size_t)nxt * kistride];
+        if (nxt >= 1) {
+            ld_slice<EPL>(pk2, dkh0 + (size_t)(nxt - 1) * sbstride, c);
+            ld_slice<EPL>(pv2, dvh0 + (size_t)(nxt - 1) * sbstride, c);
+            pki2 = dki0[(size_t)(nxt - 1) * kistride];
+        }
     } else {
         ld_slice_nt<EPL>(pk1, dkb0 + (size_t)nxt * sbstride, c);
         ld_slice_nt<EPL>(pv1, dvb0 + (size_t)nxt * sbstride, c);
@@ -869,6 +959,30 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
             cp = fmaf(K[e], pk[e], fmaf(V[e], pv[e], cp));
         }
     };
+    // MB: the writer epilogue's key gradient at this snapshot, d kbuf = d kb + 2 K dnsq with
+    // dnsq = -0.5 kinv^3 dkinv where |K|^2 >= 1e-12 (slotmem.hip's backward); K is the snapshot's value
+    auto combine = [&](float* pk, float dki) {
+        float nsq = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) nsq = fmaf(K[e], K[e], nsq);
+        nsq = rowsum16(nsq);
+        const float ki = rsq_clamped(nsq);
+        const float coef = nsq >= 1e-12f ? -(ki * ki * ki) * dki : 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) pk[e] = fmaf(coef, K[e], pk[e]);
+    };
+    auto enter_mb = [&](const u32x2* hk, const u32x2* hv, float hki) {
+        float pk[EPL], pv[EPL];
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            pk[4 * q + 0] = __uint_as_float(hk[q].x << 16); pk[4 * q + 1] = __uint_as_float(hk[q].x & 0xffff0000u);
+            pk[4 * q + 2] = __uint_as_float(hk[q].y << 16); pk[4 * q + 3] = __uint_as_float(hk[q].y & 0xffff0000u);
+            pv[4 * q + 0] = __uint_as_float(hv[q].x << 16); pv[4 * q + 1] = __uint_as_float(hv[q].x & 0xffff0000u);
+            pv[4 * q + 2] = __uint_as_float(hv[q].y << 16); pv[4 * q + 3] = __uint_as_float(hv[q].y & 0xffff0000u);
+        }
+        combine(pk, hki);
+        enter(pk, pv);
+    };
     // lane c sums the row group's 16 partials of step 16m + c (same wave wrote them: wave barrier only)
     // A row's Dn slice of one chunk is 64 bytes, half a 128-byte line; the odd chunk's value is held until
     // the even chunk below it is done, and both halves of the line are stored together (written a chunk
@@ -898,7 +1012,30 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
                 | (a4.z == n ? 4u : 0u) << (4 * u) | (a4.w == n ? 8u : 0u) << (4 * u);
         }
         if (!live) hm = 0;
-        if constexpr (G8) {
+        if constexpr (G8 && MB) {
+            // The same schedule for the writer-epilogue contract: a set is 2 NQ + 1 = 5 loads (the bf16 K
+            // and V slice pieces and dkinv), refilled at steps 15..11 (set 2) and 7..3 (set 1); every wait
+            // lets the latest refill's 5 loads fly.
+            constexpr int NSM = 2 * NQ + 1;
+            using FLY = std::integral_constant<int, NSM>;
+#pragma unroll
+            for (int i = 15; i >= 16 - NSM; i--) { step(i, 16 * m + i, hm); refill_mb(hk2, hv2, hi2, 2 * m, 15 - i); }
+#pragma unroll 1
+            for (int i = 15 - NSM; i >= 9; i--) step(i, 16 * m + i, hm);
+            step(8, 16 * m + 8, hm);
+            vm_wait_mb(hk1, hv1, hi1, false);
+            enter_mb(hk1, hv1, hi1);
+#pragma unroll
+            for (int i = 7; i >= 8 - NSM; i--) { step(i, 16 * m + i, hm); if (m > 0) refill_mb(hk1, hv1, hi1, 2 * m - 1, 7 - i); }
+#pragma unroll 1
+            for (int i = 7 - NSM; i >= 1; i--) step(i, 16 * m + i, hm);
+            if (m > 0) store_chunk(buf ^ 1, FLY());
+            step(0, 16 * m, hm);
+            vm_wait_mb(hk2, hv2, hi2, m == 0);
+            enter_mb(hk2, hv2, hi2);
+            emit_dn(m);
+            if (m > 0) load_chunk(m - 2);
+        } else if constexpr (G8) {
             // G == 8, T % 16 == 0: boundaries at i = 8 (block 2m + 1, set 1) and i = 0 (block 2m, set 2).
             // Each set is refilled untracked and in place, ONE load per step so the vector-memory queue
             // never fills: set 2 (block 2m) during steps 15..12 of this chunk, set 1 (block 2m - 1, used by
@@ -906,7 +1043,8 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
             // the NS = 2 NQ loads of the latest refill are younger than the data it needs:
             //   set 1 at i = 8       (refilled in the previous chunk; younger: this chunk's set-2 loads),
             //   tokens before i = 0  (loaded at the previous chunk's end; younger: both refills),
-            //   set 2 after i = 0    (refilled at steps 15..12; younger: the set-1 loads of steps 7..4).
+            //   set 2 after i = 0    (refilled at steps 15..12; younger: the set-1 loads of steps 7..4 --
+            //                         except in the last chunk, which waits for all).
             // A write adds younger operations, which only makes a wait stricter.
             using FLY = std::integral_constant<int, 2 * NQ>;
             auto refill = [&](f32x4* gk, f32x4* gv, int blk, int q) {     // load q of a set's 2 NQ
@@ -919,7 +1057,7 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
 #pragma unroll 1
             for (int i = 15 - 2 * NQ; i >= 9; i--) step(i, 16 * m + i, hm);
             step(8, 16 * m + 8, hm);
-            vm_wait<NQ>(gk1, gv1);
+            vm_wait<NQ>(gk1, gv1, false);
             enter(reinterpret_cast<const float*>(gk1), reinterpret_cast<const float*>(gv1));
             // (no set-1 refill in the last chunk: nothing would wait for it, and a load still in flight when
             // the loop ends would land in registers the code after the loop may be given)
@@ -929,7 +1067,7 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
             for (int i = 7 - 2 * NQ; i >= 1; i--) step(i, 16 * m + i, hm);
             if (m > 0) store_chunk(buf ^ 1, FLY());
             step(0, 16 * m, hm);
-            vm_wait<NQ>(gk2, gv2);
+            vm_wait<NQ>(gk2, gv2, m == 0);             // the last chunk issued no set-1 refill after set 2
             enter(reinterpret_cast<const float*>(gk2), reinterpret_cast<const float*>(gv2));
             emit_dn(m);
             if (m > 0) load_chunk(m - 2);
@@ -940,14 +1078,22 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
                 const int t = 16 * m + i;
                 step(i, t, hm);
                 if (t == tb) {
+                    if constexpr (MB) combine(pk1, pki1);
                     enter(pk1, pv1);
 #pragma unroll
                     for (int e = 0; e < EPL; e++) { pk1[e] = pk2[e]; pv1[e] = pv2[e]; }
+                    pki1 = pki2;
                     nxt -= 1;
                     tb -= G;
                     if (nxt >= 1) {
-                        ld_slice_nt<EPL>(pk2, dkb0 + (size_t)(nxt - 1) * sbstride, c);
-                        ld_slice_nt<EPL>(pv2, dvb0 + (size_t)(nxt - 1) * sbstride, c);
+                        if constexpr (MB) {
+                            ld_slice<EPL>(pk2, dkh0 + (size_t)(nxt - 1) * sbstride, c);
+                            ld_slice<EPL>(pv2, dvh0 + (size_t)(nxt - 1) * sbstride, c);
+                            pki2 = dki0[(size_t)(nxt - 1) * kistride];
+                        } else {
+                            ld_slice_nt<EPL>(pk2, dkb0 + (size_t)(nxt - 1) * sbstride, c);
+                            ld_slice_nt<EPL>(pv2, dvb0 + (size_t)(nxt - 1) * sbstride, c);
+                        }
                     }
                 }
             }
@@ -1776,7 +1922,10 @@ __global__ __launch_bounds__(256) void reduce_parts(const float* __restrict__ pa
 template <int D, typename TI>
 hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
     dim3 grid(B * a.H), block(FWD_THREADS);
-#define SLOT_CF(PP) if (a.N <= 4 * CHAIN_WAVES * PP) { hipLaunchKernelGGL((chain_fwd<D, PP, TI>), grid, block, 0, st, a); return hipGetLastError(); }
+#define SLOT_CF(PP) if (a.N <= 4 * CHAIN_WAVES * PP) { \
+        if (a.kbm) hipLaunchKernelGGL((chain_fwd<D, PP, TI, true>), grid, block, 0, st, a); \
+        else hipLaunchKernelGGL((chain_fwd<D, PP, TI, false>), grid, block, 0, st, a); \
+        return hipGetLastError(); }
     SLOT_CF(1) SLOT_CF(2) SLOT_CF(4) SLOT_CF(8) SLOT_CF(16)
 #undef SLOT_CF
     return hipErrorInvalidValue;
@@ -1914,28 +2063,34 @@ static int check_common(int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, i
     return 0;
 }
 
-extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dtype,
-                            const float* gate, const float* fr, int fr_per_token, const float* temp,
-                            int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
-                            float eps, int occ_bin,
-                            const float* k0, const float* v0, const float* o0,
-                            float* kbuf, float* vbuf, int32_t* am,
-                            float* kold, float* vold, float* oold, float* cslog,
-                            float* kfin, float* vfin, float* ofin, void* stream) {
+// The forward of both contracts: fp32 snapshots (kbuf, vbuf) or, when kbm is set, the writer epilogue's
+// bf16 copies with kinv and valid (kbm, vbm, kinvm, validm).
+static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
+                    const float* gate, const float* fr, int fr_per_token, const float* temp,
+                    int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                    float eps, int occ_bin,
+                    const float* k0, const float* v0, const float* o0,
+                    float* kbuf, float* vbuf, bf16_t* kbm, bf16_t* vbm, float* kinvm, uint8_t* validm,
+                    int32_t* am, float* kold, float* vold, float* oold, float* cslog,
+                    float* kfin, float* vfin, float* ofin, void* stream) {
     if (int r = check_common(B, T, H, N, D, G, dtype)) return r;
-    if (!k || !q || !v || !gate || !fr || !temp || !kbuf || !vbuf || !am || !kfin || !vfin || !ofin)
+    const bool mem = kbm != nullptr;
+    if (!k || !q || !v || !gate || !fr || !temp || !am || !kfin || !vfin || !ofin ||
+        (mem ? (!vbm || !kinvm || !validm) : (!kbuf || !vbuf)))
         return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd: a required pointer is NULL");
+    if (mem) { kbuf = vbuf = nullptr; }
     if ((kold == nullptr) != (oold == nullptr) || (kold == nullptr) != (vold == nullptr) ||
         (kold == nullptr) != (cslog == nullptr))
         return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd: kold, vold, oold and cslog must be all set or all NULL");
-    if (!al16(k) || !al16(q) || !al16(v) || !al16(kbuf) || !al16(vbuf) || !al16(kfin) || !al16(vfin) ||
-        (kold && (!al16(kold) || !al16(vold))) || (k0 && !al16(k0)) || (v0 && !al16(v0)))
+    if (!al16(k) || !al16(q) || !al16(v) || !al16(kbuf) || !al16(vbuf) || !al16(kbm) || !al16(vbm) ||
+        !al16(kfin) || !al16(vfin) || (kold && (!al16(kold) || !al16(vold))) || (k0 && !al16(k0)) || (v0 && !al16(v0)))
         return fail(SLOTSCAN_ERR_ALIGN, "slotscan_fwd: row buffers must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     const int NB = (int)((T + G - 1) / G);
     ChainFwdArgs ca{q, k, gate, fr, temp, k0, o0, kbuf, am, kold, oold, cslog, kfin, ofin,
-                    (int)T, (int)H, (int)N, (int)G, NB, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0, 0, (int)T};
-    RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB, 0, (int)T};
+                    (int)T, (int)H, (int)N, (int)G, NB, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0, 0, (int)T,
+                    kbm, kinvm, validm};
+    RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB, 0, (int)T, vbm};
     // Long sequences run as a two-stream pipeline over step chunks of a multiple of G: the key chain of
     // chunk c + 1 (latency-bound, caller's stream) overlaps the value replay of chunk c (HBM-bound, the
     // library's side stream).  Both kernels carry their state through kfin / ofin and vfin in place
@@ -1966,13 +2121,14 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
         }
         {
             slothost::Scope sc(SLOTSCAN_K_ROWS_FWD, rs);
+#define SLOT_RF(DD, TT) { if (mem) hipLaunchKernelGGL((rows_fwd<DD, TT, true>), grid, block, 0, rs, ra); \
+                          else hipLaunchKernelGGL((rows_fwd<DD, TT, false>), grid, block, 0, rs, ra); }
             if (D == 128) {
-                if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_fwd<128, bf16_t>), grid, block, 0, rs, ra);
-                else hipLaunchKernelGGL((rows_fwd<128, float>), grid, block, 0, rs, ra);
+                if (dtype == SLOTSCAN_BF16) SLOT_RF(128, bf16_t) else SLOT_RF(128, float)
             } else {
-                if (dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((rows_fwd<64, bf16_t>), grid, block, 0, rs, ra);
-                else hipLaunchKernelGGL((rows_fwd<64, float>), grid, block, 0, rs, ra);
+                if (dtype == SLOTSCAN_BF16) SLOT_RF(64, bf16_t) else SLOT_RF(64, float)
             }
+#undef SLOT_RF
             e = hipGetLastError();
         }
         if (e != hipSuccess) return hip_fail(e, "rows_fwd launch");
@@ -1984,27 +2140,61 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
     return 0;
 }
 
+extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dtype,
+                            const float* gate, const float* fr, int fr_per_token, const float* temp,
+                            int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                            float eps, int occ_bin,
+                            const float* k0, const float* v0, const float* o0,
+                            float* kbuf, float* vbuf, int32_t* am,
+                            float* kold, float* vold, float* oold, float* cslog,
+                            float* kfin, float* vfin, float* ofin, void* stream) {
+    if (!kbuf || !vbuf) return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd: a required pointer is NULL");
+    return scan_fwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, k0, v0, o0,
+                    kbuf, vbuf, nullptr, nullptr, nullptr, nullptr, am, kold, vold, oold, cslog,
+                    kfin, vfin, ofin, stream);
+}
+
+extern "C" int slotscan_fwd_mem(const void* k, const void* q, const void* v, int dtype,
+                                const float* gate, const float* fr, int fr_per_token, const float* temp,
+                                int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                                float eps, int occ_bin,
+                                const float* k0, const float* v0, const float* o0,
+                                void* kb, void* vb, float* kinv, uint8_t* valid, int32_t* am,
+                                float* kold, float* vold, float* oold, float* cslog,
+                                float* kfin, float* vfin, float* ofin, void* stream) {
+    if (!kb || !vb || !kinv || !valid) return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd_mem: a required pointer is NULL");
+    return scan_fwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, k0, v0, o0,
+                    nullptr, nullptr, (bf16_t*)kb, (bf16_t*)vb, kinv, valid, am, kold, vold, oold, cslog,
+                    kfin, vfin, ofin, stream);
+}
+
 extern "C" size_t slotscan_bwd_workspace(int64_t B, int64_t T, int64_t H, int64_t N) {
     // Dn (B*H, N, T) fp32, then the per-chain partials (B*H, 2) fp32, 256-byte aligned
     const size_t dn = (size_t)B * H * N * T * sizeof(float);
     return ((dn + 255) & ~(size_t)255) + (size_t)B * H * 2 * sizeof(float);
 }
 
-extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dtype,
-                            const float* gate, const float* fr, int fr_per_token, const float* temp,
-                            int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
-                            float eps, int occ_bin,
-                            const int32_t* am, const float* kold, const float* vold, const float* oold,
-                            const float* cslog, const float* kfin, const float* vfin, const float* ofin,
-                            const float* dkbuf, const float* dvbuf, void* workspace,
-                            void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
-                            void* stream) {
+// The backward of both contracts: fp32 snapshot gradients (dkbuf, dvbuf) or, when dkbm is set, the
+// gradients of the writer epilogue's bf16 copies and of kinv (dkbm, dvbm, dkinvm).
+static int scan_bwd(const void* k, const void* q, const void* v, int dtype,
+                    const float* gate, const float* fr, int fr_per_token, const float* temp,
+                    int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                    float eps, int occ_bin,
+                    const int32_t* am, const float* kold, const float* vold, const float* oold,
+                    const float* cslog, const float* kfin, const float* vfin, const float* ofin,
+                    const float* dkbuf, const float* dvbuf, const bf16_t* dkbm, const bf16_t* dvbm,
+                    const float* dkinvm, void* workspace,
+                    void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
+                    void* stream) {
     if (int r = check_common(B, T, H, N, D, G, dtype)) return r;
+    const bool mem = dkbm != nullptr;
     if (!k || !q || !v || !gate || !fr || !temp || !am || !kold || !vold || !oold || !cslog || !kfin || !vfin || !ofin ||
-        !dkbuf || !dvbuf || !workspace || !dk || !dq || !dv || !dgate || !dfr || !dtemp)
+        (mem ? (!dvbm || !dkinvm) : (!dkbuf || !dvbuf)) || !workspace || !dk || !dq || !dv || !dgate || !dfr || !dtemp)
         return fail(SLOTSCAN_ERR_NULL, "slotscan_bwd: a required pointer is NULL");
+    if (mem) { dkbuf = dvbuf = nullptr; }
     if (!al16(k) || !al16(q) || !al16(v) || !al16(kold) || !al16(vold) || !al16(kfin) || !al16(vfin) ||
-        !al16(dkbuf) || !al16(dvbuf) || !al16(dk) || !al16(dv) || ((uintptr_t)workspace & 255u))
+        !al16(dkbuf) || !al16(dvbuf) || !al16(dkbm) || !al16(dvbm) || !al16(dk) || !al16(dv) ||
+        ((uintptr_t)workspace & 255u))
         return fail(SLOTSCAN_ERR_ALIGN, "slotscan_bwd: row buffers must be 16-byte aligned (workspace 256)");
     hipStream_t st = (hipStream_t)stream;
     const int NB = (int)((T + G - 1) / G);
@@ -2012,14 +2202,16 @@ extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dty
     const size_t dnb = (size_t)B * H * N * T * sizeof(float);
     float* part = (float*)((char*)workspace + ((dnb + 255) & ~(size_t)255));
     RowsBwdArgs ra{k, v, gate, am, kold, vold, kfin, vfin, dkbuf, dvbuf, dk, dv, dn,
-                   (int)T, (int)H, (int)N, (int)G, NB};
+                   (int)T, (int)H, (int)N, (int)G, NB, dkbm, dvbm, dkinvm};
     dim3 grid((unsigned)(B * H), (unsigned)((N + 31) / 32)), block(512);
     hipError_t e;
     {
         slothost::Scope sc(SLOTSCAN_K_ROWS_BWD, st);
         const bool g8 = G == 8 && T % 16 == 0;          // two boundaries per chunk at fixed positions
-#define SLOT_RB(DD, TT) { if (g8) hipLaunchKernelGGL((rows_bwd<DD, TT, true>), grid, block, 0, st, ra); \
-                          else hipLaunchKernelGGL((rows_bwd<DD, TT, false>), grid, block, 0, st, ra); }
+#define SLOT_RB(DD, TT) { if (mem) { if (g8 && DD == 128) hipLaunchKernelGGL((rows_bwd<DD, TT, DD == 128, true>), grid, block, 0, st, ra); \
+                                     else hipLaunchKernelGGL((rows_bwd<DD, TT, false, true>), grid, block, 0, st, ra); } \
+                          else if (g8) hipLaunchKernelGGL((rows_bwd<DD, TT, true, false>), grid, block, 0, st, ra); \
+                          else hipLaunchKernelGGL((rows_bwd<DD, TT, false, false>), grid, block, 0, st, ra); }
         if (D == 128) {
             if (dtype == SLOTSCAN_BF16) SLOT_RB(128, bf16_t) else SLOT_RB(128, float)
         } else {
@@ -2045,4 +2237,34 @@ extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dty
     }
     if (e != hipSuccess) return hip_fail(e, "reduce_parts launch");
     return 0;
+}
+
+extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dtype,
+                            const float* gate, const float* fr, int fr_per_token, const float* temp,
+                            int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                            float eps, int occ_bin,
+                            const int32_t* am, const float* kold, const float* vold, const float* oold,
+                            const float* cslog, const float* kfin, const float* vfin, const float* ofin,
+                            const float* dkbuf, const float* dvbuf, void* workspace,
+                            void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
+                            void* stream) {
+    if (!dkbuf || !dvbuf) return fail(SLOTSCAN_ERR_NULL, "slotscan_bwd: a required pointer is NULL");
+    return scan_bwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, am, kold, vold,
+                    oold, cslog, kfin, vfin, ofin, dkbuf, dvbuf, nullptr, nullptr, nullptr, workspace,
+                    dk, dq, dv, dgate, dfr, dtemp, stream);
+}
+
+extern "C" int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
+                                const float* gate, const float* fr, int fr_per_token, const float* temp,
+                                int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                                float eps, int occ_bin,
+                                const int32_t* am, const float* kold, const float* vold, const float* oold,
+                                const float* cslog, const float* kfin, const float* vfin, const float* ofin,
+                                const void* dkb, const void* dvb, const float* dkinv, void* workspace,
+                                void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
+                                void* stream) {
+    if (!dkb || !dvb || !dkinv) return fail(SLOTSCAN_ERR_NULL, "slotscan_bwd_mem: a required pointer is NULL");
+    return scan_bwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, am, kold, vold,
+                    oold, cslog, kfin, vfin, ofin, nullptr, nullptr, (const bf16_t*)dkb, (const bf16_t*)dvb, dkinv,
+                    workspace, dk, dq, dv, dgate, dfr, dtemp, stream);
 }

@@ -8,7 +8,9 @@ Drop-in surface (same names, arguments, layouts and autograd contract as the ref
                                                                               gqa25/slotkern_kv.py:29-41
     kv_scan(k, v, gate, fr, N, temp, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
             occ_bin=False)                                                    gqa25/slotkern_kvt.py:298-302
-plus kv_scan_stream(...) -- forward only, with a carried (K, V, o) state in and out, for chunked streaming.
+plus kv_scan_stream(...) -- forward only, with a carried (K, V, o) state in and out, for chunked streaming,
+and kv_scan_mem(...) -- the scan with the writer epilogue fused in (memlm_sh.py:453-456 then :473-475),
+returning the bf16 copies with kinv and valid instead of the fp32 snapshots.
 
 Layouts: k, q (B,T,H,DK); v (B,T,H,DV); gate (B,T,H); fr one value or (B,T,H) (per-token when fr.dim()==3,
 slotkern_cuda.py:491); temp a float or 0-d tensor.  Returns fp32 kbuf (B,ceil(T/G),H,N,DK) and vbuf
@@ -63,13 +65,19 @@ def _prep(k, q, v, gate, fr, temp, hard_gate):
     return dt, k_, q_, v_, g, fr_, frt, temp_
 
 
-def _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, state=None):
+def _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, state=None, mem=False):
+    """One forward launch.  mem=False: returns (kbuf, vbuf, am, logs..., final state).  mem=True: the writer
+    epilogue is fused in, and the first two results are replaced by the four (kb, vb, kinv, valid)."""
     B, T, H, D = k_.shape
     NB = (T + G - 1) // G
     dev = k_.device
     f32 = torch.float32
     e = lambda *s, dtype=f32: torch.empty(*s, device=dev, dtype=dtype)
-    kbuf, vbuf = e(B, NB, H, N, D), e(B, NB, H, N, D)
+    if mem:
+        kbuf, vbuf = e(B, NB, H, N, D, dtype=torch.bfloat16), e(B, NB, H, N, D, dtype=torch.bfloat16)
+        kinv, valid = e(B, NB, H, N), e(B, NB, H, N, dtype=torch.bool)
+    else:
+        kbuf, vbuf = e(B, NB, H, N, D), e(B, NB, H, N, D)
     am = e(B, T, H, dtype=torch.int32)
     kold = vold = oold = cslog = None
     if logs:
@@ -80,11 +88,15 @@ def _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, state=Non
         k0, v0, o0 = (x.contiguous().to(f32) for x in state)
         if k0.shape != (B * H, N, D) or v0.shape != (B * H, N, D) or o0.shape != (B * H, N):
             raise ValueError("state must be (K (B*H,N,D), V (B*H,N,D), o (B*H,N))")
-    rc = L.lib().slotscan_fwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
-                              int(frt), L.ptr(temp_), B, T, H, N, D, G, float(eps), int(bool(occ_bin)),
-                              L.ptr(k0), L.ptr(v0), L.ptr(o0), L.ptr(kbuf), L.ptr(vbuf), L.ptr(am),
-                              L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(cslog), L.ptr(kfin), L.ptr(vfin),
-                              L.ptr(ofin), L.stream_of(dev))
+    head = (L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_), int(frt), L.ptr(temp_),
+            B, T, H, N, D, G, float(eps), int(bool(occ_bin)), L.ptr(k0), L.ptr(v0), L.ptr(o0))
+    tail = (L.ptr(am), L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(cslog), L.ptr(kfin), L.ptr(vfin),
+            L.ptr(ofin), L.stream_of(dev))
+    if mem:
+        rc = L.lib().slotscan_fwd_mem(*head, L.ptr(kbuf), L.ptr(vbuf), L.ptr(kinv), L.ptr(valid), *tail)
+        L.check(rc, "slotscan_fwd_mem")
+        return (kbuf, vbuf, kinv, valid), am, kold, vold, oold, cslog, kfin, vfin, ofin
+    rc = L.lib().slotscan_fwd(*head, L.ptr(kbuf), L.ptr(vbuf), *tail)
     L.check(rc, "slotscan_fwd")
     return kbuf, vbuf, am, kold, vold, oold, cslog, kfin, vfin, ofin
 
@@ -106,30 +118,70 @@ class _KVScanHip(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dkbuf, dvbuf):
-        k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, cslog, kfin, vfin, ofin = ctx.saved_tensors
-        N, G, frt, eps, occ_bin, dt, fr_shape, temp_is_tensor = ctx.meta
-        B, T, H, D = k_.shape
+        N, G = ctx.meta[:2]
+        B, T, H, D = ctx.saved_tensors[0].shape
         NB = (T + G - 1) // G
-        dev = k_.device
         f32 = torch.float32
-        z = lambda: torch.zeros(B, NB, H, N, D, device=dev, dtype=f32)
+        z = lambda: torch.zeros(B, NB, H, N, D, device=ctx.saved_tensors[0].device, dtype=f32)
         dkbuf = z() if dkbuf is None else dkbuf.contiguous().to(f32)
         dvbuf = z() if dvbuf is None else dvbuf.contiguous().to(f32)
-        ws = torch.empty(L.lib().slotscan_bwd_workspace(B, T, H, N), device=dev, dtype=torch.uint8)
-        dk, dq, dv = torch.empty_like(k_), torch.empty_like(q_), torch.empty_like(v_)
-        dg = torch.empty(B, T, H, device=dev, dtype=f32)
-        dfr = torch.empty_like(fr_)
-        dtemp = torch.empty(1, device=dev, dtype=f32)
-        rc = L.lib().slotscan_bwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
-                                  int(frt), L.ptr(temp_), B, T, H, N, D, G, float(eps), int(occ_bin),
-                                  L.ptr(am), L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(cslog), L.ptr(kfin),
-                                  L.ptr(vfin), L.ptr(ofin), L.ptr(dkbuf), L.ptr(dvbuf), L.ptr(ws),
-                                  L.ptr(dk), L.ptr(dq), L.ptr(dv), L.ptr(dg), L.ptr(dfr), L.ptr(dtemp),
-                                  L.stream_of(dev))
-        L.check(rc, "slotscan_bwd")
-        dfr = dfr.reshape(fr_shape) if not frt else dfr
-        dtemp = dtemp.reshape(()) if temp_is_tensor else None
-        return dk, dq, dv, dg, dfr, dtemp, None, None, None, None, None
+        return _bwd(ctx, (dkbuf, dvbuf), mem=False) + (None,) * 5
+
+
+def _bwd(ctx, grads, mem):
+    """One backward launch: grads = (dkbuf, dvbuf) fp32, or (dkb, dvb bf16, dkinv fp32) with mem=True.
+    Returns the gradients of (k, q, v, gate, fr, temp)."""
+    k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, cslog, kfin, vfin, ofin = ctx.saved_tensors
+    N, G, frt, eps, occ_bin, dt, fr_shape, temp_is_tensor = ctx.meta
+    B, T, H, D = k_.shape
+    dev = k_.device
+    f32 = torch.float32
+    ws = torch.empty(L.lib().slotscan_bwd_workspace(B, T, H, N), device=dev, dtype=torch.uint8)
+    dk, dq, dv = torch.empty_like(k_), torch.empty_like(q_), torch.empty_like(v_)
+    dg = torch.empty(B, T, H, device=dev, dtype=f32)
+    dfr = torch.empty_like(fr_)
+    dtemp = torch.empty(1, device=dev, dtype=f32)
+    args = (L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_), int(frt), L.ptr(temp_),
+            B, T, H, N, D, G, float(eps), int(occ_bin), L.ptr(am), L.ptr(kold), L.ptr(vold), L.ptr(oold),
+            L.ptr(cslog), L.ptr(kfin), L.ptr(vfin), L.ptr(ofin)) + tuple(L.ptr(x) for x in grads) + \
+        (L.ptr(ws), L.ptr(dk), L.ptr(dq), L.ptr(dv), L.ptr(dg), L.ptr(dfr), L.ptr(dtemp), L.stream_of(dev))
+    name = "slotscan_bwd_mem" if mem else "slotscan_bwd"
+    L.check(getattr(L.lib(), name)(*args), name)
+    dfr = dfr.reshape(fr_shape) if not frt else dfr
+    dtemp = dtemp.reshape(()) if temp_is_tensor else None
+    return dk, dq, dv, dg, dfr, dtemp
+
+
+class _KVScanMemHip(torch.autograd.Function):
+    """The scan with the writer epilogue fused in: forward returns (kb, vb, kinv, valid) directly."""
+
+    @staticmethod
+    def forward(ctx, k, q, v, gate, fr, temp, N, G, hard_gate, eps, occ_bin):
+        D = k.shape[-1]
+        if v.shape[-1] != D:
+            raise ValueError("the HIP scan needs DK == DV")
+        dt, k_, q_, v_, g, fr_, frt, temp_ = _prep(k, q, v, gate, fr, temp, hard_gate)
+        logs = any(ctx.needs_input_grad[:6])
+        (kb, vb, kinv, valid), am, kold, vold, oold, cslog, kfin, vfin, ofin = _fwd(
+            k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, mem=True)
+        if logs:
+            ctx.save_for_backward(k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, cslog, kfin, vfin, ofin)
+        ctx.meta = (int(N), int(G), frt, float(eps), bool(occ_bin), dt, tuple(fr.shape), torch.is_tensor(temp))
+        ctx.mark_non_differentiable(valid)
+        return kb, vb, kinv, valid
+
+    @staticmethod
+    def backward(ctx, dkb, dvb, dkinv, _dvalid):
+        N, G = ctx.meta[:2]
+        B, T, H, D = ctx.saved_tensors[0].shape
+        NB = (T + G - 1) // G
+        dev = ctx.saved_tensors[0].device
+        bf = torch.bfloat16
+        dkb = torch.zeros(B, NB, H, N, D, device=dev, dtype=bf) if dkb is None else dkb.contiguous().to(bf)
+        dvb = torch.zeros(B, NB, H, N, D, device=dev, dtype=bf) if dvb is None else dvb.contiguous().to(bf)
+        dkinv = torch.zeros(B, NB, H, N, device=dev, dtype=torch.float32) if dkinv is None \
+            else dkinv.contiguous().to(torch.float32)
+        return _bwd(ctx, (dkb, dvb, dkinv), mem=True) + (None,) * 5
 
 
 def kv_scan_c(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
@@ -142,6 +194,23 @@ def kv_scan_c(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e
         raise NotImplementedError(why)
     return _KVScanHip.apply(k, k if q is None else q, v, gate, fr, temp, N, int(G), bool(hard_gate), eps,
                             bool(occ_bin))
+
+
+def kv_scan_mem(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
+                occ_bin=False, dtype=torch.bfloat16):
+    """kv_scan_g followed by the writer layer's full-precision epilogue, in one forward and one backward
+    (memlm_sh.py:453-456 then :473-475): returns (kb, vb, kinv, valid) with kb, vb the snapshots in bf16,
+    kinv = rsqrt(max(|K|^2, 1e-12)) fp32 and valid = |K|^2 > 1e-12 (bool), each (B, ceil(T/G), H, N[, D]).
+    The fp32 snapshots are never materialised.  Same modes as kv_scan_c; only the bf16 copies (the
+    activation dtype of training) are emitted."""
+    if dtype != torch.bfloat16:
+        raise NotImplementedError("the fused scan + epilogue emits bf16 copies only; use kv_scan_g and "
+                                  "writer_epilogue for another dtype")
+    why = _unsupported(hard, detach_addr, k.shape[-1], v.shape[-1], N)
+    if why:
+        raise NotImplementedError(why)
+    return _KVScanMemHip.apply(k, k if q is None else q, v, gate, fr, temp, N, int(G), bool(hard_gate), eps,
+                               bool(occ_bin))
 
 
 def kv_scan_g(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
