@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Slot-scan fwd+bwd throughput on one MI355X (BASELINE metric, config 2).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config3*|config4|config5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config2_mem|config3*|config4|config5]
 
 One step = one hard-address slot scan forward (kv_scan_c) plus its backward (torch.autograd.grad of the two
 snapshot outputs against fixed upstream gradients) over one synthetic batch already resident in HBM:
@@ -9,6 +9,9 @@ B=64, T=1024 (65,536 tokens), H=6 heads, N=192 slots, DK=DV=128, G=8, temp=16, p
 hard, detached address (the reference's training setting, run_sh25.sh:213, 222-224).  k, q, v are bf16
 N(0,1) with k and q L2-normalised, gate = sigmoid(N(0,1.5)) bf16, fr ~ U[0,2) bf16, upstream gradients
 N(0,1) drawn in bf16 and passed as fp32 -- all drawn on the GPU from a seeded generator (seed 1).
+
+--workload config2_mem runs the writer layer's scan with its epilogue fused in (kv_scan_mem: bf16 copies,
+kinv, valid) and also times the two-pass path (kv_scan_c then writer_epilogue) on the same inputs.
 
 --workload config4 measures the read instead: one step = the 6 independent reader-layer reads of the frozen
 store, forward only, with the read kernel's HBM and MFMA fractions.
@@ -36,6 +39,8 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 
 WORKLOADS = {
     "config2": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8),
+    # the writer layer's scan with its epilogue fused in (bf16 copies, kinv, valid), against the two-pass path
+    "config2_mem": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8, mem=True),
     "config3": dict(kind="scan", B=64, T=1024, H=6, N=96, D=128, G=8),
     "config3_t512": dict(kind="scan", B=128, T=512, H=6, N=96, D=128, G=8),
     "config3_t256": dict(kind="scan", B=256, T=256, H=6, N=96, D=128, G=8),
@@ -49,21 +54,26 @@ WORKLOADS = {
 }
 
 
-def algorithmic_bytes(B, T, H, N, D, G):
+def algorithmic_bytes(B, T, H, N, D, G, mem=False):
     """Per-kernel and per-step algorithmic HBM bytes (inputs read once, outputs written once; logs, Dn and
     staging are implementation choices and are not counted).  Token tensors bf16, snapshots fp32, gate and
-    fr bf16 as the caller holds them (the kernels read the fp32 copies the wrapper makes: 4 B each)."""
+    fr bf16 as the caller holds them (the kernels read the fp32 copies the wrapper makes: 4 B each).
+    mem: the fused writer epilogue -- bf16 snapshot copies, plus kinv (fp32) and valid (1 B) per key row
+    out and dkinv (fp32) per key row in."""
     tok = B * T * H
     NB = (T + G - 1) // G
-    snap = B * NB * H * N * D * 4
+    rows = B * NB * H * N
+    snap = rows * D * (2 if mem else 4)
+    kx_f, kx_b = (rows * 5, rows * 4) if mem else (0, 0)
     row = tok * D * 2
     per_kernel = {
-        "chain_fwd": 2 * row + 2 * tok * 4 + snap,          # q, k, gate, fr in; kbuf out
-        "rows_fwd": row + tok * 4 + snap,                   # v, gate in; vbuf out
-        "rows_bwd": 2 * snap + 2 * row + tok * 4 + 2 * row,  # dkbuf, dvbuf, k, v, gate in; dk, dv out
-        "chain_bwd": row + 2 * tok * 4 + row + 2 * tok * 4,  # q, gate, fr in; dq, dgate, dfr out
+        "chain_fwd": 2 * row + 2 * tok * 4 + snap + kx_f,          # q, k, gate, fr in; kbuf (kinv, valid) out
+        "rows_fwd": row + tok * 4 + snap,                          # v, gate in; vbuf out
+        "rows_bwd": 2 * snap + kx_b + 2 * row + tok * 4 + 2 * row,  # dkbuf, dvbuf (dkinv), k, v, gate in; dk, dv out
+        "chain_bwd": row + 2 * tok * 4 + row + 2 * tok * 4,        # q, gate, fr in; dq, dgate, dfr out
     }
-    step = (3 * row + 2 * tok * 2 + 2 * snap) + (2 * snap + 3 * row + 2 * tok * 2 + 3 * row + 2 * tok * 2)
+    step = (3 * row + 2 * tok * 2 + 2 * snap + kx_f) + \
+        (2 * snap + kx_b + 3 * row + 2 * tok * 2 + 3 * row + 2 * tok * 2)
     return per_kernel, step
 
 
@@ -114,14 +124,21 @@ def cpu_baseline(W, seed=1, Bs=12):
     NB = (T + G - 1) // G
     dkb = rng.standard_normal((Bs, NB, H, N, D)).astype(f)
     dvb = rng.standard_normal((Bs, NB, H, N, D)).astype(f)
+    mem = W.get("mem", False)
+    dki = rng.standard_normal((Bs, NB, H, N)).astype(f)
     t0 = time.perf_counter()
     kb, vb, info = SO.scan_forward(k, v, g, fr, N, 16.0, G=G, hard=True, q=q, occ_bin=True, dtype=f)
+    if mem:                                  # the epilogue (memlm_sh.py:474-475) and its autograd
+        nsq = (kb * kb).sum(-1)
+        kinv = 1.0 / np.sqrt(np.maximum(nsq, f(1e-12)))
+        valid = nsq > 1e-12                  # (numpy has no bf16: the copies' cast is not timed)
+        dkb = dkb + 2 * kb * np.where(nsq >= 1e-12, -0.5 * kinv ** 3 * dki, 0.0).astype(f)[..., None]
     SO.scan_backward(k, v, g, fr, N, 16.0, kb, vb, info, dkb, dvb, G=G, hard=True, q=q, occ_bin=True,
                      detach_addr=True, dtype=f)
     dt = time.perf_counter() - t0
     return dict(value=round(Bs * T / dt, 1), unit="tokens/s", cores=1, kind="port",
                 sample=f"B={Bs} slice of the workload (T={T}, H={H}, N={N}, D={D}, G={G}), fp32 numpy oracle "
-                       f"fwd+bwd, {dt:.1f} s", seconds=round(dt, 2))
+                       f"fwd+bwd{' with the writer epilogue' if mem else ''}, {dt:.1f} s", seconds=round(dt, 2))
 
 
 def cpu_baseline_read(W, seed=3, Bs=32):
@@ -339,11 +356,26 @@ def main():
     dkb = rn(B, NB, H, N, D).to(torch.bfloat16).float()
     dvb = rn(B, NB, H, N, D).to(torch.bfloat16).float()
     inputs = (k, q, v, gate, fr, temp)
+    mem = W.get("mem", False)
+    kw = dict(G=G, hard=True, hard_gate=False, detach_addr=True, q=q, occ_bin=True)
 
-    def step():
-        kb, vb = KH.kv_scan_c(k, v, gate, fr, N, temp, G=G, hard=True, hard_gate=False, detach_addr=True, q=q,
-                              occ_bin=True)
-        return torch.autograd.grad((kb, vb), inputs, (dkb, dvb))
+    if mem:
+        import slotmem_hip as MH
+        dkb, dvb = dkb.to(torch.bfloat16), dvb.to(torch.bfloat16)
+        dki = rn(B, NB, H, N)
+
+        def step():
+            kb, vb, kinv, _valid = KH.kv_scan_mem(k, v, gate, fr, N, temp, **kw)
+            return torch.autograd.grad((kb, vb, kinv), inputs, (dkb, dvb, dki))
+
+        def step_two_pass():                 # the same outputs through the scan, then the epilogue
+            kbuf, vbuf = KH.kv_scan_c(k, v, gate, fr, N, temp, **kw)
+            kb, vb, kinv, _valid = MH.writer_epilogue(kbuf, vbuf, dtype=torch.bfloat16)
+            return torch.autograd.grad((kb, vb, kinv), inputs, (dkb, dvb, dki))
+    else:
+        def step():
+            kb, vb = KH.kv_scan_c(k, v, gate, fr, N, temp, **kw)
+            return torch.autograd.grad((kb, vb), inputs, (dkb, dvb))
 
     for _ in range(args.warmup):
         step()
@@ -364,8 +396,18 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     ms = (t1 - t0) * 1e3 / args.steps
+    two_pass_ms = None
+    if mem:
+        for _ in range(args.warmup):
+            step_two_pass()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        for _ in range(args.steps):
+            step_two_pass()
+        torch.cuda.synchronize()
+        two_pass_ms = (time.perf_counter() - t2) * 1e3 / args.steps
     tokens = B * T
-    per_kernel_bytes, step_bytes = algorithmic_bytes(B, T, H, N, D, G)
+    per_kernel_bytes, step_bytes = algorithmic_bytes(B, T, H, N, D, G, mem=mem)
     kern_ms = {name: tot / cnt for name, (tot, cnt) in prof.items()}
     # the forward runs as a chunk pipeline (several launches per step): per-launch bytes are the per-step
     # bytes over the launches per step
@@ -375,7 +417,8 @@ def main():
     ach = launch_bytes[dom] / (kern_ms[dom] * 1e-3) / 1e9
     traffic = measured_traffic(args.workload).get(dom)
     out = {
-        "metric": "slot-scan fwd+bwd tokens/s at B64 T1024 H6 S192 d128; % HBM/MFMA roofline",
+        "metric": ("slot-scan + writer epilogue fwd+bwd tokens/s at B64 T1024 H6 S192 d128" if mem else
+                   "slot-scan fwd+bwd tokens/s at B64 T1024 H6 S192 d128; % HBM/MFMA roofline"),
         "value": round(tokens / (ms * 1e-3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -385,7 +428,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 state, bf16 tokens",
+        "dtype": "f32 state, bf16 tokens" + (", bf16 copies" if mem else ""),
         "data": "synthetic (seeded GPU generator, seed 1)",
         "config": {"workload": args.workload, "B": B, "T": T, "H": H, "N": N, "D": D, "G": G, "temp": 16.0,
                    "mode": "hard, detach_addr, occ_bin, per-token fr", "tokens_per_step": tokens},
@@ -399,6 +442,9 @@ def main():
         "kernels_ms": {n: round(x, 4) for n, x in kern_ms.items()},
         "launches_per_step": {n: round(x, 2) for n, x in per_step.items()},
     }
+    if mem:
+        out["two_pass_ms_per_step"] = round(two_pass_ms, 4)
+        out["speedup_vs_two_pass"] = round(two_pass_ms / ms, 3)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(W)
     print(json.dumps(out), flush=True)
