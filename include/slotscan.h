@@ -118,10 +118,13 @@ int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
                      void* stream);
 
 /* Per-kernel timing (the reference's kvu/prof_cuda.py:9-20 wraps each compiled kernel's launch in CUDA
- * events; this is the same facility inside the library).  While enabled, every kernel launch is bracketed
- * by two hipEvents recorded on its stream.  slotscan_profile_read waits for the recorded events, writes
- * the summed milliseconds and launch counts per kernel id (SLOTSCAN_K_*) into total_ms[nk] / count[nk],
- * and clears the records.  Returns 0, or SLOTSCAN_ERR_HIP if an event query failed. */
+ * events; this is the same facility inside the library).  slotscan_profile(mask): 0 disables timing;
+ * otherwise every launch of a kernel whose bit (1 << SLOTSCAN_K_*) is set in mask -- -1 = every kernel --
+ * gets a pair of hipEvents stamped with the kernel's own start and end (hipExtLaunchKernel).  Each timed
+ * launch costs the stream a few microseconds, so a caller timing a whole step times only the kernels it
+ * needs.  slotscan_profile_read waits for the recorded events, writes the summed milliseconds and launch
+ * counts per kernel id into total_ms[nk] / count[nk], and clears the records.  Returns 0, or
+ * SLOTSCAN_ERR_HIP if an event query failed. */
 #define SLOTSCAN_K_CHAIN_FWD 0
 #define SLOTSCAN_K_ROWS_FWD 1
 #define SLOTSCAN_K_ROWS_BWD 2

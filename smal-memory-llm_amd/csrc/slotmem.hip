@@ -254,11 +254,11 @@ extern "C" int slotmem_epilogue_fwd(const float* kbuf, const float* vbuf, int64_
     {
         slothost::Scope sc(SLOTSCAN_K_MEM, st);
         if (D == 128) {
-            if (out_dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((mem_epilogue<128, bf16_t>), grid, block, 0, st, a);
-            else hipLaunchKernelGGL((mem_epilogue<128, float>), grid, block, 0, st, a);
+            if (out_dtype == SLOTSCAN_BF16) slothost::launch((mem_epilogue<128, bf16_t>), grid, block, 0, st, a);
+            else slothost::launch((mem_epilogue<128, float>), grid, block, 0, st, a);
         } else {
-            if (out_dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((mem_epilogue<64, bf16_t>), grid, block, 0, st, a);
-            else hipLaunchKernelGGL((mem_epilogue<64, float>), grid, block, 0, st, a);
+            if (out_dtype == SLOTSCAN_BF16) slothost::launch((mem_epilogue<64, bf16_t>), grid, block, 0, st, a);
+            else slothost::launch((mem_epilogue<64, float>), grid, block, 0, st, a);
         }
         e = hipGetLastError();
     }
@@ -280,11 +280,11 @@ extern "C" int slotmem_epilogue_bwd(const float* kbuf, const void* dkout, const 
     {
         slothost::Scope sc(SLOTSCAN_K_MEM_BWD, st);
         if (D == 128) {
-            if (grad_dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((mem_epilogue_bwd<128, bf16_t>), grid, block, 0, st, a);
-            else hipLaunchKernelGGL((mem_epilogue_bwd<128, float>), grid, block, 0, st, a);
+            if (grad_dtype == SLOTSCAN_BF16) slothost::launch((mem_epilogue_bwd<128, bf16_t>), grid, block, 0, st, a);
+            else slothost::launch((mem_epilogue_bwd<128, float>), grid, block, 0, st, a);
         } else {
-            if (grad_dtype == SLOTSCAN_BF16) hipLaunchKernelGGL((mem_epilogue_bwd<64, bf16_t>), grid, block, 0, st, a);
-            else hipLaunchKernelGGL((mem_epilogue_bwd<64, float>), grid, block, 0, st, a);
+            if (grad_dtype == SLOTSCAN_BF16) slothost::launch((mem_epilogue_bwd<64, bf16_t>), grid, block, 0, st, a);
+            else slothost::launch((mem_epilogue_bwd<64, float>), grid, block, 0, st, a);
         }
         e = hipGetLastError();
     }
@@ -303,8 +303,8 @@ extern "C" int slotmem_codes(const float* x, int64_t rows, int64_t D, int bits, 
     hipError_t e;
     {
         slothost::Scope sc(SLOTSCAN_K_MEM, st);
-        if (D == 128) hipLaunchKernelGGL(mem_codes<128>, grid, block, 0, st, a);
-        else hipLaunchKernelGGL(mem_codes<64>, grid, block, 0, st, a);
+        if (D == 128) slothost::launch(mem_codes<128>, grid, block, 0, st, a);
+        else slothost::launch(mem_codes<64>, grid, block, 0, st, a);
         e = hipGetLastError();
     }
     return e == hipSuccess ? 0 : hip_fail(e, "mem_codes launch");

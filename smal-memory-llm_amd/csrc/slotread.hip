@@ -911,11 +911,11 @@ extern "C" int slotread_fwd(const void* q, const void* kbuf, const void* vbuf, c
             if (split < 1) split = 1;
             ra.MC = (int)(((tiles + split - 1) / split) * 16);
             dim3 wgrid((unsigned)slabs, (unsigned)((G * NQ + ra.MC - 1) / ra.MC)), wblock(WIDE_THREADS);
-            if (D == 128) hipLaunchKernelGGL(read_fwd_wide<128>, wgrid, wblock, 0, st, ra);
-            else hipLaunchKernelGGL(read_fwd_wide<64>, wgrid, wblock, 0, st, ra);
+            if (D == 128) slothost::launch(read_fwd_wide<128>, wgrid, wblock, 0, st, ra);
+            else slothost::launch(read_fwd_wide<64>, wgrid, wblock, 0, st, ra);
         } else {
-            if (D == 128) hipLaunchKernelGGL(read_fwd<128>, grid, block, 0, st, ra);
-            else hipLaunchKernelGGL(read_fwd<64>, grid, block, 0, st, ra);
+            if (D == 128) slothost::launch(read_fwd<128>, grid, block, 0, st, ra);
+            else slothost::launch(read_fwd<64>, grid, block, 0, st, ra);
         }
         e = hipGetLastError();
     }
@@ -944,11 +944,11 @@ extern "C" int slotread_bwd(const void* q, const void* kbuf, const void* vbuf, c
     {
         slothost::Scope sc(SLOTSCAN_K_READ_BWD, st);
         if (D == 128) {
-            if (acc) hipLaunchKernelGGL((read_bwd<128, true>), grid, block, 0, st, ra);
-            else hipLaunchKernelGGL((read_bwd<128, false>), grid, block, 0, st, ra);
+            if (acc) slothost::launch((read_bwd<128, true>), grid, block, 0, st, ra);
+            else slothost::launch((read_bwd<128, false>), grid, block, 0, st, ra);
         } else {
-            if (acc) hipLaunchKernelGGL((read_bwd<64, true>), grid, block, 0, st, ra);
-            else hipLaunchKernelGGL((read_bwd<64, false>), grid, block, 0, st, ra);
+            if (acc) slothost::launch((read_bwd<64, true>), grid, block, 0, st, ra);
+            else slothost::launch((read_bwd<64, false>), grid, block, 0, st, ra);
         }
         e = hipGetLastError();
     }

@@ -39,6 +39,7 @@
 // Token inputs (q, k, gate, fr; in the backward also the undo log, Dn and the cosine log) are staged in
 // LDS as fp32 in double-buffered chunks.
 #include "slot_common.h"
+#include "slot_host.h"
 
 using namespace slot;
 typedef uint64_t u64;
@@ -1923,8 +1924,8 @@ template <int D, typename TI>
 hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
     dim3 grid(B * a.H), block(FWD_THREADS);
 #define SLOT_CF(PP) if (a.N <= 4 * CHAIN_WAVES * PP) { \
-        if (a.kbm) hipLaunchKernelGGL((chain_fwd<D, PP, TI, true>), grid, block, 0, st, a); \
-        else hipLaunchKernelGGL((chain_fwd<D, PP, TI, false>), grid, block, 0, st, a); \
+        if (a.kbm) slothost::launch((chain_fwd<D, PP, TI, true>), grid, block, 0, st, a); \
+        else slothost::launch((chain_fwd<D, PP, TI, false>), grid, block, 0, st, a); \
         return hipGetLastError(); }
     SLOT_CF(1) SLOT_CF(2) SLOT_CF(4) SLOT_CF(8) SLOT_CF(16)
 #undef SLOT_CF
@@ -1935,16 +1936,16 @@ hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
     if (a.occb) {                                        // windowed kernel, four waves
         constexpr int NW = 4;
         dim3 grid(B * a.H), block(64 * NW);
-        if (a.N <= 64) hipLaunchKernelGGL((chain_bwd_w<D, 1, NW, TI>), grid, block, 0, st, a);
-        else if (a.N <= 128) hipLaunchKernelGGL((chain_bwd_w<D, 2, NW, TI>), grid, block, 0, st, a);
-        else if (a.N <= 192) hipLaunchKernelGGL((chain_bwd_w<D, 3, NW, TI>), grid, block, 0, st, a);
+        if (a.N <= 64) slothost::launch((chain_bwd_w<D, 1, NW, TI>), grid, block, 0, st, a);
+        else if (a.N <= 128) slothost::launch((chain_bwd_w<D, 2, NW, TI>), grid, block, 0, st, a);
+        else if (a.N <= 192) slothost::launch((chain_bwd_w<D, 3, NW, TI>), grid, block, 0, st, a);
         else return hipErrorInvalidValue;
         return hipGetLastError();
     }
     dim3 grid(B * a.H), block(CHAIN_THREADS);
 #define SLOT_CB(PP) if (a.N <= 4 * CHAIN_WAVES * PP) { \
-        if (a.occb) hipLaunchKernelGGL((chain_bwd<D, PP, TI, true>), grid, block, 0, st, a); \
-        else hipLaunchKernelGGL((chain_bwd<D, PP, TI, false>), grid, block, 0, st, a); \
+        if (a.occb) slothost::launch((chain_bwd<D, PP, TI, true>), grid, block, 0, st, a); \
+        else slothost::launch((chain_bwd<D, PP, TI, false>), grid, block, 0, st, a); \
         return hipGetLastError(); }
     SLOT_CB(1) SLOT_CB(2) SLOT_CB(4) SLOT_CB(8) SLOT_CB(16)
 #undef SLOT_CB
@@ -1955,7 +1956,6 @@ hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
 
 // ======================================================================================== C-ABI
 #include "slotscan.h"
-#include "slot_host.h"
 #include <algorithm>
 #include <mutex>
 #include <vector>
@@ -1965,6 +1965,7 @@ hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
 namespace slotprof {
 std::mutex mu;
 bool on = false;
+uint32_t mask = 0;                                   // kernel ids timed while on
 std::vector<hipEvent_t> pool;
 struct Rec { int kid; hipEvent_t a, b; };
 std::vector<Rec> recs;
@@ -1977,19 +1978,33 @@ hipEvent_t get() {
 }  // namespace slotprof
 
 namespace slothost {
+Scope*& current_scope() {
+    static thread_local Scope* cur = nullptr;
+    return cur;
+}
 Scope::Scope(int k, hipStream_t s) : kid(k), st(s) {
-    if (!slotprof::on) return;
+    prev = current_scope();
+    current_scope() = this;
+    if (!slotprof::on || kid < 0 || kid >= 32 || !((slotprof::mask >> kid) & 1u)) return;
     std::lock_guard<std::mutex> g(slotprof::mu);
     a = slotprof::get();
-    if (a) hipEventRecord(a, st);
+    b = slotprof::get();
+    if (!a || !b) {
+        if (a) slotprof::pool.push_back(a);
+        if (b) slotprof::pool.push_back(b);
+        a = b = nullptr;
+    }
 }
 Scope::~Scope() {
+    current_scope() = prev;
     if (!a) return;
     std::lock_guard<std::mutex> g(slotprof::mu);
-    hipEvent_t b = slotprof::get();
-    if (!b) return;
-    hipEventRecord(b, st);
-    slotprof::recs.push_back({kid, a, b});
+    if (used) {
+        slotprof::recs.push_back({kid, a, b});
+    } else {
+        slotprof::pool.push_back(a);
+        slotprof::pool.push_back(b);
+    }
 }
 
 static std::mutex side_mu;
@@ -2033,6 +2048,7 @@ using slothost::al16;
 extern "C" int slotscan_profile(int enable) {
     std::lock_guard<std::mutex> g(slotprof::mu);
     slotprof::on = enable != 0;
+    slotprof::mask = (uint32_t)enable;
     return 0;
 }
 
@@ -2121,8 +2137,8 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
         }
         {
             slothost::Scope sc(SLOTSCAN_K_ROWS_FWD, rs);
-#define SLOT_RF(DD, TT) { if (mem) hipLaunchKernelGGL((rows_fwd<DD, TT, true>), grid, block, 0, rs, ra); \
-                          else hipLaunchKernelGGL((rows_fwd<DD, TT, false>), grid, block, 0, rs, ra); }
+#define SLOT_RF(DD, TT) { if (mem) slothost::launch((rows_fwd<DD, TT, true>), grid, block, 0, rs, ra); \
+                          else slothost::launch((rows_fwd<DD, TT, false>), grid, block, 0, rs, ra); }
             if (D == 128) {
                 if (dtype == SLOTSCAN_BF16) SLOT_RF(128, bf16_t) else SLOT_RF(128, float)
             } else {
@@ -2208,10 +2224,10 @@ static int scan_bwd(const void* k, const void* q, const void* v, int dtype,
     {
         slothost::Scope sc(SLOTSCAN_K_ROWS_BWD, st);
         const bool g8 = G == 8 && T % 16 == 0;          // two boundaries per chunk at fixed positions
-#define SLOT_RB(DD, TT) { if (mem) { if (g8 && DD == 128) hipLaunchKernelGGL((rows_bwd<DD, TT, DD == 128, true>), grid, block, 0, st, ra); \
-                                     else hipLaunchKernelGGL((rows_bwd<DD, TT, false, true>), grid, block, 0, st, ra); } \
-                          else if (g8) hipLaunchKernelGGL((rows_bwd<DD, TT, true, false>), grid, block, 0, st, ra); \
-                          else hipLaunchKernelGGL((rows_bwd<DD, TT, false, false>), grid, block, 0, st, ra); }
+#define SLOT_RB(DD, TT) { if (mem) { if (g8 && DD == 128) slothost::launch((rows_bwd<DD, TT, DD == 128, true>), grid, block, 0, st, ra); \
+                                     else slothost::launch((rows_bwd<DD, TT, false, true>), grid, block, 0, st, ra); } \
+                          else if (g8) slothost::launch((rows_bwd<DD, TT, true, false>), grid, block, 0, st, ra); \
+                          else slothost::launch((rows_bwd<DD, TT, false, false>), grid, block, 0, st, ra); }
         if (D == 128) {
             if (dtype == SLOTSCAN_BF16) SLOT_RB(128, bf16_t) else SLOT_RB(128, float)
         } else {
@@ -2231,7 +2247,7 @@ static int scan_bwd(const void* k, const void* q, const void* v, int dtype,
     if (e != hipSuccess) return hip_fail(e, "chain_bwd launch");
     {
         slothost::Scope sc(SLOTSCAN_K_REDUCE, st);
-        hipLaunchKernelGGL(reduce_parts, dim3(1), dim3(256), 0, st, part, (int)(B * H), dtemp,
+        slothost::launch(reduce_parts, dim3(1), dim3(256), 0, st, part, (int)(B * H), dtemp,
                            fr_per_token ? (float*)nullptr : dfr);
         e = hipGetLastError();
     }

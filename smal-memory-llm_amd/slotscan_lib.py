@@ -92,9 +92,18 @@ KERNEL_NAMES = ("chain_fwd", "rows_fwd", "rows_bwd", "chain_bwd", "reduce_parts"
                 "mem_bwd", "spare")
 
 
-def profile(enable):
-    """Start (True) or stop (False) per-kernel HIP-event timing inside the library."""
-    check(lib().slotscan_profile(int(bool(enable))), "slotscan_profile")
+def profile(enable, kernels=None):
+    """Start (True) or stop (False) per-kernel HIP-event timing inside the library; `kernels` (names from
+    KERNEL_NAMES) restricts the timing to those kernels, None times every kernel."""
+    if not enable:
+        mask = 0
+    elif kernels is None:
+        mask = -1
+    else:
+        mask = 0
+        for k in kernels:
+            mask |= 1 << KERNEL_NAMES.index(k)
+    check(lib().slotscan_profile(int(mask)), "slotscan_profile")
 
 
 def profile_read():
