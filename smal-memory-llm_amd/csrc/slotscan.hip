@@ -1796,25 +1796,28 @@ void chain_bwd_w(ChainBwdArgs a) {
             if ((k4 & 1) == 1) __builtin_amdgcn_sched_barrier(0);
         }
         // S7: undo the window's writes (reverse order) in this wave's dims, logging
-        //     d_s = Kh(kold_s) - Kh_{a_s}(after write s).  First every event's Kh(kold_s) in place (this wave's
-        //     dims of s_ko: no other wave reads them after B2), then one short dependent step per event.
-#pragma unroll
-        for (int i = 0; i < WIN; i++) {
-            const float ki = rsq_clamped(readlanef(knrm, i));
-#pragma unroll
-            for (int nb = 0; nb < NBW; nb++) s_ko[i][d0 + 16 * nb + c] *= ki;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        //     d_s = Kh(kold_s) - Kh_{a_s}(after write s).  Each event's kold slice is read XD events ahead
+        //     and normalised on use, so the dependent steps do not wait on an LDS round trip.
         const int am_l = s_am[lane & (WIN - 1)];         // lane i (< 16) holds the row written at window step i
+        const float kil = rsq_clamped(knrm);             // lane i: 1 / max(|kold_i|, 1e-6)
+        constexpr int XD = 3;
+        float xo[WIN][NBW];
+#pragma unroll
+        for (int i = WIN - 1; i >= WIN - XD; i--)
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++) xo[i][nb] = s_ko[i][d0 + 16 * nb + c];
 #pragma unroll
         for (int i = WIN - 1; i >= 0; i--) {             // program order keeps repeated rows sequential
+            if (i - XD >= 0) {
+#pragma unroll
+                for (int nb = 0; nb < NBW; nb++) xo[i - XD][nb] = s_ko[i - XD][d0 + 16 * nb + c];
+            }
             if (i < nt) {
                 const int ar = __builtin_amdgcn_readlane(am_l, i);
+                const float ki = readlanef(kil, i);
                 float x[NBW];
 #pragma unroll
-                for (int nb = 0; nb < NBW; nb++) x[nb] = s_ko[i][d0 + 16 * nb + c];
+                for (int nb = 0; nb < NBW; nb++) x[nb] = xo[i][nb] * ki;
                 const int ag = ar / KK, kk = ar - KK * ag;
                 const int ch = kk >> 4, e = kk & 15;
                 const bool mine = grp == ag;
