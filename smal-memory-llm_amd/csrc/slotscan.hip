@@ -1670,16 +1670,17 @@ void chain_bwd_w(ChainBwdArgs a) {
         }
         // S4: the softmax adjoint of this wave's steps, over every row.  With a_n = e_n / SS over the eligible
         // rows, sum over taken rows of dz_n = (g * SSD_taken - sa * SS_taken) / SS, so dfr needs no extra
-        // reduction.
-        // the SPW steps of this wave in lockstep groups of GS: one interleaved wave max and one interleaved
-        // wave sum per group, branch-free free-row search; the per-step stores are gathered to lanes
-        // 0 .. SPW-1 at the end.  z is recomputed from the cosine where needed (fewer live registers).
+        // reduction.  The shift of the exponentials is the z of the row the forward wrote: the forward chose
+        // it as the maximum of these same z over the eligible rows, so no wave max is needed (a softmax is
+        // exact for any shift; this one keeps every exponent <= 0 up to rounding).
+        // The SPW steps of this wave in lockstep groups of GS: one interleaved wave sum per group, branch-free
+        // free-row search; the per-step stores are gathered to lanes 0 .. SPW-1 at the end.
         float dgv[SPW], dfv[SPW];
         bool livev[SPW];
 #pragma unroll
         for (int i0 = 0; i0 < SPW; i0 += GS) {
             int ai[GS];
-            float g[GS], frv[GS], lm[GS], cs[GS][RPL], dw[GS][RPL];
+            float g[GS], frv[GS], Mv[GS], cs[GS][RPL], dw[GS][RPL], ev[GS][RPL];
 #pragma unroll
             for (int ii = 0; ii < GS; ii++) {                 // steps past nt hold zeros: W = 0, no stores
                 const int i = SPW * wave + i0 + ii;
@@ -1687,7 +1688,8 @@ void chain_bwd_w(ChainBwdArgs a) {
                 ai[ii] = s_am[i];
                 g[ii] = s_g[i];
                 frv[ii] = frt ? s_fr[i] : fr_s;
-                lm[ii] = -INFINITY;
+                const int aj = ai[ii] >> 6, al = ai[ii] & 63;
+                float zsel = 0.f;
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
                     const int n = lane + 64 * j;
@@ -1695,11 +1697,11 @@ void chain_bwd_w(ChainBwdArgs a) {
                     cs[ii][j] = n < N ? s_cs[i * N + n] : 0.f;
                     dw[ii][j] = s_dn[n][i];
                     const float z = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
-                    lm[ii] = fmaxf(lm[ii], tj ? z : -INFINITY);
+                    zsel = aj == j ? z : zsel;
                 }
+                Mv[ii] = readlanef(zsel, al);
             }
-            wavemax_k<GS>(lm);                                 // lm[ii] = the wave max over taken rows
-            float ls[2 * GS];                                  // [ii]: sum e, [GS + ii]: sum e * dw
+            float ls[2 * GS];                                  // [ii]: sum e, [GS + ii]: sum e * dw (taken rows)
 #pragma unroll
             for (int ii = 0; ii < GS; ii++) {
                 const int i = SPW * wave + i0 + ii;
@@ -1708,7 +1710,8 @@ void chain_bwd_w(ChainBwdArgs a) {
                 for (int j = 0; j < RPL; j++) {
                     const bool tj = (tk[j] >> i) & 1u;
                     const float z = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
-                    const float e = tj ? __expf(z - lm[ii]) : 0.f;
+                    const float e = tj ? __expf(z - Mv[ii]) : 0.f;
+                    ev[ii][j] = e;
                     s0 += e;
                     s1 = fmaf(e, dw[ii][j], s1);
                 }
@@ -1733,11 +1736,9 @@ void chain_bwd_w(ChainBwdArgs a) {
                     FZ = mf ? zf : FZ;
                     FD = mf ? df : FD;
                 }
-                const float wm = lm[ii];
-                const float M = FO >= 0 ? fmaxf(wm, FZ) : wm;       // the first free row competes too
-                const float sc = wm == -INFINITY ? 0.f : __expf(wm - M);
-                const float SSt = ls[ii] * sc, SSDt = ls[GS + ii] * sc;
-                const float ef = FO >= 0 ? __expf(FZ - M) : 0.f;
+                const float M = Mv[ii];
+                const float SSt = ls[ii], SSDt = ls[GS + ii];
+                const float ef = FO >= 0 ? __expf(FZ - M) : 0.f;   // the first free row competes too
                 const float SS = FO >= 0 ? SSt + ef : SSt;
                 const float SSD = FO >= 0 ? fmaf(ef, FD, SSDt) : SSDt;
                 const float rss = livev[i0 + ii] ? __builtin_amdgcn_rcpf(SS) : 0.f, sa = (g[ii] * SSD) * rss;
@@ -1745,9 +1746,7 @@ void chain_bwd_w(ChainBwdArgs a) {
                 for (int j = 0; j < RPL; j++) {
                     const int n = lane + 64 * j;
                     const bool tj = (tk[j] >> i) & 1u;
-                    const bool elig = tj || (n < N && n == FO);
-                    const float z = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
-                    const float as = elig ? __expf(z - M) * rss : 0.f;
+                    const float as = tj ? ev[ii][j] * rss : (n < N && n == FO) ? ef * rss : 0.f;
                     const float dz = as * (g[ii] * dw[ii][j] - sa);
                     dtemp_acc = fmaf(dz, cs[ii][j], dtemp_acc);
                     s_W[i][n] = temp * dz;
