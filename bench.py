@@ -430,8 +430,9 @@ def main():
     ach = launch_bytes[dom] / (dom_ms * 1e-3) / 1e9
     traffic = measured_traffic(args.workload).get(dom)
     out = {
-        "metric": ("slot-scan + writer epilogue fwd+bwd tokens/s at B64 T1024 H6 S192 d128" if mem else
-                   "slot-scan fwd+bwd tokens/s at B64 T1024 H6 S192 d128; % HBM/MFMA roofline"),
+        "metric": (f"slot-scan + writer epilogue fwd+bwd tokens/s at B{B} T{T} H{H} S{N} d{D}" if mem else
+                   "slot-scan fwd+bwd tokens/s at B64 T1024 H6 S192 d128; % HBM/MFMA roofline"
+                   if args.workload == "config2" else f"slot-scan fwd+bwd tokens/s at B{B} T{T} H{H} S{N} d{D}"),
         "value": round(tokens / (ms * 1e-3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
