@@ -134,7 +134,9 @@ int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
 #define SLOTSCAN_K_READ_BWD 6
 #define SLOTSCAN_K_MEM 7
 #define SLOTSCAN_K_MEM_BWD 8
-#define SLOTSCAN_NK 10
+#define SLOTSCAN_K_WIN_FWD 9
+#define SLOTSCAN_K_WIN_BWD 10
+#define SLOTSCAN_NK 12
 int slotscan_profile(int enable);
 int slotscan_profile_read(double* total_ms, int64_t* count, int nk);
 

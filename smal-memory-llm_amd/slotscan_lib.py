@@ -44,6 +44,9 @@ SIGNATURES = {
     "slotmem_epilogue_fwd": (_i32, [_vp, _vp, _i64, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp]),
     "slotmem_epilogue_bwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i64, _i32, _vp, _vp, _vp]),
     "slotmem_codes": (_i32, [_vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp]),
+    "slotwin_fwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp]),
+    "slotwin_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                           _vp, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None
@@ -89,7 +92,7 @@ def dtype_code(dt):
 
 
 KERNEL_NAMES = ("chain_fwd", "rows_fwd", "rows_bwd", "chain_bwd", "reduce_parts", "read_fwd", "read_bwd", "mem_fwd",
-                "mem_bwd", "spare")
+                "mem_bwd", "win_fwd", "win_bwd", "spare")
 
 
 def profile(enable, kernels=None):
