@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Slot-scan fwd+bwd throughput on one MI355X (BASELINE metric, config 2).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config2_mem|config3*|config4|config5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config2_mem|config3*|config4|config5|read_train|window_train]
 
 One step = one hard-address slot scan forward (kv_scan_c) plus its backward (torch.autograd.grad of the two
 snapshot outputs against fixed upstream gradients) over one synthetic batch already resident in HBM:
@@ -53,6 +53,9 @@ WORKLOADS = {
     "config5": dict(kind="stream", B=8, T=131072, H=6, N=192, D=128, G=8, chunk=1024),
     # one reader layer of training at the config-2 memory: G = 8 tokens per block, NQ = 2, forward + backward
     "read_train": dict(kind="read", B=64, T=1024, H=6, N=192, D=128, G=8, NQ=2, layers=1, backward=True),
+    # one layer's 16-token window at the training shape (run_sh25.sh:223): 4 K/V heads x 128, kv_nq 4 (the
+    # main call plus the 12 extra queries on the same K/V heads), forward + backward
+    "window_train": dict(kind="window", B=64, T=1024, Hk=4, D=128, W=16, NQ=4),
 }
 
 
@@ -239,6 +242,78 @@ def bench_stream(args, W):
     print(json.dumps(out), flush=True)
 
 
+def window_bytes(B, T, Hq, Hk, D):
+    """Algorithmic HBM bytes of one window call: forward q, k, v in, out and the fp32 log-sum-exp out;
+    backward q, k, v, out, dout and the log-sum-exp in, dq, dk, dv out (bf16 tokens)."""
+    row = B * T * D * 2
+    fwd = row * (2 * Hq + 2 * Hk) + B * T * Hq * 4
+    bwd = row * (3 * Hq + 2 * Hk) + B * T * Hq * 4 + row * (Hq + 2 * Hk)
+    return fwd, bwd
+
+
+def bench_window(args, W):
+    """One layer's rolling window (memlm_sh.py:482-492) at the training shape: window(cq, ck, cv) over the
+    Hk K/V heads plus window(cq2, ck, cv) for the Hk (NQ - 1) extra queries, forward and backward."""
+    import torch
+    import slotwin_hip as WH
+    import slotscan_lib as L
+
+    B, T, Hk, D, Wn, NQ = (W[x] for x in ("B", "T", "Hk", "D", "W", "NQ"))
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(6)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=gen).to(torch.bfloat16)
+    view = lambda x: x.transpose(1, 2).requires_grad_()           # (B, T, H, D) viewed as (B, H, T, D)
+    cq, ck, cv = view(rn(B, T, Hk, D)), view(rn(B, T, Hk, D)), view(rn(B, T, Hk, D))
+    cq2 = view(rn(B, T, Hk * (NQ - 1), D))
+    do1, do2 = rn(B, Hk, T, D), rn(B, Hk * (NQ - 1), T, D)
+    leaves = (cq, cq2, ck, cv)
+
+    def step():
+        o1 = WH.window(cq, ck, cv, Wn)
+        o2 = WH.window(cq2, ck, cv, Wn)
+        return torch.autograd.grad((o1, o2), leaves, (do1, do2))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    L.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    L.profile(False)
+    prof = L.profile_read()
+    ms = (t1 - t0) * 1e3 / args.steps
+    f1, b1 = window_bytes(B, T, Hk, Hk, D)
+    f2, b2 = window_bytes(B, T, Hk * (NQ - 1), Hk, D)
+    step_bytes = f1 + b1 + f2 + b2
+    kms = {n: tot / cnt for n, (tot, cnt) in prof.items()}
+    fwd_ms = prof["win_fwd"][0] / args.steps
+    bwd_ms = prof["win_bwd"][0] / args.steps
+    out = {
+        "metric": f"window attention fwd+bwd tokens/s (W{Wn}, {Hk} K/V heads x {D}, kv_nq {NQ}, B{B} T{T})",
+        "value": round(B * T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded GPU generator, seed 6)",
+        "config": {"workload": args.workload, "B": B, "T": T, "Hk": Hk, "Hq": [Hk, Hk * (NQ - 1)], "D": D, "W": Wn,
+                   "tokens_per_step": B * T},
+        "roofline": {"bound": "hbm", "kernel": "win_fwd + win_bwd (step)",
+                     "achieved": round(step_bytes / ((fwd_ms + bwd_ms) * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(step_bytes / ((fwd_ms + bwd_ms) * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "algorithmic_bytes_per_step": step_bytes,
+                     "kernel_ms_per_step": round(fwd_ms + bwd_ms, 4)},
+        "fwd_roofline": {"achieved": round((f1 + f2) / (fwd_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBPS,
+                         "frac": round((f1 + f2) / (fwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                         "algorithmic_bytes": f1 + f2, "ms": round(fwd_ms, 4)},
+        "bwd_roofline": {"achieved": round((b1 + b2) / (bwd_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBPS,
+                         "frac": round((b1 + b2) / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                         "algorithmic_bytes": b1 + b2, "ms": round(bwd_ms, 4)},
+        "kernels_ms": {n: round(x, 4) for n, x in kms.items()},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def bench_read(args, W):
     import torch
     import slotread_hip as RH
@@ -338,6 +413,8 @@ def main():
         return bench_read(args, W)
     if W["kind"] == "stream":
         return bench_stream(args, W)
+    if W["kind"] == "window":
+        return bench_window(args, W)
 
     import torch
     import slotkern_hip as KH
