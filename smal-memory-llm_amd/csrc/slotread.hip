@@ -777,26 +777,50 @@ __global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
                 dr_t[(4 * g + i) * RST + u * 16 + c] = (bf16_t)(v2[i >> 1] >> (16 * (i & 1)));
         }
         wave_lds_sync();
+        // K^T (A: row dim 16dt + c, k = slot 16 nt + 4g + i) goes through this wave's own rows of s_part,
+        // which are free until its partials are written, half the dims at a time: the key rows are read
+        // again as 16-byte loads (cache hits: (b) just read them) and written transposed.  Gathering the
+        // operand as 2-byte loads from the key rows cost more than the rest of the kernel.
+        constexpr int KTS = READ_TPW * 16 + 4;              // K^T row stride (bf16): 8-byte aligned rows
+        constexpr int HD = D / 2;
+        static_assert(HD * KTS * 2 <= 16 * OST * 4, "a K^T half fits the wave's partial rows");
+        bf16_t* kt_w = reinterpret_cast<bf16_t*>(s_part + w * 16 * OST);
+        f32x4 o[DT];
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            f32x4 o = {0.f, 0.f, 0.f, 0.f};
+        for (int dt = 0; dt < DT; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            if (hh) wave_lds_sync();                          // the first half's reads are done
 #pragma unroll
             for (int u = 0; u < READ_TPW; u++) {
-                const int nb = (w * TPW + u) * 16 + 4 * g;       // A: row dim 16dt + c, k = slot nb + i
-                uint32_t e4[4];
+                const int n = (w * TPW + u) * 16 + c;
+                const bool in = tile[u] && n < N;
+                const size_t nc = (size_t)min(n, N - 1) * D;  // clamped address, then select
 #pragma unroll
-                for (int i = 0; i < 4; i++) {                     // clamped address, then select
-                    const uint32_t x = Kb[(size_t)min(nb + i, N - 1) * D + dt * 16 + c];
-                    e4[i] = (tile[u] && nb + i < N) ? x : 0u;
+                for (int k2 = 0; k2 < HD / 32; k2++) {
+                    const uint4 kx = *reinterpret_cast<const uint4*>(Kb + nc + (hh * (HD / 32) + k2) * 32 + 8 * g);
+                    const uint32_t w4[4] = {in ? kx.x : 0u, in ? kx.y : 0u, in ? kx.z : 0u, in ? kx.w : 0u};
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        kt_w[(k2 * 32 + 8 * g + e) * KTS + u * 16 + c] = (bf16_t)(w4[e >> 1] >> (16 * (e & 1)));
                 }
-                uint2 kT;
-                kT.x = e4[0] | (e4[1] << 16);
-                kT.y = e4[2] | (e4[3] << 16);
-                const uint2 drT = *reinterpret_cast<const uint2*>(dr_t + c * RST + u * 16 + 4 * g);   // B: k = slot, column m = c
-                o = mfma_k16(kT, drT, o);
             }
-            *reinterpret_cast<f32x4*>(s_part + (w * 16 + c) * OST + dt * 16 + 4 * g) = o;
+            wave_lds_sync();
+#pragma unroll
+            for (int d2 = 0; d2 < HD / 16; d2++) {
+                const int dt = hh * (HD / 16) + d2;
+#pragma unroll
+                for (int u = 0; u < READ_TPW; u++) {
+                    const uint2 kT = *reinterpret_cast<const uint2*>(kt_w + (d2 * 16 + c) * KTS + u * 16 + 4 * g);
+                    const uint2 drT = *reinterpret_cast<const uint2*>(dr_t + c * RST + u * 16 + 4 * g);   // B: k = slot, column m = c
+                    o[dt] = mfma_k16(kT, drT, o[dt]);
+                }
+            }
         }
+        wave_lds_sync();                                      // every lane's K^T reads are done
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+            *reinterpret_cast<f32x4*>(s_part + (w * 16 + c) * OST + dt * 16 + 4 * g) = o[dt];
         __syncthreads();
         {
             constexpr int EPT = D / 16;
