@@ -291,7 +291,9 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
 template <int D>
 struct WideSmem {
     static constexpr int KST = D + 8;            // key row stride (bf16)
-    static constexpr int VTS = WIDE_NP + 8;      // transposed value row stride (bf16)
+    // Transposed value row stride (bf16): 98 dwords, 2 mod 32 banks, so the 16 rows one 8-byte read
+    // instruction touches (lanes c = 0..15 of a group) fall on 32 distinct banks.
+    static constexpr int VTS = WIDE_NP + 4;
 };
 
 template <int D>
