@@ -117,6 +117,33 @@ int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
                      void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
                      void* stream);
 
+/* General-mode scan: every mode the row-sparse kernels above do not cover -- soft write addresses
+ * (hard = 0), the attached address gradient (detach_addr = 0), DK != DV -- as the reference runs them on its
+ * general Triton scan (gqa25/slotkern_cuda.py:539-542 -> gqa25/slotkern_kvg.py:257-265; forward
+ * slotkern_kvt._kvfwd, backward slotkern_kvg._kvbwd_g).  DK and DV each 64 or 128, N <= SLOTSCAN_MAX_SLOTS.
+ *
+ * slotscan_gen_fwd: the forward of slotkern_kvg._KVScanG (slotkern_kvg.py:210-230).
+ *   kbuf (B, ceil(T/G), H, N, DK), vbuf (.., DV), obuf (B, ceil(T/G), H, N) fp32: the PRE-write state at
+ *   t = 0, G, 2G, ...;  am (B, T, H) int32, hard = 1 only: the row each step wrote (first maximum).
+ * slotscan_gen_bwd: the backward (slotkern_kvg.py:233-253) for the upstream gradients dkbuf, dvbuf (fp32,
+ *   shaped like kbuf, vbuf), from the forward's kbuf, vbuf, obuf and am.  Writes dk, dq (B, T, H, DK),
+ *   dv (B, T, H, DV) in the token dtype, dgate (B, T, H), dfr (fr's shape), dtemp (1).  workspace:
+ *   slotscan_gen_bwd_workspace(B, H, N, DK, DV, G) bytes, 16-byte aligned: the replay scratch (about
+ *   G * N * (DK + DV) fp32 per chain) and the per-chain partials.
+ * Other arguments as in slotscan_fwd / slotscan_bwd. */
+int slotscan_gen_fwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
+                     const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
+                     int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
+                     int hard, float* kbuf, float* vbuf, float* obuf, int32_t* am, void* stream);
+size_t slotscan_gen_bwd_workspace(int64_t B, int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G);
+int slotscan_gen_bwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
+                     const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
+                     int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
+                     int hard, int detach_addr, const float* kbuf, const float* vbuf,
+                     const float* obuf, const int32_t* am, const float* dkbuf, const float* dvbuf,
+                     void* workspace, void* dk, void* dq, void* dv, float* dgate, float* dfr,
+                     float* dtemp, void* stream);
+
 /* Per-kernel timing (the reference's kvu/prof_cuda.py:9-20 wraps each compiled kernel's launch in CUDA
  * events; this is the same facility inside the library).  slotscan_profile(mask): 0 disables timing;
  * otherwise every launch of a kernel whose bit (1 << SLOTSCAN_K_*) is set in mask -- -1 = every kernel --
@@ -136,7 +163,9 @@ int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
 #define SLOTSCAN_K_MEM_BWD 8
 #define SLOTSCAN_K_WIN_FWD 9
 #define SLOTSCAN_K_WIN_BWD 10
-#define SLOTSCAN_NK 12
+#define SLOTSCAN_K_GEN_FWD 11
+#define SLOTSCAN_K_GEN_BWD 12
+#define SLOTSCAN_NK 14
 int slotscan_profile(int enable);
 int slotscan_profile_read(double* total_ms, int64_t* count, int nk);
 

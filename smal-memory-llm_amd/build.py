@@ -13,7 +13,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SOURCES = [os.path.join(HERE, "csrc", f) for f in ("slotscan.hip", "slotread.hip", "slotmem.hip", "slotwin.hip")]
+SOURCES = [os.path.join(HERE, "csrc", f) for f in ("slotscan.hip", "slotread.hip", "slotmem.hip", "slotwin.hip", "slotgen.hip")]
 OUT = os.path.join(HERE, "libslotscan.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

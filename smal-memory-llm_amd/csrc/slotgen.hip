@@ -1,0 +1,757 @@
+// General-mode slot scan for MI355X (gfx950): soft write addresses (hard = false) and the attached address
+// gradient (detach_addr = false), any DK, DV in {64, 128}, N <= 192.  The hard + detached mode has its own
+// row-sparse kernels (slotscan.hip); every other mode runs here, as the reference runs every other mode on
+// its general Triton scan (/root/reference/gqa25/slotkern_cuda.py:539-542 -> slotkern_kvg.py:257-265).
+//
+// Semantics (reference: slotkern_kv.py:66-123; the adjoints of slotkern_kvt.py:157-171 with the stride-G
+// gradient entry of slotkern_kvg.py:165-168).  Per (b, h) chain, state K (N, DK), V (N, DV), o (N) from zero;
+// for t = 0..T-1:
+//   t % G == 0: emit (K, V, o), the PRE-write state
+//   s_n = temp <K_n / max(|K_n|, 1e-6), q_t / max(|q_t|, 1e-6)>,  z_n = s_n - fr_t (occ_bin ? [o_n >= eps] : o_n)
+//   only occupied rows (o_n >= eps) and the lowest-index free row compete
+//   a = softmax(z) (soft) or onehot(argmax z), first maximum wins (hard; the gradient is straight-through
+//   the softmax, slotkern_kv.py:108-110);  w = g_t a
+//   K <- (1-w) K + w k_t,  V <- (1-w) V + w v_t,  o <- (1-w) o + w
+// Backward, per stride-G segment in reverse: replay the segment from its emitted copy into per-chain
+// scratch (the pre-write K, V and five row scalars of every step), then walk it backward:
+//   dw_n = <k_t - K_n, dK_n> + <v_t - V_n, dV_n> + (1 - o_n) do_n
+//   dk_t = sum_n w_n dK_n,  dv_t = sum_n w_n dV_n,  dgate_t = sum_n a_n dw_n
+//   dz_n = a_s,n (g dw_n - sum_m a_s,m g dw_m)                       (a_s the soft address, 0 off the mask)
+//   dfr_t = -sum_n occ_n dz_n,  dtemp += sum_n dz_n s_n / temp,  dq_t = qinv (dqn - qn <qn, dqn>),
+//   dqn = temp sum_n dz_n kn_n  (qinv dqn where |q_t| < 1e-6)
+//   attached address only: dK_n += dz_n kinv_n (temp qn - s_n kn_n)  (temp dz_n kinv_n qn where |K_n| < 1e-6)
+//   carry: dK = (1-w) dK, dV = (1-w) dV, do = (1-w) do - fr_t dz (no -fr dz under occ_bin);
+//   at a segment's first step the emitted copy's gradient (dkbuf, dvbuf) joins dK, dV.
+//
+// gfx950 mapping.  One workgroup of 8 waves per chain; the state lives in registers.  Lane = 4 row-lanes
+// (the wave's 16-lane DPP rows) x 16 dim-lanes: a lane holds RPL rows x DK/16 key dims (and DV/16 value
+// dims), wave w rows w*4*RPL .. (w+1)*4*RPL - 1, so a row dot product is a 16-lane DPP reduction and a sum
+// over rows is a 4-row permlane reduction plus one LDS exchange across the waves.  Each step of the
+// forward (and of the backward's replay) needs one workgroup barrier: every wave posts its (max, sum) of
+// the competing scores, its first free row and its best row to a double-buffered LDS slot, and all waves
+// combine the 8 posts.  Each step of the backward's walk also needs one barrier: the waves post the
+// address-gradient sums and their dk/dv partials; the previous step's dq/dfr/dtemp partials ride along on
+// the same exchange.  The scratch is written and read in 16-byte units, each row by its 16 dim-lanes.
+#include "slot_common.h"
+#include "slotscan.h"
+#include "slot_host.h"
+
+using namespace slot;
+using slothost::fail;
+using slothost::hip_fail;
+using slothost::al16;
+
+namespace {
+
+#define GEN_WAVES 8
+#define GEN_THREADS (64 * GEN_WAVES)
+constexpr float GEN_NORM_EPS = 1e-6f;
+
+struct GenArgs {
+    const void* k; const void* q; const void* v;
+    const float* gate; const float* fr; const float* temp;
+    int frt, T, H, N, G, NB, occ_bin, hard, detach;
+    float eps;
+    float* kbuf; float* vbuf; float* obuf; int32_t* am;          // forward outputs (am: hard only)
+    const float* dkbuf; const float* dvbuf;                       // backward inputs
+    float* scr; int64_t scr_chain;                                 // replay scratch, floats per chain
+    void* dk; void* dq; void* dv; float* dg; float* dfr; float* part;
+};
+
+// ---- token loads (f32 or bf16 tokens, always fp32 registers)
+template <typename TI, int N> __device__ __forceinline__ void ldtok(const TI* p, float* x) {
+    if constexpr (sizeof(TI) == 4) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            const float4 f = ld4(reinterpret_cast<const float*>(p) + i);
+            x[i] = f.x; x[i + 1] = f.y; x[i + 2] = f.z; x[i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            const float4 f = ld4(reinterpret_cast<const bf16_t*>(p) + i);
+            x[i] = f.x; x[i + 1] = f.y; x[i + 2] = f.z; x[i + 3] = f.w;
+        }
+    }
+}
+template <typename TI> __device__ __forceinline__ void sttok4(TI* p, float4 v) {
+    if constexpr (sizeof(TI) == 4) st4(reinterpret_cast<float*>(p), v);
+    else st4(reinterpret_cast<bf16_t*>(p), v);
+}
+
+// The two lanes' copies a permlane swap returns: [0] from the lower 16-lane row (or 32-lane half), [1] from
+// the upper one, at every lane -- so pairs of values swapped separately stay matched.
+__device__ __forceinline__ void swap16(float x, float& lo, float& hi) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    lo = __uint_as_float(p[0]); hi = __uint_as_float(p[1]);
+}
+__device__ __forceinline__ void swap32(float x, float& lo, float& hi) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    lo = __uint_as_float(p[0]); hi = __uint_as_float(p[1]);
+}
+
+// (max, sum of exp(z - max)) of two partial softmax sums; an empty part has sum 0.
+__device__ __forceinline__ void ms_merge(float m0, float s0, float m1, float s1, float& m, float& s) {
+    m = fmaxf(m0, m1);
+    s = (s0 > 0.f ? s0 * __expf(m0 - m) : 0.f) + (s1 > 0.f ? s1 * __expf(m1 - m) : 0.f);
+}
+// Lower (index, value) wins; index INT_MAX = none.
+__device__ __forceinline__ void idx_merge(int i0, float v0, int i1, float v1, int& i, float& v) {
+    const bool lo = i0 <= i1;
+    i = lo ? i0 : i1; v = lo ? v0 : v1;
+}
+// Larger value wins, the lower index on a tie (first maximum); index INT_MAX = none.
+__device__ __forceinline__ void best_merge(float z0, int i0, float z1, int i1, float& z, int& i) {
+    const bool first = (i1 == INT_MAX) || (i0 != INT_MAX && (z0 > z1 || (z0 == z1 && i0 < i1)));
+    z = first ? z0 : z1; i = first ? i0 : i1;
+}
+
+// Sum over the 4 row-lanes (lanes c, c+16, c+32, c+48).
+__device__ __forceinline__ float rows4_sum(float x) { return sum4rows(x); }
+
+// One step's address over the chain: every lane gets its rows' soft address a_s, the address a used for the
+// write (a_s, or the one-hot of `hard_row`), and the winning row of the hard argmax.  xf is the workgroup
+// exchange slot of this step: [wave][8] = {softmax max, sum, first-free index, its z, best z, best index}.
+template <int RPL>
+__device__ __forceinline__ int gen_address(const float (&z)[RPL], const float (&o)[RPL], int nbase, int N,
+                                           float eps, bool hard, int hard_row, float* xf, int w, int lane,
+                                           float (&as)[RPL], float (&ad)[RPL]) {
+    float m = -INFINITY, s = 0.f;
+    int ff = INT_MAX; float zff = 0.f;
+    float bz = 0.f; int bi = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+        const int n = nbase + j;
+        if (n < N && o[j] >= eps) {
+            const float m2 = fmaxf(m, z[j]);
+            s = (s > 0.f ? s * __expf(m - m2) : 0.f) + __expf(z[j] - m2);
+            m = m2;
+            if (bi == INT_MAX || z[j] > bz) { bz = z[j]; bi = n; }
+        } else if (n < N && ff == INT_MAX) {
+            ff = n; zff = z[j];
+        }
+    }
+    // across the 4 row-lanes
+    {
+        float m0, m1, s0, s1, a0, a1, b0, b1, c0, c1, d0, d1;
+        swap16(m, m0, m1); swap16(s, s0, s1); ms_merge(m0, s0, m1, s1, m, s);
+        swap16(__int_as_float(ff), a0, a1); swap16(zff, b0, b1);
+        idx_merge(__float_as_int(a0), b0, __float_as_int(a1), b1, ff, zff);
+        swap16(bz, c0, c1); swap16(__int_as_float(bi), d0, d1);
+        best_merge(c0, __float_as_int(d0), c1, __float_as_int(d1), bz, bi);
+        swap32(m, m0, m1); swap32(s, s0, s1); ms_merge(m0, s0, m1, s1, m, s);
+        swap32(__int_as_float(ff), a0, a1); swap32(zff, b0, b1);
+        idx_merge(__float_as_int(a0), b0, __float_as_int(a1), b1, ff, zff);
+        swap32(bz, c0, c1); swap32(__int_as_float(bi), d0, d1);
+        best_merge(c0, __float_as_int(d0), c1, __float_as_int(d1), bz, bi);
+    }
+    if (lane == 0) {
+        float4* p = reinterpret_cast<float4*>(xf + w * 8);
+        p[0] = make_float4(m, s, __int_as_float(ff), zff);
+        p[1] = make_float4(bz, __int_as_float(bi), 0.f, 0.f);
+    }
+    __syncthreads();
+    float M = -INFINITY, S = 0.f, Z = 0.f, BZ = 0.f;
+    int FF = INT_MAX, BI = INT_MAX;
+#pragma unroll
+    for (int ww = 0; ww < GEN_WAVES; ww++) {
+        const float4 p0 = reinterpret_cast<const float4*>(xf + ww * 8)[0];
+        const float4 p1 = reinterpret_cast<const float4*>(xf + ww * 8)[1];
+        ms_merge(M, S, p0.x, p0.y, M, S);
+        idx_merge(FF, Z, __float_as_int(p0.z), p0.w, FF, Z);
+        best_merge(BZ, BI, p1.x, __float_as_int(p1.y), BZ, BI);
+    }
+    if (FF != INT_MAX) {                      // the first free row competes too
+        ms_merge(M, S, Z, 1.f, M, S);
+        best_merge(BZ, BI, Z, FF, BZ, BI);
+    }
+    const float rS = 1.f / S;
+    const int row = hard ? (hard_row >= 0 ? hard_row : BI) : -1;
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+        const int n = nbase + j;
+        const bool comp = n < N && (o[j] >= eps || n == FF);
+        as[j] = comp ? __expf(z[j] - M) * rS : 0.f;
+        ad[j] = hard ? (n == row ? 1.f : 0.f) : as[j];
+    }
+    return BI;
+}
+
+// Scores of one step: z, the raw scaled cosine s, |K_n| and 1 / max(|q|, 1e-6).
+template <int RPL, int DPK>
+__device__ __forceinline__ void gen_scores(const float (&K)[RPL][DPK], const float (&o)[RPL], const float* qt,
+                                           float temp, float frt, float eps, bool occ_bin, float (&z)[RPL],
+                                           float (&sr)[RPL], float (&kn)[RPL], float& qinv) {
+    float qq = 0.f;
+#pragma unroll
+    for (int i = 0; i < DPK; i++) qq = fmaf(qt[i], qt[i], qq);
+    qq = rowsum16(qq);
+    qinv = 1.f / fmaxf(sqrtf(qq), GEN_NORM_EPS);
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+        float d = 0.f, n2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPK; i++) { d = fmaf(K[j][i], qt[i], d); n2 = fmaf(K[j][i], K[j][i], n2); }
+        d = rowsum16(d);
+        n2 = rowsum16(n2);
+        kn[j] = sqrtf(n2);
+        const float kinv = 1.f / fmaxf(kn[j], GEN_NORM_EPS);
+        sr[j] = temp * (d * kinv * qinv);
+        const float occ = occ_bin ? (o[j] >= eps ? 1.f : 0.f) : o[j];
+        z[j] = sr[j] - frt * occ;
+    }
+}
+
+template <int RPL, int DPK, int DPV>
+__device__ __forceinline__ void gen_update(float (&K)[RPL][DPK], float (&V)[RPL][DPV], float (&o)[RPL],
+                                           const float (&wr)[RPL], const float* kt, const float* vt) {
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+        const float omw = 1.f - wr[j];
+#pragma unroll
+        for (int i = 0; i < DPK; i++) K[j][i] = fmaf(omw, K[j][i], wr[j] * kt[i]);
+#pragma unroll
+        for (int i = 0; i < DPV; i++) V[j][i] = fmaf(omw, V[j][i], wr[j] * vt[i]);
+        o[j] = fmaf(omw, o[j], wr[j]);
+    }
+}
+
+template <int RPL, int DPK, int DPV>
+__device__ __forceinline__ void gen_load_state(const GenArgs& a, int b, int h, int tb, int nbase, int dl,
+                                               float (&K)[RPL][DPK], float (&V)[RPL][DPV], float (&o)[RPL]) {
+    constexpr int DK = DPK * 16, DV = DPV * 16;
+    const size_t base = ((size_t)b * a.NB + tb) * a.H + h;
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+        const int n = nbase + j;
+        const bool ok = n < a.N;
+        const size_t r = base * a.N + (ok ? n : 0);
+#pragma unroll
+        for (int i = 0; i < DPK; i += 4) {
+            const float4 f = ok ? ld4(a.kbuf + r * DK + dl * DPK + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            K[j][i] = f.x; K[j][i + 1] = f.y; K[j][i + 2] = f.z; K[j][i + 3] = f.w;
+        }
+#pragma unroll
+        for (int i = 0; i < DPV; i += 4) {
+            const float4 f = ok ? ld4(a.vbuf + r * DV + dl * DPV + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            V[j][i] = f.x; V[j][i + 1] = f.y; V[j][i + 2] = f.z; V[j][i + 3] = f.w;
+        }
+        o[j] = ok ? a.obuf[r] : 0.f;
+    }
+}
+
+// ------------------------------------------------------------------------------------------- forward
+template <typename TI, int DK, int DV, int RPL>
+__global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
+    constexpr int DPK = DK / 16, DPV = DV / 16, RPW = 4 * RPL;
+    __shared__ __align__(16) float xf[2][GEN_WAVES * 8];
+    const int chain = blockIdx.x, b = chain / a.H, h = chain % a.H;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, dl = lane & 15;
+    const int nbase = w * RPW + (lane >> 4) * RPL;
+    const TI* kp = static_cast<const TI*>(a.k);
+    const TI* qp = static_cast<const TI*>(a.q);
+    const TI* vp = static_cast<const TI*>(a.v);
+    const float temp = a.temp[0];
+    float K[RPL][DPK], V[RPL][DPV], o[RPL];
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+#pragma unroll
+        for (int i = 0; i < DPK; i++) K[j][i] = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPV; i++) V[j][i] = 0.f;
+        o[j] = 0.f;
+    }
+    auto tok = [&](int t) { return ((size_t)b * a.T + t) * a.H + h; };
+    float kt[DPK], qt[DPK], vt[DPV];
+    ldtok<TI, DPK>(kp + tok(0) * DK + dl * DPK, kt);
+    ldtok<TI, DPK>(qp + tok(0) * DK + dl * DPK, qt);
+    ldtok<TI, DPV>(vp + tok(0) * DV + dl * DPV, vt);
+    for (int t = 0; t < a.T; t++) {
+        if (t % a.G == 0) {                   // emit the pre-write state
+            const size_t base = (((size_t)b * a.NB + t / a.G) * a.H + h) * a.N;
+#pragma unroll
+            for (int j = 0; j < RPL; j++) {
+                const int n = nbase + j;
+                if (n < a.N) {
+#pragma unroll
+                    for (int i = 0; i < DPK; i += 4)
+                        st4(a.kbuf + (base + n) * DK + dl * DPK + i, make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]));
+#pragma unroll
+                    for (int i = 0; i < DPV; i += 4)
+                        st4(a.vbuf + (base + n) * DV + dl * DPV + i, make_float4(V[j][i], V[j][i + 1], V[j][i + 2], V[j][i + 3]));
+                    if (dl == 0) a.obuf[base + n] = o[j];
+                }
+            }
+        }
+        const size_t ti = tok(t);
+        const float g = a.gate[ti];
+        const float frt = a.frt ? a.fr[ti] : a.fr[0];
+        float kn_[DPK], qn_[DPK], vn_[DPV];
+        if (t + 1 < a.T) {
+            ldtok<TI, DPK>(kp + tok(t + 1) * DK + dl * DPK, kn_);
+            ldtok<TI, DPK>(qp + tok(t + 1) * DK + dl * DPK, qn_);
+            ldtok<TI, DPV>(vp + tok(t + 1) * DV + dl * DPV, vn_);
+        }
+        float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
+        gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, z, sr, knr, qinv);
+        const int best = gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, -1, xf[t & 1], w, lane, as, ad);
+        if (a.hard && threadIdx.x == 0) a.am[ti] = best;
+#pragma unroll
+        for (int j = 0; j < RPL; j++) wr[j] = g * ad[j];
+        gen_update<RPL, DPK, DPV>(K, V, o, wr, kt, vt);
+        if (t + 1 < a.T) {
+#pragma unroll
+            for (int i = 0; i < DPK; i++) { kt[i] = kn_[i]; qt[i] = qn_[i]; }
+#pragma unroll
+            for (int i = 0; i < DPV; i++) vt[i] = vn_[i];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------- backward
+// Scratch per chain and segment step s: K (NP, DK), V (NP, DV), then five row scalars (NP each): o, a_s,
+// a, s, |K|; then qinv per step.  NP = 32 * RPL.
+template <int DK, int DV, int RPL>
+struct GenScr {
+    static constexpr int NP = 32 * RPL;
+    static constexpr int64_t step = (int64_t)NP * (DK + DV + 5);
+    static int64_t chain(int G) { return step * G + ((G + 3) / 4) * 4; }
+};
+
+template <typename TI, int DK, int DV, int RPL>
+__global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
+    constexpr int DPK = DK / 16, DPV = DV / 16, RPW = 4 * RPL;
+    using SC = GenScr<DK, DV, RPL>;
+    constexpr int NP = SC::NP;
+    constexpr int P1W = DK + DV + 4;          // per wave: dk, dv partials, then {sum a dw, sum a_s g dw}
+    constexpr int P2W = DK + 4;               // per wave: dqn partial, then {sum occ dz, sum dz s}
+    __shared__ __align__(16) float xf[2][GEN_WAVES * 8];
+    __shared__ __align__(16) float p1[2][GEN_WAVES * P1W];
+    __shared__ __align__(16) float p2[2][GEN_WAVES * P2W];
+    const int chain = blockIdx.x, b = chain / a.H, h = chain % a.H;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, dl = lane & 15, rl = lane >> 4;
+    const int nbase = w * RPW + rl * RPL;
+    const TI* kp = static_cast<const TI*>(a.k);
+    const TI* qp = static_cast<const TI*>(a.q);
+    const TI* vp = static_cast<const TI*>(a.v);
+    TI* dkp = static_cast<TI*>(a.dk);
+    TI* dqp = static_cast<TI*>(a.dq);
+    TI* dvp = static_cast<TI*>(a.dv);
+    const float temp = a.temp[0];
+    float* scr = a.scr + (size_t)chain * a.scr_chain;
+    float* scr_qinv = scr + SC::step * a.G;
+    auto tok = [&](int t) { return ((size_t)b * a.T + t) * a.H + h; };
+
+    float dK[RPL][DPK], dV[RPL][DPV], dO[RPL];
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+#pragma unroll
+        for (int i = 0; i < DPK; i++) dK[j][i] = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPV; i++) dV[j][i] = 0.f;
+        dO[j] = 0.f;
+    }
+    float dfr_acc = 0.f, dtemp_acc = 0.f;     // wave 1, every lane the same
+    int pend_t = -1;                          // the walk step whose dq/dfr/dtemp partials are in p2
+    float pend_qinv = 0.f;                    // and its 1 / max(|q|, 1e-6)
+    int par = 0;                              // exchange-slot parity, flipped once per barrier
+
+    // Wave 1 finishes a walk step from the p2 posts: dq_t, dfr_t (per token) and the dfr/dtemp sums.
+    auto finish_q = [&](int t, float qinv, const float* q2) {
+        if (w != 1) return;
+        const size_t ti = tok(t);
+        float qt[DPK];
+        ldtok<TI, DPK>(qp + ti * DK + dl * DPK, qt);
+        float dqn[DPK];
+#pragma unroll
+        for (int i = 0; i < DPK; i++) dqn[i] = 0.f;
+        float sfo = 0.f, sds = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < GEN_WAVES; ww++) {
+#pragma unroll
+            for (int i = 0; i < DPK; i += 4) {
+                const float4 f = *reinterpret_cast<const float4*>(q2 + ww * P2W + dl * DPK + i);
+                dqn[i] += f.x; dqn[i + 1] += f.y; dqn[i + 2] += f.z; dqn[i + 3] += f.w;
+            }
+            sfo += q2[ww * P2W + DK];
+            sds += q2[ww * P2W + DK + 1];
+        }
+        float pr = 0.f, qq = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPK; i++) { pr = fmaf(qt[i] * qinv, dqn[i], pr); qq = fmaf(qt[i], qt[i], qq); }
+        pr = rowsum16(pr);
+        qq = rowsum16(qq);
+        const bool small = sqrtf(qq) < GEN_NORM_EPS;
+        if (rl == 0) {
+            float r[DPK];
+#pragma unroll
+            for (int i = 0; i < DPK; i++) r[i] = small ? qinv * dqn[i] : qinv * (dqn[i] - qt[i] * qinv * pr);
+#pragma unroll
+            for (int i = 0; i < DPK; i += 4)
+                sttok4<TI>(dqp + ti * DK + dl * DPK + i, make_float4(r[i], r[i + 1], r[i + 2], r[i + 3]));
+        }
+        if (a.frt) { if (lane == 0) a.dfr[ti] = -sfo; }
+        else dfr_acc -= sfo;
+        dtemp_acc += sds / temp;
+    };
+
+    for (int tb = a.NB - 1; tb >= 0; tb--) {
+        const int t0 = tb * a.G, t1 = min(t0 + a.G, a.T);
+        // ---- replay the segment from its emitted copy, keeping every step's pre-write state
+        {
+            float K[RPL][DPK], V[RPL][DPV], o[RPL];
+            gen_load_state<RPL, DPK, DPV>(a, b, h, tb, nbase, dl, K, V, o);
+            for (int t = t0; t < t1; t++) {
+                const int s = t - t0;
+                float* sk = scr + SC::step * s;
+                float* sv = sk + NP * DK;
+                float* ss = sv + NP * DV;
+#pragma unroll
+                for (int j = 0; j < RPL; j++) {
+                    const int n = nbase + j;
+#pragma unroll
+                    for (int i = 0; i < DPK; i += 4)
+                        st4(sk + n * DK + dl * DPK + i, make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]));
+#pragma unroll
+                    for (int i = 0; i < DPV; i += 4)
+                        st4(sv + n * DV + dl * DPV + i, make_float4(V[j][i], V[j][i + 1], V[j][i + 2], V[j][i + 3]));
+                }
+                const size_t ti = tok(t);
+                float kt[DPK], qt[DPK], vt[DPV];
+                ldtok<TI, DPK>(kp + ti * DK + dl * DPK, kt);
+                ldtok<TI, DPK>(qp + ti * DK + dl * DPK, qt);
+                ldtok<TI, DPV>(vp + ti * DV + dl * DPV, vt);
+                const float g = a.gate[ti];
+                const float frt = a.frt ? a.fr[ti] : a.fr[0];
+                float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
+                gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, z, sr, knr, qinv);
+                gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, a.hard ? a.am[ti] : -1, xf[par], w, lane, as, ad);
+                par ^= 1;
+                if (dl == 0) {
+#pragma unroll
+                    for (int j = 0; j < RPL; j++) {
+                        const int n = nbase + j;
+                        ss[n] = o[j]; ss[NP + n] = as[j]; ss[2 * NP + n] = ad[j]; ss[3 * NP + n] = sr[j];
+                        ss[4 * NP + n] = knr[j];
+                    }
+                }
+                if (threadIdx.x == 0) scr_qinv[s] = qinv;
+#pragma unroll
+                for (int j = 0; j < RPL; j++) wr[j] = g * ad[j];
+                gen_update<RPL, DPK, DPV>(K, V, o, wr, kt, vt);
+            }
+        }
+        __syncthreads();                      // the replay's scratch is visible to every wave
+        // ---- walk the segment backward
+        for (int t = t1 - 1; t >= t0; t--) {
+            const int s = t - t0;
+            const float* sk = scr + SC::step * s;
+            const float* sv = sk + NP * DK;
+            const float* ss = sv + NP * DV;
+            const size_t ti = tok(t);
+            float K[RPL][DPK], V[RPL][DPV];
+            float o[RPL], as[RPL], ad[RPL], sr[RPL], knr[RPL];
+#pragma unroll
+            for (int j = 0; j < RPL; j++) {
+                const int n = nbase + j;
+#pragma unroll
+                for (int i = 0; i < DPK; i += 4) {
+                    const float4 f = ld4(sk + n * DK + dl * DPK + i);
+                    K[j][i] = f.x; K[j][i + 1] = f.y; K[j][i + 2] = f.z; K[j][i + 3] = f.w;
+                }
+#pragma unroll
+                for (int i = 0; i < DPV; i += 4) {
+                    const float4 f = ld4(sv + n * DV + dl * DPV + i);
+                    V[j][i] = f.x; V[j][i + 1] = f.y; V[j][i + 2] = f.z; V[j][i + 3] = f.w;
+                }
+                o[j] = ss[n]; as[j] = ss[NP + n]; ad[j] = ss[2 * NP + n]; sr[j] = ss[3 * NP + n];
+                knr[j] = ss[4 * NP + n];
+            }
+            float kt[DPK], qt[DPK], vt[DPV];
+            ldtok<TI, DPK>(kp + ti * DK + dl * DPK, kt);
+            ldtok<TI, DPK>(qp + ti * DK + dl * DPK, qt);
+            ldtok<TI, DPV>(vp + ti * DV + dl * DPV, vt);
+            const float g = a.gate[ti];
+            const float frt = a.frt ? a.fr[ti] : a.fr[0];
+            const float qinv = scr_qinv[s];
+
+            // dw per row; dk_t, dv_t partials; the two address sums
+            float dw[RPL], wr[RPL];
+            float pg = 0.f, pa = 0.f;
+#pragma unroll
+            for (int j = 0; j < RPL; j++) {
+                float x = 0.f;
+#pragma unroll
+                for (int i = 0; i < DPK; i++) x = fmaf(kt[i] - K[j][i], dK[j][i], x);
+#pragma unroll
+                for (int i = 0; i < DPV; i++) x = fmaf(vt[i] - V[j][i], dV[j][i], x);
+                x = rowsum16(x);
+                dw[j] = fmaf(1.f - o[j], dO[j], x);
+                wr[j] = g * ad[j];
+                pg = fmaf(ad[j], dw[j], pg);
+                pa = fmaf(as[j], g * dw[j], pa);
+            }
+            pg = rows4_sum(pg);
+            pa = rows4_sum(pa);
+            float* q1 = p1[par];
+            {
+                float pk[DPK], pv[DPV];
+#pragma unroll
+                for (int i = 0; i < DPK; i++) {
+                    float x = 0.f;
+#pragma unroll
+                    for (int j = 0; j < RPL; j++) x = fmaf(wr[j], dK[j][i], x);
+                    pk[i] = rows4_sum(x);
+                }
+#pragma unroll
+                for (int i = 0; i < DPV; i++) {
+                    float x = 0.f;
+#pragma unroll
+                    for (int j = 0; j < RPL; j++) x = fmaf(wr[j], dV[j][i], x);
+                    pv[i] = rows4_sum(x);
+                }
+                if (rl == 0) {
+#pragma unroll
+                    for (int i = 0; i < DPK; i += 4)
+                        *reinterpret_cast<float4*>(q1 + w * P1W + dl * DPK + i) = make_float4(pk[i], pk[i + 1], pk[i + 2], pk[i + 3]);
+#pragma unroll
+                    for (int i = 0; i < DPV; i += 4)
+                        *reinterpret_cast<float4*>(q1 + w * P1W + DK + dl * DPV + i) = make_float4(pv[i], pv[i + 1], pv[i + 2], pv[i + 3]);
+                }
+                if (lane == 0) { q1[w * P1W + DK + DV] = pg; q1[w * P1W + DK + DV + 1] = pa; }
+            }
+            __syncthreads();
+            if (pend_t >= 0) finish_q(pend_t, pend_qinv, p2[par ^ 1]);
+            float SG = 0.f, SA = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < GEN_WAVES; ww++) { SG += q1[ww * P1W + DK + DV]; SA += q1[ww * P1W + DK + DV + 1]; }
+            if (w == 0) {                     // dk_t, dv_t and dgate_t
+                constexpr int CK = DK / 4, CV = DV / 4;
+                if (lane < CK + CV) {
+                    const int off = lane < CK ? 4 * lane : DK + 4 * (lane - CK);
+                    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int ww = 0; ww < GEN_WAVES; ww++) {
+                        const float4 f = *reinterpret_cast<const float4*>(q1 + ww * P1W + off);
+                        r.x += f.x; r.y += f.y; r.z += f.z; r.w += f.w;
+                    }
+                    if (lane < CK) sttok4<TI>(dkp + ti * DK + off, r);
+                    else sttok4<TI>(dvp + ti * DV + (off - DK), r);
+                }
+                if (lane == 0) a.dg[ti] = SG;
+            }
+            // dz and the search-side partials
+            float dz[RPL], kinv[RPL];
+            float sfo = 0.f, sds = 0.f;
+#pragma unroll
+            for (int j = 0; j < RPL; j++) {
+                dz[j] = as[j] * (g * dw[j] - SA);
+                kinv[j] = 1.f / fmaxf(knr[j], GEN_NORM_EPS);
+                const float occ = a.occ_bin ? (o[j] >= a.eps ? 1.f : 0.f) : o[j];
+                sfo = fmaf(occ, dz[j], sfo);
+                sds = fmaf(dz[j], sr[j], sds);
+            }
+            sfo = rows4_sum(sfo);
+            sds = rows4_sum(sds);
+            float* q2 = p2[par];
+            {
+                float pq[DPK];
+#pragma unroll
+                for (int i = 0; i < DPK; i++) {
+                    float x = 0.f;
+#pragma unroll
+                    for (int j = 0; j < RPL; j++) x = fmaf(dz[j] * kinv[j], K[j][i], x);
+                    pq[i] = rows4_sum(temp * x);
+                }
+                if (rl == 0) {
+#pragma unroll
+                    for (int i = 0; i < DPK; i += 4)
+                        *reinterpret_cast<float4*>(q2 + w * P2W + dl * DPK + i) = make_float4(pq[i], pq[i + 1], pq[i + 2], pq[i + 3]);
+                }
+                if (lane == 0) { q2[w * P2W + DK] = sfo; q2[w * P2W + DK + 1] = sds; }
+            }
+            pend_t = t;
+            pend_qinv = qinv;
+            par ^= 1;
+            // carry to the pre-write adjoint
+#pragma unroll
+            for (int j = 0; j < RPL; j++) {
+                const float omw = 1.f - wr[j];
+                if (!a.detach) {
+                    const float c = dz[j] * kinv[j];
+                    const bool small = knr[j] < GEN_NORM_EPS;
+#pragma unroll
+                    for (int i = 0; i < DPK; i++) {
+                        const float qn = qt[i] * qinv;
+                        const float m = small ? c * temp * qn : c * (temp * qn - sr[j] * K[j][i] * kinv[j]);
+                        dK[j][i] = fmaf(omw, dK[j][i], m);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < DPK; i++) dK[j][i] *= omw;
+                }
+#pragma unroll
+                for (int i = 0; i < DPV; i++) dV[j][i] *= omw;
+                dO[j] = a.occ_bin ? omw * dO[j] : fmaf(omw, dO[j], -frt * dz[j]);
+            }
+            if (t == t0) {                    // the emitted copy's gradient enters at the segment's first step
+                const size_t base = (((size_t)b * a.NB + tb) * a.H + h) * a.N;
+#pragma unroll
+                for (int j = 0; j < RPL; j++) {
+                    const int n = nbase + j;
+                    if (n < a.N) {
+#pragma unroll
+                        for (int i = 0; i < DPK; i += 4) {
+                            const float4 f = ld4(a.dkbuf + (base + n) * DK + dl * DPK + i);
+                            dK[j][i] += f.x; dK[j][i + 1] += f.y; dK[j][i + 2] += f.z; dK[j][i + 3] += f.w;
+                        }
+#pragma unroll
+                        for (int i = 0; i < DPV; i += 4) {
+                            const float4 f = ld4(a.dvbuf + (base + n) * DV + dl * DPV + i);
+                            dV[j][i] += f.x; dV[j][i + 1] += f.y; dV[j][i + 2] += f.z; dV[j][i + 3] += f.w;
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();                      // the walk's reads are done before the next replay overwrites
+        if (pend_t >= 0) { finish_q(pend_t, pend_qinv, p2[par ^ 1]); pend_t = -1; }
+    }
+    if (w == 1 && lane == 0) {
+        a.part[2 * chain] = dfr_acc;
+        a.part[2 * chain + 1] = dtemp_acc;
+    }
+}
+
+// dfr (scalar fr) and dtemp: the sums of the per-chain partials, in a fixed order.
+__global__ __launch_bounds__(256) void gen_reduce(const float* part, int chains, int frt, float* dfr, float* dtemp) {
+    __shared__ float sh[2][4];
+    float x = 0.f, y = 0.f;
+    for (int c = threadIdx.x; c < chains; c += 256) { x += part[2 * c]; y += part[2 * c + 1]; }
+    x = wavesum(x);
+    y = wavesum(y);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sh[0][w] = x; sh[1][w] = y; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (!frt) dfr[0] = sh[0][0] + sh[0][1] + sh[0][2] + sh[0][3];
+        dtemp[0] = sh[1][0] + sh[1][1] + sh[1][2] + sh[1][3];
+    }
+}
+
+static int gen_rpl(int64_t N) { return N <= 64 ? 2 : (N <= 128 ? 4 : 6); }
+
+template <typename TI, int DK, int DV>
+static void launch_fwd(int rpl, dim3 grid, hipStream_t st, const GenArgs& a) {
+    if (rpl == 2) slothost::launch(gen_fwd<TI, DK, DV, 2>, grid, dim3(GEN_THREADS), 0, st, a);
+    else if (rpl == 4) slothost::launch(gen_fwd<TI, DK, DV, 4>, grid, dim3(GEN_THREADS), 0, st, a);
+    else slothost::launch(gen_fwd<TI, DK, DV, 6>, grid, dim3(GEN_THREADS), 0, st, a);
+}
+template <typename TI, int DK, int DV>
+static void launch_bwd(int rpl, dim3 grid, hipStream_t st, const GenArgs& a) {
+    if (rpl == 2) slothost::launch(gen_bwd<TI, DK, DV, 2>, grid, dim3(GEN_THREADS), 0, st, a);
+    else if (rpl == 4) slothost::launch(gen_bwd<TI, DK, DV, 4>, grid, dim3(GEN_THREADS), 0, st, a);
+    else slothost::launch(gen_bwd<TI, DK, DV, 6>, grid, dim3(GEN_THREADS), 0, st, a);
+}
+template <typename TI>
+static void dispatch(bool bwd, int64_t DK, int64_t DV, int rpl, dim3 grid, hipStream_t st, const GenArgs& a) {
+    if (DK == 64 && DV == 64) (bwd ? launch_bwd<TI, 64, 64> : launch_fwd<TI, 64, 64>)(rpl, grid, st, a);
+    else if (DK == 64) (bwd ? launch_bwd<TI, 64, 128> : launch_fwd<TI, 64, 128>)(rpl, grid, st, a);
+    else if (DV == 64) (bwd ? launch_bwd<TI, 128, 64> : launch_fwd<TI, 128, 64>)(rpl, grid, st, a);
+    else (bwd ? launch_bwd<TI, 128, 128> : launch_fwd<TI, 128, 128>)(rpl, grid, st, a);
+}
+
+static int64_t scr_chain(int64_t DK, int64_t DV, int rpl, int64_t G) {
+    const int64_t NP = 32 * rpl;
+    return NP * (DK + DV + 5) * G + ((G + 3) / 4) * 4;
+}
+
+}  // namespace
+
+// ======================================================================================== C-ABI
+static int check_gen(int64_t B, int64_t T, int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, int dtype) {
+    if (B < 1 || T < 1 || H < 1 || N < 1 || G < 1) return fail(SLOTSCAN_ERR_SHAPE, "slotscan_gen: B, T, H, N and G must be >= 1");
+    if ((DK != 64 && DK != 128) || (DV != 64 && DV != 128))
+        return fail(SLOTSCAN_ERR_SHAPE, "slotscan_gen: DK and DV must each be 64 or 128");
+    if (N > SLOTSCAN_MAX_SLOTS) return fail(SLOTSCAN_ERR_SHAPE, "slotscan_gen: N exceeds SLOTSCAN_MAX_SLOTS (192)");
+    if (dtype != SLOTSCAN_F32 && dtype != SLOTSCAN_BF16) return fail(SLOTSCAN_ERR_DTYPE, "token dtype must be f32 or bf16");
+    if (B * H > 0x7fffffffLL || T > 0x7fffffffLL || G > 0x7fffffffLL)
+        return fail(SLOTSCAN_ERR_SHAPE, "slotscan_gen: B*H and T must fit in int32");
+    return 0;
+}
+
+extern "C" int slotscan_gen_fwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
+                                const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
+                                int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
+                                int hard, float* kbuf, float* vbuf, float* obuf, int32_t* am, void* stream) {
+    if (int r = check_gen(B, T, H, N, DK, DV, G, dtype)) return r;
+    if (!k || !q || !v || !gate || !fr || !temp || !kbuf || !vbuf || !obuf || (hard && !am))
+        return fail(SLOTSCAN_ERR_NULL, "slotscan_gen_fwd: a required pointer is NULL");
+    if (!al16(k) || !al16(q) || !al16(v) || !al16(kbuf) || !al16(vbuf))
+        return fail(SLOTSCAN_ERR_ALIGN, "slotscan_gen_fwd: k, q, v, kbuf, vbuf must be 16-byte aligned");
+    GenArgs a{};
+    a.k = k; a.q = q; a.v = v; a.gate = gate; a.fr = fr; a.temp = temp;
+    a.frt = fr_per_token != 0; a.T = (int)T; a.H = (int)H; a.N = (int)N; a.G = (int)G;
+    a.NB = (int)((T + G - 1) / G); a.occ_bin = occ_bin != 0; a.hard = hard != 0; a.detach = 1; a.eps = eps;
+    a.kbuf = kbuf; a.vbuf = vbuf; a.obuf = obuf; a.am = am;
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 grid((unsigned)(B * H));
+    hipError_t e;
+    {
+        slothost::Scope sc(SLOTSCAN_K_GEN_FWD, st);
+        if (dtype == SLOTSCAN_BF16) dispatch<bf16_t>(false, DK, DV, gen_rpl(N), grid, st, a);
+        else dispatch<float>(false, DK, DV, gen_rpl(N), grid, st, a);
+        e = hipGetLastError();
+    }
+    return e == hipSuccess ? 0 : hip_fail(e, "gen_fwd launch");
+}
+
+extern "C" size_t slotscan_gen_bwd_workspace(int64_t B, int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G) {
+    const int64_t per = scr_chain(DK, DV, gen_rpl(N), G);
+    const size_t scr = (size_t)B * H * per * sizeof(float);
+    return ((scr + 255) & ~(size_t)255) + (size_t)B * H * 2 * sizeof(float);
+}
+
+extern "C" int slotscan_gen_bwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
+                                const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
+                                int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
+                                int hard, int detach_addr, const float* kbuf, const float* vbuf,
+                                const float* obuf, const int32_t* am, const float* dkbuf, const float* dvbuf,
+                                void* workspace, void* dk, void* dq, void* dv, float* dgate, float* dfr,
+                                float* dtemp, void* stream) {
+    if (int r = check_gen(B, T, H, N, DK, DV, G, dtype)) return r;
+    if (!k || !q || !v || !gate || !fr || !temp || !kbuf || !vbuf || !obuf || (hard && !am) || !dkbuf ||
+        !dvbuf || !workspace || !dk || !dq || !dv || !dgate || !dfr || !dtemp)
+        return fail(SLOTSCAN_ERR_NULL, "slotscan_gen_bwd: a required pointer is NULL");
+    if (!al16(k) || !al16(q) || !al16(v) || !al16(kbuf) || !al16(vbuf) || !al16(dkbuf) || !al16(dvbuf) ||
+        !al16(workspace) || ((uintptr_t)dk & 7u) || ((uintptr_t)dq & 7u) || ((uintptr_t)dv & 7u))
+        return fail(SLOTSCAN_ERR_ALIGN, "slotscan_gen_bwd: 16-byte aligned inputs and workspace, 8-byte aligned dk, dq, dv");
+    const int rpl = gen_rpl(N);
+    GenArgs a{};
+    a.k = k; a.q = q; a.v = v; a.gate = gate; a.fr = fr; a.temp = temp;
+    a.frt = fr_per_token != 0; a.T = (int)T; a.H = (int)H; a.N = (int)N; a.G = (int)G;
+    a.NB = (int)((T + G - 1) / G); a.occ_bin = occ_bin != 0; a.hard = hard != 0; a.detach = detach_addr != 0;
+    a.eps = eps;
+    a.kbuf = const_cast<float*>(kbuf); a.vbuf = const_cast<float*>(vbuf); a.obuf = const_cast<float*>(obuf);
+    a.am = const_cast<int32_t*>(am); a.dkbuf = dkbuf; a.dvbuf = dvbuf;
+    a.scr = (float*)workspace; a.scr_chain = scr_chain(DK, DV, rpl, G);
+    const size_t scr = (size_t)B * H * a.scr_chain * sizeof(float);
+    a.part = (float*)((char*)workspace + ((scr + 255) & ~(size_t)255));
+    a.dk = dk; a.dq = dq; a.dv = dv; a.dg = dgate; a.dfr = dfr;
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e;
+    {
+        slothost::Scope sc(SLOTSCAN_K_GEN_BWD, st);
+        if (dtype == SLOTSCAN_BF16) dispatch<bf16_t>(true, DK, DV, rpl, dim3((unsigned)(B * H)), st, a);
+        else dispatch<float>(true, DK, DV, rpl, dim3((unsigned)(B * H)), st, a);
+        e = hipGetLastError();
+    }
+    if (e != hipSuccess) return hip_fail(e, "gen_bwd launch");
+    {
+        slothost::Scope sc(SLOTSCAN_K_REDUCE, st);
+        slothost::launch(gen_reduce, dim3(1), dim3(256), 0, st, (const float*)a.part, (int)(B * H),
+                         (int)a.frt, dfr, dtemp);
+        e = hipGetLastError();
+    }
+    return e == hipSuccess ? 0 : hip_fail(e, "gen_reduce launch");
+}

@@ -23,9 +23,12 @@ shape; dtemp is 0-d.  A missing upstream gradient is zeros (slotkern_cuda.py:521
 fp32; bf16 token inputs are read as bf16 and their gradients written as bf16 (autograd would cast them to
 the input dtype anyway); other dtypes are cast to fp32 first.
 
-Supported mode: hard=True with detach_addr=True, DK == DV in {64, 128}, N <= 192 -- the model's training
-setting (run_sh25.sh:213, 222-223) and exactly the mode the reference's CUDA kernels cover
-(slotkern_cuda.py:540).  Other modes raise NotImplementedError: there is no Triton or CPU fallback here.
+Modes: hard=True with detach_addr=True and DK == DV in {64, 128} -- the model's training setting
+(run_sh25.sh:213, 222-223) and the mode the reference's CUDA kernels cover (slotkern_cuda.py:540) -- runs
+the row-sparse kernels.  Every other mode (soft addresses, the attached address gradient, DK != DV, each of
+DK and DV in {64, 128}) runs the general-mode kernels (slotscan_gen_fwd / slotscan_gen_bwd), as the
+reference runs it on its general Triton scan (slotkern_cuda.py:539-542).  N <= 192 in both.  Anything else
+raises NotImplementedError: there is no Triton or CPU fallback here.
 """
 import torch
 
@@ -36,12 +39,22 @@ _SUPPORTED_D = (64, 128)
 
 
 def _unsupported(hard, detach_addr, DK, DV, N):
+    """Why the row-sparse kernels (hard + detached address, DK == DV) cannot run this call, or None."""
     if not hard:
-        return "the soft write address (hard=False) is not implemented by the HIP scan"
+        return "the soft write address (hard=False) is not implemented by the row-sparse HIP scan"
     if not detach_addr:
-        return "an attached address gradient (detach_addr=False) is not implemented by the HIP scan"
+        return "an attached address gradient (detach_addr=False) is not implemented by the row-sparse HIP scan"
     if DK != DV or DK not in _SUPPORTED_D:
         return f"the HIP scan needs DK == DV in {_SUPPORTED_D} (got DK={DK}, DV={DV})"
+    if N > L.lib().slotscan_max_slots(DK):
+        return f"the HIP scan supports at most {L.lib().slotscan_max_slots(DK)} slots (got N={N})"
+    return None
+
+
+def _unsupported_gen(DK, DV, N):
+    """Why the general-mode kernels cannot run this call, or None."""
+    if DK not in _SUPPORTED_D or DV not in _SUPPORTED_D:
+        return f"the HIP scan needs DK and DV in {_SUPPORTED_D} (got DK={DK}, DV={DV})"
     if N > L.lib().slotscan_max_slots(DK):
         return f"the HIP scan supports at most {L.lib().slotscan_max_slots(DK)} slots (got N={N})"
     return None
@@ -152,6 +165,58 @@ def _bwd(ctx, grads, mem):
     return dk, dq, dv, dg, dfr, dtemp
 
 
+class _KVScanGenHip(torch.autograd.Function):
+    """Every mode outside hard + detached address (slotkern_kvg._KVScanG, slotkern_kvg.py:208-253): the
+    general-mode kernels, whose backward replays each stride-G segment from its emitted copy."""
+
+    @staticmethod
+    def forward(ctx, k, q, v, gate, fr, temp, N, G, hard, hard_gate, eps, detach_addr, occ_bin):
+        dt, k_, q_, v_, g, fr_, frt, temp_ = _prep(k, q, v, gate, fr, temp, hard_gate)
+        B, T, H, DK = k_.shape
+        DV = v_.shape[-1]
+        NB = (T + G - 1) // G
+        dev = k_.device
+        f32 = torch.float32
+        kbuf = torch.empty(B, NB, H, N, DK, device=dev, dtype=f32)
+        vbuf = torch.empty(B, NB, H, N, DV, device=dev, dtype=f32)
+        obuf = torch.empty(B, NB, H, N, device=dev, dtype=f32)
+        am = torch.empty(B, T, H, device=dev, dtype=torch.int32) if hard else None
+        rc = L.lib().slotscan_gen_fwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
+                                      int(frt), L.ptr(temp_), B, T, H, N, DK, DV, G, float(eps), int(occ_bin),
+                                      int(hard), L.ptr(kbuf), L.ptr(vbuf), L.ptr(obuf), L.ptr(am),
+                                      L.stream_of(dev))
+        L.check(rc, "slotscan_gen_fwd")
+        ctx.save_for_backward(k_, q_, v_, g, fr_, temp_, kbuf, vbuf, obuf, am)
+        ctx.meta = (int(N), int(G), bool(hard), float(eps), bool(detach_addr), bool(occ_bin), frt, dt,
+                    tuple(fr.shape), torch.is_tensor(temp))
+        return kbuf, vbuf
+
+    @staticmethod
+    def backward(ctx, dkbuf, dvbuf):
+        k_, q_, v_, g, fr_, temp_, kbuf, vbuf, obuf, am = ctx.saved_tensors
+        N, G, hard, eps, detach_addr, occ_bin, frt, dt, fr_shape, temp_is_tensor = ctx.meta
+        B, T, H, DK = k_.shape
+        DV = v_.shape[-1]
+        dev = k_.device
+        f32 = torch.float32
+        dkbuf = torch.zeros_like(kbuf) if dkbuf is None else dkbuf.contiguous().to(f32)
+        dvbuf = torch.zeros_like(vbuf) if dvbuf is None else dvbuf.contiguous().to(f32)
+        ws = torch.empty(L.lib().slotscan_gen_bwd_workspace(B, H, N, DK, DV, G), device=dev, dtype=torch.uint8)
+        dk, dq, dv = torch.empty_like(k_), torch.empty_like(q_), torch.empty_like(v_)
+        dg = torch.empty(B, T, H, device=dev, dtype=f32)
+        dfr = torch.empty_like(fr_)
+        dtemp = torch.empty(1, device=dev, dtype=f32)
+        rc = L.lib().slotscan_gen_bwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
+                                      int(frt), L.ptr(temp_), B, T, H, N, DK, DV, G, float(eps), int(occ_bin),
+                                      int(hard), int(detach_addr), L.ptr(kbuf), L.ptr(vbuf), L.ptr(obuf),
+                                      L.ptr(am), L.ptr(dkbuf), L.ptr(dvbuf), L.ptr(ws), L.ptr(dk), L.ptr(dq),
+                                      L.ptr(dv), L.ptr(dg), L.ptr(dfr), L.ptr(dtemp), L.stream_of(dev))
+        L.check(rc, "slotscan_gen_bwd")
+        dfr = dfr.reshape(fr_shape) if not frt else dfr
+        dtemp = dtemp.reshape(()) if temp_is_tensor else None
+        return dk, dq, dv, dg, dfr, dtemp, None, None, None, None, None, None, None
+
+
 class _KVScanMemHip(torch.autograd.Function):
     """The scan with the writer epilogue fused in: forward returns (kb, vb, kinv, valid) directly."""
 
@@ -186,14 +251,17 @@ class _KVScanMemHip(torch.autograd.Function):
 
 def kv_scan_c(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
               nw=None, nwb=None, occ_bin=False):
-    """Hard + detached-address slot scan on gfx950 (the mode slotkern_cuda.kv_scan_c runs on its own kernels,
-    slotkern_cuda.py:536-543).  nw / nwb (the reference's warp counts) are accepted and ignored: the launch
+    """The slot scan on gfx950 in every mode of slotkern_cuda.kv_scan_c (slotkern_cuda.py:536-543): hard +
+    detached address on the row-sparse kernels, every other mode on the general-mode kernels.  nw / nwb (the reference's warp counts) are accepted and ignored: the launch
     shape here is fixed by the gfx950 design, not tuned per call."""
-    why = _unsupported(hard, detach_addr, k.shape[-1], v.shape[-1], N)
+    if _unsupported(hard, detach_addr, k.shape[-1], v.shape[-1], N) is None:
+        return _KVScanHip.apply(k, k if q is None else q, v, gate, fr, temp, N, int(G), bool(hard_gate), eps,
+                                bool(occ_bin))
+    why = _unsupported_gen(k.shape[-1], v.shape[-1], N)
     if why:
         raise NotImplementedError(why)
-    return _KVScanHip.apply(k, k if q is None else q, v, gate, fr, temp, N, int(G), bool(hard_gate), eps,
-                            bool(occ_bin))
+    return _KVScanGenHip.apply(k, k if q is None else q, v, gate, fr, temp, N, int(G), bool(hard), bool(hard_gate),
+                               eps, bool(detach_addr), bool(occ_bin))
 
 
 def kv_scan_mem(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,

@@ -38,6 +38,11 @@ SIGNATURES = {
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "slotscan_bwd_mem": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
                                 _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32] + [_vp] * 19),
+    "slotscan_gen_fwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
+                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32] + [_vp] * 5),
+    "slotscan_gen_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "slotscan_gen_bwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
+                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32] + [_vp] * 14),
     "slotread_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "slotread_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -92,7 +97,7 @@ def dtype_code(dt):
 
 
 KERNEL_NAMES = ("chain_fwd", "rows_fwd", "rows_bwd", "chain_bwd", "reduce_parts", "read_fwd", "read_bwd", "mem_fwd",
-                "mem_bwd", "win_fwd", "win_bwd", "spare")
+                "mem_bwd", "win_fwd", "win_bwd", "gen_fwd", "gen_bwd", "spare")
 
 
 def profile(enable, kernels=None):
