@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Slot-scan fwd+bwd throughput on one MI355X (BASELINE metric, config 2).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config2_mem|config3*|config4|config5|read_train|window_train]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config2_mem|config2_soft|config3*|config4|config5|read_train|window_train]
 
 One step = one hard-address slot scan forward (kv_scan_c) plus its backward (torch.autograd.grad of the two
 snapshot outputs against fixed upstream gradients) over one synthetic batch already resident in HBM:
@@ -12,6 +12,9 @@ N(0,1) drawn in bf16 and passed as fp32 -- all drawn on the GPU from a seeded ge
 
 --workload config2_mem runs the writer layer's scan with its epilogue fused in (kv_scan_mem: bf16 copies,
 kinv, valid) and also times the two-pass path (kv_scan_c then writer_epilogue) on the same inputs.
+
+--workload config2_soft runs the same shape with soft write addresses and the attached address gradient (the
+reference's kv_scan_g defaults, on the general-mode kernels).
 
 --workload config4 measures the read instead: one step = the 6 independent reader-layer reads of the frozen
 store, forward only, with the read kernel's HBM and MFMA fractions.
@@ -43,6 +46,7 @@ WORKLOADS = {
     "config2": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8),
     # the writer layer's scan with its epilogue fused in (bf16 copies, kinv, valid), against the two-pass path
     "config2_mem": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8, mem=True),
+    "config2_soft": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8, soft=True),
     "config3": dict(kind="scan", B=64, T=1024, H=6, N=96, D=128, G=8),
     "config3_t512": dict(kind="scan", B=128, T=512, H=6, N=96, D=128, G=8),
     "config3_t256": dict(kind="scan", B=256, T=256, H=6, N=96, D=128, G=8),
@@ -59,18 +63,27 @@ WORKLOADS = {
 }
 
 
-def algorithmic_bytes(B, T, H, N, D, G, mem=False):
+def algorithmic_bytes(B, T, H, N, D, G, mem=False, soft=False):
     """Per-kernel and per-step algorithmic HBM bytes (inputs read once, outputs written once; logs, Dn and
     staging are implementation choices and are not counted).  Token tensors bf16, snapshots fp32, gate and
     fr bf16 as the caller holds them (the kernels read the fp32 copies the wrapper makes: 4 B each).
     mem: the fused writer epilogue -- bf16 snapshot copies, plus kinv (fp32) and valid (1 B) per key row
-    out and dkinv (fp32) per key row in."""
+    out and dkinv (fp32) per key row in.  soft: the general-mode kernels, whose forward also emits the
+    occupancy snapshot (fp32 per row) and whose backward reads the three snapshots back (the replay
+    scratch is an implementation choice and is not counted)."""
     tok = B * T * H
     NB = (T + G - 1) // G
     rows = B * NB * H * N
     snap = rows * D * (2 if mem else 4)
     kx_f, kx_b = (rows * 5, rows * 4) if mem else (0, 0)
     row = tok * D * 2
+    if soft:
+        per_kernel = {
+            "gen_fwd": 3 * row + 2 * tok * 4 + 2 * snap + rows * 4,
+            "gen_bwd": 3 * row + 2 * tok * 4 + 2 * snap + rows * 4 + 2 * snap + 3 * row + 2 * tok * 4,
+        }
+        step = (3 * row + 2 * tok * 2 + 2 * snap) + (2 * snap + 3 * row + 2 * tok * 2 + 3 * row + 2 * tok * 2)
+        return per_kernel, step
     per_kernel = {
         "chain_fwd": 2 * row + 2 * tok * 4 + snap + kx_f,          # q, k, gate, fr in; kbuf (kinv, valid) out
         "rows_fwd": row + tok * 4 + snap,                          # v, gate in; vbuf out
@@ -130,20 +143,22 @@ def cpu_baseline(W, seed=1, Bs=12):
     dkb = rng.standard_normal((Bs, NB, H, N, D)).astype(f)
     dvb = rng.standard_normal((Bs, NB, H, N, D)).astype(f)
     mem = W.get("mem", False)
+    hard = not W.get("soft", False)
     dki = rng.standard_normal((Bs, NB, H, N)).astype(f)
     t0 = time.perf_counter()
-    kb, vb, info = SO.scan_forward(k, v, g, fr, N, 16.0, G=G, hard=True, q=q, occ_bin=True, dtype=f)
+    kb, vb, info = SO.scan_forward(k, v, g, fr, N, 16.0, G=G, hard=hard, q=q, occ_bin=True, dtype=f)
     if mem:                                  # the epilogue (memlm_sh.py:474-475) and its autograd
         nsq = (kb * kb).sum(-1)
         kinv = 1.0 / np.sqrt(np.maximum(nsq, f(1e-12)))
         valid = nsq > 1e-12                  # (numpy has no bf16: the copies' cast is not timed)
         dkb = dkb + 2 * kb * np.where(nsq >= 1e-12, -0.5 * kinv ** 3 * dki, 0.0).astype(f)[..., None]
-    SO.scan_backward(k, v, g, fr, N, 16.0, kb, vb, info, dkb, dvb, G=G, hard=True, q=q, occ_bin=True,
-                     detach_addr=True, dtype=f)
+    SO.scan_backward(k, v, g, fr, N, 16.0, kb, vb, info, dkb, dvb, G=G, hard=hard, q=q, occ_bin=True,
+                     detach_addr=hard, dtype=f)
     dt = time.perf_counter() - t0
     return dict(value=round(Bs * T / dt, 1), unit="tokens/s", cores=1, kind="port",
                 sample=f"B={Bs} slice of the workload (T={T}, H={H}, N={N}, D={D}, G={G}), fp32 numpy oracle "
-                       f"fwd+bwd{' with the writer epilogue' if mem else ''}, {dt:.1f} s", seconds=round(dt, 2))
+                       f"fwd+bwd{' with the writer epilogue' if mem else ''}{'' if hard else ', soft address, attached'}, "
+                       f"{dt:.1f} s", seconds=round(dt, 2))
 
 
 def cpu_baseline_read(W, seed=3, Bs=32):
@@ -436,7 +451,8 @@ def main():
     dvb = rn(B, NB, H, N, D).to(torch.bfloat16).float()
     inputs = (k, q, v, gate, fr, temp)
     mem = W.get("mem", False)
-    kw = dict(G=G, hard=True, hard_gate=False, detach_addr=True, q=q, occ_bin=True)
+    soft = W.get("soft", False)
+    kw = dict(G=G, hard=not soft, hard_gate=False, detach_addr=not soft, q=q, occ_bin=True)
 
     if mem:
         import slotmem_hip as MH
@@ -465,7 +481,7 @@ def main():
     torch.cuda.synchronize()
     L.profile(False)
     warm = L.profile_read()
-    per_kernel_bytes, step_bytes = algorithmic_bytes(B, T, H, N, D, G, mem=mem)
+    per_kernel_bytes, step_bytes = algorithmic_bytes(B, T, H, N, D, G, mem=mem, soft=soft)
     dom = max((n for n in warm if n in per_kernel_bytes), key=lambda n: warm[n][0] / warm[n][1], default=None)
     L.profile(True, kernels=None if dom is None else [dom])
     t0 = time.perf_counter()
@@ -522,7 +538,8 @@ def main():
         "dtype": "f32 state, bf16 tokens" + (", bf16 copies" if mem else ""),
         "data": "synthetic (seeded GPU generator, seed 1)",
         "config": {"workload": args.workload, "B": B, "T": T, "H": H, "N": N, "D": D, "G": G, "temp": 16.0,
-                   "mode": "hard, detach_addr, occ_bin, per-token fr", "tokens_per_step": tokens},
+                   "mode": ("soft address, attached address gradient" if soft else "hard, detach_addr") +
+                           ", occ_bin, per-token fr", "tokens_per_step": tokens},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": launch_bytes[dom],

@@ -13,7 +13,7 @@
 //   the softmax, slotkern_kv.py:108-110);  w = g_t a
 //   K <- (1-w) K + w k_t,  V <- (1-w) V + w v_t,  o <- (1-w) o + w
 // Backward, per stride-G segment in reverse: replay the segment from its emitted copy into per-chain
-// scratch (the pre-write K, V and five row scalars of every step), then walk it backward:
+// scratch (the pre-write K and seven row scalars of every step), then walk it backward:
 //   dw_n = <k_t - K_n, dK_n> + <v_t - V_n, dV_n> + (1 - o_n) do_n
 //   dk_t = sum_n w_n dK_n,  dv_t = sum_n w_n dV_n,  dgate_t = sum_n a_n dw_n
 //   dz_n = a_s,n (g dw_n - sum_m a_s,m g dw_m)                       (a_s the soft address, 0 off the mask)
@@ -22,6 +22,9 @@
 //   attached address only: dK_n += dz_n kinv_n (temp qn - s_n kn_n)  (temp dz_n kinv_n qn where |K_n| < 1e-6)
 //   carry: dK = (1-w) dK, dV = (1-w) dV, do = (1-w) do - fr_t dz (no -fr dz under occ_bin);
 //   at a segment's first step the emitted copy's gradient (dkbuf, dvbuf) joins dK, dV.
+// Inside a segment dV only scales (dV(t+) = c(t) D, c the product of (1 - w) over the later steps), so the
+// value term of dw is c(t) (<v_t, D> - <V(t), D>), and <V(t), D> follows the forward recurrence from the
+// emitted copy: the value state is never replayed or stored.
 //
 // gfx950 mapping.  One workgroup of 8 waves per chain; the state lives in registers.  Lane = 4 row-lanes
 // (the wave's 16-lane DPP rows) x 16 dim-lanes: a lane holds RPL rows x DK/16 key dims (and DV/16 value
@@ -216,9 +219,12 @@ __device__ __forceinline__ void gen_update(float (&K)[RPL][DPK], float (&V)[RPL]
     }
 }
 
+// The emitted copy of segment tb: keys and occupancy into registers, and per row P = <V_n, D_n> with the
+// value adjoint D (registers dV) that enters the segment's walk.
 template <int RPL, int DPK, int DPV>
-__device__ __forceinline__ void gen_load_state(const GenArgs& a, int b, int h, int tb, int nbase, int dl,
-                                               float (&K)[RPL][DPK], float (&V)[RPL][DPV], float (&o)[RPL]) {
+__device__ __forceinline__ void gen_load_keys(const GenArgs& a, int b, int h, int tb, int nbase, int dl,
+                                              const float (&dV)[RPL][DPV], float (&K)[RPL][DPK], float (&o)[RPL],
+                                              float (&P)[RPL]) {
     constexpr int DK = DPK * 16, DV = DPV * 16;
     const size_t base = ((size_t)b * a.NB + tb) * a.H + h;
 #pragma unroll
@@ -231,11 +237,14 @@ __device__ __forceinline__ void gen_load_state(const GenArgs& a, int b, int h, i
             const float4 f = ok ? ld4(a.kbuf + r * DK + dl * DPK + i) : make_float4(0.f, 0.f, 0.f, 0.f);
             K[j][i] = f.x; K[j][i + 1] = f.y; K[j][i + 2] = f.z; K[j][i + 3] = f.w;
         }
+        float x = 0.f;
 #pragma unroll
         for (int i = 0; i < DPV; i += 4) {
             const float4 f = ok ? ld4(a.vbuf + r * DV + dl * DPV + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            V[j][i] = f.x; V[j][i + 1] = f.y; V[j][i + 2] = f.z; V[j][i + 3] = f.w;
+            x = fmaf(f.x, dV[j][i], x); x = fmaf(f.y, dV[j][i + 1], x);
+            x = fmaf(f.z, dV[j][i + 2], x); x = fmaf(f.w, dV[j][i + 3], x);
         }
+        P[j] = rowsum16(x);
         o[j] = ok ? a.obuf[r] : 0.f;
     }
 }
@@ -309,12 +318,12 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------- backward
-// Scratch per chain and segment step s: K (NP, DK), V (NP, DV), then five row scalars (NP each): o, a_s,
-// a, s, |K|; then qinv per step.  NP = 32 * RPL.
+// Scratch per chain and segment step s: K (NP, DK), then seven row scalars (NP each): o, a_s, a, s, |K|,
+// P = <V, D> and e = <v_t, D>; then qinv per step.  NP = 32 * RPL.
 template <int DK, int DV, int RPL>
 struct GenScr {
     static constexpr int NP = 32 * RPL;
-    static constexpr int64_t step = (int64_t)NP * (DK + DV + 5);
+    static constexpr int64_t step = (int64_t)NP * (DK + 7);
     static int64_t chain(int G) { return step * G + ((G + 3) / 4) * 4; }
 };
 
@@ -399,22 +408,21 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
         const int t0 = tb * a.G, t1 = min(t0 + a.G, a.T);
         // ---- replay the segment from its emitted copy, keeping every step's pre-write state
         {
-            float K[RPL][DPK], V[RPL][DPV], o[RPL];
-            gen_load_state<RPL, DPK, DPV>(a, b, h, tb, nbase, dl, K, V, o);
+            // The value state itself is not replayed: inside a segment the value adjoint only scales,
+            // dV(t+) = c(t) D with D the adjoint entering the segment, so the walk needs just the row
+            // scalars P(t) = <V(t), D> (P <- (1-w) P + w e from the emitted copy) and e(t) = <v_t, D>.
+            float K[RPL][DPK], o[RPL], P[RPL];
+            gen_load_keys<RPL, DPK, DPV>(a, b, h, tb, nbase, dl, dV, K, o, P);
             for (int t = t0; t < t1; t++) {
                 const int s = t - t0;
                 float* sk = scr + SC::step * s;
-                float* sv = sk + NP * DK;
-                float* ss = sv + NP * DV;
+                float* ss = sk + NP * DK;
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
                     const int n = nbase + j;
 #pragma unroll
                     for (int i = 0; i < DPK; i += 4)
                         st4(sk + n * DK + dl * DPK + i, make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]));
-#pragma unroll
-                    for (int i = 0; i < DPV; i += 4)
-                        st4(sv + n * DV + dl * DPV + i, make_float4(V[j][i], V[j][i + 1], V[j][i + 2], V[j][i + 3]));
                 }
                 const size_t ti = tok(t);
                 float kt[DPK], qt[DPK], vt[DPV];
@@ -427,30 +435,46 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, z, sr, knr, qinv);
                 gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, a.hard ? a.am[ti] : -1, xf[par], w, lane, as, ad);
                 par ^= 1;
+                float e[RPL];
+#pragma unroll
+                for (int j = 0; j < RPL; j++) {
+                    float x = 0.f;
+#pragma unroll
+                    for (int i = 0; i < DPV; i++) x = fmaf(vt[i], dV[j][i], x);
+                    e[j] = rowsum16(x);
+                }
                 if (dl == 0) {
 #pragma unroll
                     for (int j = 0; j < RPL; j++) {
                         const int n = nbase + j;
                         ss[n] = o[j]; ss[NP + n] = as[j]; ss[2 * NP + n] = ad[j]; ss[3 * NP + n] = sr[j];
-                        ss[4 * NP + n] = knr[j];
+                        ss[4 * NP + n] = knr[j]; ss[5 * NP + n] = P[j]; ss[6 * NP + n] = e[j];
                     }
                 }
                 if (threadIdx.x == 0) scr_qinv[s] = qinv;
 #pragma unroll
-                for (int j = 0; j < RPL; j++) wr[j] = g * ad[j];
-                gen_update<RPL, DPK, DPV>(K, V, o, wr, kt, vt);
+                for (int j = 0; j < RPL; j++) {
+                    wr[j] = g * ad[j];
+                    const float omw = 1.f - wr[j];
+#pragma unroll
+                    for (int i = 0; i < DPK; i++) K[j][i] = fmaf(omw, K[j][i], wr[j] * kt[i]);
+                    o[j] = fmaf(omw, o[j], wr[j]);
+                    P[j] = fmaf(omw, P[j], wr[j] * e[j]);
+                }
             }
         }
         __syncthreads();                      // the replay's scratch is visible to every wave
         // ---- walk the segment backward
+        float cV[RPL];                        // dV(t+) = cV D: the product of (1 - w) over the steps walked
+#pragma unroll
+        for (int j = 0; j < RPL; j++) cV[j] = 1.f;
         for (int t = t1 - 1; t >= t0; t--) {
             const int s = t - t0;
             const float* sk = scr + SC::step * s;
-            const float* sv = sk + NP * DK;
-            const float* ss = sv + NP * DV;
+            const float* ss = sk + NP * DK;
             const size_t ti = tok(t);
-            float K[RPL][DPK], V[RPL][DPV];
-            float o[RPL], as[RPL], ad[RPL], sr[RPL], knr[RPL];
+            float K[RPL][DPK];
+            float o[RPL], as[RPL], ad[RPL], sr[RPL], knr[RPL], Pv[RPL], ev[RPL];
 #pragma unroll
             for (int j = 0; j < RPL; j++) {
                 const int n = nbase + j;
@@ -459,18 +483,12 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                     const float4 f = ld4(sk + n * DK + dl * DPK + i);
                     K[j][i] = f.x; K[j][i + 1] = f.y; K[j][i + 2] = f.z; K[j][i + 3] = f.w;
                 }
-#pragma unroll
-                for (int i = 0; i < DPV; i += 4) {
-                    const float4 f = ld4(sv + n * DV + dl * DPV + i);
-                    V[j][i] = f.x; V[j][i + 1] = f.y; V[j][i + 2] = f.z; V[j][i + 3] = f.w;
-                }
                 o[j] = ss[n]; as[j] = ss[NP + n]; ad[j] = ss[2 * NP + n]; sr[j] = ss[3 * NP + n];
-                knr[j] = ss[4 * NP + n];
+                knr[j] = ss[4 * NP + n]; Pv[j] = ss[5 * NP + n]; ev[j] = ss[6 * NP + n];
             }
-            float kt[DPK], qt[DPK], vt[DPV];
+            float kt[DPK], qt[DPK];
             ldtok<TI, DPK>(kp + ti * DK + dl * DPK, kt);
             ldtok<TI, DPK>(qp + ti * DK + dl * DPK, qt);
-            ldtok<TI, DPV>(vp + ti * DV + dl * DPV, vt);
             const float g = a.gate[ti];
             const float frt = a.frt ? a.fr[ti] : a.fr[0];
             const float qinv = scr_qinv[s];
@@ -483,9 +501,8 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 float x = 0.f;
 #pragma unroll
                 for (int i = 0; i < DPK; i++) x = fmaf(kt[i] - K[j][i], dK[j][i], x);
-#pragma unroll
-                for (int i = 0; i < DPV; i++) x = fmaf(vt[i] - V[j][i], dV[j][i], x);
                 x = rowsum16(x);
+                x = fmaf(cV[j], ev[j] - Pv[j], x);      // <v_t - V(t), dV(t+)>
                 dw[j] = fmaf(1.f - o[j], dO[j], x);
                 wr[j] = g * ad[j];
                 pg = fmaf(ad[j], dw[j], pg);
@@ -592,6 +609,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 }
 #pragma unroll
                 for (int i = 0; i < DPV; i++) dV[j][i] *= omw;
+                cV[j] *= omw;
                 dO[j] = a.occ_bin ? omw * dO[j] : fmaf(omw, dO[j], -frt * dz[j]);
             }
             if (t == t0) {                    // the emitted copy's gradient enters at the segment's first step
@@ -663,7 +681,8 @@ static void dispatch(bool bwd, int64_t DK, int64_t DV, int rpl, dim3 grid, hipSt
 
 static int64_t scr_chain(int64_t DK, int64_t DV, int rpl, int64_t G) {
     const int64_t NP = 32 * rpl;
-    return NP * (DK + DV + 5) * G + ((G + 3) / 4) * 4;
+    (void)DV;
+    return NP * (DK + 7) * G + ((G + 3) / 4) * 4;
 }
 
 }  // namespace
