@@ -20,8 +20,9 @@
  *     forward computed it, so the backward rebuilds the forward's soft address without recomputing scores.
  *   - Return value: 0 on success, else one of the SLOTSCAN_ERR_* codes; slotscan_last_error() then holds a
  *     message (per calling thread).
- *   - Semantics: hard address, detached address gradient (slotkern_cuda.py:536-543); hard_gate is applied by
- *     the caller by passing the binarised gate (slotkern_cuda.py:490).
+ *   - Semantics: slotscan_fwd / slotscan_bwd (and the _mem pair): hard address, detached address gradient,
+ *     DK == DV (slotkern_cuda.py:536-543); slotscan_gen_fwd / slotscan_gen_bwd: every other mode.  hard_gate
+ *     is applied by the caller by passing the binarised gate (slotkern_cuda.py:490).
  */
 #ifndef SLOTSCAN_H
 #define SLOTSCAN_H
