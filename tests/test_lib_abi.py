@@ -30,6 +30,26 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert n in L.SIGNATURES, f"{n} has no ctypes signature in slotscan_lib"
 
 
+def _declared_arity():
+    """name -> number of parameters, from every prototype in include/*.h."""
+    out = {}
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        txt = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(slot\w+)\s*\(([^)]*)\)\s*;", txt, flags=re.M):
+            params = m.group(2).strip()
+            out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_ctypes_signatures_match_the_prototypes():
+    """Every binding in slotscan_lib passes exactly as many arguments as the C prototype takes: a missing or
+    extra pointer would shift every later argument of the call."""
+    arity = _declared_arity()
+    assert set(arity) == set(_declared())
+    for name, n in arity.items():
+        assert len(L.SIGNATURES[name][1]) == n, f"{name}: ctypes binds {len(L.SIGNATURES[name][1])} args, C has {n}"
+
+
 def test_single_hip_runtime_in_process():
     """The library binds to the HIP runtime torch already loaded (same SONAME), not a second copy."""
     L.lib()
