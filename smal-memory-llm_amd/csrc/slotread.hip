@@ -275,7 +275,7 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
 // ------------------------------------------------------------------------------------ wide query blocks
 // Blocks with many queries (the frozen-store fan-out: one block of T*NQ queries per head) invert the split:
 // the workgroup stages the block's keys (row-major) and values (TRANSPOSED, slot-contiguous) in LDS once,
-// and each of its 8 waves owns whole 16-query tiles against ALL slots, so the softmax is wave-local (no
+// and each of its 16 waves owns whole 16-query tiles against ALL slots, so the softmax is wave-local (no
 // workgroup barrier after staging).  Per tile and wave:
 //   S^T = K Q^T     12 x D/32 MFMA 16x16x32, A = key rows from LDS (16 B per lane), B = queries from HBM
 //                   (loaded one tile ahead);
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
 //                   4g+i of tile 2c and 16+4g+i of tile 2c+1 as the 8 k-slots of lane group g), A = the
 //                   same 8 slots of one value dimension, two 8-byte reads from the transposed LDS copy;
 //   store           4 consecutive dims of one query per lane and tile (8 bytes), token-major.
-#define WIDE_WAVES 8
+#define WIDE_WAVES 16
 #define WIDE_THREADS (64 * WIDE_WAVES)
 #define WIDE_NP 192                              // staged slots (N rounded up to 32, at most 192)
 
@@ -324,12 +324,12 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
 
     // ---- stage keys, transposed values and kinv/valid (rows >= N are zero / invalid)
     {
-        constexpr int KCH = WIDE_NP * (D / 8) / WIDE_THREADS;           // 16-byte key chunks per thread
-        static_assert(KCH * WIDE_THREADS == WIDE_NP * (D / 8), "key staging must cover every chunk");
+        constexpr int KTOT = WIDE_NP * (D / 8);
+        constexpr int KCH = (KTOT + WIDE_THREADS - 1) / WIDE_THREADS;  // 16-byte key chunks per thread
         uint4 xk[KCH];
 #pragma unroll
         for (int it = 0; it < KCH; it++) {
-            const int e = threadIdx.x + WIDE_THREADS * it;
+            const int e = min(threadIdx.x + WIDE_THREADS * it, KTOT - 1);
             const int n = e / (D / 8), cc = e % (D / 8);
             xk[it] = n < N ? *reinterpret_cast<const uint4*>(Kb + (size_t)n * D + cc * 8) : make_uint4(0, 0, 0, 0);
         }
@@ -358,6 +358,7 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
 #pragma unroll
         for (int it = 0; it < KCH; it++) {
             const int e = threadIdx.x + WIDE_THREADS * it;
+            if (e >= KTOT) break;
             const int n = e / (D / 8), cc = e % (D / 8);
             *reinterpret_cast<uint4*>(sK + n * KST + cc * 8) = xk[it];
         }
@@ -930,7 +931,7 @@ extern "C" int slotread_fwd(const void* q, const void* kbuf, const void* vbuf, c
     {
         slothost::Scope sc(SLOTSCAN_K_READ_FWD, st);
         if (G * NQ >= READ_WIDE_MIN_M) {
-            // many queries per block: each workgroup takes a range of whole 16-query tiles for its 8 waves
+            // many queries per block: each workgroup takes a range of whole 16-query tiles for its 16 waves
             const int64_t tiles = (G * NQ + 15) / 16;
             int64_t split = (READ_WIDE_TARGET_WGS + slabs - 1) / slabs;
             if (split > (tiles + WIDE_WAVES - 1) / WIDE_WAVES) split = (tiles + WIDE_WAVES - 1) / WIDE_WAVES;
