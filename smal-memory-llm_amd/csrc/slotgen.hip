@@ -220,10 +220,10 @@ __device__ __forceinline__ void gen_update(float (&K)[RPL][DPK], float (&V)[RPL]
 }
 
 // The emitted copy of segment tb: keys and occupancy into registers, and per row P = <V_n, D_n> with the
-// value adjoint D (registers dV) that enters the segment's walk.
+// value adjoint D that enters the segment's walk (this lane's rows at dvr + j * DV, in LDS).
 template <int RPL, int DPK, int DPV>
 __device__ __forceinline__ void gen_load_keys(const GenArgs& a, int b, int h, int tb, int nbase, int dl,
-                                              const float (&dV)[RPL][DPV], float (&K)[RPL][DPK], float (&o)[RPL],
+                                              const float* dvr, float (&K)[RPL][DPK], float (&o)[RPL],
                                               float (&P)[RPL]) {
     constexpr int DK = DPK * 16, DV = DPV * 16;
     const size_t base = ((size_t)b * a.NB + tb) * a.H + h;
@@ -241,8 +241,8 @@ __device__ __forceinline__ void gen_load_keys(const GenArgs& a, int b, int h, in
 #pragma unroll
         for (int i = 0; i < DPV; i += 4) {
             const float4 f = ok ? ld4(a.vbuf + r * DV + dl * DPV + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            x = fmaf(f.x, dV[j][i], x); x = fmaf(f.y, dV[j][i + 1], x);
-            x = fmaf(f.z, dV[j][i + 2], x); x = fmaf(f.w, dV[j][i + 3], x);
+            const float4 d = *reinterpret_cast<const float4*>(dvr + j * DV + i);
+            x = fmaf(f.x, d.x, x); x = fmaf(f.y, d.y, x); x = fmaf(f.z, d.z, x); x = fmaf(f.w, d.w, x);
         }
         P[j] = rowsum16(x);
         o[j] = ok ? a.obuf[r] : 0.f;
@@ -351,13 +351,18 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
     float* scr_qinv = scr + SC::step * a.G;
     auto tok = [&](int t) { return ((size_t)b * a.T + t) * a.H + h; };
 
-    float dK[RPL][DPK], dV[RPL][DPV], dO[RPL];
+    // The value adjoint lives in LDS: inside a segment it only scales, dV(t+) = cV(t) D, so the walk reads
+    // D and keeps the per-row factors cV in registers; D is rewritten once per segment (at its first step).
+    // Each lane reads and writes only its own rows and dims.
+    __shared__ __align__(16) float sD[NP * DV];
+    float* dvr = sD + nbase * DV + dl * DPV;
+    float dK[RPL][DPK], dO[RPL];
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
 #pragma unroll
         for (int i = 0; i < DPK; i++) dK[j][i] = 0.f;
 #pragma unroll
-        for (int i = 0; i < DPV; i++) dV[j][i] = 0.f;
+        for (int i = 0; i < DPV; i += 4) *reinterpret_cast<float4*>(dvr + j * DV + i) = make_float4(0.f, 0.f, 0.f, 0.f);
         dO[j] = 0.f;
     }
     float dfr_acc = 0.f, dtemp_acc = 0.f;     // wave 1, every lane the same
@@ -412,7 +417,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             // dV(t+) = c(t) D with D the adjoint entering the segment, so the walk needs just the row
             // scalars P(t) = <V(t), D> (P <- (1-w) P + w e from the emitted copy) and e(t) = <v_t, D>.
             float K[RPL][DPK], o[RPL], P[RPL];
-            gen_load_keys<RPL, DPK, DPV>(a, b, h, tb, nbase, dl, dV, K, o, P);
+            gen_load_keys<RPL, DPK, DPV>(a, b, h, tb, nbase, dl, dvr, K, o, P);
             for (int t = t0; t < t1; t++) {
                 const int s = t - t0;
                 float* sk = scr + SC::step * s;
@@ -440,7 +445,11 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 for (int j = 0; j < RPL; j++) {
                     float x = 0.f;
 #pragma unroll
-                    for (int i = 0; i < DPV; i++) x = fmaf(vt[i], dV[j][i], x);
+                    for (int i = 0; i < DPV; i += 4) {
+                        const float4 d = *reinterpret_cast<const float4*>(dvr + j * DV + i);
+                        x = fmaf(vt[i], d.x, x); x = fmaf(vt[i + 1], d.y, x);
+                        x = fmaf(vt[i + 2], d.z, x); x = fmaf(vt[i + 3], d.w, x);
+                    }
                     e[j] = rowsum16(x);
                 }
                 if (dl == 0) {
@@ -521,11 +530,15 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                     pk[i] = rows4_sum(x);
                 }
 #pragma unroll
-                for (int i = 0; i < DPV; i++) {
-                    float x = 0.f;
+                for (int i = 0; i < DPV; i += 4) {             // dV(t+) = cV D
+                    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-                    for (int j = 0; j < RPL; j++) x = fmaf(wr[j], dV[j][i], x);
-                    pv[i] = rows4_sum(x);
+                    for (int j = 0; j < RPL; j++) {
+                        const float c = wr[j] * cV[j];
+                        const float4 d = *reinterpret_cast<const float4*>(dvr + j * DV + i);
+                        x.x = fmaf(c, d.x, x.x); x.y = fmaf(c, d.y, x.y); x.z = fmaf(c, d.z, x.z); x.w = fmaf(c, d.w, x.w);
+                    }
+                    pv[i] = rows4_sum(x.x); pv[i + 1] = rows4_sum(x.y); pv[i + 2] = rows4_sum(x.z); pv[i + 3] = rows4_sum(x.w);
                 }
                 if (rl == 0) {
 #pragma unroll
@@ -607,8 +620,6 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
 #pragma unroll
                     for (int i = 0; i < DPK; i++) dK[j][i] *= omw;
                 }
-#pragma unroll
-                for (int i = 0; i < DPV; i++) dV[j][i] *= omw;
                 cV[j] *= omw;
                 dO[j] = a.occ_bin ? omw * dO[j] : fmaf(omw, dO[j], -frt * dz[j]);
             }
@@ -617,17 +628,20 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
                     const int n = nbase + j;
-                    if (n < a.N) {
+                    const bool ok = n < a.N;
+                    if (ok) {
 #pragma unroll
                         for (int i = 0; i < DPK; i += 4) {
                             const float4 f = ld4(a.dkbuf + (base + n) * DK + dl * DPK + i);
                             dK[j][i] += f.x; dK[j][i + 1] += f.y; dK[j][i + 2] += f.z; dK[j][i + 3] += f.w;
                         }
+                    }
 #pragma unroll
-                        for (int i = 0; i < DPV; i += 4) {
-                            const float4 f = ld4(a.dvbuf + (base + n) * DV + dl * DPV + i);
-                            dV[j][i] += f.x; dV[j][i + 1] += f.y; dV[j][i + 2] += f.z; dV[j][i + 3] += f.w;
-                        }
+                    for (int i = 0; i < DPV; i += 4) {      // the next segment's D = cV D + dvbuf
+                        float4* d = reinterpret_cast<float4*>(dvr + j * DV + i);
+                        const float4 f = ok ? ld4(a.dvbuf + (base + n) * DV + dl * DPV + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                        const float4 x = *d;
+                        *d = make_float4(fmaf(cV[j], x.x, f.x), fmaf(cV[j], x.y, f.y), fmaf(cV[j], x.z, f.z), fmaf(cV[j], x.w, f.w));
                     }
                 }
             }
