@@ -13,7 +13,7 @@
 //   the softmax, slotkern_kv.py:108-110);  w = g_t a
 //   K <- (1-w) K + w k_t,  V <- (1-w) V + w v_t,  o <- (1-w) o + w
 // Backward, per stride-G segment in reverse: replay the segment from its emitted copy into per-chain
-// scratch (the pre-write K and seven row scalars of every step), then walk it backward:
+// scratch (the pre-write K and six row scalars of every step), then walk it backward:
 //   dw_n = <k_t - K_n, dK_n> + <v_t - V_n, dV_n> + (1 - o_n) do_n
 //   dk_t = sum_n w_n dK_n,  dv_t = sum_n w_n dV_n,  dgate_t = sum_n a_n dw_n
 //   dz_n = a_s,n (g dw_n - sum_m a_s,m g dw_m)                       (a_s the soft address, 0 off the mask)
@@ -318,12 +318,12 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------- backward
-// Scratch per chain and segment step s: K (NP, DK), then seven row scalars (NP each): o, a_s, a, s, |K|,
-// P = <V, D> and e = <v_t, D>; then qinv per step.  NP = 32 * RPL.
+// Scratch per chain and segment step s: K (NP, DK), then six row scalars (NP each): o, a_s, a, s, |K| and
+// e - P = <v_t, D> - <V, D>; then qinv per step.  NP = 32 * RPL.
 template <int DK, int DV, int RPL>
 struct GenScr {
     static constexpr int NP = 32 * RPL;
-    static constexpr int64_t step = (int64_t)NP * (DK + 7);
+    static constexpr int64_t step = (int64_t)NP * (DK + 6);
     static int64_t chain(int G) { return step * G + ((G + 3) / 4) * 4; }
 };
 
@@ -457,7 +457,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                     for (int j = 0; j < RPL; j++) {
                         const int n = nbase + j;
                         ss[n] = o[j]; ss[NP + n] = as[j]; ss[2 * NP + n] = ad[j]; ss[3 * NP + n] = sr[j];
-                        ss[4 * NP + n] = knr[j]; ss[5 * NP + n] = P[j]; ss[6 * NP + n] = e[j];
+                        ss[4 * NP + n] = knr[j]; ss[5 * NP + n] = e[j] - P[j];
                     }
                 }
                 if (threadIdx.x == 0) scr_qinv[s] = qinv;
@@ -483,7 +483,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             const float* ss = sk + NP * DK;
             const size_t ti = tok(t);
             float K[RPL][DPK];
-            float o[RPL], as[RPL], ad[RPL], sr[RPL], knr[RPL], Pv[RPL], ev[RPL];
+            float o[RPL], as[RPL], ad[RPL], sr[RPL], knr[RPL], ep[RPL];
 #pragma unroll
             for (int j = 0; j < RPL; j++) {
                 const int n = nbase + j;
@@ -493,7 +493,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                     K[j][i] = f.x; K[j][i + 1] = f.y; K[j][i + 2] = f.z; K[j][i + 3] = f.w;
                 }
                 o[j] = ss[n]; as[j] = ss[NP + n]; ad[j] = ss[2 * NP + n]; sr[j] = ss[3 * NP + n];
-                knr[j] = ss[4 * NP + n]; Pv[j] = ss[5 * NP + n]; ev[j] = ss[6 * NP + n];
+                knr[j] = ss[4 * NP + n]; ep[j] = ss[5 * NP + n];
             }
             float kt[DPK], qt[DPK];
             ldtok<TI, DPK>(kp + ti * DK + dl * DPK, kt);
@@ -511,7 +511,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
 #pragma unroll
                 for (int i = 0; i < DPK; i++) x = fmaf(kt[i] - K[j][i], dK[j][i], x);
                 x = rowsum16(x);
-                x = fmaf(cV[j], ev[j] - Pv[j], x);      // <v_t - V(t), dV(t+)>
+                x = fmaf(cV[j], ep[j], x);              // <v_t - V(t), dV(t+)> = cV (e - P)
                 dw[j] = fmaf(1.f - o[j], dO[j], x);
                 wr[j] = g * ad[j];
                 pg = fmaf(ad[j], dw[j], pg);
@@ -696,7 +696,7 @@ static void dispatch(bool bwd, int64_t DK, int64_t DV, int rpl, dim3 grid, hipSt
 static int64_t scr_chain(int64_t DK, int64_t DV, int rpl, int64_t G) {
     const int64_t NP = 32 * rpl;
     (void)DV;
-    return NP * (DK + 7) * G + ((G + 3) / 4) * 4;
+    return NP * (DK + 6) * G + ((G + 3) / 4) * 4;
 }
 
 }  // namespace
