@@ -111,6 +111,8 @@ CASES = [  # B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg
     (2, 10, 2, 40, 64, 128, 5, True, False, False, False, True, False),     # hard, attached, scalar fr
     (1, 75, 3, 40, 64, 128, 8, True, True, False, False, True, False),      # hard, detached, DK != DV, T % G != 0
     (1, 5, 2, 20, 128, 128, 8, False, False, True, False, True, False),     # T < G
+    (2, 1, 1, 1, 64, 64, 1, False, False, True, False, True, False),        # T = 1, N = 1, G = 1
+    (1, 40, 2, 7, 64, 64, 1, False, False, True, True, True, True),         # G = 1 (every step emitted)
 ]
 
 
@@ -141,3 +143,22 @@ def test_gen_scan_refuses_unsupported():
         KH.kv_scan_c(k, v, g, fr, 400, TEMP, G=8, hard=False, detach_addr=True, q=q)
     with pytest.raises(NotImplementedError):
         KH.kv_scan_c(k, v[..., :32].contiguous(), g, fr, 16, TEMP, G=8, hard=False, q=q)
+
+
+def test_scan_kv_defaults_match_oracle():
+    """The reference's default call, scan_kv(k, v, gate, fr, N, temp) (slotkern_kv.py:29-41): G = 1, soft
+    address, attached address gradient, q = k, scalar fr."""
+    B, T, H, N, D = 1, 24, 2, 12, 64
+    k, _, v, g, fr = scan_inputs(B, T, H, D, 9, sep_q=False, frt=False)
+    wk, wv = upstream((B, T, H, N, D), 77)
+    kk, vv, gg, ff = (x.to(DEV).requires_grad_() for x in (k, v, g, fr))
+    kb, vb = KH.scan_kv(kk, vv, gg, ff, N, TEMP)
+    ((kb * wk.to(DEV)).sum() + (vb * wv.to(DEV)).sum()).backward()
+    torch.cuda.synchronize()
+    okb, ovb, info = SO.scan_forward(np64(k), np64(v), np64(g), np64(fr), N, TEMP, G=1)
+    ogr = SO.scan_backward(np64(k), np64(v), np64(g), np64(fr), N, TEMP, okb, ovb, info, np64(wk), np64(wv), G=1)
+    assert _rel(kb.detach().cpu(), okb) < 1e-5 and _rel(vb.detach().cpu(), ovb) < 1e-5
+    for name, got, ref in (("dk", kk.grad, ogr["dk"] + ogr["dq"]), ("dv", vv.grad, ogr["dv"]),
+                           ("dgate", gg.grad, ogr["dgate"]), ("dfr", ff.grad, ogr["dfr"])):
+        e = _rel(got.detach().double().cpu().numpy().reshape(np.shape(ref)), ref)
+        assert e < 1e-4, f"{name} rel err {e:.3e}"
