@@ -125,7 +125,10 @@ int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
  *
  * slotscan_gen_fwd: the forward of slotkern_kvg._KVScanG (slotkern_kvg.py:210-230).
  *   kbuf (B, ceil(T/G), H, N, DK), vbuf (.., DV), obuf (B, ceil(T/G), H, N) fp32: the PRE-write state at
- *   t = 0, G, 2G, ...;  am (B, T, H) int32, hard = 1 only: the row each step wrote (first maximum).
+ *   t = 0, G, 2G, ...;  am (B, T, H) int32, hard = 1 only: the row each step wrote (first maximum);
+ *   wb (B, T, H, N) fp32 or NULL: every step's write distribution before the gate (one-hot when hard),
+ *   ref_scan_kv's return_w output (slotkern_kv.py:115-117).  pin: ref_scan_kv's pin (slotkern_kv.py:88-101),
+ *   a row with |K| < 1e-6 scores 0 and takes no address gradient.
  * slotscan_gen_bwd: the backward (slotkern_kvg.py:233-253) for the upstream gradients dkbuf, dvbuf (fp32,
  *   shaped like kbuf, vbuf), from the forward's kbuf, vbuf, obuf and am.  Writes dk, dq (B, T, H, DK),
  *   dv (B, T, H, DV) in the token dtype, dgate (B, T, H), dfr (fr's shape), dtemp (1).  workspace:
@@ -135,12 +138,13 @@ int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
 int slotscan_gen_fwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
                      const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
                      int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
-                     int hard, float* kbuf, float* vbuf, float* obuf, int32_t* am, void* stream);
+                     int hard, int pin, float* kbuf, float* vbuf, float* obuf, int32_t* am, float* wb,
+                     void* stream);
 size_t slotscan_gen_bwd_workspace(int64_t B, int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G);
 int slotscan_gen_bwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
                      const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
                      int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
-                     int hard, int detach_addr, const float* kbuf, const float* vbuf,
+                     int hard, int detach_addr, int pin, const float* kbuf, const float* vbuf,
                      const float* obuf, const int32_t* am, const float* dkbuf, const float* dvbuf,
                      void* workspace, void* dk, void* dq, void* dv, float* dgate, float* dfr,
                      float* dtemp, void* stream);

@@ -20,6 +20,8 @@
 //   dfr_t = -sum_n occ_n dz_n,  dtemp += sum_n dz_n s_n / temp,  dq_t = qinv (dqn - qn <qn, dqn>),
 //   dqn = temp sum_n dz_n kn_n  (qinv dqn where |q_t| < 1e-6)
 //   attached address only: dK_n += dz_n kinv_n (temp qn - s_n kn_n)  (temp dz_n kinv_n qn where |K_n| < 1e-6)
+//   pin (the reference's ref_scan_kv default, slotkern_kv.py:88-101): s_n = 0 where |K_n| < 1e-6, and those
+//   rows' dz is cut from dtemp, dq and the attached key gradient (dfr and the occupancy carry keep it)
 //   carry: dK = (1-w) dK, dV = (1-w) dV, do = (1-w) do - fr_t dz (no -fr dz under occ_bin);
 //   at a segment's first step the emitted copy's gradient (dkbuf, dvbuf) joins dK, dV.
 // Inside a segment dV only scales (dV(t+) = c(t) D, c the product of (1 - w) over the later steps), so the
@@ -53,9 +55,10 @@ constexpr float GEN_NORM_EPS = 1e-6f;
 struct GenArgs {
     const void* k; const void* q; const void* v;
     const float* gate; const float* fr; const float* temp;
-    int frt, T, H, N, G, NB, occ_bin, hard, detach;
+    int frt, T, H, N, G, NB, occ_bin, hard, detach, pin;
     float eps;
     float* kbuf; float* vbuf; float* obuf; int32_t* am;          // forward outputs (am: hard only)
+    float* wb;                                                    // optional: the address of every step
     const float* dkbuf; const float* dvbuf;                       // backward inputs
     float* scr; int64_t scr_chain;                                 // replay scratch, floats per chain
     void* dk; void* dq; void* dv; float* dg; float* dfr; float* part;
@@ -183,8 +186,8 @@ __device__ __forceinline__ int gen_address(const float (&z)[RPL], const float (&
 // Scores of one step: z, the raw scaled cosine s, |K_n| and 1 / max(|q|, 1e-6).
 template <int RPL, int DPK>
 __device__ __forceinline__ void gen_scores(const float (&K)[RPL][DPK], const float (&o)[RPL], const float* qt,
-                                           float temp, float frt, float eps, bool occ_bin, float (&z)[RPL],
-                                           float (&sr)[RPL], float (&kn)[RPL], float& qinv) {
+                                           float temp, float frt, float eps, bool occ_bin, bool pin,
+                                           float (&z)[RPL], float (&sr)[RPL], float (&kn)[RPL], float& qinv) {
     float qq = 0.f;
 #pragma unroll
     for (int i = 0; i < DPK; i++) qq = fmaf(qt[i], qt[i], qq);
@@ -200,6 +203,7 @@ __device__ __forceinline__ void gen_scores(const float (&K)[RPL][DPK], const flo
         kn[j] = sqrtf(n2);
         const float kinv = 1.f / fmaxf(kn[j], GEN_NORM_EPS);
         sr[j] = temp * (d * kinv * qinv);
+        if (pin && kn[j] < GEN_NORM_EPS) sr[j] = 0.f;   // pinned: a (near-)zero row scores 0
         const float occ = occ_bin ? (o[j] >= eps ? 1.f : 0.f) : o[j];
         z[j] = sr[j] - frt * occ;
     }
@@ -302,9 +306,14 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
             ldtok<TI, DPV>(vp + tok(t + 1) * DV + dl * DPV, vn_);
         }
         float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
-        gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, z, sr, knr, qinv);
+        gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, a.pin, z, sr, knr, qinv);
         const int best = gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, -1, xf[t & 1], w, lane, as, ad);
         if (a.hard && threadIdx.x == 0) a.am[ti] = best;
+        if (a.wb && dl == 0) {
+#pragma unroll
+            for (int j = 0; j < RPL; j++)
+                if (nbase + j < a.N) a.wb[ti * a.N + nbase + j] = ad[j];
+        }
 #pragma unroll
         for (int j = 0; j < RPL; j++) wr[j] = g * ad[j];
         gen_update<RPL, DPK, DPV>(K, V, o, wr, kt, vt);
@@ -437,7 +446,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 const float g = a.gate[ti];
                 const float frt = a.frt ? a.fr[ti] : a.fr[0];
                 float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
-                gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, z, sr, knr, qinv);
+                gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, a.pin, z, sr, knr, qinv);
                 gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, a.hard ? a.am[ti] : -1, xf[par], w, lane, as, ad);
                 par ^= 1;
                 float e[RPL];
@@ -571,15 +580,16 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 if (lane == 0) a.dg[ti] = SG;
             }
             // dz and the search-side partials
-            float dz[RPL], kinv[RPL];
+            float dz[RPL], ds[RPL], kinv[RPL];      // ds: dz with the pinned rows' score path cut
             float sfo = 0.f, sds = 0.f;
 #pragma unroll
             for (int j = 0; j < RPL; j++) {
                 dz[j] = as[j] * (g * dw[j] - SA);
+                ds[j] = (a.pin && knr[j] < GEN_NORM_EPS) ? 0.f : dz[j];
                 kinv[j] = 1.f / fmaxf(knr[j], GEN_NORM_EPS);
                 const float occ = a.occ_bin ? (o[j] >= a.eps ? 1.f : 0.f) : o[j];
                 sfo = fmaf(occ, dz[j], sfo);
-                sds = fmaf(dz[j], sr[j], sds);
+                sds = fmaf(ds[j], sr[j], sds);
             }
             sfo = rows4_sum(sfo);
             sds = rows4_sum(sds);
@@ -590,7 +600,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 for (int i = 0; i < DPK; i++) {
                     float x = 0.f;
 #pragma unroll
-                    for (int j = 0; j < RPL; j++) x = fmaf(dz[j] * kinv[j], K[j][i], x);
+                    for (int j = 0; j < RPL; j++) x = fmaf(ds[j] * kinv[j], K[j][i], x);
                     pq[i] = rows4_sum(temp * x);
                 }
                 if (rl == 0) {
@@ -608,7 +618,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             for (int j = 0; j < RPL; j++) {
                 const float omw = 1.f - wr[j];
                 if (!a.detach) {
-                    const float c = dz[j] * kinv[j];
+                    const float c = ds[j] * kinv[j];
                     const bool small = knr[j] < GEN_NORM_EPS;
 #pragma unroll
                     for (int i = 0; i < DPK; i++) {
@@ -716,7 +726,8 @@ static int check_gen(int64_t B, int64_t T, int64_t H, int64_t N, int64_t DK, int
 extern "C" int slotscan_gen_fwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
                                 const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
                                 int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
-                                int hard, float* kbuf, float* vbuf, float* obuf, int32_t* am, void* stream) {
+                                int hard, int pin, float* kbuf, float* vbuf, float* obuf, int32_t* am, float* wb,
+                                void* stream) {
     if (int r = check_gen(B, T, H, N, DK, DV, G, dtype)) return r;
     if (!k || !q || !v || !gate || !fr || !temp || !kbuf || !vbuf || !obuf || (hard && !am))
         return fail(SLOTSCAN_ERR_NULL, "slotscan_gen_fwd: a required pointer is NULL");
@@ -726,7 +737,8 @@ extern "C" int slotscan_gen_fwd(const void* k, const void* q, const void* v, int
     a.k = k; a.q = q; a.v = v; a.gate = gate; a.fr = fr; a.temp = temp;
     a.frt = fr_per_token != 0; a.T = (int)T; a.H = (int)H; a.N = (int)N; a.G = (int)G;
     a.NB = (int)((T + G - 1) / G); a.occ_bin = occ_bin != 0; a.hard = hard != 0; a.detach = 1; a.eps = eps;
-    a.kbuf = kbuf; a.vbuf = vbuf; a.obuf = obuf; a.am = am;
+    a.pin = pin != 0;
+    a.kbuf = kbuf; a.vbuf = vbuf; a.obuf = obuf; a.am = am; a.wb = wb;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)(B * H));
     hipError_t e;
@@ -748,7 +760,7 @@ extern "C" size_t slotscan_gen_bwd_workspace(int64_t B, int64_t H, int64_t N, in
 extern "C" int slotscan_gen_bwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
                                 const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
                                 int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
-                                int hard, int detach_addr, const float* kbuf, const float* vbuf,
+                                int hard, int detach_addr, int pin, const float* kbuf, const float* vbuf,
                                 const float* obuf, const int32_t* am, const float* dkbuf, const float* dvbuf,
                                 void* workspace, void* dk, void* dq, void* dv, float* dgate, float* dfr,
                                 float* dtemp, void* stream) {
@@ -764,7 +776,7 @@ extern "C" int slotscan_gen_bwd(const void* k, const void* q, const void* v, int
     a.k = k; a.q = q; a.v = v; a.gate = gate; a.fr = fr; a.temp = temp;
     a.frt = fr_per_token != 0; a.T = (int)T; a.H = (int)H; a.N = (int)N; a.G = (int)G;
     a.NB = (int)((T + G - 1) / G); a.occ_bin = occ_bin != 0; a.hard = hard != 0; a.detach = detach_addr != 0;
-    a.eps = eps;
+    a.eps = eps; a.pin = pin != 0;
     a.kbuf = const_cast<float*>(kbuf); a.vbuf = const_cast<float*>(vbuf); a.obuf = const_cast<float*>(obuf);
     a.am = const_cast<int32_t*>(am); a.dkbuf = dkbuf; a.dvbuf = dvbuf;
     a.scr = (float*)workspace; a.scr_chain = scr_chain(DK, DV, rpl, G);

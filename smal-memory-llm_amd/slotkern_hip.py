@@ -8,6 +8,8 @@ Drop-in surface (same names, arguments, layouts and autograd contract as the ref
                                                                               gqa25/slotkern_kv.py:29-41
     kv_scan(k, v, gate, fr, N, temp, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
             occ_bin=False)                                                    gqa25/slotkern_kvt.py:298-302
+    ref_scan_kv(k, v, gate, fr, N, temp, G=1, hard=False, hard_gate=False, eps=1e-4, return_w=False,
+                detach_addr=False, q=None, pin=True, occ_bin=False)           gqa25/slotkern_kv.py:54-64
 plus kv_scan_stream(...) -- forward only, with a carried (K, V, o) state in and out, for chunked streaming,
 and kv_scan_mem(...) -- the scan with the writer epilogue fused in (memlm_sh.py:453-456 then :473-475),
 returning the bf16 copies with kinv and valid instead of the fp32 snapshots.
@@ -170,7 +172,8 @@ class _KVScanGenHip(torch.autograd.Function):
     general-mode kernels, whose backward replays each stride-G segment from its emitted copy."""
 
     @staticmethod
-    def forward(ctx, k, q, v, gate, fr, temp, N, G, hard, hard_gate, eps, detach_addr, occ_bin):
+    def forward(ctx, k, q, v, gate, fr, temp, N, G, hard, hard_gate, eps, detach_addr, occ_bin, pin=False,
+                return_w=False):
         dt, k_, q_, v_, g, fr_, frt, temp_ = _prep(k, q, v, gate, fr, temp, hard_gate)
         B, T, H, DK = k_.shape
         DV = v_.shape[-1]
@@ -181,20 +184,24 @@ class _KVScanGenHip(torch.autograd.Function):
         vbuf = torch.empty(B, NB, H, N, DV, device=dev, dtype=f32)
         obuf = torch.empty(B, NB, H, N, device=dev, dtype=f32)
         am = torch.empty(B, T, H, device=dev, dtype=torch.int32) if hard else None
+        wb = torch.empty(B, T, H, N, device=dev, dtype=f32) if return_w else None
         rc = L.lib().slotscan_gen_fwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
                                       int(frt), L.ptr(temp_), B, T, H, N, DK, DV, G, float(eps), int(occ_bin),
-                                      int(hard), L.ptr(kbuf), L.ptr(vbuf), L.ptr(obuf), L.ptr(am),
-                                      L.stream_of(dev))
+                                      int(hard), int(pin), L.ptr(kbuf), L.ptr(vbuf), L.ptr(obuf), L.ptr(am),
+                                      L.ptr(wb), L.stream_of(dev))
         L.check(rc, "slotscan_gen_fwd")
         ctx.save_for_backward(k_, q_, v_, g, fr_, temp_, kbuf, vbuf, obuf, am)
         ctx.meta = (int(N), int(G), bool(hard), float(eps), bool(detach_addr), bool(occ_bin), frt, dt,
-                    tuple(fr.shape), torch.is_tensor(temp))
+                    tuple(fr.shape), torch.is_tensor(temp), bool(pin))
+        if return_w:
+            ctx.mark_non_differentiable(wb)
+            return kbuf, vbuf, wb
         return kbuf, vbuf
 
     @staticmethod
-    def backward(ctx, dkbuf, dvbuf):
+    def backward(ctx, dkbuf, dvbuf, _dwb=None):
         k_, q_, v_, g, fr_, temp_, kbuf, vbuf, obuf, am = ctx.saved_tensors
-        N, G, hard, eps, detach_addr, occ_bin, frt, dt, fr_shape, temp_is_tensor = ctx.meta
+        N, G, hard, eps, detach_addr, occ_bin, frt, dt, fr_shape, temp_is_tensor, pin = ctx.meta
         B, T, H, DK = k_.shape
         DV = v_.shape[-1]
         dev = k_.device
@@ -208,13 +215,14 @@ class _KVScanGenHip(torch.autograd.Function):
         dtemp = torch.empty(1, device=dev, dtype=f32)
         rc = L.lib().slotscan_gen_bwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
                                       int(frt), L.ptr(temp_), B, T, H, N, DK, DV, G, float(eps), int(occ_bin),
-                                      int(hard), int(detach_addr), L.ptr(kbuf), L.ptr(vbuf), L.ptr(obuf),
+                                      int(hard), int(detach_addr), int(pin), L.ptr(kbuf), L.ptr(vbuf),
+                                      L.ptr(obuf),
                                       L.ptr(am), L.ptr(dkbuf), L.ptr(dvbuf), L.ptr(ws), L.ptr(dk), L.ptr(dq),
                                       L.ptr(dv), L.ptr(dg), L.ptr(dfr), L.ptr(dtemp), L.stream_of(dev))
         L.check(rc, "slotscan_gen_bwd")
         dfr = dfr.reshape(fr_shape) if not frt else dfr
         dtemp = dtemp.reshape(()) if temp_is_tensor else None
-        return dk, dq, dv, dg, dfr, dtemp, None, None, None, None, None, None, None
+        return dk, dq, dv, dg, dfr, dtemp, None, None, None, None, None, None, None, None, None
 
 
 class _KVScanMemHip(torch.autograd.Function):
@@ -304,6 +312,23 @@ def kv_scan(k, v, gate, fr, N, temp, hard=False, hard_gate=False, eps=1e-4, deta
     return kv_scan_c(k, v, gate, fr, N, temp, G=1, hard=hard, hard_gate=hard_gate, eps=eps,
                      detach_addr=detach_addr, q=q)
 
+
+def ref_scan_kv(k, v, gate, fr, N, temp, G=1, hard=False, hard_gate=False, eps=1e-4, return_w=False,
+                detach_addr=False, q=None, pin=True, occ_bin=False):
+    """The reference's torch scan (slotkern_kv.py:54-64, _ref_scan_kv_impl :66-123) on the gfx950 kernels:
+    same signature, defaults and outputs.  pin (its default) scores a row with |K| < 1e-6 as 0 and cuts its
+    address gradient (slotkern_kv.py:88-101); memlm_sh calls it with pin=False (memlm_sh.py:461), which is
+    the function the other entry points compute.  return_w=True adds the write distribution of every step
+    before the gate, (B, T, H, N) fp32 -- one-hot in hard mode (slotkern_kv.py:115-117); here it carries no
+    gradient.  GPU tensors only: the reference also runs on the CPU, this package has no CPU path."""
+    if not pin and not return_w and _unsupported(hard, detach_addr, k.shape[-1], v.shape[-1], N) is None:
+        return kv_scan_c(k, v, gate, fr, N, temp, G=G, hard=hard, hard_gate=hard_gate, eps=eps,
+                         detach_addr=detach_addr, q=q, occ_bin=occ_bin)
+    why = _unsupported_gen(k.shape[-1], v.shape[-1], N)
+    if why:
+        raise NotImplementedError(why)
+    return _KVScanGenHip.apply(k, k if q is None else q, v, gate, fr, temp, N, int(G), bool(hard), bool(hard_gate),
+                               eps, bool(detach_addr), bool(occ_bin), bool(pin), bool(return_w))
 
 @torch.no_grad()
 def kv_scan_stream(k, v, gate, fr, N, temp, G=8, hard_gate=False, eps=1e-4, q=None, occ_bin=False, state=None):

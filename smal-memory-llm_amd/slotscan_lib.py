@@ -39,10 +39,10 @@ SIGNATURES = {
     "slotscan_bwd_mem": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
                                 _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32] + [_vp] * 19),
     "slotscan_gen_fwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
-                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32] + [_vp] * 5),
+                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32] + [_vp] * 6),
     "slotscan_gen_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "slotscan_gen_bwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
-                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32] + [_vp] * 14),
+                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32, _i32] + [_vp] * 14),
     "slotread_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "slotread_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _vp, _vp, _vp, _vp, _vp, _vp]),

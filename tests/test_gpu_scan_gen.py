@@ -40,7 +40,7 @@ def _inputs(B, T, H, DK, DV, seed, frt, sep_q, dtype):
     return k, q, v, g, fr
 
 
-def run_case(B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg, seed=3, dtype=torch.float32):
+def run_case(B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg, seed=3, dtype=torch.float32, pin=False):
     print(f"gen case B{B} T{T} H{H} N{N} DK{DK} DV{DV} G{G} hard={hard} detach={detach} frt={frt} occb={occb} "
           f"q={sep_q} hardg={hardg} {dtype}", flush=True)
     k, q, v, g, fr = _inputs(B, T, H, DK, DV, seed, frt, sep_q, dtype)
@@ -50,8 +50,9 @@ def run_case(B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg, seed=
     dev = lambda x: None if x is None else x.to(DEV).requires_grad_()
     kk, qq, vv, gg, ff = dev(k), dev(q), dev(v), dev(g), dev(fr)
     tp = torch.tensor(TEMP, device=DEV, requires_grad=True)
-    kb, vb = KH.kv_scan_c(kk, vv, gg, ff, N, tp, G=G, hard=hard, hard_gate=hardg, eps=1e-4, detach_addr=detach,
-                          q=qq, occ_bin=occb)
+    entry = KH.ref_scan_kv if pin else KH.kv_scan_c     # ref_scan_kv's default pin=True
+    kb, vb = entry(kk, vv, gg, ff, N, tp, G=G, hard=hard, hard_gate=hardg, eps=1e-4, detach_addr=detach, q=qq,
+                   occ_bin=occb)
     assert kb.grad_fn is not None and type(kb.grad_fn).__name__.startswith("_KVScanGenHip")
     am = kb.grad_fn.saved_tensors[9]
     ((kb * wk.to(DEV)).sum() + (vb * wv.to(DEV)).sum()).backward()
@@ -60,9 +61,9 @@ def run_case(B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg, seed=
     kn, qn, vn, gn, frn = np64(k), np64(q), np64(v), np64(g), np64(fr)
     am_np = am.cpu().numpy().astype(np.int64) if hard else None
     okb, ovb, info = SO.scan_forward(kn, vn, gn, frn, N, TEMP, G=G, hard=hard, hard_gate=hardg, eps=1e-4,
-                                     detach_addr=detach, q=qn, occ_bin=occb, teacher=am_np)
+                                     detach_addr=detach, q=qn, occ_bin=occb, teacher=am_np, pin=pin)
     ogr = SO.scan_backward(kn, vn, gn, frn, N, TEMP, okb, ovb, info, np64(wk), np64(wv), G=G, hard=hard,
-                           hard_gate=hardg, eps=1e-4, detach_addr=detach, q=qn, occ_bin=occb)
+                           hard_gate=hardg, eps=1e-4, detach_addr=detach, q=qn, occ_bin=occb, pin=pin)
     if hard:
         bad = ~info["agree"]
         assert bad.sum() == 0 or np.abs(info["margin"][bad]).max() < 1e-4, \
@@ -79,7 +80,7 @@ def run_case(B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg, seed=
         errs[name] = _rel(got.detach().double().cpu().numpy().reshape(np.shape(ref)), ref)
     print("   rel err:", {x: f"{e:.1e}" for x, e in errs.items()}, flush=True)
     tol = {name: (1e-5 if name in ("kbuf", "vbuf") else (1e-4 if dtype == torch.float32 else 1e-2)) for name in errs}
-    if hard and not detach:
+    if hard and not detach and not pin:
         # The attached hard address is ill-conditioned (see CASES): dgate = dw[row] is ~1e3x smaller than the
         # dK it is summed from.  The bar is calibrated by the oracle evaluated in float32 on the same maths:
         # the kernel may differ from fp64 by at most 10x what that fp32 evaluation does (never below 1e-4).
@@ -162,3 +163,39 @@ def test_scan_kv_defaults_match_oracle():
                            ("dgate", gg.grad, ogr["dgate"]), ("dfr", ff.grad, ogr["dfr"])):
         e = _rel(got.detach().double().cpu().numpy().reshape(np.shape(ref)), ref)
         assert e < 1e-4, f"{name} rel err {e:.3e}"
+
+
+@pytest.mark.parametrize("hard,detach", [(False, False), (True, False), (False, True)])
+def test_ref_scan_kv_pin_matches_oracle(hard, detach):
+    """ref_scan_kv with its default pin=True (slotkern_kv.py:88-101): near-zero rows score 0 and take no
+    address gradient -- which also keeps the hard + attached chain finite over a long sequence."""
+    run_case(1, 64, 2, 40, 64, 128, 8, hard, detach, True, True, True, False, seed=11, pin=True)
+
+
+@pytest.mark.parametrize("hard", [False, True])
+def test_ref_scan_kv_return_w(hard):
+    """return_w: every step's write distribution before the gate (slotkern_kv.py:115-117), checked against
+    the oracle's address rebuilt from the G = 1 snapshots (the pre-write state of every step)."""
+    B, T, H, N, D = 1, 30, 2, 24, 64
+    k, q, v, g, fr = _inputs(B, T, H, D, D, 12, True, True, torch.float32)
+    kb, vb, wb = KH.ref_scan_kv(k.to(DEV), v.to(DEV), g.to(DEV), fr.to(DEV), N, TEMP, hard=hard, q=q.to(DEV),
+                                return_w=True)
+    torch.cuda.synchronize()
+    wb = wb.cpu().numpy().astype(np.float64)
+    assert wb.shape == (B, T, H, N)
+    kn, qn, vn, gn, frn = np64(k), np64(q), np64(v), np64(g), np64(fr)
+    teacher = wb.argmax(-1) if hard else None
+    okb, ovb, info = SO.scan_forward(kn, vn, gn, frn, N, TEMP, G=1, hard=hard, q=qn, pin=True, teacher=teacher)
+    if hard:
+        bad = ~info["agree"]
+        assert bad.sum() == 0 or np.abs(info["margin"][bad]).max() < 1e-4
+    assert _rel(kb.cpu(), okb) < 1e-5
+    for t in range(T):
+        zm = SO._step_scores(okb[:, t], info["obuf"][:, t], qn[:, t], TEMP, SO._fr_at(frn, t), 1e-4, False, True)[2]
+        if hard:
+            a = np.zeros_like(zm)
+            np.put_along_axis(a, teacher[:, t][..., None], 1.0, -1)
+            assert np.array_equal(wb[:, t], a)
+        else:
+            a = SO._softmax(zm)
+            assert np.abs(wb[:, t] - a).max() < 1e-5, t
