@@ -113,6 +113,18 @@ def read_bwd_algorithmic(B, T, H, N, D, NQ, NB):
     return tok * (2 * D + 2 * D + 2) + 2 * cp + B * NB * H * N * 5 + tok * 2 * D + 2 * cp + B * NB * H * N * 4 + tok * 4
 
 
+def copy_calibration(dev):
+    """One 1 GiB device-to-device copy (reads 1 GiB, writes 1 GiB), so that HBM byte counters of the same
+    run (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) can be scaled by what they report for it."""
+    import torch
+    src = torch.empty(1 << 28, device=dev, dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def measured_traffic(workload):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled by a copy kernel of known
     size), read from the committed summary profiles/hbm_traffic_<workload>.md; {} when there is none."""
@@ -372,6 +384,8 @@ def bench_read(args, W):
     t1 = time.perf_counter()
     L.profile(False)
     prof = L.profile_read()
+    if args.copy_calibration:
+        copy_calibration(torch.device("cuda:0"))
     ms = (t1 - t0) * 1e3 / args.steps
     tot, cnt = prof["read_fwd"]
     kms = tot / cnt
@@ -495,12 +509,7 @@ def main():
         warm = {n: (tot / args.steps, cnt / args.steps) for n, (tot, cnt) in prof.items()}
         dom = max((n for n in warm if n in per_kernel_bytes), key=lambda n: warm[n][0] / warm[n][1])
     if args.copy_calibration:
-        src = torch.empty(1 << 28, device=dev, dtype=torch.float32).fill_(1.0)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        copy_calibration(dev)
     ms = (t1 - t0) * 1e3 / args.steps
     two_pass_ms = None
     if mem:
