@@ -277,14 +277,19 @@ def kv_scan_mem(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=
     """kv_scan_g followed by the writer layer's full-precision epilogue, in one forward and one backward
     (memlm_sh.py:453-456 then :473-475): returns (kb, vb, kinv, valid) with kb, vb the snapshots in bf16,
     kinv = rsqrt(max(|K|^2, 1e-12)) fp32 and valid = |K|^2 > 1e-12 (bool), each (B, ceil(T/G), H, N[, D]).
-    The fp32 snapshots are never materialised.  Same modes as kv_scan_c; only the bf16 copies (the
-    activation dtype of training) are emitted."""
+    In the row-sparse mode (hard, detached address, DK == DV) the fp32 snapshots are never materialised.
+    Every other mode runs the general-mode scan and then the epilogue kernels (two passes, the same
+    outputs and autograd).  Only the bf16 copies (the activation dtype of training) are emitted."""
     if dtype != torch.bfloat16:
         raise NotImplementedError("the fused scan + epilogue emits bf16 copies only; use kv_scan_g and "
                                   "writer_epilogue for another dtype")
-    why = _unsupported(hard, detach_addr, k.shape[-1], v.shape[-1], N)
-    if why:
-        raise NotImplementedError(why)
+    if _unsupported(hard, detach_addr, k.shape[-1], v.shape[-1], N) is not None:
+        why = _unsupported_gen(k.shape[-1], v.shape[-1], N)
+        if why:
+            raise NotImplementedError(why)
+        kbuf, vbuf = kv_scan_c(k, v, gate, fr, N, temp, G=G, hard=hard, hard_gate=hard_gate, eps=eps,
+                               detach_addr=detach_addr, q=q, occ_bin=occ_bin)
+        return MH.writer_epilogue(kbuf, vbuf, dtype=dtype)
     return _KVScanMemHip.apply(k, k if q is None else q, v, gate, fr, temp, N, int(G), bool(hard_gate), eps,
                                bool(occ_bin))
 

@@ -183,11 +183,8 @@ def test_stream_chunks_equal_one_shot():
 
 def test_unsupported_modes_raise():
     k, q, v, g, fr = (x.to(DEV) for x in scan_inputs(1, 8, 1, 64, 0))
-    # the fused scan + epilogue runs the row-sparse kernels only (soft and attached modes: kv_scan_c)
     with pytest.raises(NotImplementedError):
-        KH.kv_scan_mem(k, v, g, fr, 16, TEMP, G=8, hard=False, detach_addr=True, q=q)
-    with pytest.raises(NotImplementedError):
-        KH.kv_scan_mem(k, v, g, fr, 16, TEMP, G=8, hard=True, detach_addr=False, q=q)
+        KH.kv_scan_mem(k, v, g, fr, 400, TEMP, G=8, hard=False, detach_addr=True, q=q)
     with pytest.raises(NotImplementedError):
         KH.kv_scan(k, v, g, fr, 16, TEMP, hard=True, detach_addr=True, occ_bin=True)
     with pytest.raises(NotImplementedError):

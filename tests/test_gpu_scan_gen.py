@@ -199,3 +199,24 @@ def test_ref_scan_kv_return_w(hard):
         else:
             a = SO._softmax(zm)
             assert np.abs(wb[:, t] - a).max() < 1e-5, t
+
+
+def test_scan_mem_general_mode_equals_scan_then_epilogue():
+    """kv_scan_mem in a general mode (soft, attached) = kv_scan_c then the writer epilogue, values and
+    gradients bitwise (it is that composition), and the epilogue's kinv matches the fp32 snapshots."""
+    import slotmem_hip as MH
+    k, q, v, g, fr = (x.to(DEV) for x in _inputs(1, 40, 2, 128, 128, 21, True, True, torch.bfloat16))
+    outs = []
+    for fused in (True, False):
+        kk, qq = k.clone().requires_grad_(), q.clone().requires_grad_()
+        if fused:
+            kb, vb, kinv, valid = KH.kv_scan_mem(kk, v, g, fr, 64, TEMP, G=8, hard=False, q=qq)
+        else:
+            kbuf, vbuf = KH.kv_scan_c(kk, v, g, fr, 64, TEMP, G=8, hard=False, q=qq)
+            kb, vb, kinv, valid = MH.writer_epilogue(kbuf, vbuf)
+            ref_kinv = torch.rsqrt(kbuf.detach().pow(2).sum(-1).clamp_min(1e-12))
+            assert torch.allclose(kinv, ref_kinv, rtol=2e-6, atol=0)
+        (kb.float().sum() + vb.float().square().sum() + kinv.sum()).backward()
+        outs.append((kb.detach(), vb.detach(), kinv.detach(), valid, kk.grad, qq.grad))
+    for x, y in zip(*outs):
+        assert torch.equal(x, y)

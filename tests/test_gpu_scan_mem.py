@@ -153,8 +153,10 @@ def test_scan_mem_missing_upstream_gradients():
 
 
 def test_scan_mem_refuses_other_copy_dtypes():
+    """Only bf16 copies are emitted, in every mode (the general modes compose the scan and the epilogue:
+    tests/test_gpu_scan_gen.py)."""
     k, q, v, g, fr = (x.to(DEV) for x in scan_inputs(1, 16, 1, 64, 0))
     with pytest.raises(NotImplementedError):
         KH.kv_scan_mem(k, v, g, fr, 16, TEMP, G=8, hard=True, detach_addr=True, q=q, dtype=torch.float32)
     with pytest.raises(NotImplementedError):
-        KH.kv_scan_mem(k, v, g, fr, 16, TEMP, G=8, hard=False, detach_addr=True, q=q)
+        KH.kv_scan_mem(k, v, g, fr, 16, TEMP, G=8, hard=False, detach_addr=True, q=q, dtype=torch.float16)
