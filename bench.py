@@ -433,7 +433,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the scan has no cross-GPU exchange and this build runs on "
-              "single-GPU boxes (every (batch, head) chain is independent; see the sharding note in DESIGN.md)",
+              "single-GPU boxes (every (batch, head) chain is independent, so N GPUs would each run B/N of the "
+              "batch)",
               file=sys.stderr)
         sys.exit(2)
 
