@@ -220,3 +220,19 @@ def test_scan_mem_general_mode_equals_scan_then_epilogue():
         outs.append((kb.detach(), vb.detach(), kinv.detach(), valid, kk.grad, qq.grad))
     for x, y in zip(*outs):
         assert torch.equal(x, y)
+
+
+def test_ref_scan_kv_unpinned_hard_detached_is_kv_scan_c():
+    """ref_scan_kv(pin=False) in the training mode (hard, detached, DK == DV: memlm_sh.py:461's call) runs
+    the row-sparse kernels: outputs and gradients bitwise equal to kv_scan_c's."""
+    k, q, v, g, fr = (x.to(DEV) for x in _inputs(1, 64, 2, 128, 128, 31, True, True, torch.float32))
+    res = []
+    for entry in (KH.kv_scan_c, KH.ref_scan_kv):
+        kk, qq = k.clone().requires_grad_(), q.clone().requires_grad_()
+        extra = {} if entry is KH.kv_scan_c else {"pin": False}
+        kb, vb = entry(kk, v, g, fr, 96, TEMP, G=8, hard=True, detach_addr=True, q=qq, occ_bin=True, **extra)
+        assert type(kb.grad_fn).__name__.startswith("_KVScanHip")
+        (kb.square().sum() + vb.sum()).backward()
+        res.append((kb.detach(), vb.detach(), kk.grad, qq.grad))
+    for x, y in zip(*res):
+        assert torch.equal(x, y)
