@@ -68,6 +68,15 @@ int slotscan_fwd(const void* k, const void* q, const void* v, int dtype,
  * per-chain partials.  The reference allocates Dn inside _KVScanC.backward (slotkern_cuda.py:524). */
 size_t slotscan_bwd_workspace(int64_t B, int64_t T, int64_t H, int64_t N);
 
+/* Which backward kernels slotscan_bwd (mem = 0) or slotscan_bwd_mem (mem = 1) runs for a shape, as a bit
+ * set; no GPU work.  SLOTSCAN_PLAN_ROWS_UNTRACKED: the row kernel's G = 8 variant with explicitly counted
+ * loads, used when G == 8, T % 16 == 0 (D == 128 for mem) and a batch row's snapshot gradients span at
+ * most 4 GiB (its loads use 32-bit offsets); otherwise the compiler-tracked variant runs.  Returns -1 for
+ * an invalid shape.  No counterpart in the reference (whose backward has one kernel per direction): it lets
+ * a caller, and the CPU tests, see the choice the library makes. */
+#define SLOTSCAN_PLAN_ROWS_UNTRACKED 1
+int slotscan_bwd_plan(int64_t T, int64_t H, int64_t N, int64_t D, int64_t G, int mem);
+
 /* Backward scan.  Replaces _KVScanC.backward's launches (slotkern_cuda.py:514-533).
  *   dkbuf, dvbuf  upstream gradients of kbuf, vbuf (fp32, same layout; pass zeros for a missing one)
  *   workspace     >= slotscan_bwd_workspace(...) bytes, 256-byte aligned

@@ -2186,6 +2186,24 @@ extern "C" int slotscan_fwd_mem(const void* k, const void* q, const void* v, int
                     kfin, vfin, ofin, stream);
 }
 
+// The untracked G = 8 row kernel (rows_bwd<.., G8 = true, ..>) needs two snapshot boundaries at fixed
+// positions in every 16-step chunk, and it addresses a batch row's snapshot gradients as 32-bit byte
+// offsets from the row's base: it runs only where every such offset fits (NB * H * N * D elements of 4 B,
+// or 2 B for the bf16 gradients of the fused contract, which is built for D = 128 only).
+static bool rows_bwd_untracked(int64_t T, int64_t H, int64_t N, int64_t D, int64_t G, bool mem) {
+    if (G != 8 || T % 16 != 0 || (mem && D != 128)) return false;
+    const int64_t NB = (T + G - 1) / G;
+    return (uint64_t)NB * (uint64_t)H * (uint64_t)N * (uint64_t)D * (mem ? 2u : 4u) <= 0xffffffffull;
+}
+
+extern "C" int slotscan_bwd_plan(int64_t T, int64_t H, int64_t N, int64_t D, int64_t G, int mem) {
+    if (T < 1 || H < 1 || N < 1 || G < 1) {
+        fail(SLOTSCAN_ERR_SHAPE, "T, H, N and G must be >= 1");
+        return -1;
+    }
+    return rows_bwd_untracked(T, H, N, D, G, mem != 0) ? SLOTSCAN_PLAN_ROWS_UNTRACKED : 0;
+}
+
 extern "C" size_t slotscan_bwd_workspace(int64_t B, int64_t T, int64_t H, int64_t N) {
     // Dn (B*H, N, T) fp32, then the per-chain partials (B*H, 2) fp32, 256-byte aligned
     const size_t dn = (size_t)B * H * N * T * sizeof(float);
@@ -2225,7 +2243,7 @@ static int scan_bwd(const void* k, const void* q, const void* v, int dtype,
     hipError_t e;
     {
         slothost::Scope sc(SLOTSCAN_K_ROWS_BWD, st);
-        const bool g8 = G == 8 && T % 16 == 0;          // two boundaries per chunk at fixed positions
+        const bool g8 = rows_bwd_untracked(T, H, N, D, G, mem);
 #define SLOT_RB(DD, TT) { if (mem) { if (g8 && DD == 128) slothost::launch((rows_bwd<DD, TT, DD == 128, true>), grid, block, 0, st, ra); \
                                      else slothost::launch((rows_bwd<DD, TT, false, true>), grid, block, 0, st, ra); } \
                           else if (g8) slothost::launch((rows_bwd<DD, TT, true, false>), grid, block, 0, st, ra); \

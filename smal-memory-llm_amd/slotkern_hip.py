@@ -302,9 +302,14 @@ def kv_scan_g(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e
 
 
 def scan_kv(k, v, gate, fr, N, temp, G=1, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None):
-    """slotkern_kv.scan_kv's signature (slotkern_kv.py:29-41).  Errors are raised, never swallowed."""
-    return kv_scan_c(k, v, gate, fr, N, temp, G=G, hard=hard, hard_gate=hard_gate, eps=eps,
-                     detach_addr=detach_addr, q=q)
+    """slotkern_kv.scan_kv's signature and dispatch (slotkern_kv.py:29-41): at G = 1 the unpinned kernel
+    function (the reference's Triton kv_scan), at G > 1 ref_scan_kv with its default pin=True (rows with
+    |K| < 1e-6 score 0 and take no address gradient).  Errors are raised, never swallowed."""
+    if int(G) == 1:
+        return kv_scan_c(k, v, gate, fr, N, temp, G=1, hard=hard, hard_gate=hard_gate, eps=eps,
+                         detach_addr=detach_addr, q=q)
+    return ref_scan_kv(k, v, gate, fr, N, temp, G=G, hard=hard, hard_gate=hard_gate, eps=eps,
+                       detach_addr=detach_addr, q=q)
 
 
 def kv_scan(k, v, gate, fr, N, temp, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,

@@ -30,6 +30,7 @@ SIGNATURES = {
     "slotscan_fwd_mem": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
                                 _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32] + [_vp] * 16),
     "slotscan_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64]),
+    "slotscan_bwd_plan": (_i32, [_i64, _i64, _i64, _i64, _i64, _i32]),
     "slotscan_profile": (_i32, [_i32]),
     "slotscan_profile_read": (_i32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), _i32]),
     "slotscan_bwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,

@@ -1,0 +1,21 @@
+"""CPU checks of properties of the compiled gfx950 kernels that the code relies on, read from the compiler's
+per-kernel resource report of the current build (build.resource_report; a device-only compile when the
+report is stale).  No GPU work."""
+import re
+
+import build
+
+
+def test_untracked_rows_kernels_use_no_scratch():
+    """rows_bwd's G = 8 variant issues its gradient, token and undo loads through inline asm that the compiler
+    does not track and waits for them with hand-counted `s_waitcnt vmcnt(n)` (csrc/slotscan.hip, rows_bwd).
+    On gfx9 one vector-memory counter covers loads, stores and scratch accesses, so a scratch spill or reload
+    inside the counted window would break every count without any error.  The counts are only valid while
+    every such instantiation has no scratch at all."""
+    rep = build.resource_report("slotscan.hip")
+    g8 = {n: d for n, d in rep.items() if re.fullmatch(r"void rows_bwd<\d+, [\w ]+, true, (true|false)>", n)}
+    assert len(g8) == 6, sorted(g8)          # D 128: bf16 / f32 tokens x both contracts; D 64: fp32 contract
+    for name, d in g8.items():
+        assert d["ScratchSize [bytes/lane]"] == "0", f"{name} uses scratch: {d}"
+        assert d["VGPRs Spill"] == "0", f"{name} spills: {d}"
+        assert d["Dynamic Stack"] == "False", name

@@ -1,0 +1,167 @@
+"""GPU parity at the benchmarked shapes: bench.py's own scan workloads (configs 2 and 3) run at full size --
+full grid, full length -- and are checked on sampled chains.
+
+Config 2 is B=64, T=1024, H=6, N=192, D=128, G=8: 384 chains (two rounds of workgroups on 256 CUs), the
+forward's 8-chunk two-stream pipeline, 4.83 GB snapshot buffers.  Chains are independent, so three
+size-independent checks cover the whole launch without an fp64 run over all of it:
+  1. batch-slice consistency: the sampled batch rows run alone (a small launch) give bitwise the same
+     snapshots, address log, final occupancy and per-token gradients as the full-size launch;
+  2. the fp64 oracle on the sampled rows (every head), teacher-forced along the GPU's addresses: addresses
+     bit-exact or certified near-ties (|fp64 margin| < 1e-4; the count is printed), final occupancy masks
+     identical, snapshots within 1e-5 relative to max, gradients within 1e-2 (bf16 tokens, bf16 gradients);
+     dtemp, a sum over the launch's chains, is checked on the small launch at 1e-4;
+  3. run-twice determinism at full size, every output and gradient bitwise.
+The reference's own acceptance runs at T = 1024 and counts differing rows (kvu/test_cuda.py:11-28, 59-70).
+Inputs are bench.scan_workload_inputs: drawn on the GPU from the workload's seeded generator."""
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import read_oracle as RO
+from oracle import scan_oracle as SO
+
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    import slotkern_hip as KH
+
+TEMP = 16.0
+
+
+def _rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def _np(x):
+    return x.detach().double().cpu().numpy()
+
+
+def _run(W, ins, mem):
+    """One forward + backward of the workload's step.  ins = (k, q, v, gate, fr, temp, dkb, dvb, dki) with
+    the first six leaves.  Returns (outputs, am, ofin, grads) -- outputs (kbuf, vbuf) or (kb, vb, kinv,
+    valid), am (B,T,H) and ofin (B*H,N) from the saved undo log."""
+    k, q, v, gate, fr, temp, dkb, dvb, dki = ins
+    kw = dict(G=W["G"], hard=True, hard_gate=False, detach_addr=True, q=q, occ_bin=True)
+    leaves = (k, q, v, gate, fr, temp)
+    if mem:
+        outs = KH.kv_scan_mem(k, v, gate, fr, W["N"], temp, **kw)
+        diff, ups = outs[:3], (dkb.to(torch.bfloat16), dvb.to(torch.bfloat16), dki)
+    else:
+        outs = KH.kv_scan_c(k, v, gate, fr, W["N"], temp, **kw)
+        diff, ups = outs, (dkb, dvb)
+    saved = outs[0].grad_fn.saved_tensors
+    am, ofin = saved[6].clone(), saved[13].clone()
+    del saved
+    grads = dict(zip(("dk", "dq", "dv", "dgate", "dfr", "dtemp"), torch.autograd.grad(diff, leaves, ups)))
+    torch.cuda.synchronize()
+    return tuple(x.detach() for x in outs), am, ofin, grads
+
+
+def _slice(ins, bs):
+    """The sampled batch rows of the inputs as new leaves (temp shared in value)."""
+    k, q, v, gate, fr, temp, dkb, dvb, dki = ins
+    idx = torch.tensor(bs, device=k.device)
+    leaf = lambda x: x.detach()[idx].clone().requires_grad_()
+    return (leaf(k), leaf(q), leaf(v), leaf(gate), leaf(fr), temp.detach().clone().requires_grad_(),
+            dkb[idx], dvb[idx], dki[idx])
+
+
+def _oracle_check(W, ins_s, run_s, mem):
+    """fp64 oracle on the small launch's rows, teacher-forced on its addresses.  Returns (errors, flips)."""
+    k, q, v, gate, fr, _temp, dkb, dvb, dki = ins_s
+    outs, am, ofin, grads = run_s
+    N, G = W["N"], W["G"]
+    kn, qn, vn, gn, frn = _np(k), _np(q), _np(v), _np(gate), _np(fr)
+    okb, ovb, info = SO.scan_forward(kn, vn, gn, frn, N, TEMP, G=G, hard=True, eps=1e-4, detach_addr=True,
+                                     q=qn, occ_bin=True, teacher=am.cpu().numpy().astype(np.int64))
+    bad = ~info["agree"]
+    assert bad.sum() == 0 or np.abs(info["margin"][bad]).max() < 1e-4, \
+        f"{bad.sum()} address disagreements, worst fp64 margin {np.abs(info['margin'][bad]).max():.3e}"
+    assert bad.sum() <= 2, f"too many near-tie flips: {bad.sum()}"
+    Bs, _, H, _ = k.shape
+    of = ofin.cpu().numpy().reshape(Bs, H, N)
+    assert np.array_equal(of >= 1e-4, info["ofin"] >= 1e-4)
+    errs = {}
+    if mem:
+        kinv_o, valid_o = RO.writer_epilogue(okb)
+        assert np.array_equal(outs[3].cpu().numpy(), valid_o)
+        errs["kb"] = _rel(outs[0].float().cpu(), okb)
+        errs["vb"] = _rel(outs[1].float().cpu(), ovb)
+        ki = outs[2].double().cpu().numpy()
+        errs["kinv"] = _rel(ki[valid_o], kinv_o[valid_o]) if valid_o.any() else 0.0
+        if (~valid_o).any():                                # rsqrt(1e-12) on both sides
+            np.testing.assert_allclose(ki[~valid_o], kinv_o[~valid_o], rtol=1e-6)
+        nsq = (okb * okb).sum(-1)
+        dnsq = np.where(nsq >= 1e-12, -0.5 * kinv_o ** 3 * _np(dki), 0.0)
+        up_k = _np(dkb.to(torch.bfloat16)) + 2.0 * okb * dnsq[..., None]
+        up_v = _np(dvb.to(torch.bfloat16))
+    else:
+        errs["kbuf"] = _rel(outs[0].cpu(), okb)
+        errs["vbuf"] = _rel(outs[1].cpu(), ovb)
+        up_k, up_v = _np(dkb), _np(dvb)
+    ogr = SO.scan_backward(kn, vn, gn, frn, N, TEMP, okb, ovb, info, up_k, up_v, G=G, hard=True, eps=1e-4,
+                           detach_addr=True, q=qn, occ_bin=True)
+    for name in ("dk", "dq", "dv", "dgate", "dfr", "dtemp"):
+        ref = ogr[name]
+        errs[name] = _rel(_np(grads[name]).reshape(np.shape(ref)), ref)
+    return errs, int(bad.sum())
+
+
+def _fullsize_case(name, bs, mem=False, twice=False):
+    W = dict(bench.WORKLOADS[name])
+    dev = torch.device("cuda:0")
+    print(f"full-size case {name} mem={mem} B{W['B']} T{W['T']} H{W['H']} N{W['N']} D{W['D']} G{W['G']} "
+          f"sampled rows {bs}", flush=True)
+    k, q, v, gate, fr, temp, dkb, dvb, rn = bench.scan_workload_inputs(W, dev)
+    NB = (W["T"] + W["G"] - 1) // W["G"]
+    dki = rn(W["B"], NB, W["H"], W["N"])
+    ins = (k, q, v, gate, fr, temp, dkb, dvb, dki)
+    full = _run(W, ins, mem)
+    if twice:                                               # 3. run-twice determinism at full size
+        again = _run(W, ins, mem)
+        for x, y in zip(full[0] + full[1:3], again[0] + again[1:3]):
+            assert torch.equal(x, y)
+        for n in full[3]:
+            assert torch.equal(full[3][n], again[3][n]), n
+        del again
+        print("   full size: run twice bitwise identical", flush=True)
+    idx = torch.tensor(bs, device=dev)
+    ins_s = _slice(ins, bs)
+    small = _run(W, ins_s, mem)
+    # 1. batch-slice consistency, bitwise
+    H = W["H"]
+    rows = torch.tensor([b * H + h for b in bs for h in range(H)], device=dev)
+    for i, (x, y) in enumerate(zip(full[0], small[0])):
+        assert torch.equal(x[idx], y), f"output {i}"
+    assert torch.equal(full[1][idx], small[1]), "address log"
+    assert torch.equal(full[2][rows], small[2]), "final occupancy"
+    for n in ("dk", "dq", "dv", "dgate", "dfr"):
+        assert torch.equal(full[3][n][idx], small[3][n]), n
+    print("   sampled rows: full-size launch == small launch, bitwise", flush=True)
+    del full
+    torch.cuda.empty_cache()
+    # 2. the fp64 oracle on the sampled rows
+    errs, flips = _oracle_check(W, ins_s, small, mem)
+    print("   rel err vs fp64 oracle:", {x: f"{e:.1e}" for x, e in errs.items()}, "flips:", flips, flush=True)
+    for x, e in errs.items():
+        tol = 1e-5 if x in ("kbuf", "vbuf", "kinv") else (2 ** -8 if x in ("kb", "vb") else
+                                                           (1e-4 if x == "dtemp" else 1e-2))
+        assert e < tol, f"{x} rel err {e:.3e} >= {tol}"
+
+
+def test_config2_fullsize_sampled_chains_and_determinism():
+    _fullsize_case("config2", (0, 31, 63), twice=True)
+
+
+def test_config2_mem_fullsize_sampled_chains():
+    """The fused scan + writer epilogue on the same batch (bf16 copies, kinv, valid)."""
+    _fullsize_case("config2", (0, 31, 63), mem=True)
+
+
+@pytest.mark.parametrize("name,bs", [("config3_t128", (0, 255, 511)), ("config3", (0, 31, 63))])
+def test_config3_fullsize_sampled_chains(name, bs):
+    """Encoder memory (N = 96): 3,072 chains of 128 steps (one forward launch), and 384 chains of 1,024."""
+    _fullsize_case(name, bs)

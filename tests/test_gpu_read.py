@@ -176,3 +176,50 @@ def test_read_backward_is_deterministic():
     b = run_grad_case(2, 64, 2, 2, 192, 128, 8, seed=8)
     for name in a:
         assert torch.equal(a[name], b[name]), name
+
+
+def test_shared_read_matches_the_readers_formula():
+    """slotread_hip.shared_read, the replacement of SharedMixer._read from the projected queries on
+    (memlm_sh.py:379-397), against the oracle read with the reader's own preparation: q / max(|q|, 1e-6) in
+    q's dtype (:379), the multiplier exp(log_rsel) * exp(C tanh(s / C)) with C = 2 (:383-393, run_sh25.sh:223),
+    NQ = 2 and T not a multiple of G (the padded tail, :380-382).  Gradients of q (through the
+    normalisation), the copies, kinv, log_rsel and s are checked at the bf16 read bar."""
+    B, T, H, NQ, N, D, G, C = 2, 61, 3, 2, 192, 128, 8, 2.0
+    _, K, V, kinv, valid, _ = make_read_inputs(B, T, H, NQ, N, D, G, seed=19)
+    gen = torch.Generator().manual_seed(20)
+    q = (3.0 * torch.randn(B, T, H, NQ, D, generator=gen)).to(torch.bfloat16)   # projected, not unit
+    s = torch.randn(B, T, H, NQ, generator=gen)
+    drd = torch.randn(B, T, H, NQ, D, generator=gen).to(torch.bfloat16)
+    lr = float(np.log(8.0))
+    c = lambda t: t.to(DEV).requires_grad_()
+    qq, kk, vv, ki, ss = c(q), c(K), c(V), c(kinv), c(s)
+    lrs = torch.tensor(lr, device=DEV, requires_grad=True)
+    rd = RH.shared_read(qq, kk, vv, ki, valid.to(DEV), lrs, G, s=ss, rsharp=C)
+    rd.backward(drd.to(DEV))
+    torch.cuda.synchronize()
+    # the oracle: the reader's preparation in float64 (the normalised query rounded to bf16 as q's dtype)
+    qf = q.double().numpy()
+    nrm = np.maximum(np.sqrt((qf * qf).sum(-1, keepdims=True)), 1e-6)
+    qhat = RO.bf16_round(qf / RO.bf16_round(nrm)).astype(np.float64)
+    th = np.tanh(s.double().numpy() / C)
+    scale = np.exp(lr) * np.exp(C * th)
+    NB = (T + G - 1) // G
+    f = lambda t: t.double().numpy()
+    qh, sh, dh = to_blocks(qhat, G, NB), to_blocks(scale, G, NB), to_blocks(f(drd), G, NB)
+    ref, cache = RO.read_forward(qh, f(K), f(V), f(kinv), valid.numpy(), sh, bf16=True)
+    ref = from_blocks(ref, T, NQ)
+    gr = RO.read_backward(qh, f(K), f(V), f(kinv), valid.numpy(), sh, cache, dh)
+    dqh = from_blocks(gr["dq"], T, NQ)
+    dscale = from_blocks(gr["dscale"], T, NQ)
+    qn = qf / nrm
+    want = dict(rd=ref, dq=(dqh - qn * (dqh * qn).sum(-1, keepdims=True)) / nrm, dkbuf=gr["dkbuf"],
+                dbuf=gr["dbuf"], dkinv=gr["dkinv"], dlog_rsel=np.array((dscale * scale).sum()),
+                ds=dscale * scale * (1.0 - th * th))
+    got = dict(rd=rd, dq=qq.grad, dkbuf=kk.grad, dbuf=vv.grad, dkinv=ki.grad, dlog_rsel=lrs.grad, ds=ss.grad)
+    for name, r_ in want.items():
+        g_ = got[name].detach().double().cpu().numpy().reshape(np.shape(r_))
+        den = max(np.abs(r_).max(), 1e-30)
+        err = np.abs(g_ - r_)
+        print(f"   {name}: max rel err {err.max() / den:.2e}  mean {err.mean() / den:.2e}", flush=True)
+        assert err.max() <= 2e-2 * den, name
+        assert err.mean() <= 3e-3 * den, name

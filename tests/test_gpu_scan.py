@@ -115,6 +115,10 @@ CASES = [  # B, T, H, N, D, G, frt, occb, sep_q, hardg
     (1, 5, 2, 20, 64, 8, True, True, True, False),          # T < G
     (1, 600, 2, 96, 64, 8, True, True, True, False),        # T >= 512: chunked two-stream forward
     (1, 520, 2, 64, 64, 7, False, False, True, False),      # chunked forward, G = 7, no occ_bin
+    # G = 1, the default of kv_scan and scan_kv (slotkern_kvt.py:298, slotkern_kv.py:29): every step emits
+    (1, 100, 2, 64, 64, 1, True, False, True, False),       # T % 16 != 0, no occ_bin (kv_scan refuses it)
+    (2, 45, 2, 192, 128, 1, True, True, True, False),       # config 2 slot count, occ_bin, T % 16 != 0
+    (1, 530, 1, 96, 128, 1, False, False, True, False),     # G = 1 through the chunked two-stream forward
 ]
 
 
@@ -213,3 +217,22 @@ def test_stream_quantised_emission_equals_quantised_one_shot():
     dec = MH.fq_decode(kc1[0], kc1[1], D).cpu().numpy()
     from oracle import read_oracle as RO
     np.testing.assert_array_equal(dec, RO.fq(kb1.cpu().numpy(), 8, D)[0])
+
+
+def test_g1_entry_points_run_the_row_sparse_kernels():
+    """kv_scan (G = 1 by signature, slotkern_kvt.py:298-302) and scan_kv at its default G = 1 in the training
+    mode (hard, detached address) run the row-sparse kernels: outputs and gradients bitwise equal to
+    kv_scan_c(G=1), whose parity with the oracle the G = 1 rows of CASES check."""
+    k, q, v, g, fr = (x.to(DEV) for x in scan_inputs(2, 77, 2, 64, 43))
+    res = []
+    for entry in ("kv_scan_c", "kv_scan", "scan_kv"):
+        kk, qq = k.clone().requires_grad_(), q.clone().requires_grad_()
+        extra = {"G": 1} if entry == "kv_scan_c" else {}
+        kb, vb = getattr(KH, entry)(kk, v, g, fr, 64, TEMP, hard=True, detach_addr=True, q=qq, **extra)
+        assert type(kb.grad_fn).__name__.startswith("_KVScanHip"), entry
+        assert kb.shape == (2, 77, 2, 64, 64)
+        (kb.square().sum() + vb.sum()).backward()
+        res.append((kb.detach(), vb.detach(), kk.grad, qq.grad))
+    for other in res[1:]:
+        for x, y in zip(res[0], other):
+            assert torch.equal(x, y)

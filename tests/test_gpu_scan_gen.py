@@ -40,7 +40,10 @@ def _inputs(B, T, H, DK, DV, seed, frt, sep_q, dtype):
     return k, q, v, g, fr
 
 
-def run_case(B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg, seed=3, dtype=torch.float32, pin=False):
+def run_case(B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg, seed=3, dtype=torch.float32, pin=False,
+             entry=None, calibrate=None):
+    """calibrate: widen each bar to this multiple of the fp32 oracle's own error against fp64 (the same maths
+    evaluated in float32, normalising before the dot as the reference does, slotkern_kvt.py:84-90)."""
     print(f"gen case B{B} T{T} H{H} N{N} DK{DK} DV{DV} G{G} hard={hard} detach={detach} frt={frt} occb={occb} "
           f"q={sep_q} hardg={hardg} {dtype}", flush=True)
     k, q, v, g, fr = _inputs(B, T, H, DK, DV, seed, frt, sep_q, dtype)
@@ -50,7 +53,8 @@ def run_case(B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg, seed=
     dev = lambda x: None if x is None else x.to(DEV).requires_grad_()
     kk, qq, vv, gg, ff = dev(k), dev(q), dev(v), dev(g), dev(fr)
     tp = torch.tensor(TEMP, device=DEV, requires_grad=True)
-    entry = KH.ref_scan_kv if pin else KH.kv_scan_c     # ref_scan_kv's default pin=True
+    if entry is None:
+        entry = KH.ref_scan_kv if pin else KH.kv_scan_c     # ref_scan_kv's default pin=True
     kb, vb = entry(kk, vv, gg, ff, N, tp, G=G, hard=hard, hard_gate=hardg, eps=1e-4, detach_addr=detach, q=qq,
                    occ_bin=occb)
     assert kb.grad_fn is not None and type(kb.grad_fn).__name__.startswith("_KVScanGenHip")
@@ -80,20 +84,27 @@ def run_case(B, T, H, N, DK, DV, G, hard, detach, frt, occb, sep_q, hardg, seed=
         errs[name] = _rel(got.detach().double().cpu().numpy().reshape(np.shape(ref)), ref)
     print("   rel err:", {x: f"{e:.1e}" for x, e in errs.items()}, flush=True)
     tol = {name: (1e-5 if name in ("kbuf", "vbuf") else (1e-4 if dtype == torch.float32 else 1e-2)) for name in errs}
-    if hard and not detach and not pin:
+    if calibrate is None and hard and not detach and not pin:
         # The attached hard address is ill-conditioned (see CASES): dgate = dw[row] is ~1e3x smaller than the
         # dK it is summed from.  The bar is calibrated by the oracle evaluated in float32 on the same maths:
         # the kernel may differ from fp64 by at most 10x what that fp32 evaluation does (never below 1e-4).
+        calibrate = 10.0
+    if calibrate:
         f32 = np.float32
-        kb32, vb32, info32 = SO.scan_forward(kn, vn, gn, frn, N, TEMP, G=G, hard=True, hard_gate=hardg, eps=1e-4,
-                                             detach_addr=False, q=qn, occ_bin=occb, teacher=am_np, dtype=f32)
-        g32 = SO.scan_backward(kn, vn, gn, frn, N, TEMP, kb32, vb32, info32, np64(wk), np64(wv), G=G, hard=True,
-                               hard_gate=hardg, eps=1e-4, detach_addr=False, q=qn, occ_bin=occb, dtype=f32)
+        kb32, vb32, info32 = SO.scan_forward(kn, vn, gn, frn, N, TEMP, G=G, hard=hard, hard_gate=hardg, eps=1e-4,
+                                             detach_addr=detach, q=qn, occ_bin=occb, teacher=am_np, dtype=f32,
+                                             pin=pin)
+        g32 = SO.scan_backward(kn, vn, gn, frn, N, TEMP, kb32, vb32, info32, np64(wk), np64(wv), G=G, hard=hard,
+                               hard_gate=hardg, eps=1e-4, detach_addr=detach, q=qn, occ_bin=occb, dtype=f32,
+                               pin=pin)
+        e32 = {"kbuf": _rel(np.asarray(kb32, np.float64), okb), "vbuf": _rel(np.asarray(vb32, np.float64), ovb)}
         for name in grads:
             ref32 = g32[name] + (g32["dq"] if name == "dk" and not sep_q else 0)
             ref64 = ogr[name] + (ogr["dq"] if name == "dk" and not sep_q else 0)
-            e32 = _rel(np.asarray(ref32, np.float64).reshape(np.shape(ref64)), ref64)
-            tol[name] = max(tol[name], 10 * e32)
+            e32[name] = _rel(np.asarray(ref32, np.float64).reshape(np.shape(ref64)), ref64)
+        for name in e32:
+            tol[name] = max(tol[name], calibrate * e32[name])
+        print("   fp32 oracle's own rel err:", {x: f"{e:.1e}" for x, e in e32.items()}, flush=True)
         print("   fp32-oracle-calibrated bar:", {x: f"{t:.1e}" for x, t in tol.items()}, flush=True)
     for name, e in errs.items():
         assert e < tol[name], f"{name} rel err {e:.3e} >= {tol[name]:.3e}"
@@ -236,3 +247,21 @@ def test_ref_scan_kv_unpinned_hard_detached_is_kv_scan_c():
         res.append((kb.detach(), vb.detach(), kk.grad, qq.grad))
     for x, y in zip(*res):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("detach", [False, True])
+def test_gen_scan_soft_full_length(detach):
+    """Soft addresses over T = 1024 at the config-2 head shape (N = 192, D = 128, G = 8, occ_bin, per-token
+    fr), attached and detached address gradient.  The reference records that its general scan drifted
+    3.7e-3 from its own torch scan by T = 512 when the score was formed dot-first (slotkern_kvt.py:84-90):
+    here each bar is 1e-5 / 1e-4 or 4x the fp32 oracle's own error against fp64, whichever is larger."""
+    run_case(1, 1024, 2, 192, 128, 128, 8, False, detach, True, True, True, False, seed=41, calibrate=4.0)
+
+
+def test_scan_kv_strided_is_pinned():
+    """scan_kv at G > 1 is the reference's torch scan with its default pin=True (slotkern_kv.py:39-41), here
+    in the hard mode with the attached address gradient, whose unpinned function overflows fp32 within ~20
+    steps while the pinned one stays finite over a long chain."""
+    sk = lambda k, v, g, fr, N, temp, G, hard, hard_gate, eps, detach_addr, q, occ_bin: KH.scan_kv(
+        k, v, g, fr, N, temp, G=G, hard=hard, hard_gate=hard_gate, eps=eps, detach_addr=detach_addr, q=q)
+    run_case(1, 64, 2, 40, 64, 64, 8, True, False, True, False, True, False, seed=13, pin=True, entry=sk)

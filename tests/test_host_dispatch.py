@@ -30,3 +30,16 @@ def test_cpu_tensors_are_refused_not_computed():
         KH.kv_scan_c(k, k, g, torch.tensor([1.0]), 8, 16.0, G=2, hard=False)
     with pytest.raises(RuntimeError, match="GPU tensors only"):
         KH.kv_scan_c(k, k, g, torch.tensor([1.0]), 8, 16.0, G=2, hard=True, detach_addr=True)
+
+
+def test_scan_kv_dispatch_follows_the_reference(monkeypatch):
+    """scan_kv: G = 1 runs the unpinned kernel function (the reference's Triton kv_scan), G > 1 the
+    reference's torch scan with its default pin=True (slotkern_kv.py:39-41)."""
+    calls = []
+    monkeypatch.setattr(KH, "kv_scan_c", lambda *a, **kw: calls.append(("kv_scan_c", kw["G"])))
+    monkeypatch.setattr(KH, "ref_scan_kv", lambda *a, **kw: calls.append(("ref_scan_kv", kw["G"], kw.get("pin", True))))
+    k = torch.randn(1, 4, 1, 64)
+    g = torch.rand(1, 4, 1)
+    KH.scan_kv(k, k, g, torch.tensor([1.0]), 8, 16.0)
+    KH.scan_kv(k, k, g, torch.tensor([1.0]), 8, 16.0, G=8, hard=True, detach_addr=True)
+    assert calls == [("kv_scan_c", 1), ("ref_scan_kv", 8, True)]

@@ -93,3 +93,38 @@ def test_dtype_codes():
     assert L.dtype_code(torch.bfloat16) == L.SLOTSCAN_BF16
     with pytest.raises(TypeError):
         L.dtype_code(torch.float16)
+
+
+@pytest.mark.parametrize("T,H,N,D,G,mem,untracked", [
+    (1024, 6, 192, 128, 8, 0, True),        # config 2
+    (1024, 6, 192, 128, 8, 1, True),        # config 2, fused epilogue
+    (1024, 6, 192, 64, 8, 1, False),        # the fused contract's untracked kernel is built for D = 128
+    (1000, 6, 192, 128, 8, 0, False),       # T % 16 != 0
+    (1024, 6, 192, 128, 7, 0, False),       # G != 8
+    (58240, 6, 192, 128, 8, 0, True),       # NB * H * N * D * 4 = 4,293,918,720 B: just fits 32 bits
+    (58256, 6, 192, 128, 8, 0, False),      # 4,295,098,368 B: past 2^32, the tracked kernel runs
+    (58256, 6, 192, 128, 8, 1, True),       # bf16 gradients: half the bytes
+    (116512, 6, 192, 128, 8, 1, False),
+])
+def test_bwd_plan_untracked_rows_kernel_guard(T, H, N, D, G, mem, untracked):
+    """The untracked G = 8 row kernel forms a batch row's snapshot-gradient offsets in 32 bits: the library
+    uses it only where they fit (slotscan_bwd_plan exposes the choice; no GPU work)."""
+    plan = L.lib().slotscan_bwd_plan(T, H, N, D, G, mem)
+    assert plan >= 0
+    assert bool(plan & 1) == untracked
+    assert L.lib().slotscan_bwd_plan(0, H, N, D, G, mem) == -1
+
+
+def test_integration_doc_stubs_match_the_bindings():
+    """Every `lib.<name>.argtypes = ...` line in INTEGRATION.md binds exactly the argument list of the C
+    prototype (the same types, in order, as slotscan_lib.SIGNATURES): a maintainer copies these stubs."""
+    txt = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    found = re.findall(r"^lib\.(\w+)\.argtypes = (.+)$", txt, flags=re.M)
+    assert len(found) >= 5
+    env = {"vp": ctypes.c_void_p, "i64": ctypes.c_int64, "i32": ctypes.c_int, "f32": ctypes.c_float,
+           "ctypes": ctypes}
+    arity = _declared_arity()
+    for name, expr in found:
+        got = eval(expr, env)                                 # noqa: S307 -- the repository's own doc
+        assert len(got) == arity[name], f"{name}: the doc binds {len(got)} args, C has {arity[name]}"
+        assert got == L.SIGNATURES[name][1], f"{name}: the doc's argument types differ from the binding"
