@@ -93,6 +93,26 @@ int slotscan_bwd(const void* k, const void* q, const void* v, int dtype,
                  void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
                  void* stream);
 
+/* Allocation-free variant of slotscan_bwd.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, results and kernels as slotscan_bwd, without `workspace`: the backward's
+ * scratch (Dn and the per-chain partials) lives in a file-scope device array of
+ * SLOTSCAN_NOALLOC_SCRATCH_BYTES that each device holds for the life of the process.  Shapes whose
+ * slotscan_bwd_workspace(B, T, H, N) exceeds it return SLOTSCAN_ERR_SHAPE before any GPU work
+ * (B*H*N*T <= about 16.7 M: e.g. B*H = 48 chains of T = 1024 steps at N = 192).  The call allocates
+ * nothing (with kernel timing, slotscan_profile, off).  Every call on a device shares that device's array:
+ * calls that overlap on one device race, so a caller serialises them (one stream, or events). */
+#define SLOTSCAN_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int slotscan_bwd_noalloc(const void* k, const void* q, const void* v, int dtype,
+                         const float* gate, const float* fr, int fr_per_token, const float* temp,
+                         int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                         float eps, int occ_bin,
+                         const int32_t* am, const float* kold, const float* vold, const float* oold,
+                         const float* cslog, const float* kfin, const float* vfin, const float* ofin,
+                         const float* dkbuf, const float* dvbuf,
+                         void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
+                         void* stream);
+
 /* Forward scan with the writer epilogue fused in.  Replaces kv_scan_g followed by the full-precision epilogue
  * of the writer layer (memlm_sh.py:453-456 then :473-475):
  *     nsq = kbuf.pow(2).sum(-1);  mem = (kbuf.to(bf16), vbuf.to(bf16), rsqrt(nsq.clamp_min(1e-12)), nsq > 1e-12)

@@ -2290,6 +2290,56 @@ extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dty
                     dk, dq, dv, dgate, dfr, dtemp, stream);
 }
 
+// ------------------------------------------------------------------ allocation-free backward
+// The backward's workspace (Dn and the per-chain partials) in a file-scope device array, for callers that
+// cannot allocate.  Each device holds its own copy for the life of the process; its address is fetched once
+// per device (with that device current) and kept, because in host code the array's name is not a device
+// address.  Every element the kernels read is written earlier in the same call (Dn by rows_bwd for every
+// (row, step) that chain_bwd reads; each chain's partials by chain_bwd before reduce_parts), so nothing has
+// to start at zero, and calls that overlap on one device race on the array.
+static __device__ __align__(256) unsigned char scratch[SLOTSCAN_NOALLOC_SCRATCH_BYTES];
+static std::mutex scratch_mu;
+static void* scratch_dev[64];
+
+static int scratch_ptr(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(SLOTSCAN_ERR_HIP, "device id out of range");
+    std::lock_guard<std::mutex> g(scratch_mu);
+    if (!scratch_dev[dev]) {
+        void* p = nullptr;
+        if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return hip_fail(e, "hipGetSymbolAddress");
+        if (!p || ((uintptr_t)p & 255u)) return fail(SLOTSCAN_ERR_HIP, "scratch array address is not 256-byte aligned");
+        scratch_dev[dev] = p;
+    }
+    *out = scratch_dev[dev];
+    return 0;
+}
+
+extern "C" int slotscan_bwd_noalloc(const void* k, const void* q, const void* v, int dtype,
+                                    const float* gate, const float* fr, int fr_per_token, const float* temp,
+                                    int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                                    float eps, int occ_bin,
+                                    const int32_t* am, const float* kold, const float* vold, const float* oold,
+                                    const float* cslog, const float* kfin, const float* vfin, const float* ofin,
+                                    const float* dkbuf, const float* dvbuf,
+                                    void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
+                                    void* stream) {
+    if (int r = check_common(B, T, H, N, D, G, dtype)) return r;
+    const unsigned __int128 need = (unsigned __int128)(uint64_t)(B * H) * (uint64_t)N * (uint64_t)T * 4u + 255u +
+                                   (unsigned __int128)(uint64_t)(B * H) * 8u;
+    if (need > (unsigned __int128)SLOTSCAN_NOALLOC_SCRATCH_BYTES)
+        return fail(SLOTSCAN_ERR_SHAPE, "slotscan_bwd_noalloc: B*H*N*T*4 (+ partials) exceeds the static scratch of "
+                                        "SLOTSCAN_NOALLOC_SCRATCH_BYTES; use slotscan_bwd with a workspace");
+    if (!dkbuf || !dvbuf) return fail(SLOTSCAN_ERR_NULL, "slotscan_bwd_noalloc: a required pointer is NULL");
+    void* ws = nullptr;
+    if (int r = scratch_ptr(&ws)) return r;
+    return scan_bwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, am, kold, vold,
+                    oold, cslog, kfin, vfin, ofin, dkbuf, dvbuf, nullptr, nullptr, nullptr, ws,
+                    dk, dq, dv, dgate, dfr, dtemp, stream);
+}
+
 extern "C" int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
                                 const float* gate, const float* fr, int fr_per_token, const float* temp,
                                 int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,

@@ -37,6 +37,8 @@ SIGNATURES = {
                             _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "slotscan_bwd_noalloc": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
+                                    _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32] + [_vp] * 17),
     "slotscan_bwd_mem": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
                                 _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32] + [_vp] * 19),
     "slotscan_gen_fwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
