@@ -24,8 +24,8 @@ algorithmic HBM bytes per launch over its average launch time, measured with HIP
 library on the launch stream during the timed region; `step_roofline` applies the same formula to the
 whole step's algorithmic bytes.  Only the dominant kernel carries timing events during the timed steps (each
 timed launch costs its stream a few microseconds); `kernels_ms` times every kernel on the last warm-up
-step.  `cpu_baseline` is the repository's CPU oracle (numpy, fp32, one thread)
-timed on a bounded B-slice of the same workload on this host.
+step.  `cpu_baseline` is the fp32 torch restatement of the reference's torch scan (oracle/torch_scan.py)
+timed with autograd on this host's cores: a B = 1 slice of the same workload, with config 1 beside it.
 """
 import argparse
 import json
@@ -161,61 +161,107 @@ def measured_traffic(workload):
     return out
 
 
-def cpu_baseline(W, seed=1, Bs=12):
-    """The fp32 numpy oracle (oracle/scan_oracle.py), fwd+bwd on a B-slice of the same workload."""
-    import numpy as np
-    from oracle import scan_oracle as SO
-    T, H, N, D, G = W["T"], W["H"], W["N"], W["D"], W["G"]
-    rng = np.random.default_rng(seed)
-    f = np.float32
-    unit = lambda x: (x / np.linalg.norm(x, axis=-1, keepdims=True)).astype(f)
-    k = unit(rng.standard_normal((Bs, T, H, D)).astype(f))
-    q = unit(rng.standard_normal((Bs, T, H, D)).astype(f))
-    v = rng.standard_normal((Bs, T, H, D)).astype(f)
-    g = (1 / (1 + np.exp(-1.5 * rng.standard_normal((Bs, T, H))))).astype(f)
-    fr = rng.uniform(0, 2, (Bs, T, H)).astype(f)
-    NB = (T + G - 1) // G
-    dkb = rng.standard_normal((Bs, NB, H, N, D)).astype(f)
-    dvb = rng.standard_normal((Bs, NB, H, N, D)).astype(f)
-    mem = W.get("mem", False)
+def _host_cpu():
+    """(model name, cores this process may run on) of the host, for the CPU baseline's record."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, len(os.sched_getaffinity(0))
+
+
+def _timed(fn, reps=3):
+    """Median wall-clock seconds of `reps` runs after one warm-up run."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baseline(W, seed=1):
+    """The scan's fp32 torch restatement (oracle/torch_scan.py, the reference's own torch loop
+    slotkern_kv.py:66-123) forward plus autograd backward on this host's cores, all of them
+    (torch.set_num_threads over the CPUs this process may use): BASELINE config 1 in full, and a B = 1
+    slice of the workload at its full T, H, N, D (the full batch's autograd graph would need on the order of
+    100 GB of saved per-step state).  Median of 3 runs after one warm-up each.  `value` is the slice's
+    tokens/s; config 1's is reported beside it."""
+    import torch
+    from oracle.torch_scan import scan_torch
+    model, cores = _host_cpu()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
     hard = not W.get("soft", False)
-    dki = rng.standard_normal((Bs, NB, H, N)).astype(f)
-    t0 = time.perf_counter()
-    kb, vb, info = SO.scan_forward(k, v, g, fr, N, 16.0, G=G, hard=hard, q=q, occ_bin=True, dtype=f)
-    if mem:                                  # the epilogue (memlm_sh.py:474-475) and its autograd
-        nsq = (kb * kb).sum(-1)
-        kinv = 1.0 / np.sqrt(np.maximum(nsq, f(1e-12)))
-        valid = nsq > 1e-12                  # (numpy has no bf16: the copies' cast is not timed)
-        dkb = dkb + 2 * kb * np.where(nsq >= 1e-12, -0.5 * kinv ** 3 * dki, 0.0).astype(f)[..., None]
-    SO.scan_backward(k, v, g, fr, N, 16.0, kb, vb, info, dkb, dvb, G=G, hard=hard, q=q, occ_bin=True,
-                     detach_addr=hard, dtype=f)
-    dt = time.perf_counter() - t0
-    return dict(value=round(Bs * T / dt, 1), unit="tokens/s", cores=1, kind="port",
-                sample=f"B={Bs} slice of the workload (T={T}, H={H}, N={N}, D={D}, G={G}), fp32 numpy oracle "
-                       f"fwd+bwd{' with the writer epilogue' if mem else ''}{'' if hard else ', soft address, attached'}, "
-                       f"{dt:.1f} s", seconds=round(dt, 2))
+    mem = W.get("mem", False)
+
+    def case(B, T, H, N, D, G, sd):
+        gen = torch.Generator().manual_seed(sd)
+        r = lambda *s: torch.randn(*s, generator=gen)
+        unit = lambda x: x / x.norm(dim=-1, keepdim=True)
+        k, q, v = unit(r(B, T, H, D)).requires_grad_(), unit(r(B, T, H, D)).requires_grad_(), r(B, T, H, D).requires_grad_()
+        g = torch.sigmoid(1.5 * r(B, T, H)).requires_grad_()
+        fr = (2 * torch.rand(B, T, H, generator=gen)).requires_grad_()
+        temp = torch.tensor(16.0, requires_grad=True)
+        NB = (T + G - 1) // G
+        dkb, dvb = r(B, NB, H, N, D), r(B, NB, H, N, D)
+        dki = r(B, NB, H, N)
+
+        def step():
+            kb, vb = scan_torch(k, v, g, fr, N, temp, G=G, hard=hard, detach_addr=hard, q=q, occ_bin=True)
+            outs, ups = (kb, vb), (dkb, dvb)
+            if mem:                          # the writer epilogue (memlm_sh.py:474-475) and its autograd
+                kinv = torch.rsqrt(kb.pow(2).sum(-1).clamp_min(1e-12))
+                outs, ups = (kb.to(torch.bfloat16), vb.to(torch.bfloat16), kinv), (dkb, dvb, dki)
+            torch.autograd.grad(outs, (k, q, v, g, fr, temp), ups)
+        return _timed(step)
+
+    try:
+        t1 = case(2, 128, 1, 64, 64, 8, 0)                              # BASELINE config 1
+        ts = case(1, W["T"], W["H"], W["N"], W["D"], W["G"], seed)      # B = 1 slice of the workload
+    finally:
+        torch.set_num_threads(prev)
+    mode = ("hard, detached address" if hard else "soft address, attached") + (", writer epilogue" if mem else "")
+    return dict(value=round(W["T"] / ts, 1), unit="tokens/s", cores=cores, kind="port",
+                sample=f"B=1 slice of the workload (T={W['T']}, H={W['H']}, N={W['N']}, D={W['D']}, G={W['G']}, "
+                       f"{mode}): fp32 torch restatement of the reference's torch scan (oracle/torch_scan.py), "
+                       f"forward + autograd backward, median of 3 after a warm-up, {ts:.2f} s per run",
+                seconds=round(ts, 3), threads=cores, cpu_model=model, os_cpu_count=os.cpu_count(),
+                config1={"tokens_per_s": round(2 * 128 / t1, 1), "seconds": round(t1, 4),
+                         "shape": "B=2, T=128, H=1, N=64, D=64, G=8, fwd+bwd, fp32"})
 
 
-def cpu_baseline_read(W, seed=3, Bs=32):
-    """The numpy oracle read (oracle/read_oracle.py, fp64 einsums with the bf16 roundings), one reader layer
-    on a B-slice of the workload."""
-    import numpy as np
-    from oracle import read_oracle as RO
-    T, H, N, D, NQ = W["T"], W["H"], W["N"], W["D"], W["NQ"]
-    rng = np.random.default_rng(seed)
-    unit = lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True)
-    K = unit(rng.standard_normal((Bs, 1, H, N, D)))
-    V = rng.standard_normal((Bs, 1, H, N, D))
-    q = unit(rng.standard_normal((Bs, 1, H, T * NQ, D)))
-    sc = np.log1p(np.exp(rng.standard_normal((Bs, 1, H, T * NQ)))) + 1.0
-    kinv = np.ones((Bs, 1, H, N))
-    valid = np.ones((Bs, 1, H, N), bool)
-    t0 = time.perf_counter()
-    RO.read_forward(q, K, V, kinv, valid, sc, bf16=True)
-    dt = time.perf_counter() - t0
-    return dict(value=round(Bs * T / dt, 1), unit="tokens/s (one reader layer)", cores=1, kind="port",
-                sample=f"B={Bs} slice, one reader layer (T={T}, H={H}, N={N}, D={D}), numpy oracle read, {dt:.2f} s",
-                seconds=round(dt, 2))
+def cpu_baseline_read(W, seed=3):
+    """The read's fp32 torch restatement (oracle/torch_scan.read_torch, memlm_sh.py:383-395) on this host's
+    cores: the whole workload (every reader layer at the full batch), median of 3 after a warm-up."""
+    import torch
+    from oracle.torch_scan import read_torch
+    model, cores = _host_cpu()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    Bs, T, H, N, D, NQ, layers = W["B"], W["T"], W["H"], W["N"], W["D"], W["NQ"], W["layers"]
+    gen = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=gen)
+    unit = lambda x: x / x.norm(dim=-1, keepdim=True)
+    K, V = unit(r(Bs, 1, H, N, D)), r(Bs, 1, H, N, D)
+    q = unit(r(Bs, 1, H, T * NQ, D))
+    sc = torch.nn.functional.softplus(r(Bs, 1, H, T * NQ)) + 1.0
+    kinv, valid = torch.ones(Bs, 1, H, N), torch.ones(Bs, 1, H, N, dtype=torch.bool)
+    try:
+        with torch.no_grad():
+            dt = _timed(lambda: [read_torch(q, K, V, kinv, valid, sc) for _ in range(layers)])
+    finally:
+        torch.set_num_threads(prev)
+    return dict(value=round(Bs * T / dt, 1), unit="tokens/s", cores=cores, kind="port",
+                sample=f"the whole workload: {layers} reader layers at B={Bs} (T={T}, H={H}, N={N}, D={D}), fp32 "
+                       f"torch restatement of the read (oracle/torch_scan.read_torch), median of 3 after a "
+                       f"warm-up, {dt:.3f} s per run",
+                seconds=round(dt, 4), threads=cores, cpu_model=model)
 
 
 def bench_stream(args, W):

@@ -1,6 +1,9 @@
-"""Independent torch statement of the slot-scan forward, used by the tests ONLY to obtain gradients by
-autograd (float64 on the CPU).  It pins the oracle's hand-written backward: autograd derives the
-adjoints from this forward, the oracle writes them out by hand.
+"""Independent torch statement of the slot-scan forward -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module: the tests use it
+(float64 on the CPU) to obtain gradients by autograd, which pins the numpy oracle's hand-written backward
+(autograd derives the adjoints from this forward, scan_oracle.py writes them out by hand); bench.py times it
+in float32 with autograd on the host's cores as the CPU baseline.  The product path never imports it.
 
 Follows /root/reference/gqa25/slotkern_kv.py:66-123 (the reference's own torch loop), with teacher
 forcing added so that a hard-address run can follow a given address sequence."""
@@ -49,3 +52,13 @@ def scan_torch(k, v, gate, fr, N, temp, G=1, hard=False, hard_gate=False, eps=1e
         V = (1 - w) * V + w * v[:, t].unsqueeze(2)
         o = (1 - w[..., 0]) * o + w[..., 0]
     return torch.stack(kb, 1), torch.stack(vb, 1)
+
+
+def read_torch(qh, kbuf, buf, kinv, valid, scale):
+    """The kernel-level core of SharedMixer._read (/root/reference/gqa25/memlm_sh.py:383-395) in torch, in the
+    inputs' dtype: per (b, block, head), qh (B,NB,H,M,DK) unit queries against that block's copy kbuf
+    (B,NB,H,N,DK), scores times kinv (B,NB,H,N) and the per-query multiplier scale (B,NB,H,M), the softmax
+    over the valid rows (an all-invalid block reads 0), then the value contraction with buf (B,NB,H,N,DV)."""
+    sc = torch.einsum("bjhmd,bjhnd->bjhmn", qh, kbuf) * kinv.unsqueeze(-2) * scale.unsqueeze(-1)
+    att = torch.nan_to_num(torch.softmax(sc.masked_fill(~valid.unsqueeze(-2), float("-inf")), -1))
+    return torch.einsum("bjhmn,bjhnv->bjhmv", att, buf)

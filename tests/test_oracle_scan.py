@@ -2,7 +2,7 @@
 
 Forward: closed forms, fill-order and tie-break rules, stride and chunking identities, the per-token /
 scalar fr identity, and an independent scalar loop.  Backward: torch autograd of an independent torch
-forward (tests/torch_scan_ref.py) in every mode, and central finite differences in soft mode."""
+forward (oracle/torch_scan.py) in every mode, and central finite differences in soft mode."""
 import itertools
 import math
 
@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import scan_oracle as SO
-from torch_scan_ref import scan_torch
+from oracle.torch_scan import scan_torch
 
 
 def _inputs(B, T, H, DK, DV, seed, per_token_fr=False, sep_q=False, clustered=False):
