@@ -380,6 +380,8 @@ def bench_window(args, W):
     t1 = time.perf_counter()
     L.profile(False)
     prof = L.profile_read()
+    if args.copy_calibration:
+        copy_calibration(dev)
     ms = (t1 - t0) * 1e3 / args.steps
     f1, b1 = window_bytes(B, T, Hk, Hk, D)
     f2, b2 = window_bytes(B, T, Hk * (NQ - 1), Hk, D)
