@@ -64,8 +64,9 @@ int slotscan_fwd(const void* k, const void* q, const void* v, int dtype,
                  float* kold, float* vold, float* oold, float* cslog,
                  float* kfin, float* vfin, float* ofin, void* stream);
 
-/* Bytes of device workspace slotscan_bwd needs: the row adjoint Dn (B*H, N, T) fp32 plus (B*H, 2) fp32
- * per-chain partials.  The reference allocates Dn inside _KVScanC.backward (slotkern_cuda.py:524). */
+/* Bytes of device workspace slotscan_bwd needs: the row adjoint Dn (B*H, N, T) fp32 plus (B*H*chunks, 2)
+ * fp32 partials of the address backward, which runs each chain as concurrent chunks of its steps (chunks
+ * depends on B*H and T only).  The reference allocates Dn inside _KVScanC.backward (slotkern_cuda.py:524). */
 size_t slotscan_bwd_workspace(int64_t B, int64_t T, int64_t H, int64_t N);
 
 /* Which backward kernels slotscan_bwd (mem = 0) or slotscan_bwd_mem (mem = 1) runs for a shape, as a bit

@@ -1115,8 +1115,9 @@ struct ChainBwdArgs {
     const void* q; const float* gate; const float* fr; const float* temp;
     const int32_t* am; const float* kold; const float* oold; const float* cslog; const float* kfin; const float* ofin;
     const float* dn;                                     // (B*H, N, T)
-    void* dq; float* dg; float* dfr; float* part;        // part (B*H, 2): dtemp and scalar-dfr partials
+    void* dq; float* dg; float* dfr; float* part;        // part (B*H*chunks, 2): dtemp and scalar-dfr partials
     int T, H, N; float eps; int frt, occb;
+    int wpc;                                             // chain_bwd_w: windows per chunk (grid.y = chunks)
 };
 
 // OCCB (occ_bin) is a template flag: with it the occupancy enters only through [o >= eps] and its
@@ -1439,7 +1440,10 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 // Windowed address backward for the occ_bin mode.  With occupancy entering only through [o >= eps], the
 // adjoint of step t needs no carry from step t + 1: given the replayed occupancy at t, the logged cosines
 // and Dn, every step's softmax adjoint is independent.  The chain is therefore processed in windows of
-// WIN = 16 steps (reverse order), by NW = 4 or 8 waves:
+// WIN = 16 steps (reverse order), by NW = 4 or 8 waves.  The chain is also cut into chunks of `wpc` windows, one
+// workgroup each (grid (B*H, chunks)): nothing carries across steps except the keys and the occupancy, and the
+// state at a chunk's end t_end is exact from the undo log -- row n holds kold (oold) of the first write to n at
+// or after t_end, or kfin (ofin) when no later step writes it -- so the chunks run concurrently:
 //   replay   every lane replays the occupancy of its slot rows (n = lane + 64 j) backwards through the
 //            window, recording taken_n(t);
 //   softmax  wave w owns steps SPW w .. SPW w + SPW - 1 of the window (SPW = 16 / NW): the whole masked
@@ -1505,18 +1509,54 @@ void chain_bwd_w(ChainBwdArgs a) {
     const bool frt = a.frt != 0;
     const int d0 = wave * DW;                           // this wave's first dim
 
-    // ---- Kh_end (the final keys, normalised) into the B-operand layout; full-row norms through LDS
+    // ---- this chunk: windows [m_lo, m_hi), steps up to t_end.  s_fw[n]: the first step at or after t_end that
+    // writes row n (T: none), from the address log with LDS integer minima (order-independent)
+    const int nwin = (T + WIN - 1) / WIN;
+    const int m_lo = blockIdx.y * a.wpc, m_hi = min(nwin, m_lo + a.wpc);
+    const int t_end = min(m_hi * WIN, T);
+    int* s_fw = reinterpret_cast<int*>(s_cs);           // [NR], before the first window
+    for (int n = tid; n < NR; n += NT) s_fw[n] = T;
+    __syncthreads();
+    for (int t = t_end + tid; t < T; t += NT) atomicMin(&s_fw[min(max(a.am[tok0 + (size_t)t * H], 0), NR - 1)], t);
+    __syncthreads();
+    // the key row n holds at t_end: kold of its first later write, else the final key
+    auto key_src = [&](int row) -> const float* {
+        const int fw = s_fw[row];
+        return fw < T ? a.kold + (tok0 + (size_t)fw * H) * D : a.kfin + ((size_t)bh * N + row) * D;
+    };
+
+    // ---- Kh at t_end (normalised) into the B-operand layout; full-row norms through LDS.  A row restored from
+    // kold is normalised exactly as the window undo (S2, S7) normalises it -- quarter sums in the same order,
+    // then sum4rows -- so a chunk starts from bitwise the keys the sequential reverse pass would hold there,
+    // and the results do not depend on the chunking.
     f32x16 Kv[NBW][NCH];
 #define KREG(kk, nb) Kv[nb][(kk) >> 4][(kk) & 15]
     {
         float* s_nrm = &s_W[0][0];                      // [NW][NR] scratch before the first window
+        float* s_n2 = s_nrm + NW * NR;                  // [NR]: |kold row|^2 in the undo's order
+        for (int r0 = wave * 16; r0 < NR; r0 += NW * 16) {
+            const int row = r0 + c;                     // lane (row c, quarter grp), as S2
+            const int fw = row < N ? s_fw[row] : T;
+            float ss = 0.f;
+            if (fw < T) {
+                const float* src = a.kold + (tok0 + (size_t)fw * H) * D + grp * (D / 4);
+#pragma unroll
+                for (int u = 0; u < D / 16; u++) {
+                    const float4 x = *reinterpret_cast<const float4*>(src + 4 * u);
+                    ss = fmaf(x.x, x.x, ss); ss = fmaf(x.y, x.y, ss); ss = fmaf(x.z, x.z, ss); ss = fmaf(x.w, x.w, ss);
+                }
+            }
+            const float kn = sum4rows(ss);
+            if (grp == 0) s_n2[row] = kn;
+        }
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) {
             const int row = kk + KK * grp;
+            const float* src = row < N ? key_src(row) : nullptr;
             float ss = 0.f;
 #pragma unroll
             for (int nb = 0; nb < NBW; nb++) {
-                const float x = row < N ? a.kfin[((size_t)bh * N + row) * D + d0 + 16 * nb + c] : 0.f;
+                const float x = row < N ? src[d0 + 16 * nb + c] : 0.f;
                 KREG(kk, nb) = x;
                 ss = fmaf(x, x, ss);
             }
@@ -1530,6 +1570,7 @@ void chain_bwd_w(ChainBwdArgs a) {
             float nsq = 0.f;
 #pragma unroll
             for (int w = 0; w < NW; w++) nsq += s_nrm[w * NR + row];
+            if (row < N && s_fw[row] < T) nsq = s_n2[row];
             const float ki = rsq_clamped(nsq);
 #pragma unroll
             for (int nb = 0; nb < NBW; nb++) KREG(kk, nb) *= ki;
@@ -1537,14 +1578,14 @@ void chain_bwd_w(ChainBwdArgs a) {
     }
     float o_me[RPL];
 #pragma unroll
-    for (int j = 0; j < RPL; j++) {
+    for (int j = 0; j < RPL; j++) {                    // the occupancy at t_end, likewise
         const int n = lane + 64 * j;
-        o_me[j] = n < N ? a.ofin[(size_t)bh * N + n] : 0.f;
+        const int fw = n < N ? s_fw[n] : T;
+        o_me[j] = n >= N ? 0.f : (fw < T ? a.oold[tok0 + (size_t)fw * H] : a.ofin[(size_t)bh * N + n]);
     }
 
     // ---- window prefetch into registers.  Every load is a uniform (scalar) base plus ONE 32-bit per-lane
     // offset computed once, so the prefetch costs no per-load address registers.
-    const int nwin = (T + WIN - 1) / WIN;
     float ncs[UCS], ndn[UDN];
     uint4 nko[UKO], nq[UQ];
     float nsc = 0.f;
@@ -1603,8 +1644,9 @@ void chain_bwd_w(ChainBwdArgs a) {
     };
 
     float dtemp_acc = 0.f, dfr_acc = 0.f;
-    load_win(nwin - 1);
-    for (int m = nwin - 1; m >= 0; m--) {
+    __syncthreads();                                    // s_fw (in s_cs) is read before the first window's S1
+    load_win(m_hi - 1);
+    for (int m = m_hi - 1; m >= m_lo; m--) {
         const int t0 = m * WIN, nt = min(WIN, T - t0);
         // S1: publish the prefetched window into LDS
 #pragma unroll
@@ -1777,7 +1819,7 @@ void chain_bwd_w(ChainBwdArgs a) {
         }
         __syncthreads();                                                      // B2
         // S5: prefetch the next (earlier) window while the matrix cores run
-        if (m > 0) load_win(m - 1);
+        if (m > m_lo) load_win(m - 1);
         // S6: dqn over every row for this wave's dims, with the window-end keys
         f32x4 acc[NBW];
 #pragma unroll
@@ -1900,12 +1942,14 @@ void chain_bwd_w(ChainBwdArgs a) {
         float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w++) { s0 += s_fin[0][w]; s1 += s_fin[1][w]; }
-        a.part[2 * (size_t)bh + 0] = s0;
-        a.part[2 * (size_t)bh + 1] = s1;
+        const size_t pi = (size_t)bh * gridDim.y + blockIdx.y;
+        a.part[2 * pi + 0] = s0;
+        a.part[2 * pi + 1] = s1;
     }
 }
 
-// fixed-order sum of the per-chain partials: dtemp = sum_bh part[bh][0]; scalar dfr = sum_bh part[bh][1]
+// fixed-order sum of the partials (one per chain, or per chain and chunk): dtemp = sum_i part[i][0]; scalar
+// dfr = sum_i part[i][1]
 __global__ __launch_bounds__(256) void reduce_parts(const float* __restrict__ part, int nbh, float* dtemp,
                                                     float* dfr) {
     __shared__ float s0[256], s1[256];
@@ -1933,11 +1977,24 @@ hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
 #undef SLOT_CF
     return hipErrorInvalidValue;
 }
+// chain_bwd_w's chunks: windows per chunk so that the launch has about 3,072 workgroups (six per CU slot
+// pair at two resident per CU), and at least 4 windows each, so that a chunk's start (a scan of the later
+// address log and one gather of the key rows) stays a small part of its work.
+static int chain_bwd_wpc(int64_t BH, int64_t T) {
+    const int64_t nwin = (T + WIN - 1) / WIN;
+    const int64_t w = (nwin * BH + 3071) / 3072;
+    return (int)std::min<int64_t>(nwin, std::max<int64_t>(4, w));
+}
+static int64_t chain_bwd_chunks(int64_t BH, int64_t T) {
+    const int64_t nwin = (T + WIN - 1) / WIN, w = chain_bwd_wpc(BH, T);
+    return (nwin + w - 1) / w;
+}
+
 template <int D, typename TI>
 hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
-    if (a.occb) {                                        // windowed kernel, four waves
+    if (a.occb) {                                        // windowed kernel, four waves, time chunks
         constexpr int NW = 4;
-        dim3 grid(B * a.H), block(64 * NW);
+        dim3 grid(B * a.H, (unsigned)chain_bwd_chunks((int64_t)B * a.H, a.T)), block(64 * NW);
         if (a.N <= 64) slothost::launch((chain_bwd_w<D, 1, NW, TI>), grid, block, 0, st, a);
         else if (a.N <= 128) slothost::launch((chain_bwd_w<D, 2, NW, TI>), grid, block, 0, st, a);
         else if (a.N <= 192) slothost::launch((chain_bwd_w<D, 3, NW, TI>), grid, block, 0, st, a);
@@ -2205,9 +2262,9 @@ extern "C" int slotscan_bwd_plan(int64_t T, int64_t H, int64_t N, int64_t D, int
 }
 
 extern "C" size_t slotscan_bwd_workspace(int64_t B, int64_t T, int64_t H, int64_t N) {
-    // Dn (B*H, N, T) fp32, then the per-chain partials (B*H, 2) fp32, 256-byte aligned
+    // Dn (B*H, N, T) fp32, then the partials (B*H*chunks, 2) fp32 of the address backward, 256-byte aligned
     const size_t dn = (size_t)B * H * N * T * sizeof(float);
-    return ((dn + 255) & ~(size_t)255) + (size_t)B * H * 2 * sizeof(float);
+    return ((dn + 255) & ~(size_t)255) + (size_t)B * H * chain_bwd_chunks(B * H, T) * 2 * sizeof(float);
 }
 
 // The backward of both contracts: fp32 snapshot gradients (dkbuf, dvbuf) or, when dkbm is set, the
@@ -2258,7 +2315,9 @@ static int scan_bwd(const void* k, const void* q, const void* v, int dtype,
     }
     if (e != hipSuccess) return hip_fail(e, "rows_bwd launch");
     ChainBwdArgs ca{q, gate, fr, temp, am, kold, oold, cslog, kfin, ofin, dn, dq, dgate, dfr, part,
-                    (int)T, (int)H, (int)N, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0};
+                    (int)T, (int)H, (int)N, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0,
+                    chain_bwd_wpc(B * H, T)};
+    const int nparts = (int)(occ_bin ? B * H * chain_bwd_chunks(B * H, T) : B * H);
     {
         slothost::Scope sc(SLOTSCAN_K_CHAIN_BWD, st);
         if (D == 128) e = dtype == SLOTSCAN_BF16 ? launch_chain_bwd<128, bf16_t>(ca, (int)B, st) : launch_chain_bwd<128, float>(ca, (int)B, st);
@@ -2267,7 +2326,7 @@ static int scan_bwd(const void* k, const void* q, const void* v, int dtype,
     if (e != hipSuccess) return hip_fail(e, "chain_bwd launch");
     {
         slothost::Scope sc(SLOTSCAN_K_REDUCE, st);
-        slothost::launch(reduce_parts, dim3(1), dim3(256), 0, st, part, (int)(B * H), dtemp,
+        slothost::launch(reduce_parts, dim3(1), dim3(256), 0, st, part, nparts, dtemp,
                            fr_per_token ? (float*)nullptr : dfr);
         e = hipGetLastError();
     }
@@ -2328,7 +2387,7 @@ extern "C" int slotscan_bwd_noalloc(const void* k, const void* q, const void* v,
                                     void* stream) {
     if (int r = check_common(B, T, H, N, D, G, dtype)) return r;
     const unsigned __int128 need = (unsigned __int128)(uint64_t)(B * H) * (uint64_t)N * (uint64_t)T * 4u + 255u +
-                                   (unsigned __int128)(uint64_t)(B * H) * 8u;
+                                   (unsigned __int128)(uint64_t)(B * H) * (uint64_t)chain_bwd_chunks(B * H, T) * 8u;
     if (need > (unsigned __int128)SLOTSCAN_NOALLOC_SCRATCH_BYTES)
         return fail(SLOTSCAN_ERR_SHAPE, "slotscan_bwd_noalloc: B*H*N*T*4 (+ partials) exceeds the static scratch of "
                                         "SLOTSCAN_NOALLOC_SCRATCH_BYTES; use slotscan_bwd with a workspace");

@@ -58,10 +58,17 @@ def test_single_hip_runtime_in_process():
     assert len(libs) == 1, libs
 
 
-def test_workspace_size():
-    B, T, H, N = 3, 100, 2, 40
+@pytest.mark.parametrize("B,T,H,N,chunks", [
+    (3, 100, 2, 40, 2),        # 7 windows of 16 steps, at least 4 per chunk
+    (64, 1024, 6, 192, 8),     # config 2: 384 chains x 8 chunks of 8 windows = 3,072 workgroups
+    (512, 128, 6, 96, 1),      # config 3, (512, 128): 3,072 chains already, one chunk each
+    (1, 8, 1, 16, 1),
+])
+def test_workspace_size(B, T, H, N, chunks):
+    """Dn (B*H, N, T) fp32, 256-byte aligned, then two fp32 partials per chain and time chunk of the address
+    backward."""
     dn = B * H * N * T * 4
-    assert L.lib().slotscan_bwd_workspace(B, T, H, N) == ((dn + 255) & ~255) + B * H * 2 * 4
+    assert L.lib().slotscan_bwd_workspace(B, T, H, N) == ((dn + 255) & ~255) + B * H * chunks * 2 * 4
 
 
 def _fwd_call(**over):
