@@ -1438,65 +1438,124 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 
 // ====================================================================================== chain_bwd_w
 // Windowed address backward for the occ_bin mode.  With occupancy entering only through [o >= eps], the
-// adjoint of step t needs no carry from step t + 1: given the replayed occupancy at t, the logged cosines
-// and Dn, every step's softmax adjoint is independent.  The chain is therefore processed in windows of
-// WIN = 16 steps (reverse order), by NW = 4 or 8 waves.  The chain is also cut into chunks of `wpc` windows, one
-// workgroup each (grid (B*H, chunks)): nothing carries across steps except the keys and the occupancy, and the
-// state at a chunk's end t_end is exact from the undo log -- row n holds kold (oold) of the first write to n at
-// or after t_end, or kfin (ofin) when no later step writes it -- so the chunks run concurrently:
-//   replay   every lane replays the occupancy of its slot rows (n = lane + 64 j) backwards through the
-//            window, recording taken_n(t);
-//   softmax  wave w owns steps SPW w .. SPW w + SPW - 1 of the window (SPW = 16 / NW): the whole masked
-//            softmax adjoint of a step (max,
-//            sum e, sum e dw over every row, the lowest free row) is a wave reduction, no cross-wave merge;
-//            W[t][n] = temp dz_n(t) goes to LDS;
-//   dq       wave w owns dims [w DW, (w+1) DW), DW = D / NW: dqn[t][d] = sum_n W[t][n] Kh_n(t)[d] as fp32 MFMA over
-//            the window, with Kh = K / max(|K|, 1e-6) the normalised keys (the reference's order: normalise,
-//            then contract, slotkern_kvt.py:86-90), held in registers in the MFMA B-operand layout as the
-//            keys AFTER the window's writes (Kh_end); the rows the window rewrote are corrected exactly with
-//            the undo deltas d_s = Kh(kold_s) - Kh_{a_s}(after write s), Kh_n(t) = Kh_end_n + sum over
-//            s >= t with a_s = n of d_s, as a second small MFMA (16 x 16 x DW).  Every term is bounded by
-//            |dz| (|Kh| <= 1): an empty row has Kh = 0, never K * 1e6;
-//   undo     every wave restores its dims of each rewritten row from kold (the next window's Kh_end);
-//   dq       the clamped-normalisation Jacobian of q needs <dqn, q> over all of D: one LDS exchange.
-// B-operand layout (v_mfma_f32_16x16x4f32, B[k][j] at lane 16k + j): lane l of wave w holds
-//   Kh[row kk + KK*(l >> 4)][dim w*DW + 16*nb + (l & 15)] = Kv[nb][kk >> 4][kk & 15],  kk < KK = 16*RPL,
-// nb < DW/16 (k-step kk contracts rows kk, KK + kk, 2 KK + kk, 3 KK + kk, so four consecutive k-steps of a
-// lane's A operand are one 16-byte LDS read).
-// Kv is an array of 16-float register vectors, so the undo can address row kk with a uniform dynamic index
-// (M0-relative moves, s_set_gpr_idx) instead of branching over every possible row.
-// A operand: lane l holds W[step l & 15][row kk + KK*(l >> 4)]; result lane l, register r:
-//   dqn[step 4*(l >> 4) + r][dim w*DW + 16*nb + (l & 15)].
+// adjoint of step t needs no carry from step t + 1: given the occupancy at t, the logged cosines and Dn, every
+// step's softmax adjoint is independent, and the keys enter only through dq.  The chain is cut into chunks of
+// `wpc` 16-step windows, one workgroup each (grid (B*H, chunks)): the state at a chunk's end t_end is exact
+// from the undo log -- row n holds kold (oold) of its first write at or after t_end, or kfin (ofin) when no
+// later step writes it -- so the chunks run concurrently.  A workgroup of NW = D / 16 waves walks its windows
+// in reverse:
+//   S1  publish the prefetched window: cosines and Dn step-major, kold and query rows, the step scalars;
+//   S2  |kold_i|^2 of each write (one wave: lane = (write, part)), and per write the next write to the same row
+//       inside the window and whether it is the row's first;
+//   S4  the softmax adjoints of all 16 steps at once: step s is a group of NC = NT / 16 lanes (one or two DPP
+//       rows), each lane RPC consecutive slot rows.  The occupancy at s follows from the window-end occupancy
+//       and the window's later writes; the exponentials are shifted by the largest z over the eligible rows
+//       (the occupied ones and the lowest free one, a step-group max); SS and sum e dw are step-group sums;
+//       W[s][n] = temp dz_n goes to LDS; dgate = Dn of the written row; dfr in closed form over the occupied
+//       rows; dtemp accumulates sum dz cs;
+//   S6  dqn = W Kh as fp32 MFMA (v_mfma_f32_16x16x4f32), wave w owning dims [16 w, 16 w + 16).  The normalised
+//       keys stay in LDS TRANSPOSED (dim-major, row stride P = NR + 4): k-step kk contracts rows KK g + kk for
+//       lane group g, so four consecutive k-steps of a lane's B operand are one 16-byte read, and so are its
+//       A operand's from W (the reference's order: normalise, then contract, slotkern_kvt.py:86-90);
+//   S7  the undo, every write at once: x_i = Kh(kold_i); the key after write i is Kh(kold_j) of the next write
+//       j to the same row in the window, else the window-end key; delta_i = x_i - after_i.  Then each row the
+//       window wrote takes x of its FIRST write: the keys at the window start;
+//   S8  the rewritten rows' correction, sum_{s >= t} W[t][a_s] delta_s, as a 16 x 16 x 16 MFMA;
+//   S9  dq = qinv (dqn - qhat <qhat, dqn>) (qinv dqn where |q| < 1e-6), one LDS exchange for the dot products.
+// Every Kh value is an element times rsq_clamped(|row|^2), |row|^2 summed in one fixed order (a lane's part
+// of 4-element pieces, then sum4rows) wherever a key is normalised, so a chunk starts from bitwise the keys
+// the reverse walk of the whole chain would hold there: the results do not depend on the chunking.
 #define WIN 16
 
-template <int D, int RPL, int NW, typename TI>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * NW, 64 * NW), amdgpu_waves_per_eu(NW == 8 ? 4 : 2)))
-void chain_bwd_w(ChainBwdArgs a) {
+// Reductions over the NC lanes of one step in the softmax phase: one DPP row (NC = 16) or two (NC = 32, the
+// row pair joined by a permlane16 swap); every lane of the group gets the bitwise-same result.
+template <int NC> __device__ __forceinline__ float step_sum(float v) {
+    v = rowsum16(v);
+    if constexpr (NC == 32) {
+        auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    return v;
+}
+template <int NC> __device__ __forceinline__ float step_max(float v) {
+    v = rowmax16(v);
+    if constexpr (NC == 32) {
+        auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    }
+    return v;
+}
+template <int NC> __device__ __forceinline__ int step_min(int v) {
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, SLOT_DPP_XOR1, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, SLOT_DPP_XOR2, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, SLOT_DPP_HMIR, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, SLOT_DPP_MIR, 0xF, 0xF, false));
+    if constexpr (NC == 32) {
+        auto p = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+        v = min((int)p[0], (int)p[1]);
+    }
+    return v;
+}
+
+// The lowest index over a step's lanes with two payload values: at every stage a lane takes its partner's
+// triple when the partner's index is smaller (indices are distinct or equal-with-equal-payload).
+template <int CTRL> __device__ __forceinline__ void argmin_stage(int& i, float& x, float& y) {
+    const int i2 = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false);
+    const float x2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+    const float y2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), CTRL, 0xF, 0xF, false));
+    const bool t = i2 < i;
+    i = t ? i2 : i; x = t ? x2 : x; y = t ? y2 : y;
+}
+template <int NC> __device__ __forceinline__ void step_argmin(int& i, float& x, float& y) {
+    argmin_stage<SLOT_DPP_XOR1>(i, x, y);
+    argmin_stage<SLOT_DPP_XOR2>(i, x, y);
+    argmin_stage<SLOT_DPP_HMIR>(i, x, y);
+    argmin_stage<SLOT_DPP_MIR>(i, x, y);
+    if constexpr (NC == 32) {
+        auto pi = __builtin_amdgcn_permlane16_swap((uint32_t)i, (uint32_t)i, false, false);
+        auto px = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        auto py = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+        const bool lo = (int)pi[0] <= (int)pi[1];
+        i = lo ? (int)pi[0] : (int)pi[1];
+        x = __uint_as_float(lo ? px[0] : px[1]);
+        y = __uint_as_float(lo ? py[0] : py[1]);
+    }
+}
+
+template <int D, int RPL, typename TI>
+__global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
+    constexpr int NW = D / 16;                          // waves: wave w owns dims [16 w, 16 w + 16)
     constexpr int NT = 64 * NW;
-    constexpr int SPW = WIN / NW;                       // window steps per wave in the softmax phase
-    constexpr int GS = RPL >= 3 ? 1 : SPW;              // of which processed in lockstep
     constexpr int NR = 64 * RPL;                        // slot-row capacity
     constexpr int KK = NR / 4;                          // MFMA k-steps over the rows
-    constexpr int DW = D / NW;                          // dims per wave
-    constexpr int NBW = DW / 16;                        // MFMA column blocks per wave
-    constexpr int NCH = KK / 16;                        // 16-row-group chunks of a key column block
-    constexpr int SWS = NR + 4;                         // W row stride (conflict-free A-operand reads)
-    constexpr int UKO = (WIN * D / 4 + NT - 1) / NT;    // uint4 per lane: a window's kold rows (fp32)
+    constexpr int P = NR + 4;                           // transposed key stride: 4 mod 32 banks
+    constexpr int SW = NR + 4;                          // W row stride, likewise
+    constexpr int SC = NR + 2;                          // cosine / Dn row stride (step-major): 2 mod 32
+    constexpr int KOS = D + 4;                          // kold / query row stride
+    constexpr int NC = NT / WIN;                        // lanes per step in the softmax phase
+    constexpr int RPC = NR / NC;                        // slot rows per lane in the softmax phase
+    constexpr int DPT = D / NC;                         // dims per lane in the undo (4)
     constexpr int EPU = 16 / (int)sizeof(TI);
-    constexpr int UQ = (WIN * D / EPU + NT - 1) / NT;   // uint4 per lane: a window's queries
-    constexpr int UCS = (WIN * NR + NT - 1) / NT;       // floats per lane: a window's cosines
-    constexpr int UDN = (NR * WIN + NT - 1) / NT;       // floats per lane: a window's Dn
+    constexpr int UCS = (WIN * NR + NT - 1) / NT;       // per-lane prefetch: cosines, Dn
+    constexpr int UKO = (WIN * D / 4 + NT - 1) / NT;    // kold rows (uint4)
+    constexpr int UQ = (WIN * D / EPU + NT - 1) / NT;   // query rows (uint4)
     constexpr bool BF = sizeof(TI) == 2;
-    __shared__ __align__(16) float s_ko[WIN][D];
-    __shared__ __align__(16) float s_q[WIN][D];
-    __shared__ float s_cs[WIN * NR];                    // row stride N
-    __shared__ float s_dn[NR][WIN + 1];
-    __shared__ float s_W[WIN][SWS];
-    __shared__ __align__(16) float s_delta[WIN][D];
-    __shared__ int s_am[WIN];
-    __shared__ float s_g[WIN], s_fr[WIN], s_oo[WIN];
-    __shared__ float2 s_proj[NW][WIN];
+    static_assert(DPT == 4 && RPC % 2 == 0 && (KK / 4) % 2 == 0, "layout assumptions");
+    __shared__ __align__(16) float sKT[D * P];          // normalised keys, transposed
+    __shared__ __align__(16) float sW[WIN * SW];
+    constexpr int CSN = WIN * SC > WIN * D ? WIN * SC : WIN * D;
+    __shared__ __align__(16) float sCS[CSN];            // cosines [step][row]; the undo deltas [step][D] after S4
+    __shared__ __align__(16) float sDN[WIN * SC];       // Dn [step][row]
+    __shared__ __align__(16) float sKO[WIN * KOS];      // kold rows of the window's writes
+    __shared__ __align__(16) float sQ[WIN * KOS];       // query rows
+    __shared__ float sO[NR];                            // occupancy at the window end
+    __shared__ u32 s_tkm[NR];                           // per row: bit s = occupied at window step s
+    __shared__ __align__(16) int s_am[WIN];
+    __shared__ __align__(16) float s_oo[WIN];
+    __shared__ int s_nx[WIN], s_first[WIN];
+    __shared__ float s_g[WIN], s_fr[WIN], s_kil[WIN], s_qi[WIN], s_pr[WIN];
     __shared__ float s_fin[2][NW];
+    float* sDel = sCS;
 
     const int T = a.T, H = a.H, N = a.N;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
@@ -1507,131 +1566,90 @@ void chain_bwd_w(ChainBwdArgs a) {
     const float fr_s = a.frt ? 0.f : a.fr[0];
     const float eps = a.eps;
     const bool frt = a.frt != 0;
-    const int d0 = wave * DW;                           // this wave's first dim
+    const int d0 = 16 * wave;
 
-    // ---- this chunk: windows [m_lo, m_hi), steps up to t_end.  s_fw[n]: the first step at or after t_end that
-    // writes row n (T: none), from the address log with LDS integer minima (order-independent)
+    // ---- this chunk: windows [m_lo, m_hi), steps before t_end.  s_fw[n]: the first step at or after t_end
+    // that writes row n (T: none), from the address log by LDS integer minima (order-independent)
     const int nwin = (T + WIN - 1) / WIN;
     const int m_lo = blockIdx.y * a.wpc, m_hi = min(nwin, m_lo + a.wpc);
     const int t_end = min(m_hi * WIN, T);
-    int* s_fw = reinterpret_cast<int*>(s_cs);           // [NR], before the first window
+    int* s_fw = reinterpret_cast<int*>(sW);
     for (int n = tid; n < NR; n += NT) s_fw[n] = T;
     __syncthreads();
     for (int t = t_end + tid; t < T; t += NT) atomicMin(&s_fw[min(max(a.am[tok0 + (size_t)t * H], 0), NR - 1)], t);
     __syncthreads();
-    // the key row n holds at t_end: kold of its first later write, else the final key
-    auto key_src = [&](int row) -> const float* {
-        const int fw = s_fw[row];
-        return fw < T ? a.kold + (tok0 + (size_t)fw * H) * D : a.kfin + ((size_t)bh * N + row) * D;
-    };
-
-    // ---- Kh at t_end (normalised) into the B-operand layout; full-row norms through LDS.  A row restored from
-    // kold is normalised exactly as the window undo (S2, S7) normalises it -- quarter sums in the same order,
-    // then sum4rows -- so a chunk starts from bitwise the keys the sequential reverse pass would hold there,
-    // and the results do not depend on the chunking.
-    f32x16 Kv[NBW][NCH];
-#define KREG(kk, nb) Kv[nb][(kk) >> 4][(kk) & 15]
-    {
-        float* s_nrm = &s_W[0][0];                      // [NW][NR] scratch before the first window
-        float* s_n2 = s_nrm + NW * NR;                  // [NR]: |kold row|^2 in the undo's order
-        for (int r0 = wave * 16; r0 < NR; r0 += NW * 16) {
-            const int row = r0 + c;                     // lane (row c, quarter grp), as S2
-            const int fw = row < N ? s_fw[row] : T;
-            float ss = 0.f;
-            if (fw < T) {
-                const float* src = a.kold + (tok0 + (size_t)fw * H) * D + grp * (D / 4);
+    // the keys at t_end (kold of the row's first later write, else kfin), normalised, transposed into sKT;
+    // lane (row r0 + c, part grp): 4-element pieces grp, grp + 4, grp + 8, ... of the row
+    for (int r0 = 16 * wave; r0 < NR; r0 += 16 * NW) {
+        const int row = r0 + c;
+        const int fw = row < N ? s_fw[row] : T;
+        float x[D / 4];
+        float ss = 0.f;
+        const float* src = fw < T ? a.kold + (tok0 + (size_t)fw * H) * D : a.kfin + ((size_t)bh * N + min(row, N - 1)) * D;
 #pragma unroll
-                for (int u = 0; u < D / 16; u++) {
-                    const float4 x = *reinterpret_cast<const float4*>(src + 4 * u);
-                    ss = fmaf(x.x, x.x, ss); ss = fmaf(x.y, x.y, ss); ss = fmaf(x.z, x.z, ss); ss = fmaf(x.w, x.w, ss);
-                }
-            }
-            const float kn = sum4rows(ss);
-            if (grp == 0) s_n2[row] = kn;
+        for (int u = 0; u < D / 16; u++) {
+            const float4 v = row < N ? ld4(src + 4 * (grp + 4 * u)) : make_float4(0.f, 0.f, 0.f, 0.f);
+            x[4 * u] = v.x; x[4 * u + 1] = v.y; x[4 * u + 2] = v.z; x[4 * u + 3] = v.w;
+            ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
         }
+        const float ki = rsq_clamped(sum4rows(ss));
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            const int row = kk + KK * grp;
-            const float* src = row < N ? key_src(row) : nullptr;
-            float ss = 0.f;
+        for (int u = 0; u < D / 16; u++)
 #pragma unroll
-            for (int nb = 0; nb < NBW; nb++) {
-                const float x = row < N ? src[d0 + 16 * nb + c] : 0.f;
-                KREG(kk, nb) = x;
-                ss = fmaf(x, x, ss);
-            }
-            ss = rowsum16(ss);
-            if (c == 0) s_nrm[wave * NR + row] = ss;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            const int row = kk + KK * grp;
-            float nsq = 0.f;
-#pragma unroll
-            for (int w = 0; w < NW; w++) nsq += s_nrm[w * NR + row];
-            if (row < N && s_fw[row] < T) nsq = s_n2[row];
-            const float ki = rsq_clamped(nsq);
-#pragma unroll
-            for (int nb = 0; nb < NBW; nb++) KREG(kk, nb) *= ki;
-        }
+            for (int e = 0; e < 4; e++) sKT[(4 * (grp + 4 * u) + e) * P + row] = x[4 * u + e] * ki;
     }
-    float o_me[RPL];
-#pragma unroll
-    for (int j = 0; j < RPL; j++) {                    // the occupancy at t_end, likewise
-        const int n = lane + 64 * j;
+    for (int n = tid; n < NR; n += NT) {                // the occupancy at t_end, likewise
         const int fw = n < N ? s_fw[n] : T;
-        o_me[j] = n >= N ? 0.f : (fw < T ? a.oold[tok0 + (size_t)fw * H] : a.ofin[(size_t)bh * N + n]);
+        sO[n] = n >= N ? 0.f : (fw < T ? a.oold[tok0 + (size_t)fw * H] : a.ofin[(size_t)bh * N + n]);
     }
+    __syncthreads();
 
-    // ---- window prefetch into registers.  Every load is a uniform (scalar) base plus ONE 32-bit per-lane
-    // offset computed once, so the prefetch costs no per-load address registers.
-    float ncs[UCS], ndn[UDN];
+    // ---- window prefetch into registers: every load is a per-window base plus a 32-bit element offset computed
+    // once (the step index of each is kept to mask the last window's missing steps)
+    float ncs[UCS], ndn[UCS];
     uint4 nko[UKO], nq[UQ];
     float nsc = 0.f;
-    const unsigned off_dn = (unsigned)(tid / WIN) * (unsigned)T + (unsigned)(tid % WIN);
-    constexpr int KR = NT / (D / 4);                     // kold rows per 256-lane pass
-    constexpr int QR = NT / (D / EPU);                   // query rows per pass
-    const unsigned off_ko = (unsigned)(tid / (D / 4)) * (unsigned)(H * D) + 4u * (unsigned)(tid % (D / 4));
-    const unsigned off_q = (unsigned)(tid / (D / EPU)) * (unsigned)(H * D) + (unsigned)EPU * (unsigned)(tid % (D / EPU));
+    u32 ocs[UCS], odn[UCS], oko[UKO], oq[UQ];
+    int ics[UCS], idn[UCS], iko[UKO], iq[UQ];
+#pragma unroll
+    for (int u2 = 0; u2 < UCS; u2++) {
+        const int u = tid + NT * u2;
+        const int i = u / NR, n = u % NR;                          // step-major: rows consecutive across lanes
+        ics[u2] = (u < WIN * NR && n < N) ? i : WIN;
+        ocs[u2] = (u32)(i * N + n);
+        const int n2 = u / WIN, i2 = u % WIN;                      // row-major: 16 steps of a row consecutive
+        idn[u2] = (u < WIN * NR && n2 < N) ? i2 : WIN;
+        odn[u2] = (u32)(n2 * T + i2);
+    }
+#pragma unroll
+    for (int u2 = 0; u2 < UKO; u2++) {
+        const int u = tid + NT * u2, i = u / (D / 4);
+        iko[u2] = u < WIN * D / 4 ? i : WIN;
+        oko[u2] = (u32)(i * H * D + 4 * (u % (D / 4)));
+    }
+#pragma unroll
+    for (int u2 = 0; u2 < UQ; u2++) {
+        const int u = tid + NT * u2, i = u / (D / EPU);
+        iq[u2] = u < WIN * D / EPU ? i : WIN;
+        oq[u2] = (u32)(i * H * D + EPU * (u % (D / EPU)));
+    }
     auto load_win = [&](int m) {
         const int t0 = m * WIN, nt = min(WIN, T - t0);
-        // byte offsets re-derived per window through an empty asm: the loads keep the scalar-base +
-        // 32-bit-offset form instead of 64-bit per-lane addresses hoisted out of the loop (which spill,
-        // and whose reloads would wait on this prefetch: scratch loads share the vector-memory counter)
-        u32 b_tid = 4u * (u32)tid, b_dn = 4u * off_dn, b_ko = 4u * off_ko, b_q = (u32)sizeof(TI) * off_q;
-        int tl = tid;                                    // bounds indices from a fresh copy, likewise
-        asm volatile("" : "+v"(b_tid), "+v"(b_dn), "+v"(b_ko), "+v"(b_q), "+v"(tl));
-        const char* csb = (const char*)(a.cslog + ((size_t)bh * T + t0) * N);   // (nt, N) contiguous
-        const int ncsv = nt * N;
+        const float* csb = a.cslog + ((size_t)bh * T + t0) * N;
+        const float* dnb = a.dn + (size_t)bh * N * T + t0;
+        const float* kob = a.kold + (tok0 + (size_t)t0 * H) * D;
+        const TI* qb = qp + (tok0 + (size_t)t0 * H) * D;
 #pragma unroll
         for (int u2 = 0; u2 < UCS; u2++) {
-            const char* bp = csb + (size_t)NT * u2 * sizeof(float);
-            ncs[u2] = (tl + NT * u2 < ncsv) ? *reinterpret_cast<const float*>(bp + b_tid) : 0.f;
+            ncs[u2] = ics[u2] < nt ? csb[ocs[u2]] : 0.f;
+            ndn[u2] = idn[u2] < nt ? dnb[odn[u2]] : 0.f;
         }
-        const char* dnb = (const char*)(a.dn + (size_t)bh * N * T + t0);      // row n at + n * T
 #pragma unroll
-        for (int u2 = 0; u2 < UDN; u2++) {
-            const char* bp = dnb + (size_t)(NT / WIN) * u2 * T * sizeof(float);
-            const int nn = tl / WIN + (NT / WIN) * u2;
-            ndn[u2] = (tl % WIN < nt && nn < N) ? *reinterpret_cast<const float*>(bp + b_dn) : 0.f;
-        }
-        const char* kob = (const char*)(a.kold + (tok0 + (size_t)t0 * H) * D);
+        for (int u2 = 0; u2 < UKO; u2++)
+            nko[u2] = iko[u2] < nt ? *reinterpret_cast<const uint4*>(kob + oko[u2]) : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-        for (int u2 = 0; u2 < UKO; u2++) {
-            const char* bp = kob + (size_t)KR * u2 * H * D * sizeof(float);
-            const int i = tl / (D / 4) + KR * u2;
-            nko[u2] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < nt) nko[u2] = *reinterpret_cast<const uint4*>(bp + b_ko);
-        }
-        const char* qb = (const char*)(qp + (tok0 + (size_t)t0 * H) * D);
-#pragma unroll
-        for (int u2 = 0; u2 < UQ; u2++) {
-            const char* bp = qb + (size_t)QR * u2 * H * D * sizeof(TI);
-            const int i = tl / (D / EPU) + QR * u2;
-            nq[u2] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < nt) nq[u2] = *reinterpret_cast<const uint4*>(bp + b_q);
-        }
+        for (int u2 = 0; u2 < UQ; u2++)
+            nq[u2] = iq[u2] < nt ? *reinterpret_cast<const uint4*>(qb + oq[u2]) : make_uint4(0u, 0u, 0u, 0u);
         if (tid < 4 * WIN) {
             const int kind = tid / WIN, i = tid % WIN;
             nsc = kind == 0 ? __int_as_float(-1) : 0.f;
@@ -1644,296 +1662,236 @@ void chain_bwd_w(ChainBwdArgs a) {
     };
 
     float dtemp_acc = 0.f, dfr_acc = 0.f;
-    __syncthreads();                                    // s_fw (in s_cs) is read before the first window's S1
     load_win(m_hi - 1);
     for (int m = m_hi - 1; m >= m_lo; m--) {
         const int t0 = m * WIN, nt = min(WIN, T - t0);
-        // S1: publish the prefetched window into LDS
+        // lane indices re-derived from an opaque copy every window: comparisons on them are then not loop
+        // invariant, so the compiler does not hoist dozens of 64-bit lane masks into (spilled) scalar registers
+        const int tidw = tid;
+        const int lanew = tidw & 63, cw = lanew & 15, grpw = lanew >> 4;
+        // S1: publish
 #pragma unroll
         for (int u2 = 0; u2 < UCS; u2++) {
-            const int u = tid + NT * u2;
-            if (u < WIN * NR) s_cs[u] = ncs[u2];
-        }
-#pragma unroll
-        for (int u2 = 0; u2 < UDN; u2++) {
-            const int u = tid + NT * u2;
-            if (u < NR * WIN) s_dn[u / WIN][u % WIN] = ndn[u2];
+            const int u = tidw + NT * u2;
+            if (u < WIN * NR) {
+                sCS[(u / NR) * SC + u % NR] = ncs[u2];
+                sDN[(u % WIN) * SC + u / WIN] = ndn[u2];
+            }
         }
 #pragma unroll
         for (int u2 = 0; u2 < UKO; u2++) {
-            const int u = tid + NT * u2;
-            if (u < WIN * D / 4) *reinterpret_cast<uint4*>(&s_ko[u / (D / 4)][(u % (D / 4)) * 4]) = nko[u2];
+            const int u = tidw + NT * u2;
+            if (u < WIN * D / 4) *reinterpret_cast<uint4*>(&sKO[(u / (D / 4)) * KOS + 4 * (u % (D / 4))]) = nko[u2];
         }
 #pragma unroll
         for (int u2 = 0; u2 < UQ; u2++) {
-            const int u = tid + NT * u2;
-            if (u < WIN * D / EPU) stage_store(&s_q[u / (D / EPU)][(u % (D / EPU)) * EPU], nq[u2], BF);
+            const int u = tidw + NT * u2;
+            if (u < WIN * D / EPU) stage_store(&sQ[(u / (D / EPU)) * KOS + EPU * (u % (D / EPU))], nq[u2], BF);
         }
-        if (tid < 4 * WIN) {
-            const int kind = tid / WIN, i = tid % WIN;
+        if (tidw < 4 * WIN) {
+            const int kind = tidw / WIN, i = tidw % WIN;
             if (kind == 0) s_am[i] = __float_as_int(nsc);
             else if (kind == 1) s_g[i] = nsc;
             else if (kind == 2) s_fr[i] = nsc;
             else s_oo[i] = nsc;
         }
         __syncthreads();                                                      // B1
-        // S2: |kold_i|^2 of the window's rows (every wave): lane = (row c, quarter grp)
-        float knrm;
-        {
+        // S2: |kold_i|^2 (lane = (write c, part grp), the order of the chunk start) and the same-row links
+        if (wave == 0) {
             float ss = 0.f;
 #pragma unroll
             for (int u = 0; u < D / 16; u++) {
-                const float4 x = *reinterpret_cast<const float4*>(&s_ko[c][grp * (D / 4) + 4 * u]);
+                const float4 x = ld4(&sKO[cw * KOS + 4 * (grpw + 4 * u)]);
                 ss = fmaf(x.x, x.x, ss); ss = fmaf(x.y, x.y, ss); ss = fmaf(x.z, x.z, ss); ss = fmaf(x.w, x.w, ss);
             }
-            knrm = sum4rows(ss);                         // lane l: |kold_{l & 15}|^2
-        }
-        // S3: replay the occupancy of this lane's rows backwards through the window: taken_n(t)
-        int amw[WIN];
-        float oow[WIN];
+            const float kn = sum4rows(ss);
+            if (grpw == 0) s_kil[cw] = rsq_clamped(kn);
+        } else if (wave == 1 && lanew < WIN) {
+            const int i = lanew, ai = s_am[i];
+            int nx = -1;
+            bool first = true;
 #pragma unroll
-        for (int u = 0; u < WIN / 4; u++) {
-            const int4 a4 = *reinterpret_cast<const int4*>(&s_am[4 * u]);
-            const float4 o4 = *reinterpret_cast<const float4*>(&s_oo[4 * u]);
-            amw[4 * u] = a4.x; amw[4 * u + 1] = a4.y; amw[4 * u + 2] = a4.z; amw[4 * u + 3] = a4.w;
-            oow[4 * u] = o4.x; oow[4 * u + 1] = o4.y; oow[4 * u + 2] = o4.z; oow[4 * u + 3] = o4.w;
-        }
-        u32 tk[RPL];
-#pragma unroll
-        for (int j = 0; j < RPL; j++) tk[j] = 0;
-#pragma unroll
-        for (int i = WIN - 1; i >= 0; i--) {
-#pragma unroll
-            for (int j = 0; j < RPL; j++) {
-                const int n = lane + 64 * j;
-                if (n == amw[i]) o_me[j] = oow[i];
-                if (n < N && o_me[j] >= eps) tk[j] |= 1u << i;
+            for (int j = WIN - 1; j >= 0; j--) {
+                const int aj = s_am[j];
+                if (j > i && aj == ai) nx = j;                // ends at the smallest such j
+                if (j < i && aj == ai) first = false;
             }
-        }
-        // S4: the softmax adjoint of this wave's steps, over every row.  With a_n = e_n / SS over the eligible
-        // rows, sum over taken rows of dz_n = (g * SSD_taken - sa * SS_taken) / SS, so dfr needs no extra
-        // reduction.  The shift of the exponentials is the z of the row the forward wrote: the forward chose
-        // it as the maximum of these same z over the eligible rows, so no wave max is needed (a softmax is
-        // exact for any shift; this one keeps every exponent <= 0 up to rounding).
-        // The SPW steps of this wave in lockstep groups of GS: one interleaved wave sum per group, branch-free
-        // free-row search; the per-step stores are gathered to lanes 0 .. SPW-1 at the end.
-        float dgv[SPW], dfv[SPW];
-        bool livev[SPW];
+            s_nx[i] = i < nt ? nx : -1;
+            s_first[i] = (i < nt && first) ? 1 : 0;
+        } else if (wave == 2) {                            // 1 / max(|q_t|, 1e-6), 0 where |q_t|^2 < 1e-12
+            float qq = 0.f;
 #pragma unroll
-        for (int i0 = 0; i0 < SPW; i0 += GS) {
-            int ai[GS];
-            float g[GS], frv[GS], Mv[GS], cs[GS][RPL], dw[GS][RPL], ev[GS][RPL];
-#pragma unroll
-            for (int ii = 0; ii < GS; ii++) {                 // steps past nt hold zeros: W = 0, no stores
-                const int i = SPW * wave + i0 + ii;
-                livev[i0 + ii] = i < nt;
-                ai[ii] = s_am[i];
-                g[ii] = s_g[i];
-                frv[ii] = frt ? s_fr[i] : fr_s;
-                const int aj = ai[ii] >> 6, al = ai[ii] & 63;
-                float zsel = 0.f;
-#pragma unroll
-                for (int j = 0; j < RPL; j++) {
-                    const int n = lane + 64 * j;
-                    const bool tj = (tk[j] >> i) & 1u;
-                    cs[ii][j] = n < N ? s_cs[i * N + n] : 0.f;
-                    dw[ii][j] = s_dn[n][i];
-                    const float z = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
-                    zsel = aj == j ? z : zsel;
-                }
-                Mv[ii] = readlanef(zsel, al);
+            for (int u = 0; u < D / 16; u++) {
+                const float4 x = ld4(&sQ[cw * KOS + 4 * (grpw + 4 * u)]);
+                qq = fmaf(x.x, x.x, qq); qq = fmaf(x.y, x.y, qq); qq = fmaf(x.z, x.z, qq); qq = fmaf(x.w, x.w, qq);
             }
-            float ls[2 * GS];                                  // [ii]: sum e, [GS + ii]: sum e * dw (taken rows)
-#pragma unroll
-            for (int ii = 0; ii < GS; ii++) {
-                const int i = SPW * wave + i0 + ii;
-                float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-                for (int j = 0; j < RPL; j++) {
-                    const bool tj = (tk[j] >> i) & 1u;
-                    const float z = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
-                    const float e = tj ? __expf(z - Mv[ii]) : 0.f;
-                    ev[ii][j] = e;
-                    s0 += e;
-                    s1 = fmaf(e, dw[ii][j], s1);
-                }
-                ls[ii] = s0;
-                ls[GS + ii] = s1;
-            }
-            wavesum_k<2 * GS>(ls);
-#pragma unroll
-            for (int ii = 0; ii < GS; ii++) {
-                const int i = SPW * wave + i0 + ii;
-                // the lowest free row (rows grow with j, then lane): scan j downwards with selects
-                int FO = -1;
-                float FZ = 0.f, FD = 0.f;
-#pragma unroll
-                for (int j = RPL - 1; j >= 0; j--) {
-                    const bool tj = (tk[j] >> i) & 1u;
-                    const u64 mf = __ballot(lane + 64 * j < N && !tj);
-                    const int lf = (int)__builtin_ctzll(mf | (1ull << 63));
-                    const float zj = temp * cs[ii][j] - (tj ? frv[ii] : 0.f);
-                    const float zf = readlanef(zj, lf), df = readlanef(dw[ii][j], lf);
-                    FO = mf ? 64 * j + lf : FO;
-                    FZ = mf ? zf : FZ;
-                    FD = mf ? df : FD;
-                }
-                const float M = Mv[ii];
-                const float SSt = ls[ii], SSDt = ls[GS + ii];
-                const float ef = FO >= 0 ? __expf(FZ - M) : 0.f;   // the first free row competes too
-                const float SS = FO >= 0 ? SSt + ef : SSt;
-                const float SSD = FO >= 0 ? fmaf(ef, FD, SSDt) : SSDt;
-                const float rss = livev[i0 + ii] ? __builtin_amdgcn_rcpf(SS) : 0.f, sa = (g[ii] * SSD) * rss;
-#pragma unroll
-                for (int j = 0; j < RPL; j++) {
-                    const int n = lane + 64 * j;
-                    const bool tj = (tk[j] >> i) & 1u;
-                    const float as = tj ? ev[ii][j] * rss : (n < N && n == FO) ? ef * rss : 0.f;
-                    const float dz = as * (g[ii] * dw[ii][j] - sa);
-                    dtemp_acc = fmaf(dz, cs[ii][j], dtemp_acc);
-                    s_W[i][n] = temp * dz;
-                }
-                // dgate of the written row: its Dn entry, read from the lane that holds it
-                const int aj = ai[ii] >> 6, al = ai[ii] & 63;
-                float dsel = dw[ii][0];
-#pragma unroll
-                for (int j = 1; j < RPL; j++) dsel = aj == j ? dw[ii][j] : dsel;
-                dgv[i0 + ii] = readlanef(dsel, al);
-                dfv[i0 + ii] = livev[i0 + ii] ? -(g[ii] * SSDt - sa * SSt) * rss : 0.f;
-            }
+            qq = sum4rows(qq);
+            if (grpw == 0) s_qi[cw] = qq < 1e-12f ? -rsq_clamped(qq) : rsq_clamped(qq);   // sign: no projection
         }
-        if (!frt) {
+        if (NT - 1 - tidw < NR) {                          // occupancy masks, on the last NR lanes: row n over the
+            const int n = NT - 1 - tidw;                   // window's 16 steps
+            float o = sO[n];
+            u32 mk = 0u;
 #pragma unroll
-            for (int ii = 0; ii < SPW; ii++) if (lane == 0) dfr_acc += dfv[ii];
+            for (int i = WIN - 1; i >= 0; i--) {           // backwards: o becomes the pre-write occupancy at i
+                o = s_am[i] == n ? s_oo[i] : o;
+                mk |= (n < N && o >= eps ? 1u : 0u) << i;
+            }
+            s_tkm[n] = mk;
         }
-        if (lane < SPW) {                                      // lane ii stores step SPW * wave + ii
-            float dgl = dgv[0], dfl = dfv[0];
-            bool lv = livev[0];
+        __syncthreads();                                                      // B1b
+        // S4: the softmax adjoint of every step: step s = lanes [NC s, NC s + NC), rows n0 .. n0 + RPC - 1
+        {
+            const int s = tidw / NC, r = tidw % NC, n0 = r * RPC;
+            const bool live = s < nt;
+            const float g = s_g[s], frv = frt ? s_fr[s] : fr_s;
+            float cs[RPC], dw[RPC];
 #pragma unroll
-            for (int ii = 1; ii < SPW; ii++) { dgl = lane == ii ? dgv[ii] : dgl; dfl = lane == ii ? dfv[ii] : dfl; lv = lane == ii ? livev[ii] : lv; }
-            if (lv) {
-                const size_t ix = tok0 + (size_t)(t0 + SPW * wave + lane) * H;
-                a.dg[ix] = dgl;
+            for (int j = 0; j < RPC; j += 2) {
+                const float2 x = *reinterpret_cast<const float2*>(&sCS[s * SC + n0 + j]);
+                const float2 y = *reinterpret_cast<const float2*>(&sDN[s * SC + n0 + j]);
+                cs[j] = x.x; cs[j + 1] = x.y; dw[j] = y.x; dw[j + 1] = y.y;
+            }
+            u32 tk = 0u, rows = 0u;                            // occupied at step s; below N
+#pragma unroll
+            for (int j = 0; j < RPC; j += 2) {
+                const uint2 m2 = *reinterpret_cast<const uint2*>(&s_tkm[n0 + j]);
+                tk |= ((m2.x >> s) & 1u) << j;
+                tk |= ((m2.y >> s) & 1u) << (j + 1);
+                rows |= (n0 + j < N ? 1u : 0u) << j;
+                rows |= (n0 + j + 1 < N ? 1u : 0u) << (j + 1);
+            }
+            // the lowest free row of the step with its z and Dn, and the largest z over the occupied rows
+            const u32 fm = rows & ~tk;
+            const int jf = fm ? (int)__builtin_ctz(fm) : 0;
+            float zf = 0.f, FD = 0.f, mz = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < RPC; j++) {
+                zf = j == jf ? temp * cs[j] : zf;
+                FD = j == jf ? dw[j] : FD;
+                if ((tk >> j) & 1u) mz = fmaxf(mz, fmaf(temp, cs[j], -frv));
+            }
+            int ff = fm ? n0 + jf : INT_MAX;
+            step_argmin<NC>(ff, zf, FD);
+            mz = step_max<NC>(mz);
+            const bool hasf = ff < N;
+            if (!hasf) { zf = -INFINITY; FD = 0.f; }
+            const float M = fmaxf(mz, zf);
+            float ev[RPC], s0 = 0.f, s1 = 0.f;
+#pragma unroll
+            for (int j = 0; j < RPC; j++) {
+                const float e = ((tk >> j) & 1u) ? __expf(fmaf(temp, cs[j], -frv) - M) : 0.f;
+                ev[j] = e;
+                s0 += e;
+                s1 = fmaf(e, dw[j], s1);
+            }
+            const float SSt = step_sum<NC>(s0), SSDt = step_sum<NC>(s1);
+            const float ef = hasf ? __expf(zf - M) : 0.f;
+            const float SS = SSt + ef, SSD = fmaf(ef, FD, SSDt);
+            const float rss = live ? __builtin_amdgcn_rcpf(SS) : 0.f, sa = (g * SSD) * rss;
+            float dt = 0.f;
+#pragma unroll
+            for (int j = 0; j < RPC; j += 2) {
+                float wv[2];
+#pragma unroll
+                for (int jj = 0; jj < 2; jj++) {
+                    const int n = n0 + j + jj;
+                    const float as = ((tk >> (j + jj)) & 1u) ? ev[j + jj] * rss : (n == ff ? ef * rss : 0.f);
+                    const float dz = as * (g * dw[j + jj] - sa);
+                    dt = fmaf(dz, cs[j + jj], dt);
+                    wv[jj] = temp * dz;
+                }
+                *reinterpret_cast<float2*>(&sW[s * SW + n0 + j]) = make_float2(wv[0], wv[1]);
+            }
+            dtemp_acc += dt;
+            const float pstep = temp * step_sum<NC>(dt);        // <qhat_s, dqn_s> = temp sum_n dz_n cs_n
+            if (r == 0) s_pr[s] = pstep;
+            if (r == 0 && live) {
+                const size_t ix = tok0 + (size_t)(t0 + s) * H;
+                const float dfl = -(g * SSDt - sa * SSt) * rss;
+                a.dg[ix] = sDN[s * SC + s_am[s]];              // dgate of the written row: its Dn entry
                 if (frt) a.dfr[ix] = dfl;
+                else dfr_acc += dfl;
             }
         }
         __syncthreads();                                                      // B2
+        if (tidw < WIN && s_first[tidw]) sO[s_am[tidw]] = s_oo[tidw];            // occupancy at the window start
         // S5: prefetch the next (earlier) window while the matrix cores run
         if (m > m_lo) load_win(m - 1);
-        // S6: dqn over every row for this wave's dims, with the window-end keys
-        f32x4 acc[NBW];
-#pragma unroll
-        for (int nb = 0; nb < NBW; nb++) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k4 = 0; k4 < KK / 4; k4++) {
-            const float4 av = *reinterpret_cast<const float4*>(&s_W[c][KK * grp + 4 * k4]);
-#pragma unroll
-            for (int nb = 0; nb < NBW; nb++) {
-                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, KREG(4 * k4 + 0, nb), acc[nb], 0, 0, 0);
-                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, KREG(4 * k4 + 1, nb), acc[nb], 0, 0, 0);
-                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, KREG(4 * k4 + 2, nb), acc[nb], 0, 0, 0);
-                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, KREG(4 * k4 + 3, nb), acc[nb], 0, 0, 0);
-            }
-            if ((k4 & 1) == 1) __builtin_amdgcn_sched_barrier(0);
-        }
-        // S7: undo the window's writes (reverse order) in this wave's dims, logging
-        //     d_s = Kh(kold_s) - Kh_{a_s}(after write s).  Each event's kold slice is read XD events ahead
-        //     and normalised on use, so the dependent steps do not wait on an LDS round trip.
-        const int am_l = s_am[lane & (WIN - 1)];         // lane i (< 16) holds the row written at window step i
-        const float kil = rsq_clamped(knrm);             // lane i: 1 / max(|kold_i|, 1e-6)
-        constexpr int XD = 3;
-        float xo[WIN][NBW];
-#pragma unroll
-        for (int i = WIN - 1; i >= WIN - XD; i--)
-#pragma unroll
-            for (int nb = 0; nb < NBW; nb++) xo[i][nb] = s_ko[i][d0 + 16 * nb + c];
-#pragma unroll
-        for (int i = WIN - 1; i >= 0; i--) {             // program order keeps repeated rows sequential
-            if (i - XD >= 0) {
-#pragma unroll
-                for (int nb = 0; nb < NBW; nb++) xo[i - XD][nb] = s_ko[i - XD][d0 + 16 * nb + c];
-            }
-            if (i < nt) {
-                const int ar = __builtin_amdgcn_readlane(am_l, i);
-                const float ki = readlanef(kil, i);
-                float x[NBW];
-#pragma unroll
-                for (int nb = 0; nb < NBW; nb++) x[nb] = xo[i][nb] * ki;
-                const int ag = ar / KK, kk = ar - KK * ag;
-                const int ch = kk >> 4, e = kk & 15;
-                const bool mine = grp == ag;
-                float dd[NBW];
-#pragma unroll
-                for (int cc = 0; cc < NCH; cc++) {
-                    if (ch == cc) {
-#pragma unroll
-                        for (int nb = 0; nb < NBW; nb++) {
-                            const float old = Kv[nb][cc][e];
-                            dd[nb] = x[nb] - old;
-                            Kv[nb][cc][e] = mine ? x[nb] : old;
-                        }
-                    }
-                }
-                if (mine) {
-#pragma unroll
-                    for (int nb = 0; nb < NBW; nb++) s_delta[i][d0 + 16 * nb + c] = dd[nb];
-                }
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // S8: the rewritten rows' correction, sum_{s >= t} W[t][a_s] d_s, as a 16 x 16 x DW MFMA
+        float av8[4];                                      // S8's A operand: W[c][a_s] for s = 4 kc + grp >= c
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
             const int s = 4 * kc + grp;
-            const bool ok = s < nt;
-            const float av = (ok && s >= c) ? s_W[c][s_am[s]] : 0.f;
-#pragma unroll
-            for (int nb = 0; nb < NBW; nb++) {
-                const float bv = ok ? s_delta[s][d0 + 16 * nb + c] : 0.f;
-                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[nb], 0, 0, 0);
-            }
+            av8[kc] = (s < nt && s >= c) ? sW[c * SW + s_am[s]] : 0.f;
         }
-        // S9: <dqn, q> and |q|^2 over this wave's dims for the 4 steps of this lane
-        float qv[4][NBW];
+        // S6: dqn = W Kh over every row for this wave's dims, two accumulation chains
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k4 = 0; k4 < KK / 4; k4 += 2) {
+            const float4 av = ld4(&sW[cw * SW + KK * grpw + 4 * k4]);
+            const float4 bv = ld4(&sKT[(d0 + cw) * P + KK * grpw + 4 * k4]);
+            const float4 av2 = ld4(&sW[cw * SW + KK * grpw + 4 * k4 + 4]);
+            const float4 bv2 = ld4(&sKT[(d0 + cw) * P + KK * grpw + 4 * k4 + 4]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av2.x, bv2.x, acc2, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av2.y, bv2.y, acc2, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av2.z, bv2.z, acc2, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av2.w, bv2.w, acc2, 0, 0, 0);
+        }
+        // S7: the undo of every write at once: write i = lanes [NC i, NC i + NC), dims e0 .. e0 + 3
+        const int ui = tidw / NC, ue0 = (tidw % NC) * DPT;
+        const bool uev = ui < nt;
+        const int uai = min(max(s_am[ui], 0), NR - 1);
+        float4 ux;
+        {
+            const float ki = s_kil[ui];
+            const float4 x = ld4(&sKO[ui * KOS + ue0]);
+            ux = make_float4(x.x * ki, x.y * ki, x.z * ki, x.w * ki);
+            const int nx = s_nx[ui];
+            float4 af;
+            if (nx >= 0) {
+                const float kn = s_kil[nx];
+                const float4 y = ld4(&sKO[nx * KOS + ue0]);
+                af = make_float4(y.x * kn, y.y * kn, y.z * kn, y.w * kn);
+            } else {
+                af = make_float4(sKT[(ue0 + 0) * P + uai], sKT[(ue0 + 1) * P + uai], sKT[(ue0 + 2) * P + uai],
+                                 sKT[(ue0 + 3) * P + uai]);
+            }
+            const float4 dd = uev ? make_float4(ux.x - af.x, ux.y - af.y, ux.z - af.z, ux.w - af.w)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4*>(&sDel[ui * D + ue0]) = dd;
+        }
+        __syncthreads();                                                      // B3: every read of the window-end keys done
+        if (uev && s_first[ui]) {
+            sKT[(ue0 + 0) * P + uai] = ux.x; sKT[(ue0 + 1) * P + uai] = ux.y;
+            sKT[(ue0 + 2) * P + uai] = ux.z; sKT[(ue0 + 3) * P + uai] = ux.w;
+        }
+        // S8: the rewritten rows' correction, sum_{s >= t} W[t][a_s] delta_s
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r] += acc2[r];
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            const int s = 4 * kc + grpw;
+            const float bv = s < nt ? sDel[s * D + d0 + cw] : 0.f;
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av8[kc], bv, acc, 0, 0, 0);
+        }
+        // S9: dq = qinv (dqn - qhat <qhat, dqn>), or qinv dqn where |q| < 1e-6.  <qhat, dqn> = sum_n W_n <qhat, Kh_n>
+        // and <qhat_t, Kh_n(t)> is the cosine the forward logged, so the projection needs no sum over the dims
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int st = 4 * grp + r;
-            float p = 0.f, qq = 0.f;
-#pragma unroll
-            for (int nb = 0; nb < NBW; nb++) {
-                qv[r][nb] = s_q[st][d0 + 16 * nb + c];
-                p = fmaf(acc[nb][r], qv[r][nb], p);
-                qq = fmaf(qv[r][nb], qv[r][nb], qq);
-            }
-            p = rowsum16(p);
-            qq = rowsum16(qq);
-            if (c == 0) s_proj[wave][st] = make_float2(p, qq);
-        }
-        __syncthreads();                                                      // B3
-        // S10: dq = qinv (dqn - qhat <qhat, dqn>)  (qinv dqn where |q| < 1e-6)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int st = 4 * grp + r;
+            const int st = 4 * grpw + r;
             if (st < nt) {
-                float P = 0.f, QQ = 0.f;
-#pragma unroll
-                for (int w = 0; w < NW; w++) { const float2 x = s_proj[w][st]; P += x.x; QQ += x.y; }
-                const float qi = rsq_clamped(QQ);
-                const float pr = P * qi;
-                TI* dqp = (TI*)a.dq + (tok0 + (size_t)(t0 + st) * H) * D + d0 + c;
-#pragma unroll
-                for (int nb = 0; nb < NBW; nb++) {
-                    const float dqn = acc[nb][r];
-                    const float rr = QQ < 1e-12f ? qi * dqn : qi * (dqn - (qv[r][nb] * qi) * pr);
-                    st1<TI>(dqp + 16 * nb, rr);
-                }
+                const float qs = s_qi[st], qi = fabsf(qs), pr = s_pr[st];
+                const float dqn = acc[r];
+                const float rr = qs < 0.f ? qi * dqn : qi * (dqn - (sQ[st * KOS + d0 + cw] * qi) * pr);
+                st1<TI>((TI*)a.dq + (tok0 + (size_t)(t0 + st) * H) * D + d0 + cw, rr);
             }
         }
-        __syncthreads();                                                      // B4
+        __syncthreads();                                                      // B5: the window's LDS is free
     }
-#undef KREG
     dtemp_acc = wavesum(dtemp_acc);
     dfr_acc = wavesum(dfr_acc);
     if (lane == 0) { s_fin[0][wave] = dtemp_acc; s_fin[1][wave] = dfr_acc; }
@@ -1977,12 +1935,12 @@ hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
 #undef SLOT_CF
     return hipErrorInvalidValue;
 }
-// chain_bwd_w's chunks: windows per chunk so that the launch has about 3,072 workgroups (six per CU slot
-// pair at two resident per CU), and at least 4 windows each, so that a chunk's start (a scan of the later
-// address log and one gather of the key rows) stays a small part of its work.
+// chain_bwd_w's chunks: windows per chunk so that the launch has about 1,536 workgroups (six per CU, one
+// resident at a time), and at least 4 windows each, so that a chunk's start (a scan of the later address log
+// and one gather of the key rows) stays a small part of its work.
 static int chain_bwd_wpc(int64_t BH, int64_t T) {
     const int64_t nwin = (T + WIN - 1) / WIN;
-    const int64_t w = (nwin * BH + 3071) / 3072;
+    const int64_t w = (nwin * BH + 1535) / 1536;
     return (int)std::min<int64_t>(nwin, std::max<int64_t>(4, w));
 }
 static int64_t chain_bwd_chunks(int64_t BH, int64_t T) {
@@ -1992,12 +1950,11 @@ static int64_t chain_bwd_chunks(int64_t BH, int64_t T) {
 
 template <int D, typename TI>
 hipError_t launch_chain_bwd(const ChainBwdArgs& a, int B, hipStream_t st) {
-    if (a.occb) {                                        // windowed kernel, four waves, time chunks
-        constexpr int NW = 4;
-        dim3 grid(B * a.H, (unsigned)chain_bwd_chunks((int64_t)B * a.H, a.T)), block(64 * NW);
-        if (a.N <= 64) slothost::launch((chain_bwd_w<D, 1, NW, TI>), grid, block, 0, st, a);
-        else if (a.N <= 128) slothost::launch((chain_bwd_w<D, 2, NW, TI>), grid, block, 0, st, a);
-        else if (a.N <= 192) slothost::launch((chain_bwd_w<D, 3, NW, TI>), grid, block, 0, st, a);
+    if (a.occb) {                                        // windowed kernel, D / 16 waves, time chunks
+        dim3 grid(B * a.H, (unsigned)chain_bwd_chunks((int64_t)B * a.H, a.T)), block(4 * D);
+        if (a.N <= 64) slothost::launch((chain_bwd_w<D, 1, TI>), grid, block, 0, st, a);
+        else if (a.N <= 128) slothost::launch((chain_bwd_w<D, 2, TI>), grid, block, 0, st, a);
+        else if (a.N <= 192) slothost::launch((chain_bwd_w<D, 3, TI>), grid, block, 0, st, a);
         else return hipErrorInvalidValue;
         return hipGetLastError();
     }
