@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Slot-scan fwd+bwd throughput on one MI355X (BASELINE metric, config 2).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config2_mem|config2_soft|config3*|config4|config5|read_train|window_train]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload config2|config2_mem|config2_soft|config3*|config4|config4_wo|config5|read_train|window_train]
 
 One step = one hard-address slot scan forward (kv_scan_c) plus its backward (torch.autograd.grad of the two
 snapshot outputs against fixed upstream gradients) over one synthetic batch already resident in HBM:
@@ -55,6 +55,9 @@ WORKLOADS = {
     "config4": dict(kind="read", B=64, T=1024, H=6, N=192, D=128, G=1024, NQ=1, layers=6),
     # long-context streaming: 128 chunks of 1024 tokens, state carried, int8 + per-row fp32 scale emission
     "config5": dict(kind="stream", B=8, T=131072, H=6, N=192, D=128, G=8, chunk=1024),
+    # config 4 with each reader layer's output projection into the residual (memlm_sh.py:499-501): the read,
+    # then wo_tk (d_model 2048, bias-free) added to the window output, forward only
+    "config4_wo": dict(kind="read_out", B=64, T=1024, H=6, N=192, D=128, G=1024, NQ=1, layers=6, DM=2048),
     # one reader layer of training at the config-2 memory: G = 8 tokens per block, NQ = 2, forward + backward
     "read_train": dict(kind="read", B=64, T=1024, H=6, N=192, D=128, G=8, NQ=2, layers=1, backward=True),
     # one layer's 16-token window at the training shape (run_sh25.sh:223): 4 K/V heads x 128, kv_nq 4 (the
@@ -412,6 +415,95 @@ def bench_window(args, W):
     print(json.dumps(out), flush=True)
 
 
+def bench_read_out(args, W):
+    """Config 4 with the output projection: per reader layer slot_read_out = the read kernel, then the library's
+    bf16 GEMM delta + rd wo^T into the residual (proj_gemm).  Reports the GEMM's MFMA fraction and the read
+    kernel's HBM fraction from the library's own HIP events on the launch stream, and, for comparison, the
+    same GEMM as one library call (torch.addmm, hipBLASLt) timed with events on the current stream."""
+    import torch
+    import slotread_hip as RH
+    import slotscan_lib as L
+
+    B, T, H, N, D, G, NQ, layers, DM = (W[x] for x in ("B", "T", "H", "N", "D", "G", "NQ", "layers", "DM"))
+    NB = (T + G - 1) // G
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=gen)
+    unit = lambda x: x / x.norm(dim=-1, keepdim=True)
+    bf = torch.bfloat16
+    K = unit(rn(B, NB, H, N, D)).to(bf)
+    V = rn(B, NB, H, N, D).to(bf)
+    kinv = torch.ones(B, NB, H, N, device=dev)
+    valid = torch.ones(B, NB, H, N, device=dev, dtype=torch.bool)
+    qs = [unit(rn(B, T, H, NQ, D)).to(bf) for _ in range(layers)]
+    scs = [torch.nn.functional.softplus(rn(B, T, H, NQ)) + 1.0 for _ in range(layers)]
+    KD = H * NQ * D
+    wos = [(rn(DM, KD) / KD ** 0.5).to(bf) for _ in range(layers)]
+    deltas = [rn(B, T, DM).to(bf) for _ in range(layers)]
+
+    def step():
+        with torch.no_grad():
+            return [RH.slot_read_out(qs[i], K, V, kinv, valid, scs[i], G, wos[i], delta=deltas[i])
+                    for i in range(layers)]
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    L.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    L.profile(False)
+    prof = L.profile_read()
+    ms = (t1 - t0) * 1e3 / args.steps
+    # the projection GEMM alone, same shapes (x (B*T, KD) bf16 @ wo^T into delta), timed with HIP events
+    x = torch.empty(B * T, KD, device=dev, dtype=bf).normal_()
+    d2 = deltas[0].reshape(B * T, DM)
+    for _ in range(3):
+        torch.addmm(d2, x, wos[0].t())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = max(args.steps, 10)
+    e0.record()
+    for _ in range(reps):
+        torch.addmm(d2, x, wos[0].t())
+    e1.record()
+    torch.cuda.synchronize()
+    gemm_ms = e0.elapsed_time(e1) / reps
+    tot, cnt = prof["read_fwd"]
+    rms = tot / cnt
+    ptot, pcnt = prof["proj"]
+    pms = ptot / pcnt
+    rby, rfl = read_algorithmic(B, T, H, N, D, NQ, 1, NB)
+    gfl = 2.0 * B * T * KD * DM
+    gby = 2 * (B * T * KD + DM * KD + 2 * B * T * DM)          # x, wo and delta in, the sum out (bf16)
+    out = {
+        "metric": f"slot-read + wo_tk fan-out tokens/s ({layers} reader layers, frozen store B{B} H{H} S{N} d{D}, "
+                  f"d_model {DM}, forward)",
+        "value": round(B * T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded GPU generator, seed 3)",
+        "config": {"workload": args.workload, "B": B, "T": T, "H": H, "N": N, "D": D, "NQ": NQ, "G": G,
+                   "layers": layers, "d_model": DM, "tokens_per_step": B * T},
+        "roofline": {"bound": "mfma", "kernel": "proj_gemm (wo_tk projection + residual add)",
+                     "achieved": round(gfl / (pms * 1e-3) / 1e12, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gfl / (pms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "flops_per_launch": gfl, "algorithmic_bytes_per_launch": gby,
+                     "avg_launch_ms": round(pms, 4), "hbm_gbps": round(gby / (pms * 1e-3) / 1e9, 1),
+                     "hbm_frac": round(gby / (pms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "library_gemm_ms": round(gemm_ms, 4)},
+        "read_roofline": {"bound": "hbm", "kernel": "read_fwd", "achieved": round(rby / (rms * 1e-3) / 1e9, 1),
+                          "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(rby / (rms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                          "algorithmic_bytes_per_launch": rby, "avg_launch_ms": round(rms, 4),
+                          "mfma_frac": round(rfl / (rms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "per_layer_ms": {"read_fwd": round(rms, 4), "proj_gemm": round(pms, 4), "library_gemm": round(gemm_ms, 4),
+                         "layer_total": round(ms / layers, 4)},
+        "kernels_ms": {n: round(x / c, 4) for n, (x, c) in prof.items()},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def bench_read(args, W):
     import torch
     import slotread_hip as RH
@@ -512,6 +604,8 @@ def main():
     W = WORKLOADS[args.workload]
     if W["kind"] == "read":
         return bench_read(args, W)
+    if W["kind"] == "read_out":
+        return bench_read_out(args, W)
     if W["kind"] == "stream":
         return bench_stream(args, W)
     if W["kind"] == "window":

@@ -200,6 +200,7 @@ int slotscan_gen_bwd(const void* k, const void* q, const void* v, int dtype, con
 #define SLOTSCAN_K_WIN_BWD 10
 #define SLOTSCAN_K_GEN_FWD 11
 #define SLOTSCAN_K_GEN_BWD 12
+#define SLOTSCAN_K_PROJ 13
 #define SLOTSCAN_NK 14
 int slotscan_profile(int enable);
 int slotscan_profile_read(double* total_ms, int64_t* count, int nk);

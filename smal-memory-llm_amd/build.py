@@ -24,7 +24,8 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = [os.path.join(CSRC, f) for f in ("slotscan.hip", "slotread.hip", "slotmem.hip", "slotwin.hip", "slotgen.hip")]
+SOURCES = [os.path.join(CSRC, f) for f in ("slotscan.hip", "slotread.hip", "slotmem.hip", "slotwin.hip", "slotgen.hip",
+                                                 "slotproj.hip")]
 OUT = os.path.join(HERE, "libslotscan.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -7,6 +7,15 @@
     shared_read(q, kbuf, buf, kinv, valid, log_rsel, G, s=None, rsharp=None) -> rd
         memlm_sh.py:379-397 from the projected queries: normalises q (:379), forms the per-query multiplier
         exp(log_rsel) * exp(C tanh(s / C)) (:383-393) and calls slot_read.
+    slot_read_out(q, kbuf, buf, kinv, valid, scale, G, wo, delta=None) -> delta_out
+    shared_read_out(q, kbuf, buf, kinv, valid, log_rsel, G, wo, s=None, rsharp=None, delta=None) -> delta_out
+        the read followed by the reader's output projection into the residual, delta (+)= wo_tk(rd)
+        (memlm_sh.py:499-501): the gfx950 read kernel, then the library's gfx950 bf16 GEMM (slotproj_fwd) whose
+        epilogue is the residual add (rd is written by the read kernel in the GEMM's row-major layout, so
+        nothing is copied).  A single
+        kernel doing both would have to keep a token tile x d_model fp32 output on chip; at d_model = 2048
+        that bounds the tile to 32-64 tokens, and the wo_tk weight would then stream from L2 once per tile
+        (or the read be recomputed per output slice), which costs more than the rd round trip it saves.
 
 Token tensors and the copies are bf16 (the reference casts the memory to the activation dtype,
 memlm_sh.py:475, and the einsums run in it); other float dtypes are cast to bf16 first.  kinv and scale are
@@ -97,3 +106,89 @@ def shared_read(q, kbuf, buf, kinv, valid, log_rsel, G, s=None, rsharp=None):
             sf = rsharp * torch.tanh(sf / rsharp)
         scale = scale * torch.exp(sf)
     return slot_read(qn, kbuf, buf, kinv, valid, scale, G)
+
+
+def _proj(x, w, d2):
+    """delta + x @ w^T for x (M, K), w (N, K), d2 (M, N) or None, all bf16 on one GPU: the library's gfx950 GEMM
+    with the add in its epilogue (slotproj_fwd) when N is a multiple of 256 and K of 32, else one library GEMM
+    (torch.addmm / linear: hipBLASLt) for the shapes that kernel does not tile."""
+    M, K = x.shape
+    N = w.shape[0]
+    if N % 256 == 0 and K % 32 == 0:
+        w_ = w.contiguous()
+        out = torch.empty(M, N, device=x.device, dtype=x.dtype)
+        rc = L.lib().slotproj_fwd(L.ptr(x), L.ptr(w_), None if d2 is None else L.ptr(d2), M, N, K, L.ptr(out),
+                                  L.stream_of(x.device))
+        L.check(rc, "slotproj_fwd")
+        return out
+    return torch.nn.functional.linear(x, w) if d2 is None else torch.addmm(d2, x, w.t())
+
+
+class _ReadOutHip(torch.autograd.Function):
+    """delta_out = delta + rd @ wo^T with rd the slot read, as one op: the read runs on the gfx950 kernel
+    (slotread_fwd), the projection is the library's bf16 GEMM with the residual add in its epilogue
+    (slotproj_fwd: fp32 accumulation rounded to bf16, then added to delta and rounded again, the reference's
+    bf16 Linear output and bf16 residual add), and rd -- written by the read kernel already in
+    the GEMM's row-major (B*T, H*NQ*D) layout -- is kept in bf16 for dwo, as the reference's autograd keeps it
+    for wo_tk.  The backward's two products (dRD = dDelta Wo, dWo = dDelta^T rd) are plain library GEMMs."""
+
+    @staticmethod
+    def forward(ctx, q, kbuf, buf, kinv, valid, scale, wo, delta, G):
+        rd, saved = _fwd(q, kbuf, buf, kinv, valid, scale, G)
+        B, T = rd.shape[:2]
+        x = rd.reshape(B * T, -1)
+        w = wo.to(rd.dtype)
+        if w.shape[1] != x.shape[1]:
+            raise ValueError(f"wo must be (d_model, H*NQ*D) = (*, {x.shape[1]}), got {tuple(wo.shape)}")
+        d2 = None
+        if delta is not None:
+            if delta.shape != (B, T, w.shape[0]):
+                raise ValueError(f"delta must be (B, T, d_model) = {(B, T, w.shape[0])}, got {tuple(delta.shape)}")
+            d2 = delta.reshape(B * T, -1).to(rd.dtype).contiguous()
+        out = _proj(x, w, d2)
+        ctx.save_for_backward(*saved, rd, w)
+        ctx.G = int(G)
+        ctx.meta = (wo.dtype, delta is not None, None if delta is None else delta.dtype)
+        return out.reshape(B, T, -1)
+
+    @staticmethod
+    def backward(ctx, dout):
+        q_, kb_, vb_, ki_, va_, sc_, rd, w = ctx.saved_tensors
+        wo_dtype, has_delta, delta_dtype = ctx.meta
+        B, T, H, NQ, D = q_.shape
+        _, NB, _, N, _ = kb_.shape
+        g = dout.reshape(B * T, -1).to(rd.dtype)
+        drd = torch.mm(g, w).reshape(B, T, H, NQ, D)             # dRD = dDelta Wo
+        dwo = torch.mm(g.t(), rd.reshape(B * T, -1)).to(wo_dtype)  # dWo = dDelta^T rd
+        dq = torch.empty_like(q_)
+        dkb = torch.empty_like(kb_)
+        dvb = torch.empty_like(vb_)
+        dki = torch.empty_like(ki_)
+        dsc = torch.empty_like(sc_)
+        rc = L.lib().slotread_bwd(L.ptr(q_), L.ptr(kb_), L.ptr(vb_), L.ptr(ki_), L.ptr(va_), L.ptr(sc_),
+                                  L.ptr(drd.contiguous()), B, T, H, NQ, N, D, ctx.G, L.ptr(dq), L.ptr(dkb),
+                                  L.ptr(dvb), L.ptr(dki), L.ptr(dsc), L.stream_of(q_.device))
+        L.check(rc, "slotread_bwd")
+        ddelta = dout.to(delta_dtype) if has_delta else None
+        return dq, dkb, dvb, dki, None, dsc, dwo, ddelta, None
+
+
+def slot_read_out(q, kbuf, buf, kinv, valid, scale, G, wo, delta=None):
+    """delta (+)= wo_tk(rd): the slot read followed by the reader's output projection (memlm_sh.py:499-501),
+    wo the (d_model, H*NQ*D) weight of wo_tk (bias-free, memlm_sh.py:313), delta the (B, T, d_model) window
+    output it is added to (None: the layer has no window).  Returns (B, T, d_model) in the read's dtype (bf16)."""
+    return _ReadOutHip.apply(q, kbuf, buf, kinv, valid, scale, wo, delta, int(G))
+
+
+def shared_read_out(q, kbuf, buf, kinv, valid, log_rsel, G, wo, s=None, rsharp=None, delta=None):
+    """memlm_sh.py:379-397 then :499-501: shared_read's query preparation and multiplier, the read, and the
+    wo_tk projection added to the window output delta, in one op."""
+    qn = q / q.float().norm(dim=-1, keepdim=True).clamp_min(1e-6).to(q.dtype)
+    B, T, H, NQ, _ = q.shape
+    scale = torch.exp(log_rsel.float()).expand(B, T, H, NQ)
+    if s is not None:
+        sf = s.float()
+        if rsharp:
+            sf = rsharp * torch.tanh(sf / rsharp)
+        scale = scale * torch.exp(sf)
+    return slot_read_out(qn, kbuf, buf, kinv, valid, scale, G, wo, delta=delta)

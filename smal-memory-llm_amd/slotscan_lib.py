@@ -1,4 +1,5 @@
-"""ctypes binding of libslotscan.so (declarations: include/slotscan.h, slotread.h, slotmem.h).
+"""ctypes binding of libslotscan.so (declarations: include/slotscan.h, slotread.h, slotmem.h, slotwin.h,
+slotproj.h).
 
 torch is imported BEFORE the library is opened: libslotscan.so needs libamdhip64.so.7 by SONAME, and with
 torch loaded first the dynamic loader binds it to torch's own HIP runtime, so the streams and device
@@ -52,6 +53,7 @@ SIGNATURES = {
     "slotmem_epilogue_fwd": (_i32, [_vp, _vp, _i64, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp]),
     "slotmem_epilogue_bwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i64, _i32, _vp, _vp, _vp]),
     "slotmem_codes": (_i32, [_vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp]),
+    "slotproj_fwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "slotwin_fwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp]),
     "slotwin_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                            _vp, _vp, _vp, _vp, _vp]),
@@ -100,7 +102,7 @@ def dtype_code(dt):
 
 
 KERNEL_NAMES = ("chain_fwd", "rows_fwd", "rows_bwd", "chain_bwd", "reduce_parts", "read_fwd", "read_bwd", "mem_fwd",
-                "mem_bwd", "win_fwd", "win_bwd", "gen_fwd", "gen_bwd", "spare")
+                "mem_bwd", "win_fwd", "win_bwd", "gen_fwd", "gen_bwd", "proj")
 
 
 def profile(enable, kernels=None):

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 import torch
 
+import slotscan_lib as L
 from oracle import read_oracle as RO
 
 pytestmark = pytest.mark.gpu
@@ -216,10 +217,133 @@ def test_shared_read_matches_the_readers_formula():
                 dbuf=gr["dbuf"], dkinv=gr["dkinv"], dlog_rsel=np.array((dscale * scale).sum()),
                 ds=dscale * scale * (1.0 - th * th))
     got = dict(rd=rd, dq=qq.grad, dkbuf=kk.grad, dbuf=vv.grad, dkinv=ki.grad, dlog_rsel=lrs.grad, ds=ss.grad)
+    l1 = dict(dlog_rsel=np.abs(dscale * scale).sum())      # a sum of mixed-sign terms: bar on their magnitude
     for name, r_ in want.items():
         g_ = got[name].detach().double().cpu().numpy().reshape(np.shape(r_))
-        den = max(np.abs(r_).max(), 1e-30)
+        den = max(np.abs(r_).max(), l1.get(name, 0.0), 1e-30)
         err = np.abs(g_ - r_)
         print(f"   {name}: max rel err {err.max() / den:.2e}  mean {err.mean() / den:.2e}", flush=True)
         assert err.max() <= 2e-2 * den, name
         assert err.mean() <= 3e-3 * den, name
+
+
+@pytest.mark.parametrize("with_delta", [True, False])
+def test_read_out_matches_oracle(with_delta):
+    """slotread_hip.shared_read_out, the reader's read followed by its output projection into the residual,
+    delta + wo_tk(rd) (memlm_sh.py:499-501), against the oracle read (bf16 roundings, rd rounded to bf16 as
+    the read's output) followed by an fp64 projection; backward through dRD = dDelta Wo, dWo = dDelta^T rd and
+    the read's own adjoint.  Bar: the bf16 read bar, 2e-2 of each tensor's max."""
+    B, T, H, NQ, N, D, G, C, DM = 2, 61, 3, 2, 192, 128, 8, 2.0, 256
+    _, K, V, kinv, valid, _ = make_read_inputs(B, T, H, NQ, N, D, G, seed=23)
+    gen = torch.Generator().manual_seed(24)
+    q = (3.0 * torch.randn(B, T, H, NQ, D, generator=gen)).to(torch.bfloat16)
+    s = torch.randn(B, T, H, NQ, generator=gen)
+    wo = (torch.randn(DM, H * NQ * D, generator=gen) / (H * NQ * D) ** 0.5).to(torch.bfloat16)
+    delta = torch.randn(B, T, DM, generator=gen).to(torch.bfloat16) if with_delta else None
+    dout = torch.randn(B, T, DM, generator=gen).to(torch.bfloat16)
+    lr = float(np.log(8.0))
+    c = lambda t: t.to(DEV).requires_grad_()
+    qq, kk, vv, ki, ss, ww = c(q), c(K), c(V), c(kinv), c(s), c(wo)
+    dd = c(delta) if with_delta else None
+    lrs = torch.tensor(lr, device=DEV, requires_grad=True)
+    out = RH.shared_read_out(qq, kk, vv, ki, valid.to(DEV), lrs, G, ww, s=ss, rsharp=C, delta=dd)
+    assert out.shape == (B, T, DM) and out.dtype == torch.bfloat16
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    # oracle
+    qf = q.double().numpy()
+    nrm = np.maximum(np.sqrt((qf * qf).sum(-1, keepdims=True)), 1e-6)
+    qhat = RO.bf16_round(qf / RO.bf16_round(nrm)).astype(np.float64)
+    th = np.tanh(s.double().numpy() / C)
+    scale = np.exp(lr) * np.exp(C * th)
+    NB = (T + G - 1) // G
+    f = lambda t: t.double().numpy()
+    qh, sh = to_blocks(qhat, G, NB), to_blocks(scale, G, NB)
+    rdh, cache = RO.read_forward(qh, f(K), f(V), f(kinv), valid.numpy(), sh, bf16=True)
+    rd = RO.bf16_round(from_blocks(rdh, T, NQ)).astype(np.float64).reshape(B, T, -1)
+    W = f(wo)
+    ref = rd @ W.T + (f(delta) if with_delta else 0.0)
+    g = f(dout)
+    drd = (g @ W).reshape(B, T, H, NQ, D)
+    gr = RO.read_backward(qh, f(K), f(V), f(kinv), valid.numpy(), sh, cache, to_blocks(drd, G, NB))
+    dqh = from_blocks(gr["dq"], T, NQ)
+    dscale = from_blocks(gr["dscale"], T, NQ)
+    qn = qf / nrm
+    want = dict(out=ref, dwo=g.reshape(-1, DM).T @ rd.reshape(-1, H * NQ * D),
+                dq=(dqh - qn * (dqh * qn).sum(-1, keepdims=True)) / nrm, dkbuf=gr["dkbuf"], dbuf=gr["dbuf"],
+                dkinv=gr["dkinv"], dlog_rsel=np.array((dscale * scale).sum()), ds=dscale * scale * (1.0 - th * th))
+    got = dict(out=out, dwo=ww.grad, dq=qq.grad, dkbuf=kk.grad, dbuf=vv.grad, dkinv=ki.grad, dlog_rsel=lrs.grad,
+               ds=ss.grad)
+    if with_delta:
+        want["ddelta"], got["ddelta"] = g, dd.grad
+    l1 = dict(dlog_rsel=np.abs(dscale * scale).sum())      # a sum of mixed-sign terms: bar on their magnitude
+    for name, r_ in want.items():
+        g_ = got[name].detach().double().cpu().numpy().reshape(np.shape(r_))
+        den = max(np.abs(r_).max(), l1.get(name, 0.0), 1e-30)
+        err = np.abs(g_ - r_)
+        print(f"   {name}: max rel err {err.max() / den:.2e}  mean {err.mean() / den:.2e}", flush=True)
+        assert err.max() <= 2e-2 * den, name
+        assert err.mean() <= 3e-3 * den, name
+
+
+def _bf16_ulp(x):
+    """Spacing of bf16 numbers at |x| (8 significand bits), for x of any magnitude (min normal spacing below)."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+@pytest.mark.parametrize("M,N,K,with_delta", [(1, 256, 32, True), (300, 512, 768, True), (513, 2048, 64, False),
+                                              (256, 256, 800, False)])
+def test_proj_gemm_matches_fp64(M, N, K, with_delta):
+    """slotproj_fwd, the reader's wo_tk projection with the residual add in the GEMM epilogue, against an fp64
+    GEMM of the same bf16 operands.  The kernel rounds as the reference does: the product (fp32 accumulation)
+    is rounded to bf16 -- the bf16 Linear output, memlm_sh.py:500 -- then added to delta in fp32 and rounded
+    again -- the bf16 residual add, :501.  So |out - exact| <= 1/2 bf16 ulp of the result, plus 1/2 bf16 ulp
+    of the product when there is a delta, plus the fp32 accumulation error (2^-20 * sum |rd||wo|).  Ragged M
+    (1, 300, 513) covers partial row tiles; rows past M of a larger buffer are checked untouched; K = 800 is
+    25 k stages (an odd count; the loop runs stages in pairs)."""
+    gen = torch.Generator().manual_seed(M * 7 + K)
+    a = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=gen) / K ** 0.5).to(torch.bfloat16)
+    d = torch.randn(M, N, generator=gen).to(torch.bfloat16) if with_delta else None
+    print(f"   proj M={M} N={N} K={K} delta={with_delta}", flush=True)
+    out = torch.full((M + 3, N), 7.0, dtype=torch.bfloat16, device=DEV)   # 3 guard rows past M
+    ad, wd = a.to(DEV), w.to(DEV)
+    dd = d.to(DEV) if with_delta else None
+    rc = L.lib().slotproj_fwd(L.ptr(ad), L.ptr(wd), None if dd is None else L.ptr(dd), M, N, K, L.ptr(out),
+                              L.stream_of(ad.device))
+    L.check(rc, "slotproj_fwd")
+    torch.cuda.synchronize()
+    got = out.double().cpu().numpy()
+    assert (got[M:] == 7.0).all(), "rows past M were written"
+    A, W = a.double().numpy(), w.double().numpy()
+    prod = A @ W.T
+    ref = prod + (d.double().numpy() if with_delta else 0.0)
+    bound = 0.5 * _bf16_ulp(ref) + 2.0 ** -20 * (np.abs(A) @ np.abs(W).T) + \
+        (0.5 * _bf16_ulp(prod) if with_delta else 0.0)
+    err = np.abs(got[:M] - ref)
+    print(f"   max err / bound {np.max(err / bound):.3f}", flush=True)
+    assert (err <= bound).all()
+
+
+def test_read_out_projection_runs_the_library_gemm():
+    """The read-out op's projection is the library's proj_gemm kernel (not a library GEMM) at the shapes it
+    tiles: the library's per-kernel launch count of "proj" advances by one per forward."""
+    B, T, H, NQ, N, D, G, DM = 1, 40, 2, 2, 64, 64, 4, 256
+    _, K, V, kinv, valid, _ = make_read_inputs(B, T, H, NQ, N, D, G, seed=5)
+    gen = torch.Generator().manual_seed(6)
+    q = torch.randn(B, T, H, NQ, D, generator=gen)
+    q = (q / q.norm(dim=-1, keepdim=True)).to(torch.bfloat16).to(DEV)
+    scale = torch.full((B, T, H, NQ), 4.0, device=DEV)
+    wo = torch.randn(DM, H * NQ * D, generator=gen).to(torch.bfloat16).to(DEV)
+    args = (q, K.to(DEV), V.to(DEV), kinv.to(DEV), valid.to(DEV), scale, G, wo)
+    L.profile_read()                                     # drop earlier counts
+    L.profile(True)
+    try:
+        RH.slot_read_out(*args)
+        RH.slot_read_out(*args)
+        torch.cuda.synchronize()
+    finally:
+        L.profile(False)
+    prof = L.profile_read()
+    assert prof.get("proj", (0.0, 0))[1] == 2 and prof.get("read_fwd", (0.0, 0))[1] == 2

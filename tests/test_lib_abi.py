@@ -135,3 +135,11 @@ def test_integration_doc_stubs_match_the_bindings():
         got = eval(expr, env)                                 # noqa: S307 -- the repository's own doc
         assert len(got) == arity[name], f"{name}: the doc binds {len(got)} args, C has {arity[name]}"
         assert got == L.SIGNATURES[name][1], f"{name}: the doc's argument types differ from the binding"
+
+
+@pytest.mark.parametrize("M,N,K,code", [(0, 256, 64, 1), (8, 300, 64, 1), (8, 256, 48, 1), (8, 256, 64, 3)])
+def test_proj_validation_rejects_before_launch(M, N, K, code):
+    """slotproj_fwd refuses a shape its tiles do not cover (N a multiple of 256, K of 32) or a NULL operand with
+    an error code and message, before any GPU call (so this runs without a GPU)."""
+    assert L.lib().slotproj_fwd(None, None, None, M, N, K, None, None) == code
+    assert L.lib().slotscan_last_error()
