@@ -457,6 +457,8 @@ def bench_read_out(args, W):
     t1 = time.perf_counter()
     L.profile(False)
     prof = L.profile_read()
+    if args.copy_calibration:
+        copy_calibration(dev)
     ms = (t1 - t0) * 1e3 / args.steps
     # the projection GEMM alone, same shapes (x (B*T, KD) bf16 @ wo^T into delta), timed with HIP events
     x = torch.empty(B * T, KD, device=dev, dtype=bf).normal_()
@@ -478,6 +480,7 @@ def bench_read_out(args, W):
     rby, rfl = read_algorithmic(B, T, H, N, D, NQ, 1, NB)
     gfl = 2.0 * B * T * KD * DM
     gby = 2 * (B * T * KD + DM * KD + 2 * B * T * DM)          # x, wo and delta in, the sum out (bf16)
+    mt = measured_traffic(args.workload)                        # committed rocprofv3 FETCH/WRITE summary
     out = {
         "metric": f"slot-read + wo_tk fan-out tokens/s ({layers} reader layers, frozen store B{B} H{H} S{N} d{D}, "
                   f"d_model {DM}, forward)",
@@ -489,7 +492,8 @@ def bench_read_out(args, W):
         "roofline": {"bound": "mfma", "kernel": "proj_gemm (wo_tk projection + residual add)",
                      "achieved": round(gfl / (pms * 1e-3) / 1e12, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gfl / (pms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "flops_per_launch": gfl, "algorithmic_bytes_per_launch": gby,
+                     "traffic": mt.get("proj_gemm"), "traffic_source": "profiles/hbm_traffic_config4_wo.md"
+                     if "proj_gemm" in mt else None, "flops_per_launch": gfl, "algorithmic_bytes_per_launch": gby,
                      "avg_launch_ms": round(pms, 4), "hbm_gbps": round(gby / (pms * 1e-3) / 1e9, 1),
                      "hbm_frac": round(gby / (pms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                      "library_gemm_ms": round(gemm_ms, 4)},
