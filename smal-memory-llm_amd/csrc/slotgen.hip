@@ -64,6 +64,31 @@ struct GenArgs {
     void* dk; void* dq; void* dv; float* dg; float* dfr; float* part;
 };
 
+// ---- gate and fr of 64 consecutive steps [base, base + 64) of one chain, step base + l in lane l of every
+// wave: one vector load per 64 steps, read per step with a readlane, instead of two scalar loads per step
+// (each a cache miss on the step's critical path).
+struct StepPar {
+    float g, f;
+    int base;
+};
+__device__ __forceinline__ StepPar load_steppar(const float* gate, const float* fr, int frt, int T, int H,
+                                                size_t tok0, int base, int lane) {
+    StepPar p;
+    p.base = base;
+    const int t = base + lane;
+    const bool ok = t >= 0 && t < T;
+    const size_t ti = tok0 + (size_t)(ok ? t : 0) * H;
+    p.g = ok ? gate[ti] : 0.f;
+    p.f = frt ? (ok ? fr[ti] : 0.f) : fr[0];
+    return p;
+}
+__device__ __forceinline__ float steppar_g(const StepPar& p, int t) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p.g), t - p.base));
+}
+__device__ __forceinline__ float steppar_f(const StepPar& p, int t) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p.f), t - p.base));
+}
+
 // ---- token loads (f32 or bf16 tokens, always fp32 registers)
 template <typename TI, int N> __device__ __forceinline__ void ldtok(const TI* p, float* x) {
     if constexpr (sizeof(TI) == 4) {
@@ -112,6 +137,14 @@ __device__ __forceinline__ void best_merge(float z0, int i0, float z1, int i1, f
     z = first ? z0 : z1; i = first ? i0 : i1;
 }
 
+// Workgroup barrier for an exchange through LDS only: this wave's LDS accesses complete, then s_barrier.
+// __syncthreads() would also wait for every global store the wave has in flight (its release fence), and the
+// per-step exchanges below do not need that: what they publish is in LDS.  Global data another wave reads
+// (the replay scratch) is published with __syncthreads().
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Sum over the 4 row-lanes (lanes c, c+16, c+32, c+48).
 __device__ __forceinline__ float rows4_sum(float x) { return sum4rows(x); }
 
@@ -122,54 +155,83 @@ template <int RPL>
 __device__ __forceinline__ int gen_address(const float (&z)[RPL], const float (&o)[RPL], int nbase, int N,
                                            float eps, bool hard, int hard_row, float* xf, int w, int lane,
                                            float (&as)[RPL], float (&ad)[RPL]) {
-    float m = -INFINITY, s = 0.f;
+    // Short dependency chains: maxima first, then independent exponentials summed in trees (the lane's rows,
+    // its 4 row-lanes, the 8 waves' posts), instead of an online softmax carried row by row.
+    float m = -INFINITY;
     int ff = INT_MAX; float zff = 0.f;
     float bz = 0.f; int bi = INT_MAX;
+    bool cmp[RPL];
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
         const int n = nbase + j;
-        if (n < N && o[j] >= eps) {
-            const float m2 = fmaxf(m, z[j]);
-            s = (s > 0.f ? s * __expf(m - m2) : 0.f) + __expf(z[j] - m2);
-            m = m2;
+        cmp[j] = n < N && o[j] >= eps;
+        if (cmp[j]) {
+            m = fmaxf(m, z[j]);
             if (bi == INT_MAX || z[j] > bz) { bz = z[j]; bi = n; }
         } else if (n < N && ff == INT_MAX) {
             ff = n; zff = z[j];
         }
     }
-    // across the 4 row-lanes
-    {
-        float m0, m1, s0, s1, a0, a1, b0, b1, c0, c1, d0, d1;
-        swap16(m, m0, m1); swap16(s, s0, s1); ms_merge(m0, s0, m1, s1, m, s);
+    {   // the max and the index reductions over the 4 row-lanes
+        float m0, m1, a0, a1, b0, b1, c0, c1, d0, d1;
+        swap16(m, m0, m1); m = fmaxf(m0, m1);
         swap16(__int_as_float(ff), a0, a1); swap16(zff, b0, b1);
         idx_merge(__float_as_int(a0), b0, __float_as_int(a1), b1, ff, zff);
         swap16(bz, c0, c1); swap16(__int_as_float(bi), d0, d1);
         best_merge(c0, __float_as_int(d0), c1, __float_as_int(d1), bz, bi);
-        swap32(m, m0, m1); swap32(s, s0, s1); ms_merge(m0, s0, m1, s1, m, s);
+        swap32(m, m0, m1); m = fmaxf(m0, m1);
         swap32(__int_as_float(ff), a0, a1); swap32(zff, b0, b1);
         idx_merge(__float_as_int(a0), b0, __float_as_int(a1), b1, ff, zff);
         swap32(bz, c0, c1); swap32(__int_as_float(bi), d0, d1);
         best_merge(c0, __float_as_int(d0), c1, __float_as_int(d1), bz, bi);
+    }
+    float s = 0.f;                            // sum of exp(z - m) over the wave's competing rows
+    {
+        float e[RPL];
+#pragma unroll
+        for (int j = 0; j < RPL; j++) e[j] = cmp[j] ? __expf(z[j] - m) : 0.f;
+#pragma unroll
+        for (int j = 0; j < RPL; j++) s += e[j];
+        float s0, s1;
+        swap16(s, s0, s1); s = s0 + s1;
+        swap32(s, s0, s1); s = s0 + s1;
     }
     if (lane == 0) {
         float4* p = reinterpret_cast<float4*>(xf + w * 8);
         p[0] = make_float4(m, s, __int_as_float(ff), zff);
         p[1] = make_float4(bz, __int_as_float(bi), 0.f, 0.f);
     }
-    __syncthreads();
-    float M = -INFINITY, S = 0.f, Z = 0.f, BZ = 0.f;
-    int FF = INT_MAX, BI = INT_MAX;
+    lds_barrier();
+    float4 p0[GEN_WAVES], p1[GEN_WAVES];
 #pragma unroll
     for (int ww = 0; ww < GEN_WAVES; ww++) {
-        const float4 p0 = reinterpret_cast<const float4*>(xf + ww * 8)[0];
-        const float4 p1 = reinterpret_cast<const float4*>(xf + ww * 8)[1];
-        ms_merge(M, S, p0.x, p0.y, M, S);
-        idx_merge(FF, Z, __float_as_int(p0.z), p0.w, FF, Z);
-        best_merge(BZ, BI, p1.x, __float_as_int(p1.y), BZ, BI);
+        p0[ww] = reinterpret_cast<const float4*>(xf + ww * 8)[0];
+        p1[ww] = reinterpret_cast<const float4*>(xf + ww * 8)[1];
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < GEN_WAVES; ww++) M = fmaxf(M, p0[ww].x);
+    int FF = INT_MAX; float Z = 0.f;
+    float BZ = 0.f; int BI = INT_MAX;
+#pragma unroll
+    for (int ww = 0; ww < GEN_WAVES; ww++) {   // waves in row order: the lowest index wins ties
+        idx_merge(FF, Z, __float_as_int(p0[ww].z), p0[ww].w, FF, Z);
+        best_merge(BZ, BI, p1[ww].x, __float_as_int(p1[ww].y), BZ, BI);
     }
     if (FF != INT_MAX) {                      // the first free row competes too
-        ms_merge(M, S, Z, 1.f, M, S);
+        M = fmaxf(M, Z);
         best_merge(BZ, BI, Z, FF, BZ, BI);
+    }
+    float S = FF != INT_MAX ? __expf(Z - M) : 0.f;
+    {
+        float sw[GEN_WAVES];
+#pragma unroll
+        for (int ww = 0; ww < GEN_WAVES; ww++) sw[ww] = p0[ww].y > 0.f ? p0[ww].y * __expf(p0[ww].x - M) : 0.f;
+#pragma unroll
+        for (int st = GEN_WAVES / 2; st >= 1; st /= 2)
+#pragma unroll
+            for (int ww = 0; ww < st; ww++) sw[ww] += sw[ww + st];
+        S += sw[0];
     }
     const float rS = 1.f / S;
     const int row = hard ? (hard_row >= 0 ? hard_row : BI) : -1;
@@ -275,6 +337,9 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
         o[j] = 0.f;
     }
     auto tok = [&](int t) { return ((size_t)b * a.T + t) * a.H + h; };
+    const size_t tok0 = tok(0);
+    StepPar spc = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, 0, lane);     // steps [64 i, 64 i + 64)
+    StepPar spn = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, 64, lane);    // the next 64, in flight
     float kt[DPK], qt[DPK], vt[DPV];
     ldtok<TI, DPK>(kp + tok(0) * DK + dl * DPK, kt);
     ldtok<TI, DPK>(qp + tok(0) * DK + dl * DPK, qt);
@@ -297,8 +362,12 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
             }
         }
         const size_t ti = tok(t);
-        const float g = a.gate[ti];
-        const float frt = a.frt ? a.fr[ti] : a.fr[0];
+        if (t > 0 && (t & 63) == 0) {
+            spc = spn;
+            spn = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, t + 64, lane);
+        }
+        const float g = steppar_g(spc, t);
+        const float frt = steppar_f(spc, t);
         float kn_[DPK], qn_[DPK], vn_[DPV];
         if (t + 1 < a.T) {
             ldtok<TI, DPK>(kp + tok(t + 1) * DK + dl * DPK, kn_);
@@ -327,13 +396,17 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------- backward
-// Scratch per chain and segment step s: K (NP, DK), then six row scalars (NP each): o, a_s, a, s, |K| and
-// e - P = <v_t, D> - <V, D>; then qinv per step.  NP = 32 * RPL.
+// Scratch per chain: for every segment step s six row scalars (NP each): o, a_s, a, s, |K| and
+// e - P = <v_t, D> - <V, D>; then the pre-write keys (NP, DK) of every GC-th step after the first (the
+// first step's are the emitted copy); then qinv per step.  NP = 32 * RPL.  The walk rebuilds the keys of
+// any step from the checkpoint at or before it with the updates in between (at most GC - 1), the same
+// fmaf sequence, weights and token values as the replay, so bitwise the replay's keys.
 template <int DK, int DV, int RPL>
 struct GenScr {
     static constexpr int NP = 32 * RPL;
-    static constexpr int64_t step = (int64_t)NP * (DK + 6);
-    static int64_t chain(int G) { return step * G + ((G + 3) / 4) * 4; }
+    static constexpr int GC = 4;
+    __host__ __device__ static int64_t nck(int G) { return (G - 1) / GC; }
+    __host__ __device__ static int64_t chain(int G) { return (int64_t)G * 6 * NP + nck(G) * NP * DK + ((G + 3) / 4) * 4; }
 };
 
 template <typename TI, int DK, int DV, int RPL>
@@ -357,8 +430,19 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
     TI* dvp = static_cast<TI*>(a.dv);
     const float temp = a.temp[0];
     float* scr = a.scr + (size_t)chain * a.scr_chain;
-    float* scr_qinv = scr + SC::step * a.G;
+    float* scr_s = scr;                                        // row scalars, 6 NP per step
+    float* scr_k = scr_s + (size_t)a.G * 6 * NP;               // key checkpoints, NP DK each
+    float* scr_qinv = scr_k + (size_t)SC::nck(a.G) * NP * DK;
     auto tok = [&](int t) { return ((size_t)b * a.T + t) * a.H + h; };
+    const size_t tok0 = tok(0);
+    // gate and fr through a 64-step window that ends at the current segment's end, so that the next (earlier)
+    // segments find their steps in it too: reloaded once per 64 steps (per step where G > 64)
+    StepPar sp = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, max(a.T - 64, 0), lane);
+    auto steppar = [&](int t, float& g, float& f) {
+        if (t < sp.base || t >= sp.base + 64) sp = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, max(t - 63, 0), lane);
+        g = steppar_g(sp, t);
+        f = steppar_f(sp, t);
+    };
 
     // The value adjoint lives in LDS: inside a segment it only scales, dV(t+) = cV(t) D, so the walk reads
     // D and keeps the per-row factors cV in registers; D is rewritten once per segment (at its first step).
@@ -420,6 +504,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
 
     for (int tb = a.NB - 1; tb >= 0; tb--) {
         const int t0 = tb * a.G, t1 = min(t0 + a.G, a.T);
+        if (t0 < sp.base) sp = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, max(t1 - 64, 0), lane);
         // ---- replay the segment from its emitted copy, keeping every step's pre-write state
         {
             // The value state itself is not replayed: inside a segment the value adjoint only scales,
@@ -429,22 +514,24 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             gen_load_keys<RPL, DPK, DPV>(a, b, h, tb, nbase, dl, dvr, K, o, P);
             for (int t = t0; t < t1; t++) {
                 const int s = t - t0;
-                float* sk = scr + SC::step * s;
-                float* ss = sk + NP * DK;
+                float* ss = scr_s + (size_t)s * 6 * NP;
+                if (s > 0 && s % SC::GC == 0) {             // a key checkpoint
+                    float* sk = scr_k + (size_t)(s / SC::GC - 1) * NP * DK;
 #pragma unroll
-                for (int j = 0; j < RPL; j++) {
-                    const int n = nbase + j;
+                    for (int j = 0; j < RPL; j++) {
+                        const int n = nbase + j;
 #pragma unroll
-                    for (int i = 0; i < DPK; i += 4)
-                        st4(sk + n * DK + dl * DPK + i, make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]));
+                        for (int i = 0; i < DPK; i += 4)
+                            st4(sk + n * DK + dl * DPK + i, make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]));
+                    }
                 }
                 const size_t ti = tok(t);
                 float kt[DPK], qt[DPK], vt[DPV];
                 ldtok<TI, DPK>(kp + ti * DK + dl * DPK, kt);
                 ldtok<TI, DPK>(qp + ti * DK + dl * DPK, qt);
                 ldtok<TI, DPV>(vp + ti * DV + dl * DPV, vt);
-                const float g = a.gate[ti];
-                const float frt = a.frt ? a.fr[ti] : a.fr[0];
+                float g, frt;
+                steppar(t, g, frt);
                 float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
                 gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, a.pin, z, sr, knr, qinv);
                 gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, a.hard ? a.am[ti] : -1, xf[par], w, lane, as, ad);
@@ -488,20 +575,39 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
         for (int j = 0; j < RPL; j++) cV[j] = 1.f;
         for (int t = t1 - 1; t >= t0; t--) {
             const int s = t - t0;
-            const float* sk = scr + SC::step * s;
-            const float* ss = sk + NP * DK;
+            const float* ss = scr_s + (size_t)s * 6 * NP;
             const size_t ti = tok(t);
-            // The pre-write keys are read from the scratch twice, before and after the step's barrier, rather
-            // than held across it: 8 * RPL fewer live registers through the exchange (the second read hits
-            // the cache the first one filled).
+            // The pre-write keys of step s: the checkpoint at or before it (the emitted copy for the segment's
+            // first GC steps), then the replay's updates of the steps in between.  Built twice, before and
+            // after the step's barrier, rather than held across it: 8 * RPL fewer live registers through the
+            // exchange (the second build reads what the first one brought into the cache).
             auto load_K = [&](float (&K)[RPL][DPK]) {
+                const int c = (s / SC::GC) * SC::GC;
+                const size_t base = (((size_t)b * a.NB + tb) * a.H + h) * a.N;
+                const float* ck = scr_k + (size_t)max(c / SC::GC - 1, 0) * NP * DK;
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
                     const int n = nbase + j;
+                    const bool ok = c > 0 || n < a.N;
+                    const float* src = c > 0 ? ck + n * DK : a.kbuf + (base + (ok ? n : 0)) * DK;
 #pragma unroll
                     for (int i = 0; i < DPK; i += 4) {
-                        const float4 f = ld4(sk + n * DK + dl * DPK + i);
+                        const float4 f = ok ? ld4(src + dl * DPK + i) : make_float4(0.f, 0.f, 0.f, 0.f);
                         K[j][i] = f.x; K[j][i + 1] = f.y; K[j][i + 2] = f.z; K[j][i + 3] = f.w;
+                    }
+                }
+                for (int u = c; u < s; u++) {
+                    const size_t tu = tok(t0 + u);
+                    float ku[DPK];
+                    ldtok<TI, DPK>(kp + tu * DK + dl * DPK, ku);
+                    const float gu = steppar_g(sp, t0 + u);
+                    const float* su = scr_s + (size_t)u * 6 * NP + 2 * NP + nbase;     // the address a of step u
+#pragma unroll
+                    for (int j = 0; j < RPL; j++) {
+                        const float wr = gu * su[j];
+                        const float omw = 1.f - wr;
+#pragma unroll
+                        for (int i = 0; i < DPK; i++) K[j][i] = fmaf(omw, K[j][i], wr * ku[i]);
                     }
                 }
             };
@@ -512,8 +618,8 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             };
             float kt[DPK];
             ldtok<TI, DPK>(kp + ti * DK + dl * DPK, kt);
-            const float g = a.gate[ti];
-            const float frt = a.frt ? a.fr[ti] : a.fr[0];
+            float g, frt;
+            steppar(t, g, frt);
             const float qinv = scr_qinv[s];
 
             // dw per row; dk_t, dv_t partials; the two address sums
@@ -569,7 +675,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 }
                 if (lane == 0) { q1[w * P1W + DK + DV] = pg; q1[w * P1W + DK + DV + 1] = pa; }
             }
-            __syncthreads();
+            lds_barrier();
             if (pend_t >= 0) finish_q(pend_t, pend_qinv, p2[par ^ 1]);
             float SG = 0.f, SA = 0.f;
 #pragma unroll
@@ -720,7 +826,7 @@ static void dispatch(bool bwd, int64_t DK, int64_t DV, int rpl, dim3 grid, hipSt
 static int64_t scr_chain(int64_t DK, int64_t DV, int rpl, int64_t G) {
     const int64_t NP = 32 * rpl;
     (void)DV;
-    return NP * (DK + 6) * G + ((G + 3) / 4) * 4;
+    return G * 6 * NP + ((G - 1) / 4) * NP * DK + ((G + 3) / 4) * 4;   // GenScr<...>::chain
 }
 
 }  // namespace
