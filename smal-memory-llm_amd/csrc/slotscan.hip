@@ -1530,11 +1530,13 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     constexpr int KK = NR / 4;                          // MFMA k-steps over the rows
     constexpr int P = NR + 4;                           // transposed key stride: 4 mod 32 banks
     constexpr int SW = NR + 4;                          // W row stride, likewise
-    constexpr int SC = NR + 2;                          // cosine / Dn row stride (step-major): 2 mod 32
+    constexpr int SC = NR + 4;                          // cosine / Dn row stride (step-major): 4 mod 64 banks, so
+                                                        // the Dn publish (16 steps x 4 rows per pass) hits 64 banks
     constexpr int KOS = D + 4;                          // kold / query row stride
     constexpr int NC = NT / WIN;                        // lanes per step in the softmax phase
     constexpr int RPC = NR / NC;                        // slot rows per lane in the softmax phase
-    constexpr int DPT = D / NC;                         // dims per lane in the undo (4)
+    constexpr int DPT = D / NC;                         // dims per lane in the undo (4), strided by NC
+    constexpr int DEL = D + 16;                         // undo-delta row stride: 4 steps x 16 dims per pass on 64 banks
     constexpr int EPU = 16 / (int)sizeof(TI);
     constexpr int UCS = (WIN * NR + NT - 1) / NT;       // per-lane prefetch: cosines, Dn
     constexpr int UKO = (WIN * D / 4 + NT - 1) / NT;    // kold rows (uint4)
@@ -1543,7 +1545,7 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     static_assert(DPT == 4 && RPC % 2 == 0 && (KK / 4) % 2 == 0, "layout assumptions");
     __shared__ __align__(16) float sKT[D * P];          // normalised keys, transposed
     __shared__ __align__(16) float sW[WIN * SW];
-    constexpr int CSN = WIN * SC > WIN * D ? WIN * SC : WIN * D;
+    constexpr int CSN = WIN * SC > WIN * DEL ? WIN * SC : WIN * DEL;
     __shared__ __align__(16) float sCS[CSN];            // cosines [step][row]; the undo deltas [step][D] after S4
     __shared__ __align__(16) float sDN[WIN * SC];       // Dn [step][row]
     __shared__ __align__(16) float sKO[WIN * KOS];      // kold rows of the window's writes
@@ -1841,33 +1843,28 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
             acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av2.w, bv2.w, acc2, 0, 0, 0);
         }
-        // S7: the undo of every write at once: write i = lanes [NC i, NC i + NC), dims e0 .. e0 + 3
-        const int ui = tidw / NC, ue0 = (tidw % NC) * DPT;
+        // S7: the undo of every write at once: write i = lanes [NC i, NC i + NC), dims ud + NC e.  Dims strided
+        // across lanes, so the column accesses of the transposed keys (stride P per dim) spread over the banks
+        const int ui = tidw / NC, ud = tidw % NC;
         const bool uev = ui < nt;
         const int uai = min(max(s_am[ui], 0), NR - 1);
-        float4 ux;
+        float ux[DPT];
         {
             const float ki = s_kil[ui];
-            const float4 x = ld4(&sKO[ui * KOS + ue0]);
-            ux = make_float4(x.x * ki, x.y * ki, x.z * ki, x.w * ki);
             const int nx = s_nx[ui];
-            float4 af;
-            if (nx >= 0) {
-                const float kn = s_kil[nx];
-                const float4 y = ld4(&sKO[nx * KOS + ue0]);
-                af = make_float4(y.x * kn, y.y * kn, y.z * kn, y.w * kn);
-            } else {
-                af = make_float4(sKT[(ue0 + 0) * P + uai], sKT[(ue0 + 1) * P + uai], sKT[(ue0 + 2) * P + uai],
-                                 sKT[(ue0 + 3) * P + uai]);
+            const float kn = nx >= 0 ? s_kil[nx] : 0.f;
+#pragma unroll
+            for (int e = 0; e < DPT; e++) {
+                const int d = ud + NC * e;
+                ux[e] = sKO[ui * KOS + d] * ki;
+                const float af = nx >= 0 ? sKO[nx * KOS + d] * kn : sKT[d * P + uai];
+                sDel[ui * DEL + d] = uev ? ux[e] - af : 0.f;
             }
-            const float4 dd = uev ? make_float4(ux.x - af.x, ux.y - af.y, ux.z - af.z, ux.w - af.w)
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-            *reinterpret_cast<float4*>(&sDel[ui * D + ue0]) = dd;
         }
         __syncthreads();                                                      // B3: every read of the window-end keys done
         if (uev && s_first[ui]) {
-            sKT[(ue0 + 0) * P + uai] = ux.x; sKT[(ue0 + 1) * P + uai] = ux.y;
-            sKT[(ue0 + 2) * P + uai] = ux.z; sKT[(ue0 + 3) * P + uai] = ux.w;
+#pragma unroll
+            for (int e = 0; e < DPT; e++) sKT[(ud + NC * e) * P + uai] = ux[e];
         }
         // S8: the rewritten rows' correction, sum_{s >= t} W[t][a_s] delta_s
 #pragma unroll
@@ -1875,7 +1872,7 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
             const int s = 4 * kc + grpw;
-            const float bv = s < nt ? sDel[s * D + d0 + cw] : 0.f;
+            const float bv = s < nt ? sDel[s * DEL + d0 + cw] : 0.f;
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av8[kc], bv, acc, 0, 0, 0);
         }
         // S9: dq = qinv (dqn - qhat <qhat, dqn>), or qinv dqn where |q| < 1e-6.  <qhat, dqn> = sum_n W_n <qhat, Kh_n>
