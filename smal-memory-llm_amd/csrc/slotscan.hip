@@ -1932,12 +1932,13 @@ hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
 #undef SLOT_CF
     return hipErrorInvalidValue;
 }
-// chain_bwd_w's chunks: windows per chunk so that the launch has about 1,536 workgroups (six per CU, one
-// resident at a time), and at least 4 windows each, so that a chunk's start (a scan of the later address log
-// and one gather of the key rows) stays a small part of its work.
+// chain_bwd_w's chunks: windows per chunk so that the launch has about 768 workgroups (three rounds of one
+// per CU: the 157 KB of LDS holds one), and at least 4 windows each, so that a chunk's start (a scan of the
+// later address log and one gather of the key rows) stays a small part of its work.  Measured at config 2:
+// 0.608 ms at this target (2 chunks per chain), 0.637 at 1,536 workgroups, 0.673 at 3,072.
 static int chain_bwd_wpc(int64_t BH, int64_t T) {
     const int64_t nwin = (T + WIN - 1) / WIN;
-    const int64_t w = (nwin * BH + 1535) / 1536;
+    const int64_t w = (nwin * BH + 767) / 768;
     return (int)std::min<int64_t>(nwin, std::max<int64_t>(4, w));
 }
 static int64_t chain_bwd_chunks(int64_t BH, int64_t T) {

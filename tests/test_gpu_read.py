@@ -293,7 +293,8 @@ def _bf16_ulp(x):
 
 
 @pytest.mark.parametrize("M,N,K,with_delta", [(1, 256, 32, True), (300, 512, 768, True), (513, 2048, 64, False),
-                                              (256, 256, 800, False)])
+                                              (256, 256, 800, False), (70, 512, 96, True), (200, 256, 128, True),
+                                              (257, 256, 800, True)])
 def test_proj_gemm_matches_fp64(M, N, K, with_delta):
     """slotproj_fwd, the reader's wo_tk projection with the residual add in the GEMM epilogue, against an fp64
     GEMM of the same bf16 operands.  The kernel rounds as the reference does: the product (fp32 accumulation)
@@ -301,7 +302,8 @@ def test_proj_gemm_matches_fp64(M, N, K, with_delta):
     again -- the bf16 residual add, :501.  So |out - exact| <= 1/2 bf16 ulp of the result, plus 1/2 bf16 ulp
     of the product when there is a delta, plus the fp32 accumulation error (2^-20 * sum |rd||wo|).  Ragged M
     (1, 300, 513) covers partial row tiles; rows past M of a larger buffer are checked untouched; K = 800 is
-    25 k stages (an odd count; the loop runs stages in pairs)."""
+    25 k stages (an odd count; the loop runs stages in pairs); K = 96 and 128 are 3 and 4 stages, either
+    side of where delta starts to be fetched during the k loop (4 stages or more)."""
     gen = torch.Generator().manual_seed(M * 7 + K)
     a = torch.randn(M, K, generator=gen).to(torch.bfloat16)
     w = (torch.randn(N, K, generator=gen) / K ** 0.5).to(torch.bfloat16)

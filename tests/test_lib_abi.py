@@ -60,7 +60,7 @@ def test_single_hip_runtime_in_process():
 
 @pytest.mark.parametrize("B,T,H,N,chunks", [
     (3, 100, 2, 40, 2),        # 7 windows of 16 steps, at least 4 per chunk
-    (64, 1024, 6, 192, 4),     # config 2: 384 chains x 4 chunks of 16 windows = 1,536 workgroups
+    (64, 1024, 6, 192, 2),     # config 2: 384 chains x 2 chunks of 32 windows = 768 workgroups
     (512, 128, 6, 96, 1),      # config 3, (512, 128): 3,072 chains already, one chunk each
     (1, 8, 1, 16, 1),
 ])
