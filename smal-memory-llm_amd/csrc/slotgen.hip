@@ -69,10 +69,11 @@ struct GenArgs {
 // (each a cache miss on the step's critical path).
 struct StepPar {
     float g, f;
+    int am;                                   // the written row (hard mode, backward), else -1
     int base;
 };
-__device__ __forceinline__ StepPar load_steppar(const float* gate, const float* fr, int frt, int T, int H,
-                                                size_t tok0, int base, int lane) {
+__device__ __forceinline__ StepPar load_steppar(const float* gate, const float* fr, int frt, const int32_t* am,
+                                                int T, int H, size_t tok0, int base, int lane) {
     StepPar p;
     p.base = base;
     const int t = base + lane;
@@ -80,6 +81,7 @@ __device__ __forceinline__ StepPar load_steppar(const float* gate, const float* 
     const size_t ti = tok0 + (size_t)(ok ? t : 0) * H;
     p.g = ok ? gate[ti] : 0.f;
     p.f = frt ? (ok ? fr[ti] : 0.f) : fr[0];
+    p.am = (am && ok) ? am[ti] : -1;
     return p;
 }
 __device__ __forceinline__ float steppar_g(const StepPar& p, int t) {
@@ -88,6 +90,7 @@ __device__ __forceinline__ float steppar_g(const StepPar& p, int t) {
 __device__ __forceinline__ float steppar_f(const StepPar& p, int t) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p.f), t - p.base));
 }
+__device__ __forceinline__ int steppar_am(const StepPar& p, int t) { return __builtin_amdgcn_readlane(p.am, t - p.base); }
 
 // ---- token loads (f32 or bf16 tokens, always fp32 registers)
 template <typename TI, int N> __device__ __forceinline__ void ldtok(const TI* p, float* x) {
@@ -338,8 +341,8 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
     }
     auto tok = [&](int t) { return ((size_t)b * a.T + t) * a.H + h; };
     const size_t tok0 = tok(0);
-    StepPar spc = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, 0, lane);     // steps [64 i, 64 i + 64)
-    StepPar spn = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, 64, lane);    // the next 64, in flight
+    StepPar spc = load_steppar(a.gate, a.fr, a.frt, nullptr, a.T, a.H, tok0, 0, lane);   // steps [64 i, 64 i + 64)
+    StepPar spn = load_steppar(a.gate, a.fr, a.frt, nullptr, a.T, a.H, tok0, 64, lane);  // the next 64, in flight
     float kt[DPK], qt[DPK], vt[DPV];
     ldtok<TI, DPK>(kp + tok(0) * DK + dl * DPK, kt);
     ldtok<TI, DPK>(qp + tok(0) * DK + dl * DPK, qt);
@@ -364,7 +367,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
         const size_t ti = tok(t);
         if (t > 0 && (t & 63) == 0) {
             spc = spn;
-            spn = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, t + 64, lane);
+            spn = load_steppar(a.gate, a.fr, a.frt, nullptr, a.T, a.H, tok0, t + 64, lane);
         }
         const float g = steppar_g(spc, t);
         const float frt = steppar_f(spc, t);
@@ -396,9 +399,11 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------- backward
-// Scratch per chain: for every segment step s six row scalars (NP each): o, a_s, a, s, |K| and
-// e - P = <v_t, D> - <V, D>; then the pre-write keys (NP, DK) of every GC-th step after the first (the
-// first step's are the emitted copy); then qinv per step.  NP = 32 * RPL.  The walk rebuilds the keys of
+// Scratch per chain: for every segment step s five row scalars (NP each): o, a_s, s, |K| and
+// e - P = <v_t, D> - <V, D> (the write address a is a_s, or in hard mode the logged row); then the
+// pre-write keys (NP, DK) of every GC-th step after the first (the first step's are the emitted copy); then
+// qinv per step.  NP = 32 * RPL.  The first GL steps of a segment keep their scalars, key tokens and qinv in
+// LDS instead (gen_bwd), so the walk reads them at LDS latency.  The walk rebuilds the keys of
 // any step from the checkpoint at or before it with the updates in between (at most GC - 1), the same
 // fmaf sequence, weights and token values as the replay, so bitwise the replay's keys.
 template <int DK, int DV, int RPL>
@@ -406,7 +411,7 @@ struct GenScr {
     static constexpr int NP = 32 * RPL;
     static constexpr int GC = 4;
     __host__ __device__ static int64_t nck(int G) { return (G - 1) / GC; }
-    __host__ __device__ static int64_t chain(int G) { return (int64_t)G * 6 * NP + nck(G) * NP * DK + ((G + 3) / 4) * 4; }
+    __host__ __device__ static int64_t chain(int G) { return (int64_t)G * 5 * NP + nck(G) * NP * DK + ((G + 3) / 4) * 4; }
 };
 
 template <typename TI, int DK, int DV, int RPL>
@@ -430,16 +435,17 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
     TI* dvp = static_cast<TI*>(a.dv);
     const float temp = a.temp[0];
     float* scr = a.scr + (size_t)chain * a.scr_chain;
-    float* scr_s = scr;                                        // row scalars, 6 NP per step
-    float* scr_k = scr_s + (size_t)a.G * 6 * NP;               // key checkpoints, NP DK each
+    float* scr_s = scr;                                        // row scalars, 5 NP per step
+    float* scr_k = scr_s + (size_t)a.G * 5 * NP;               // key checkpoints, NP DK each
     float* scr_qinv = scr_k + (size_t)SC::nck(a.G) * NP * DK;
     auto tok = [&](int t) { return ((size_t)b * a.T + t) * a.H + h; };
     const size_t tok0 = tok(0);
     // gate and fr through a 64-step window that ends at the current segment's end, so that the next (earlier)
     // segments find their steps in it too: reloaded once per 64 steps (per step where G > 64)
-    StepPar sp = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, max(a.T - 64, 0), lane);
+    const int32_t* amlog = a.hard ? a.am : nullptr;
+    StepPar sp = load_steppar(a.gate, a.fr, a.frt, amlog, a.T, a.H, tok0, max(a.T - 64, 0), lane);
     auto steppar = [&](int t, float& g, float& f) {
-        if (t < sp.base || t >= sp.base + 64) sp = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, max(t - 63, 0), lane);
+        if (t < sp.base || t >= sp.base + 64) sp = load_steppar(a.gate, a.fr, a.frt, amlog, a.T, a.H, tok0, max(t - 63, 0), lane);
         g = steppar_g(sp, t);
         f = steppar_f(sp, t);
     };
@@ -448,6 +454,11 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
     // D and keeps the per-row factors cV in registers; D is rewritten once per segment (at its first step).
     // Each lane reads and writes only its own rows and dims.
     __shared__ __align__(16) float sD[NP * DV];
+    // a segment's first GL steps: row scalars [step][5][NP], key tokens [step][DK], qinv [step]
+    constexpr int GL = 8;
+    __shared__ __align__(16) float lsc[GL * 5 * NP];
+    __shared__ __align__(16) float ltok[GL * DK];
+    __shared__ float lqinv[GL];
     float* dvr = sD + nbase * DV + dl * DPV;
     float dK[RPL][DPK], dO[RPL];
 #pragma unroll
@@ -504,7 +515,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
 
     for (int tb = a.NB - 1; tb >= 0; tb--) {
         const int t0 = tb * a.G, t1 = min(t0 + a.G, a.T);
-        if (t0 < sp.base) sp = load_steppar(a.gate, a.fr, a.frt, a.T, a.H, tok0, max(t1 - 64, 0), lane);
+        if (t0 < sp.base) sp = load_steppar(a.gate, a.fr, a.frt, amlog, a.T, a.H, tok0, max(t1 - 64, 0), lane);
         // ---- replay the segment from its emitted copy, keeping every step's pre-write state
         {
             // The value state itself is not replayed: inside a segment the value adjoint only scales,
@@ -514,7 +525,12 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             gen_load_keys<RPL, DPK, DPV>(a, b, h, tb, nbase, dl, dvr, K, o, P);
             for (int t = t0; t < t1; t++) {
                 const int s = t - t0;
-                float* ss = scr_s + (size_t)s * 6 * NP;
+                // explicit branches (s is uniform): a select between the LDS and the global pointer would make
+                // every access a flat one, which waits on both counters
+                auto put_s = [&](int f, int n, float v) {
+                    if (s < GL) lsc[(s * 5 + f) * NP + n] = v;
+                    else scr_s[((size_t)s * 5 + f) * NP + n] = v;
+                };
                 if (s > 0 && s % SC::GC == 0) {             // a key checkpoint
                     float* sk = scr_k + (size_t)(s / SC::GC - 1) * NP * DK;
 #pragma unroll
@@ -534,7 +550,12 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 steppar(t, g, frt);
                 float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
                 gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, a.pin, z, sr, knr, qinv);
-                gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, a.hard ? a.am[ti] : -1, xf[par], w, lane, as, ad);
+                gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, a.hard ? steppar_am(sp, t) : -1, xf[par], w, lane, as, ad);
+                if (s < GL && w == 0 && rl == 0) {             // the key token, for the walk's key rebuilds
+#pragma unroll
+                    for (int i = 0; i < DPK; i += 4)
+                        *reinterpret_cast<float4*>(ltok + s * DK + dl * DPK + i) = make_float4(kt[i], kt[i + 1], kt[i + 2], kt[i + 3]);
+                }
                 par ^= 1;
                 float e[RPL];
 #pragma unroll
@@ -552,11 +573,14 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
 #pragma unroll
                     for (int j = 0; j < RPL; j++) {
                         const int n = nbase + j;
-                        ss[n] = o[j]; ss[NP + n] = as[j]; ss[2 * NP + n] = ad[j]; ss[3 * NP + n] = sr[j];
-                        ss[4 * NP + n] = knr[j]; ss[5 * NP + n] = e[j] - P[j];
+                        put_s(0, n, o[j]); put_s(1, n, as[j]); put_s(2, n, sr[j]);
+                        put_s(3, n, knr[j]); put_s(4, n, e[j] - P[j]);
                     }
                 }
-                if (threadIdx.x == 0) scr_qinv[s] = qinv;
+                if (threadIdx.x == 0) {
+                    if (s < GL) lqinv[s] = qinv;
+                    else scr_qinv[s] = qinv;
+                }
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
                     wr[j] = g * ad[j];
@@ -575,7 +599,6 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
         for (int j = 0; j < RPL; j++) cV[j] = 1.f;
         for (int t = t1 - 1; t >= t0; t--) {
             const int s = t - t0;
-            const float* ss = scr_s + (size_t)s * 6 * NP;
             const size_t ti = tok(t);
             // The pre-write keys of step s: the checkpoint at or before it (the emitted copy for the segment's
             // first GC steps), then the replay's updates of the steps in between.  Built twice, before and
@@ -597,14 +620,30 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                     }
                 }
                 for (int u = c; u < s; u++) {
-                    const size_t tu = tok(t0 + u);
                     float ku[DPK];
-                    ldtok<TI, DPK>(kp + tu * DK + dl * DPK, ku);
+                    if (u < GL) {
+#pragma unroll
+                        for (int i = 0; i < DPK; i += 4) {
+                            const float4 f = *reinterpret_cast<const float4*>(ltok + u * DK + dl * DPK + i);
+                            ku[i] = f.x; ku[i + 1] = f.y; ku[i + 2] = f.z; ku[i + 3] = f.w;
+                        }
+                    } else {
+                        ldtok<TI, DPK>(kp + tok(t0 + u) * DK + dl * DPK, ku);
+                    }
                     const float gu = steppar_g(sp, t0 + u);
-                    const float* su = scr_s + (size_t)u * 6 * NP + 2 * NP + nbase;     // the address a of step u
+                    const int amu = a.hard ? steppar_am(sp, t0 + u) : -1;
+                    float asu[RPL];                                 // a_s of step u
+                    if (u < GL) {
+#pragma unroll
+                        for (int j = 0; j < RPL; j++) asu[j] = lsc[(u * 5 + 1) * NP + nbase + j];
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < RPL; j++) asu[j] = scr_s[((size_t)u * 5 + 1) * NP + nbase + j];
+                    }
 #pragma unroll
                     for (int j = 0; j < RPL; j++) {
-                        const float wr = gu * su[j];
+                        const float adu = a.hard ? (nbase + j == amu ? 1.f : 0.f) : asu[j];
+                        const float wr = gu * adu;
                         const float omw = 1.f - wr;
 #pragma unroll
                         for (int i = 0; i < DPK; i++) K[j][i] = fmaf(omw, K[j][i], wr * ku[i]);
@@ -613,14 +652,21 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             };
             // the row scalars likewise: read where they are used, on each side of the barrier
             auto load_s = [&](float (&x)[RPL], int f) {
+                if (s < GL) {
 #pragma unroll
-                for (int j = 0; j < RPL; j++) x[j] = ss[f * NP + nbase + j];
+                    for (int j = 0; j < RPL; j++) x[j] = lsc[(s * 5 + f) * NP + nbase + j];
+                } else {
+#pragma unroll
+                    for (int j = 0; j < RPL; j++) x[j] = scr_s[((size_t)s * 5 + f) * NP + nbase + j];
+                }
             };
             float kt[DPK];
             ldtok<TI, DPK>(kp + ti * DK + dl * DPK, kt);
             float g, frt;
             steppar(t, g, frt);
-            const float qinv = scr_qinv[s];
+            float qinv;
+            if (s < GL) qinv = lqinv[s];
+            else qinv = scr_qinv[s];
 
             // dw per row; dk_t, dv_t partials; the two address sums
             float dw[RPL], wr[RPL];
@@ -628,7 +674,12 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             {
             float K[RPL][DPK], o[RPL], as[RPL], ad[RPL], ep[RPL];
             load_K(K);
-            load_s(o, 0); load_s(as, 1); load_s(ad, 2); load_s(ep, 5);
+            load_s(o, 0); load_s(as, 1); load_s(ep, 4);
+            {
+                const int amt = a.hard ? steppar_am(sp, t) : -1;
+#pragma unroll
+                for (int j = 0; j < RPL; j++) ad[j] = a.hard ? (nbase + j == amt ? 1.f : 0.f) : as[j];
+            }
 #pragma unroll
             for (int j = 0; j < RPL; j++) {
                 float x = 0.f;
@@ -698,7 +749,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             // dz and the search-side partials
             float K[RPL][DPK], o[RPL], as[RPL], sr[RPL], knr[RPL], qt[DPK];
             load_K(K);
-            load_s(o, 0); load_s(as, 1); load_s(sr, 3); load_s(knr, 4);
+            load_s(o, 0); load_s(as, 1); load_s(sr, 2); load_s(knr, 3);
             ldtok<TI, DPK>(qp + ti * DK + dl * DPK, qt);
             float dz[RPL], ds[RPL], kinv[RPL];      // ds: dz with the pinned rows' score path cut
             float sfo = 0.f, sds = 0.f;
@@ -826,7 +877,7 @@ static void dispatch(bool bwd, int64_t DK, int64_t DV, int rpl, dim3 grid, hipSt
 static int64_t scr_chain(int64_t DK, int64_t DV, int rpl, int64_t G) {
     const int64_t NP = 32 * rpl;
     (void)DV;
-    return G * 6 * NP + ((G - 1) / 4) * NP * DK + ((G + 3) / 4) * 4;   // GenScr<...>::chain
+    return G * 5 * NP + ((G - 1) / 4) * NP * DK + ((G + 3) / 4) * 4;   // GenScr<...>::chain
 }
 
 }  // namespace
