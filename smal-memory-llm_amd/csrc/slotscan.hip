@@ -456,6 +456,7 @@ void chain_fwd(ChainFwdArgs a) {
     for (int w0 = ts; w0 < te; w0 += CT) {
         const int buf = ((w0 - ts) / CT) & 1;
         f32x16 Sr;                                      // <K_me, q_{w0+u}>
+        int amw = -1;                                   // wave 0: the window's addresses, step j in lane j
         {   // window GEMM: S^T = Q K^T, 16 rows per tile; lane l, reg r -> S[16 tau + m16][4 ag + r]
             f32x4 acc[NT];
 #pragma unroll
@@ -572,7 +573,9 @@ void chain_fwd(ChainFwdArgs a) {
             par ^= 1;
             const int amv = __builtin_amdgcn_readfirstlane((fo >= 0 && (bo < 0 || fz > bz || (fz == bz && fo < bo))) ? fo : bo);
             const size_t ix = tok0 + (size_t)t * H;
-            if (tid == 0) a.am[ix] = amv;
+            // the address log is stored once per window (below): a store every step, behind the snapshot
+            // bursts in the wave's store queue, held wave 0 on the chain's critical path
+            amw = lane == j ? amv : amw;
             if (amv >= R.rowbase && amv < R.rowbase + P) {  // this row group holds the written row
                 const int sl = amv & (P - 1);               // its register slot: the same in every lane
                 const float omw = 1.f - g;
@@ -602,6 +605,7 @@ void chain_fwd(ChainFwdArgs a) {
                 }
             }
         }
+        if (wave == 0 && lane < CT && w0 + lane < te) a.am[tok0 + (size_t)(w0 + lane) * H] = amw;
     }
 #pragma unroll
     for (int jr = 0; jr < P; jr++) {
