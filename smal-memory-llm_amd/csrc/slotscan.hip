@@ -1534,13 +1534,15 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     constexpr int KK = NR / 4;                          // MFMA k-steps over the rows
     constexpr int P = NR + 4;                           // transposed key stride: 4 mod 32 banks
     constexpr int SW = NR + 4;                          // W row stride, likewise
-    constexpr int SC = NR + 4;                          // cosine / Dn row stride (step-major): 4 mod 64 banks, so
-                                                        // the Dn publish (16 steps x 4 rows per pass) hits 64 banks
+    constexpr int SC = NR + 2;                          // cosine / Dn row stride (step-major): 2 mod 32 banks, so
+                                                        // the Dn publish (16 steps x 2 rows per 32-lane pass of
+                                                        // 4-byte accesses) hits 32 distinct banks
     constexpr int KOS = D + 4;                          // kold / query row stride
     constexpr int NC = NT / WIN;                        // lanes per step in the softmax phase
     constexpr int RPC = NR / NC;                        // slot rows per lane in the softmax phase
     constexpr int DPT = D / NC;                         // dims per lane in the undo (4), strided by NC
-    constexpr int DEL = D + 16;                         // undo-delta row stride: 4 steps x 16 dims per pass on 64 banks
+    constexpr int DEL = D + 16;                         // undo-delta row stride: 2 steps x 16 dims per 32-lane pass
+                                                        // of 4-byte reads on distinct banks
     constexpr int EPU = 16 / (int)sizeof(TI);
     constexpr int UCS = (WIN * NR + NT - 1) / NT;       // per-lane prefetch: cosines, Dn
     constexpr int UKO = (WIN * D / 4 + NT - 1) / NT;    // kold rows (uint4)
