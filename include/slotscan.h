@@ -158,26 +158,31 @@ int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
  *   t = 0, G, 2G, ...;  am (B, T, H) int32, hard = 1 only: the row each step wrote (first maximum);
  *   wb (B, T, H, N) fp32 or NULL: every step's write distribution before the gate (one-hot when hard),
  *   ref_scan_kv's return_w output (slotkern_kv.py:115-117).  pin: ref_scan_kv's pin (slotkern_kv.py:88-101),
- *   a row with |K| < 1e-6 scores 0 and takes no address gradient.
+ *   a row with |K| < 1e-6 scores 0 and takes no address gradient.  rlog: the address log the backward
+ *   replays from, slotscan_gen_log_bytes(B, T, H, N) bytes, 16-byte aligned, or NULL when no backward
+ *   follows: per (b, h) chain and step the pre-write occupancy, soft address, scaled cosine and |K| of every
+ *   row, then 1 / max(|q_t|, 1e-6) per chain and step (an implementation layout, no counterpart in the
+ *   reference, which recomputes them in its backward).
  * slotscan_gen_bwd: the backward (slotkern_kvg.py:233-253) for the upstream gradients dkbuf, dvbuf (fp32,
- *   shaped like kbuf, vbuf), from the forward's kbuf, vbuf, obuf and am.  Writes dk, dq (B, T, H, DK),
+ *   shaped like kbuf, vbuf), from the forward's kbuf, vbuf, obuf, am and rlog (required).  Writes dk, dq (B, T, H, DK),
  *   dv (B, T, H, DV) in the token dtype, dgate (B, T, H), dfr (fr's shape), dtemp (1).  workspace:
  *   slotscan_gen_bwd_workspace(B, H, N, DK, DV, G) bytes, 16-byte aligned: the replay scratch (about
- *   G * N * (DK + DV) fp32 per chain) and the per-chain partials.
+ *   G * N * (1 + DK / 4) fp32 per chain) and the per-chain partials.
  * Other arguments as in slotscan_fwd / slotscan_bwd. */
 int slotscan_gen_fwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
                      const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
                      int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
                      int hard, int pin, float* kbuf, float* vbuf, float* obuf, int32_t* am, float* wb,
-                     void* stream);
+                     float* rlog, void* stream);
+size_t slotscan_gen_log_bytes(int64_t B, int64_t T, int64_t H, int64_t N);
 size_t slotscan_gen_bwd_workspace(int64_t B, int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G);
 int slotscan_gen_bwd(const void* k, const void* q, const void* v, int dtype, const float* gate,
                      const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
                      int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
                      int hard, int detach_addr, int pin, const float* kbuf, const float* vbuf,
-                     const float* obuf, const int32_t* am, const float* dkbuf, const float* dvbuf,
-                     void* workspace, void* dk, void* dq, void* dv, float* dgate, float* dfr,
-                     float* dtemp, void* stream);
+                     const float* obuf, const int32_t* am, const float* rlog, const float* dkbuf,
+                     const float* dvbuf, void* workspace, void* dk, void* dq, void* dv, float* dgate,
+                     float* dfr, float* dtemp, void* stream);
 
 /* Per-kernel timing (the reference's kvu/prof_cuda.py:9-20 wraps each compiled kernel's launch in CUDA
  * events; this is the same facility inside the library).  slotscan_profile(mask): 0 disables timing;

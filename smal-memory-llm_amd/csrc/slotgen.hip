@@ -12,8 +12,11 @@
 //   a = softmax(z) (soft) or onehot(argmax z), first maximum wins (hard; the gradient is straight-through
 //   the softmax, slotkern_kv.py:108-110);  w = g_t a
 //   K <- (1-w) K + w k_t,  V <- (1-w) V + w v_t,  o <- (1-w) o + w
-// Backward, per stride-G segment in reverse: replay the segment from its emitted copy into per-chain
-// scratch (the pre-write K and six row scalars of every step), then walk it backward:
+// The forward logs, per step, every row's pre-write occupancy o, soft address a_s, scaled cosine s and |K|,
+// and 1 / max(|q_t|, 1e-6) (the address log, rlog).
+// Backward, per stride-G segment in reverse: replay the segment's keys from its emitted copy with the logged
+// addresses (key checkpoints and one value row scalar per step into per-chain scratch; the scores and the
+// address are not recomputed, so the replay has no cross-wave exchange), then walk it backward:
 //   dw_n = <k_t - K_n, dK_n> + <v_t - V_n, dV_n> + (1 - o_n) do_n
 //   dk_t = sum_n w_n dK_n,  dv_t = sum_n w_n dV_n,  dgate_t = sum_n a_n dw_n
 //   dz_n = a_s,n (g dw_n - sum_m a_s,m g dw_m)                       (a_s the soft address, 0 off the mask)
@@ -32,9 +35,9 @@
 // (the wave's 16-lane DPP rows) x 16 dim-lanes: a lane holds RPL rows x DK/16 key dims (and DV/16 value
 // dims), wave w rows w*4*RPL .. (w+1)*4*RPL - 1, so a row dot product is a 16-lane DPP reduction and a sum
 // over rows is a 4-row permlane reduction plus one LDS exchange across the waves.  Each step of the
-// forward (and of the backward's replay) needs one workgroup barrier: every wave posts its (max, sum) of
-// the competing scores, its first free row and its best row to a double-buffered LDS slot, and all waves
-// combine the 8 posts.  Each step of the backward's walk also needs one barrier: the waves post the
+// forward needs one workgroup barrier: every wave posts its (max, sum) of the competing scores, its first
+// free row and its best row to a double-buffered LDS slot, and all waves combine the 8 posts.  The
+// backward's replay needs none (the address comes from the log).  Each step of its walk needs one: the waves post the
 // address-gradient sums and their dk/dv partials; the previous step's dq/dfr/dtemp partials ride along on
 // the same exchange.  The scratch is written and read in 16-byte units, each row by its 16 dim-lanes.
 #include "slot_common.h"
@@ -59,6 +62,7 @@ struct GenArgs {
     float eps;
     float* kbuf; float* vbuf; float* obuf; int32_t* am;          // forward outputs (am: hard only)
     float* wb;                                                    // optional: the address of every step
+    float* rlog;                                                  // the address log (written by the forward)
     const float* dkbuf; const float* dvbuf;                       // backward inputs
     float* scr; int64_t scr_chain;                                 // replay scratch, floats per chain
     void* dk; void* dq; void* dv; float* dg; float* dfr; float* part;
@@ -108,6 +112,35 @@ template <typename TI, int N> __device__ __forceinline__ void ldtok(const TI* p,
         }
     }
 }
+// Raw token bytes of a lane's N elements (16-byte pieces), loaded one step ahead and converted only where
+// used: a prefetch held as converted fp32 registers took twice the registers, and the compiler then
+// converted (and waited for) each load right after issuing it.  `base` is uniform, `off` the lane's byte
+// offset, so the loads use a scalar base with a 32-bit lane offset.
+template <typename TI, int N> struct RawTok {
+    static constexpr int U = N * (int)sizeof(TI) / 16;
+    uint4 r[U];
+    __device__ __forceinline__ void load(const void* base, uint32_t off) {
+#pragma unroll
+        for (int u = 0; u < U; u++) r[u] = *reinterpret_cast<const uint4*>((const char*)base + off + 16 * u);
+    }
+    __device__ __forceinline__ void cvt(float* x) const {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if constexpr (sizeof(TI) == 4) {
+                x[4 * u] = __uint_as_float(r[u].x); x[4 * u + 1] = __uint_as_float(r[u].y);
+                x[4 * u + 2] = __uint_as_float(r[u].z); x[4 * u + 3] = __uint_as_float(r[u].w);
+            } else {
+                const uint32_t w[4] = {r[u].x, r[u].y, r[u].z, r[u].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    x[8 * u + 2 * k] = __uint_as_float(w[k] << 16);
+                    x[8 * u + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+                }
+            }
+        }
+    }
+};
+
 template <typename TI> __device__ __forceinline__ void sttok4(TI* p, float4 v) {
     if constexpr (sizeof(TI) == 4) st4(reinterpret_cast<float*>(p), v);
     else st4(reinterpret_cast<bf16_t*>(p), v);
@@ -288,37 +321,29 @@ __device__ __forceinline__ void gen_update(float (&K)[RPL][DPK], float (&V)[RPL]
     }
 }
 
-// The emitted copy of segment tb: keys and occupancy into registers, and per row P = <V_n, D_n> with the
-// value adjoint D that enters the segment's walk (this lane's rows at dvr + j * DV, in LDS).
-template <int RPL, int DPK, int DPV>
-__device__ __forceinline__ void gen_load_keys(const GenArgs& a, int b, int h, int tb, int nbase, int dl,
-                                              const float* dvr, float (&K)[RPL][DPK], float (&o)[RPL],
-                                              float (&P)[RPL]) {
-    constexpr int DK = DPK * 16, DV = DPV * 16;
-    const size_t base = ((size_t)b * a.NB + tb) * a.H + h;
+// X[j] <- this lane's slice of rows nbase + j of an fp32 (rows, DP * 16) slab at `base` (uniform), `off` the
+// lane's byte offset of row nbase; `nv` rows of the lane exist (the rest read 0).  All rows exist in the
+// common case (full): the loads are then unconditional, a scalar base plus one 32-bit lane offset.
+template <int RPL, int DP>
+__device__ __forceinline__ void ld_rows(float (&X)[RPL][DP], const float* base, uint32_t off, bool full, int nv) {
+    const char* p = reinterpret_cast<const char*>(base) + off;
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
-        const int n = nbase + j;
-        const bool ok = n < a.N;
-        const size_t r = base * a.N + (ok ? n : 0);
 #pragma unroll
-        for (int i = 0; i < DPK; i += 4) {
-            const float4 f = ok ? ld4(a.kbuf + r * DK + dl * DPK + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            K[j][i] = f.x; K[j][i + 1] = f.y; K[j][i + 2] = f.z; K[j][i + 3] = f.w;
+        for (int i = 0; i < DP; i += 4) {
+            const float4 f = (full || j < nv) ? *reinterpret_cast<const float4*>(p + (j * DP * 16 + i) * 4)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+            X[j][i] = f.x; X[j][i + 1] = f.y; X[j][i + 2] = f.z; X[j][i + 3] = f.w;
         }
-        float x = 0.f;
-#pragma unroll
-        for (int i = 0; i < DPV; i += 4) {
-            const float4 f = ok ? ld4(a.vbuf + r * DV + dl * DPV + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 d = *reinterpret_cast<const float4*>(dvr + j * DV + i);
-            x = fmaf(f.x, d.x, x); x = fmaf(f.y, d.y, x); x = fmaf(f.z, d.z, x); x = fmaf(f.w, d.w, x);
-        }
-        P[j] = rowsum16(x);
-        o[j] = ok ? a.obuf[r] : 0.f;
     }
 }
 
 // ------------------------------------------------------------------------------------------- forward
+// Per step, in this order: the step's token rows (loaded during the previous step) are converted; the
+// stores are issued (the snapshot at t % G == 0, the previous step's address log); the next step's token
+// rows are loaded; then the scores, the address exchange and the update run.  No store is issued between a
+// token load and its use, so the wait for the tokens never waits for stores, and the loads have a whole
+// step to arrive.  Every global access is a uniform (scalar) base plus a 32-bit lane offset.
 template <typename TI, int DK, int DV, int RPL>
 __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
     constexpr int DPK = DK / 16, DPV = DV / 16, RPW = 4 * RPL;
@@ -326,9 +351,6 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
     const int chain = blockIdx.x, b = chain / a.H, h = chain % a.H;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, dl = lane & 15;
     const int nbase = w * RPW + (lane >> 4) * RPL;
-    const TI* kp = static_cast<const TI*>(a.k);
-    const TI* qp = static_cast<const TI*>(a.q);
-    const TI* vp = static_cast<const TI*>(a.v);
     const float temp = a.temp[0];
     float K[RPL][DPK], V[RPL][DPV], o[RPL];
 #pragma unroll
@@ -341,77 +363,101 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
     }
     auto tok = [&](int t) { return ((size_t)b * a.T + t) * a.H + h; };
     const size_t tok0 = tok(0);
+    const uint32_t tk_off = (uint32_t)(dl * DPK * sizeof(TI)), tv_off = (uint32_t)(dl * DPV * sizeof(TI));
+    auto krow = [&](int t) { return (const char*)a.k + tok(t) * DK * sizeof(TI); };
+    auto qrow = [&](int t) { return (const char*)a.q + tok(t) * DK * sizeof(TI); };
+    auto vrow = [&](int t) { return (const char*)a.v + tok(t) * DV * sizeof(TI); };
+    // this lane's slice of row nbase in a snapshot slab (bytes); row nbase + j is j * D * 4 further
+    const uint32_t sk_off = (uint32_t)((nbase * DK + dl * DPK) * 4), sv_off = (uint32_t)((nbase * DV + dl * DPV) * 4);
     StepPar spc = load_steppar(a.gate, a.fr, a.frt, nullptr, a.T, a.H, tok0, 0, lane);   // steps [64 i, 64 i + 64)
     StepPar spn = load_steppar(a.gate, a.fr, a.frt, nullptr, a.T, a.H, tok0, 64, lane);  // the next 64, in flight
-    float kt[DPK], qt[DPK], vt[DPV];
-    ldtok<TI, DPK>(kp + tok(0) * DK + dl * DPK, kt);
-    ldtok<TI, DPK>(qp + tok(0) * DK + dl * DPK, qt);
-    ldtok<TI, DPV>(vp + tok(0) * DV + dl * DPV, vt);
-    for (int t = 0; t < a.T; t++) {
-        if (t % a.G == 0) {                   // emit the pre-write state
-            const size_t base = (((size_t)b * a.NB + t / a.G) * a.H + h) * a.N;
-#pragma unroll
-            for (int j = 0; j < RPL; j++) {
-                const int n = nbase + j;
-                if (n < a.N) {
-#pragma unroll
-                    for (int i = 0; i < DPK; i += 4)
-                        st4(a.kbuf + (base + n) * DK + dl * DPK + i, make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]));
-#pragma unroll
-                    for (int i = 0; i < DPV; i += 4)
-                        st4(a.vbuf + (base + n) * DV + dl * DPV + i, make_float4(V[j][i], V[j][i + 1], V[j][i + 2], V[j][i + 3]));
-                    if (dl == 0) a.obuf[base + n] = o[j];
-                }
-            }
-        }
+    RawTok<TI, DPK> rk, rq;
+    RawTok<TI, DPV> rv;
+    rk.load(krow(0), tk_off); rq.load(qrow(0), tk_off); rv.load(vrow(0), tv_off);
+    // the previous step's address log, stored at the top of the next step
+    float lo = 0.f, la = 0.f, ls = 0.f, lk = 0.f, lq = 0.f;
+    float lw[RPL];
+    int lbest = -1;
+    auto store_log = [&](int t) {
         const size_t ti = tok(t);
+        if (a.hard && threadIdx.x == 0) a.am[ti] = lbest;
+        if (a.wb && dl == 0) {
+#pragma unroll
+            for (int j = 0; j < RPL; j++)
+                if (nbase + j < a.N) a.wb[ti * a.N + nbase + j] = lw[j];
+        }
+        if (a.rlog) {                         // dim-lane j < RPL stores row nbase + j
+            const int n = nbase + dl;
+            float* rec = a.rlog + ((size_t)chain * a.T + t) * 4 * a.N;
+            if (dl < RPL && n < a.N) { rec[n] = lo; rec[a.N + n] = la; rec[2 * a.N + n] = ls; rec[3 * a.N + n] = lk; }
+            if (threadIdx.x == 0) a.rlog[(size_t)gridDim.x * a.T * 4 * a.N + (size_t)chain * a.T + t] = lq;
+        }
+    };
+    for (int t = 0; t < a.T; t++) {
+        float kt[DPK], qt[DPK], vt[DPV];
+        rk.cvt(kt); rq.cvt(qt); rv.cvt(vt);
         if (t > 0 && (t & 63) == 0) {
             spc = spn;
             spn = load_steppar(a.gate, a.fr, a.frt, nullptr, a.T, a.H, tok0, t + 64, lane);
         }
+        if (t % a.G == 0) {                   // emit the pre-write state
+            const size_t slab = (((size_t)b * a.NB + t / a.G) * a.H + h) * a.N;
+            char* kb = (char*)(a.kbuf + slab * DK);
+            char* vb = (char*)(a.vbuf + slab * DV);
+#pragma unroll
+            for (int j = 0; j < RPL; j++) {
+                if (nbase + j < a.N) {
+#pragma unroll
+                    for (int i = 0; i < DPK; i += 4)
+                        *reinterpret_cast<float4*>(kb + sk_off + (j * DK + i) * 4) = make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]);
+#pragma unroll
+                    for (int i = 0; i < DPV; i += 4)
+                        *reinterpret_cast<float4*>(vb + sv_off + (j * DV + i) * 4) = make_float4(V[j][i], V[j][i + 1], V[j][i + 2], V[j][i + 3]);
+                    if (dl == 0) a.obuf[slab + nbase + j] = o[j];
+                }
+            }
+        }
+        if (t > 0) store_log(t - 1);
+        if (t + 1 < a.T) { rk.load(krow(t + 1), tk_off); rq.load(qrow(t + 1), tk_off); rv.load(vrow(t + 1), tv_off); }
         const float g = steppar_g(spc, t);
         const float frt = steppar_f(spc, t);
-        float kn_[DPK], qn_[DPK], vn_[DPV];
-        if (t + 1 < a.T) {
-            ldtok<TI, DPK>(kp + tok(t + 1) * DK + dl * DPK, kn_);
-            ldtok<TI, DPK>(qp + tok(t + 1) * DK + dl * DPK, qn_);
-            ldtok<TI, DPV>(vp + tok(t + 1) * DV + dl * DPV, vn_);
-        }
         float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
         gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, a.pin, z, sr, knr, qinv);
-        const int best = gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, -1, xf[t & 1], w, lane, as, ad);
-        if (a.hard && threadIdx.x == 0) a.am[ti] = best;
-        if (a.wb && dl == 0) {
+        lbest = gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, -1, xf[t & 1], w, lane, as, ad);
+        lo = o[0]; la = as[0]; ls = sr[0]; lk = knr[0]; lq = qinv;
 #pragma unroll
-            for (int j = 0; j < RPL; j++)
-                if (nbase + j < a.N) a.wb[ti * a.N + nbase + j] = ad[j];
+        for (int j = 1; j < RPL; j++) {
+            const bool me = dl == j;
+            lo = me ? o[j] : lo; la = me ? as[j] : la; ls = me ? sr[j] : ls; lk = me ? knr[j] : lk;
         }
 #pragma unroll
-        for (int j = 0; j < RPL; j++) wr[j] = g * ad[j];
+        for (int j = 0; j < RPL; j++) { lw[j] = ad[j]; wr[j] = g * ad[j]; }
         gen_update<RPL, DPK, DPV>(K, V, o, wr, kt, vt);
-        if (t + 1 < a.T) {
-#pragma unroll
-            for (int i = 0; i < DPK; i++) { kt[i] = kn_[i]; qt[i] = qn_[i]; }
-#pragma unroll
-            for (int i = 0; i < DPV; i++) vt[i] = vn_[i];
-        }
     }
+    store_log(a.T - 1);
 }
 
 // ------------------------------------------------------------------------------------------- backward
-// Scratch per chain: for every segment step s five row scalars (NP each): o, a_s, s, |K| and
-// e - P = <v_t, D> - <V, D> (the write address a is a_s, or in hard mode the logged row); then the
-// pre-write keys (NP, DK) of every GC-th step after the first (the first step's are the emitted copy); then
-// qinv per step.  NP = 32 * RPL.  The first GL steps of a segment keep their scalars, key tokens and qinv in
-// LDS instead (gen_bwd), so the walk reads them at LDS latency.  The walk rebuilds the keys of
-// any step from the checkpoint at or before it with the updates in between (at most GC - 1), the same
-// fmaf sequence, weights and token values as the replay, so bitwise the replay's keys.
+// The address log (rlog): per chain and step the four row scalars o, a_s, s, |K| of rows 0..N-1 (4 N
+// floats, each quantity N-contiguous), then, after every chain's records, qinv per chain and step.
+__host__ __device__ inline size_t gen_log_floats(int64_t BH, int64_t T, int64_t N) {
+    return (size_t)BH * T * (4 * N + 1);
+}
+
+// Scratch per chain: for every segment step s the row scalar e - P = <v_t, D> - <V, D> (NP floats), then
+// the pre-write keys (NP, DK) of every GC-th step, the first included (a copy of the emitted one, so every
+// checkpoint has NP rows and is read without bounds tests).  NP = 32 * RPL.  The first GL steps of a
+// segment keep their row scalars (the four logged ones and e - P), key and query token rows and qinv in
+// LDS instead (gen_bwd), so the walk reads them at LDS latency; later steps read the logged ones from the
+// log.  The walk rebuilds the keys of any step from the checkpoint at or before it with the updates in
+// between (at most GC - 1), the same fmaf sequence, weights and token values as the replay, so bitwise the
+// replay's keys.
 template <int DK, int DV, int RPL>
 struct GenScr {
     static constexpr int NP = 32 * RPL;
     static constexpr int GC = 4;
-    __host__ __device__ static int64_t nck(int G) { return (G - 1) / GC; }
-    __host__ __device__ static int64_t chain(int G) { return (int64_t)G * 5 * NP + nck(G) * NP * DK + ((G + 3) / 4) * 4; }
+    __host__ __device__ static int64_t nck(int G) { return (G + GC - 1) / GC; }
+    __host__ __device__ static int64_t chain(int G) { return (int64_t)G * NP + nck(G) * NP * DK; }
 };
 
 template <typename TI, int DK, int DV, int RPL>
@@ -421,25 +467,38 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
     constexpr int NP = SC::NP;
     constexpr int P1W = DK + DV + 4;          // per wave: dk, dv partials, then {sum a dw, sum a_s g dw}
     constexpr int P2W = DK + 4;               // per wave: dqn partial, then {sum occ dz, sum dz s}
-    __shared__ __align__(16) float xf[2][GEN_WAVES * 8];
+    constexpr int GL = 8;                     // a segment's first GL steps keep their per-step data in LDS
+    constexpr int TU = DK * (int)sizeof(TI) / 16;   // 16-byte pieces of a key / query token row
     __shared__ __align__(16) float p1[2][GEN_WAVES * P1W];
     __shared__ __align__(16) float p2[2][GEN_WAVES * P2W];
+    // The value adjoint lives in LDS: inside a segment it only scales, dV(t+) = cV(t) D, so the walk reads
+    // D and keeps the per-row factors cV in registers; D is rewritten once per segment (at its first step).
+    // Each lane reads and writes only its own rows and dims.
+    __shared__ __align__(16) float sD[NP * DV];
+    // a segment's first GL steps: row scalars [step][5][NP] (o, a_s, s, |K| from the log, then e - P),
+    // key and query token rows [step][2][DK] in the token dtype, qinv [step]
+    __shared__ __align__(16) float lsc[GL * 5 * NP];
+    __shared__ __align__(16) uint4 ltq[GL * 2 * TU];
+    __shared__ float lqinv[GL];
     const int chain = blockIdx.x, b = chain / a.H, h = chain % a.H;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, dl = lane & 15, rl = lane >> 4;
     const int nbase = w * RPW + rl * RPL;
-    const TI* kp = static_cast<const TI*>(a.k);
-    const TI* qp = static_cast<const TI*>(a.q);
-    const TI* vp = static_cast<const TI*>(a.v);
     TI* dkp = static_cast<TI*>(a.dk);
     TI* dqp = static_cast<TI*>(a.dq);
     TI* dvp = static_cast<TI*>(a.dv);
     const float temp = a.temp[0];
     float* scr = a.scr + (size_t)chain * a.scr_chain;
-    float* scr_s = scr;                                        // row scalars, 5 NP per step
-    float* scr_k = scr_s + (size_t)a.G * 5 * NP;               // key checkpoints, NP DK each
-    float* scr_qinv = scr_k + (size_t)SC::nck(a.G) * NP * DK;
+    float* scr_e = scr;                                        // e - P, NP per step
+    float* scr_k = scr_e + (size_t)a.G * NP;                   // key checkpoints, NP DK each
+    const float* rlog = a.rlog + (size_t)chain * a.T * 4 * a.N;                 // this chain's records
+    const float* qlog = a.rlog + (size_t)gridDim.x * a.T * 4 * a.N + (size_t)chain * a.T;
     auto tok = [&](int t) { return ((size_t)b * a.T + t) * a.H + h; };
     const size_t tok0 = tok(0);
+    // lane byte offsets: in a token row, and of row nbase in (rows, DK) / (rows, DV) fp32 slabs
+    const uint32_t tk_off = (uint32_t)(dl * DPK * sizeof(TI)), tv_off = (uint32_t)(dl * DPV * sizeof(TI));
+    const uint32_t rk_off = (uint32_t)((nbase * DK + dl * DPK) * 4), rv_off = (uint32_t)((nbase * DV + dl * DPV) * 4);
+    const bool full = a.N == NP;                               // every row of every lane exists
+    const int nv = min(max(a.N - nbase, 0), RPL);              // this lane's rows that exist
     // gate and fr through a 64-step window that ends at the current segment's end, so that the next (earlier)
     // segments find their steps in it too: reloaded once per 64 steps (per step where G > 64)
     const int32_t* amlog = a.hard ? a.am : nullptr;
@@ -449,16 +508,18 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
         g = steppar_g(sp, t);
         f = steppar_f(sp, t);
     };
-
-    // The value adjoint lives in LDS: inside a segment it only scales, dV(t+) = cV(t) D, so the walk reads
-    // D and keeps the per-row factors cV in registers; D is rewritten once per segment (at its first step).
-    // Each lane reads and writes only its own rows and dims.
-    __shared__ __align__(16) float sD[NP * DV];
-    // a segment's first GL steps: row scalars [step][5][NP], key tokens [step][DK], qinv [step]
-    constexpr int GL = 8;
-    __shared__ __align__(16) float lsc[GL * 5 * NP];
-    __shared__ __align__(16) float ltok[GL * DK];
-    __shared__ float lqinv[GL];
+    // the key (which = 0) or query (1) token row of segment step s (at t), this lane's dims, as fp32
+    auto tokrow = [&](int which, int s, int t, float* x) {
+        if (s < GL) {
+            RawTok<TI, DPK> r;
+#pragma unroll
+            for (int u = 0; u < RawTok<TI, DPK>::U; u++) r.r[u] = ltq[(s * 2 + which) * TU + dl * RawTok<TI, DPK>::U + u];
+            r.cvt(x);
+        } else {
+            const TI* p = static_cast<const TI*>(which ? a.q : a.k);
+            ldtok<TI, DPK>(p + tok(t) * DK + dl * DPK, x);
+        }
+    };
     float* dvr = sD + nbase * DV + dl * DPV;
     float dK[RPL][DPK], dO[RPL];
 #pragma unroll
@@ -474,12 +535,13 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
     float pend_qinv = 0.f;                    // and its 1 / max(|q|, 1e-6)
     int par = 0;                              // exchange-slot parity, flipped once per barrier
 
-    // Wave 1 finishes a walk step from the p2 posts: dq_t, dfr_t (per token) and the dfr/dtemp sums.
-    auto finish_q = [&](int t, float qinv, const float* q2) {
+    // Wave 1 finishes a walk step (segment step ps) from the p2 posts: dq_t, dfr_t (per token) and the
+    // dfr/dtemp sums.
+    auto finish_q = [&](int t, int ps, float qinv, const float* q2) {
         if (w != 1) return;
         const size_t ti = tok(t);
         float qt[DPK];
-        ldtok<TI, DPK>(qp + ti * DK + dl * DPK, qt);
+        tokrow(1, ps, t, qt);
         float dqn[DPK];
 #pragma unroll
         for (int i = 0; i < DPK; i++) dqn[i] = 0.f;
@@ -515,48 +577,80 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
 
     for (int tb = a.NB - 1; tb >= 0; tb--) {
         const int t0 = tb * a.G, t1 = min(t0 + a.G, a.T);
+        const int ns = min(t1 - t0, GL);
         if (t0 < sp.base) sp = load_steppar(a.gate, a.fr, a.frt, amlog, a.T, a.H, tok0, max(t1 - 64, 0), lane);
-        // ---- replay the segment from its emitted copy, keeping every step's pre-write state
+        // ---- the segment's logged row scalars (o, a_s, s, |K|), qinv, and key and query token rows of its
+        // first GL steps into LDS
+        {
+            const float* rec = rlog + (size_t)t0 * 4 * a.N;
+            for (int x = threadIdx.x; x < ns * 4 * NP; x += GEN_THREADS) {
+                const int st = x / (4 * NP), r = x - st * 4 * NP, f = r / NP, n = r - f * NP;
+                lsc[(st * 5 + f) * NP + n] = n < a.N ? rec[((size_t)st * 4 + f) * a.N + n] : 0.f;
+            }
+            if (threadIdx.x < ns) lqinv[threadIdx.x] = qlog[t0 + threadIdx.x];
+            for (int x = threadIdx.x; x < ns * 2 * TU; x += GEN_THREADS) {
+                const int st = x / (2 * TU), wh = (x / TU) & 1, u = x % TU;
+                const char* row = (const char*)(wh ? a.q : a.k) + tok(t0 + st) * DK * sizeof(TI);
+                ltq[x] = reinterpret_cast<const uint4*>(row)[u];
+            }
+        }
+        __syncthreads();                      // the replay reads the logged addresses of every row group
+        // ---- replay the segment's keys from its emitted copy, keeping every step's pre-write state
         {
             // The value state itself is not replayed: inside a segment the value adjoint only scales,
             // dV(t+) = c(t) D with D the adjoint entering the segment, so the walk needs just the row
             // scalars P(t) = <V(t), D> (P <- (1-w) P + w e from the emitted copy) and e(t) = <v_t, D>.
-            float K[RPL][DPK], o[RPL], P[RPL];
-            gen_load_keys<RPL, DPK, DPV>(a, b, h, tb, nbase, dl, dvr, K, o, P);
+            // The addresses come from the forward's log, so a step needs no exchange between the waves.
+            // The next step's value row is loaded once this step's stores are issued.
+            const size_t slab = (((size_t)b * a.NB + tb) * a.H + h) * a.N;
+            float K[RPL][DPK], P[RPL];
+            ld_rows<RPL, DPK>(K, a.kbuf + slab * DK, rk_off, full, nv);
+            {
+                float Vs[RPL][DPV];
+                ld_rows<RPL, DPV>(Vs, a.vbuf + slab * DV, rv_off, full, nv);
+#pragma unroll
+                for (int j = 0; j < RPL; j++) {
+                    float x = 0.f;
+#pragma unroll
+                    for (int i = 0; i < DPV; i += 4) {
+                        const float4 d = *reinterpret_cast<const float4*>(dvr + j * DV + i);
+                        x = fmaf(Vs[j][i], d.x, x); x = fmaf(Vs[j][i + 1], d.y, x);
+                        x = fmaf(Vs[j][i + 2], d.z, x); x = fmaf(Vs[j][i + 3], d.w, x);
+                    }
+                    P[j] = rowsum16(x);
+                }
+            }
+            RawTok<TI, DPV> rv;
+            rv.load((const char*)a.v + tok(t0) * DV * sizeof(TI), tv_off);
             for (int t = t0; t < t1; t++) {
                 const int s = t - t0;
-                // explicit branches (s is uniform): a select between the LDS and the global pointer would make
-                // every access a flat one, which waits on both counters
-                auto put_s = [&](int f, int n, float v) {
-                    if (s < GL) lsc[(s * 5 + f) * NP + n] = v;
-                    else scr_s[((size_t)s * 5 + f) * NP + n] = v;
-                };
-                if (s > 0 && s % SC::GC == 0) {             // a key checkpoint
-                    float* sk = scr_k + (size_t)(s / SC::GC - 1) * NP * DK;
+                float vt[DPV];
+                rv.cvt(vt);
+                if (s % SC::GC == 0) {                      // a key checkpoint
+                    char* sk = (char*)(scr_k + (size_t)(s / SC::GC) * NP * DK) + rk_off;
 #pragma unroll
-                    for (int j = 0; j < RPL; j++) {
-                        const int n = nbase + j;
+                    for (int j = 0; j < RPL; j++)
 #pragma unroll
                         for (int i = 0; i < DPK; i += 4)
-                            st4(sk + n * DK + dl * DPK + i, make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]));
-                    }
+                            *reinterpret_cast<float4*>(sk + (j * DK + i) * 4) = make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]);
                 }
-                const size_t ti = tok(t);
-                float kt[DPK], qt[DPK], vt[DPV];
-                ldtok<TI, DPK>(kp + ti * DK + dl * DPK, kt);
-                ldtok<TI, DPK>(qp + ti * DK + dl * DPK, qt);
-                ldtok<TI, DPV>(vp + ti * DV + dl * DPV, vt);
+                if (t + 1 < t1) rv.load((const char*)a.v + tok(t + 1) * DV * sizeof(TI), tv_off);
+                float kt[DPK];
+                tokrow(0, s, t, kt);
                 float g, frt;
                 steppar(t, g, frt);
-                float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
-                gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, a.pin, z, sr, knr, qinv);
-                gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, a.hard ? steppar_am(sp, t) : -1, xf[par], w, lane, as, ad);
-                if (s < GL && w == 0 && rl == 0) {             // the key token, for the walk's key rebuilds
+                float ad[RPL];                                  // the write address (pre-gate)
+                if (a.hard) {
+                    const int amt = steppar_am(sp, t);
 #pragma unroll
-                    for (int i = 0; i < DPK; i += 4)
-                        *reinterpret_cast<float4*>(ltok + s * DK + dl * DPK + i) = make_float4(kt[i], kt[i + 1], kt[i + 2], kt[i + 3]);
+                    for (int j = 0; j < RPL; j++) ad[j] = nbase + j == amt ? 1.f : 0.f;
+                } else if (s < GL) {
+#pragma unroll
+                    for (int j = 0; j < RPL; j++) ad[j] = lsc[(s * 5 + 1) * NP + nbase + j];
+                } else {
+#pragma unroll
+                    for (int j = 0; j < RPL; j++) ad[j] = nbase + j < a.N ? rlog[((size_t)t * 4 + 1) * a.N + nbase + j] : 0.f;
                 }
-                par ^= 1;
                 float e[RPL];
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
@@ -573,22 +667,19 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
 #pragma unroll
                     for (int j = 0; j < RPL; j++) {
                         const int n = nbase + j;
-                        put_s(0, n, o[j]); put_s(1, n, as[j]); put_s(2, n, sr[j]);
-                        put_s(3, n, knr[j]); put_s(4, n, e[j] - P[j]);
+                        // explicit branches (s is uniform): a select between the LDS and the global pointer
+                        // would make every access a flat one, which waits on both counters
+                        if (s < GL) lsc[(s * 5 + 4) * NP + n] = e[j] - P[j];
+                        else scr_e[(size_t)s * NP + n] = e[j] - P[j];
                     }
-                }
-                if (threadIdx.x == 0) {
-                    if (s < GL) lqinv[s] = qinv;
-                    else scr_qinv[s] = qinv;
                 }
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
-                    wr[j] = g * ad[j];
-                    const float omw = 1.f - wr[j];
+                    const float wr = g * ad[j];
+                    const float omw = 1.f - wr;
 #pragma unroll
-                    for (int i = 0; i < DPK; i++) K[j][i] = fmaf(omw, K[j][i], wr[j] * kt[i]);
-                    o[j] = fmaf(omw, o[j], wr[j]);
-                    P[j] = fmaf(omw, P[j], wr[j] * e[j]);
+                    for (int i = 0; i < DPK; i++) K[j][i] = fmaf(omw, K[j][i], wr * kt[i]);
+                    P[j] = fmaf(omw, P[j], wr * e[j]);
                 }
             }
         }
@@ -600,36 +691,16 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
         for (int t = t1 - 1; t >= t0; t--) {
             const int s = t - t0;
             const size_t ti = tok(t);
-            // The pre-write keys of step s: the checkpoint at or before it (the emitted copy for the segment's
-            // first GC steps), then the replay's updates of the steps in between.  Built twice, before and
-            // after the step's barrier, rather than held across it: 8 * RPL fewer live registers through the
-            // exchange (the second build reads what the first one brought into the cache).
+            // The pre-write keys of step s: the checkpoint at or before it, then the replay's updates of the
+            // steps in between.  Built twice, before and after the step's barrier, rather than held across
+            // it: 8 * RPL fewer live registers through the exchange (the second build reads what the first
+            // one brought into the cache).
             auto load_K = [&](float (&K)[RPL][DPK]) {
                 const int c = (s / SC::GC) * SC::GC;
-                const size_t base = (((size_t)b * a.NB + tb) * a.H + h) * a.N;
-                const float* ck = scr_k + (size_t)max(c / SC::GC - 1, 0) * NP * DK;
-#pragma unroll
-                for (int j = 0; j < RPL; j++) {
-                    const int n = nbase + j;
-                    const bool ok = c > 0 || n < a.N;
-                    const float* src = c > 0 ? ck + n * DK : a.kbuf + (base + (ok ? n : 0)) * DK;
-#pragma unroll
-                    for (int i = 0; i < DPK; i += 4) {
-                        const float4 f = ok ? ld4(src + dl * DPK + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-                        K[j][i] = f.x; K[j][i + 1] = f.y; K[j][i + 2] = f.z; K[j][i + 3] = f.w;
-                    }
-                }
+                ld_rows<RPL, DPK>(K, scr_k + (size_t)(c / SC::GC) * NP * DK, rk_off, true, RPL);
                 for (int u = c; u < s; u++) {
                     float ku[DPK];
-                    if (u < GL) {
-#pragma unroll
-                        for (int i = 0; i < DPK; i += 4) {
-                            const float4 f = *reinterpret_cast<const float4*>(ltok + u * DK + dl * DPK + i);
-                            ku[i] = f.x; ku[i + 1] = f.y; ku[i + 2] = f.z; ku[i + 3] = f.w;
-                        }
-                    } else {
-                        ldtok<TI, DPK>(kp + tok(t0 + u) * DK + dl * DPK, ku);
-                    }
+                    tokrow(0, u, t0 + u, ku);
                     const float gu = steppar_g(sp, t0 + u);
                     const int amu = a.hard ? steppar_am(sp, t0 + u) : -1;
                     float asu[RPL];                                 // a_s of step u
@@ -638,7 +709,8 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                         for (int j = 0; j < RPL; j++) asu[j] = lsc[(u * 5 + 1) * NP + nbase + j];
                     } else {
 #pragma unroll
-                        for (int j = 0; j < RPL; j++) asu[j] = scr_s[((size_t)u * 5 + 1) * NP + nbase + j];
+                        for (int j = 0; j < RPL; j++)
+                            asu[j] = nbase + j < a.N ? rlog[((size_t)(t0 + u) * 4 + 1) * a.N + nbase + j] : 0.f;
                     }
 #pragma unroll
                     for (int j = 0; j < RPL; j++) {
@@ -655,18 +727,22 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 if (s < GL) {
 #pragma unroll
                     for (int j = 0; j < RPL; j++) x[j] = lsc[(s * 5 + f) * NP + nbase + j];
+                } else if (f < 4) {                            // logged by the forward
+#pragma unroll
+                    for (int j = 0; j < RPL; j++)
+                        x[j] = nbase + j < a.N ? rlog[((size_t)t * 4 + f) * a.N + nbase + j] : 0.f;
                 } else {
 #pragma unroll
-                    for (int j = 0; j < RPL; j++) x[j] = scr_s[((size_t)s * 5 + f) * NP + nbase + j];
+                    for (int j = 0; j < RPL; j++) x[j] = scr_e[(size_t)s * NP + nbase + j];
                 }
             };
             float kt[DPK];
-            ldtok<TI, DPK>(kp + ti * DK + dl * DPK, kt);
+            tokrow(0, s, t, kt);
             float g, frt;
             steppar(t, g, frt);
             float qinv;
             if (s < GL) qinv = lqinv[s];
-            else qinv = scr_qinv[s];
+            else qinv = qlog[t];
 
             // dw per row; dk_t, dv_t partials; the two address sums
             float dw[RPL], wr[RPL];
@@ -727,7 +803,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 if (lane == 0) { q1[w * P1W + DK + DV] = pg; q1[w * P1W + DK + DV + 1] = pa; }
             }
             lds_barrier();
-            if (pend_t >= 0) finish_q(pend_t, pend_qinv, p2[par ^ 1]);
+            if (pend_t >= 0) finish_q(pend_t, pend_t - t0, pend_qinv, p2[par ^ 1]);
             float SG = 0.f, SA = 0.f;
 #pragma unroll
             for (int ww = 0; ww < GEN_WAVES; ww++) { SG += q1[ww * P1W + DK + DV]; SA += q1[ww * P1W + DK + DV + 1]; }
@@ -750,7 +826,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             float K[RPL][DPK], o[RPL], as[RPL], sr[RPL], knr[RPL], qt[DPK];
             load_K(K);
             load_s(o, 0); load_s(as, 1); load_s(sr, 2); load_s(knr, 3);
-            ldtok<TI, DPK>(qp + ti * DK + dl * DPK, qt);
+            tokrow(1, s, t, qt);
             float dz[RPL], ds[RPL], kinv[RPL];      // ds: dz with the pinned rows' score path cut
             float sfo = 0.f, sds = 0.f;
 #pragma unroll
@@ -805,30 +881,29 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 dO[j] = a.occ_bin ? omw * dO[j] : fmaf(omw, dO[j], -frt * dz[j]);
             }
             if (t == t0) {                    // the emitted copy's gradient enters at the segment's first step
-                const size_t base = (((size_t)b * a.NB + tb) * a.H + h) * a.N;
+                const size_t slab = (((size_t)b * a.NB + tb) * a.H + h) * a.N;
+                float X[RPL][DPK];
+                ld_rows<RPL, DPK>(X, a.dkbuf + slab * DK, rk_off, full, nv);
+#pragma unroll
+                for (int j = 0; j < RPL; j++)
+#pragma unroll
+                    for (int i = 0; i < DPK; i++) dK[j][i] += X[j][i];
+                float Y[RPL][DPV];
+                ld_rows<RPL, DPV>(Y, a.dvbuf + slab * DV, rv_off, full, nv);
 #pragma unroll
                 for (int j = 0; j < RPL; j++) {
-                    const int n = nbase + j;
-                    const bool ok = n < a.N;
-                    if (ok) {
-#pragma unroll
-                        for (int i = 0; i < DPK; i += 4) {
-                            const float4 f = ld4(a.dkbuf + (base + n) * DK + dl * DPK + i);
-                            dK[j][i] += f.x; dK[j][i + 1] += f.y; dK[j][i + 2] += f.z; dK[j][i + 3] += f.w;
-                        }
-                    }
 #pragma unroll
                     for (int i = 0; i < DPV; i += 4) {      // the next segment's D = cV D + dvbuf
                         float4* d = reinterpret_cast<float4*>(dvr + j * DV + i);
-                        const float4 f = ok ? ld4(a.dvbuf + (base + n) * DV + dl * DPV + i) : make_float4(0.f, 0.f, 0.f, 0.f);
                         const float4 x = *d;
-                        *d = make_float4(fmaf(cV[j], x.x, f.x), fmaf(cV[j], x.y, f.y), fmaf(cV[j], x.z, f.z), fmaf(cV[j], x.w, f.w));
+                        *d = make_float4(fmaf(cV[j], x.x, Y[j][i]), fmaf(cV[j], x.y, Y[j][i + 1]),
+                                         fmaf(cV[j], x.z, Y[j][i + 2]), fmaf(cV[j], x.w, Y[j][i + 3]));
                     }
                 }
             }
         }
         __syncthreads();                      // the walk's reads are done before the next replay overwrites
-        if (pend_t >= 0) { finish_q(pend_t, pend_qinv, p2[par ^ 1]); pend_t = -1; }
+        if (pend_t >= 0) { finish_q(pend_t, pend_t - t0, pend_qinv, p2[par ^ 1]); pend_t = -1; }
     }
     if (w == 1 && lane == 0) {
         a.part[2 * chain] = dfr_acc;
@@ -877,7 +952,7 @@ static void dispatch(bool bwd, int64_t DK, int64_t DV, int rpl, dim3 grid, hipSt
 static int64_t scr_chain(int64_t DK, int64_t DV, int rpl, int64_t G) {
     const int64_t NP = 32 * rpl;
     (void)DV;
-    return G * 5 * NP + ((G - 1) / 4) * NP * DK + ((G + 3) / 4) * 4;   // GenScr<...>::chain
+    return G * NP + ((G + 3) / 4) * NP * DK;                           // GenScr<...>::chain
 }
 
 }  // namespace
@@ -898,18 +973,18 @@ extern "C" int slotscan_gen_fwd(const void* k, const void* q, const void* v, int
                                 const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
                                 int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
                                 int hard, int pin, float* kbuf, float* vbuf, float* obuf, int32_t* am, float* wb,
-                                void* stream) {
+                                float* rlog, void* stream) {
     if (int r = check_gen(B, T, H, N, DK, DV, G, dtype)) return r;
     if (!k || !q || !v || !gate || !fr || !temp || !kbuf || !vbuf || !obuf || (hard && !am))
         return fail(SLOTSCAN_ERR_NULL, "slotscan_gen_fwd: a required pointer is NULL");
-    if (!al16(k) || !al16(q) || !al16(v) || !al16(kbuf) || !al16(vbuf))
-        return fail(SLOTSCAN_ERR_ALIGN, "slotscan_gen_fwd: k, q, v, kbuf, vbuf must be 16-byte aligned");
+    if (!al16(k) || !al16(q) || !al16(v) || !al16(kbuf) || !al16(vbuf) || !al16(rlog))
+        return fail(SLOTSCAN_ERR_ALIGN, "slotscan_gen_fwd: k, q, v, kbuf, vbuf, rlog must be 16-byte aligned");
     GenArgs a{};
     a.k = k; a.q = q; a.v = v; a.gate = gate; a.fr = fr; a.temp = temp;
     a.frt = fr_per_token != 0; a.T = (int)T; a.H = (int)H; a.N = (int)N; a.G = (int)G;
     a.NB = (int)((T + G - 1) / G); a.occ_bin = occ_bin != 0; a.hard = hard != 0; a.detach = 1; a.eps = eps;
     a.pin = pin != 0;
-    a.kbuf = kbuf; a.vbuf = vbuf; a.obuf = obuf; a.am = am; a.wb = wb;
+    a.kbuf = kbuf; a.vbuf = vbuf; a.obuf = obuf; a.am = am; a.wb = wb; a.rlog = rlog;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)(B * H));
     hipError_t e;
@@ -922,6 +997,11 @@ extern "C" int slotscan_gen_fwd(const void* k, const void* q, const void* v, int
     return e == hipSuccess ? 0 : hip_fail(e, "gen_fwd launch");
 }
 
+extern "C" size_t slotscan_gen_log_bytes(int64_t B, int64_t T, int64_t H, int64_t N) {
+    if (B < 1 || T < 1 || H < 1 || N < 1) return 0;
+    return gen_log_floats(B * H, T, N) * sizeof(float);
+}
+
 extern "C" size_t slotscan_gen_bwd_workspace(int64_t B, int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G) {
     const int64_t per = scr_chain(DK, DV, gen_rpl(N), G);
     const size_t scr = (size_t)B * H * per * sizeof(float);
@@ -932,11 +1012,11 @@ extern "C" int slotscan_gen_bwd(const void* k, const void* q, const void* v, int
                                 const float* fr, int fr_per_token, const float* temp, int64_t B, int64_t T,
                                 int64_t H, int64_t N, int64_t DK, int64_t DV, int64_t G, float eps, int occ_bin,
                                 int hard, int detach_addr, int pin, const float* kbuf, const float* vbuf,
-                                const float* obuf, const int32_t* am, const float* dkbuf, const float* dvbuf,
-                                void* workspace, void* dk, void* dq, void* dv, float* dgate, float* dfr,
-                                float* dtemp, void* stream) {
+                                const float* obuf, const int32_t* am, const float* rlog, const float* dkbuf,
+                                const float* dvbuf, void* workspace, void* dk, void* dq, void* dv, float* dgate,
+                                float* dfr, float* dtemp, void* stream) {
     if (int r = check_gen(B, T, H, N, DK, DV, G, dtype)) return r;
-    if (!k || !q || !v || !gate || !fr || !temp || !kbuf || !vbuf || !obuf || (hard && !am) || !dkbuf ||
+    if (!k || !q || !v || !gate || !fr || !temp || !kbuf || !vbuf || !obuf || (hard && !am) || !rlog || !dkbuf ||
         !dvbuf || !workspace || !dk || !dq || !dv || !dgate || !dfr || !dtemp)
         return fail(SLOTSCAN_ERR_NULL, "slotscan_gen_bwd: a required pointer is NULL");
     if (!al16(k) || !al16(q) || !al16(v) || !al16(kbuf) || !al16(vbuf) || !al16(dkbuf) || !al16(dvbuf) ||
@@ -949,7 +1029,7 @@ extern "C" int slotscan_gen_bwd(const void* k, const void* q, const void* v, int
     a.NB = (int)((T + G - 1) / G); a.occ_bin = occ_bin != 0; a.hard = hard != 0; a.detach = detach_addr != 0;
     a.eps = eps; a.pin = pin != 0;
     a.kbuf = const_cast<float*>(kbuf); a.vbuf = const_cast<float*>(vbuf); a.obuf = const_cast<float*>(obuf);
-    a.am = const_cast<int32_t*>(am); a.dkbuf = dkbuf; a.dvbuf = dvbuf;
+    a.am = const_cast<int32_t*>(am); a.rlog = const_cast<float*>(rlog); a.dkbuf = dkbuf; a.dvbuf = dvbuf;
     a.scr = (float*)workspace; a.scr_chain = scr_chain(DK, DV, rpl, G);
     const size_t scr = (size_t)B * H * a.scr_chain * sizeof(float);
     a.part = (float*)((char*)workspace + ((scr + 255) & ~(size_t)255));

@@ -185,12 +185,15 @@ class _KVScanGenHip(torch.autograd.Function):
         obuf = torch.empty(B, NB, H, N, device=dev, dtype=f32)
         am = torch.empty(B, T, H, device=dev, dtype=torch.int32) if hard else None
         wb = torch.empty(B, T, H, N, device=dev, dtype=f32) if return_w else None
+        # the address log the backward replays from (only when a backward can follow)
+        rlog = torch.empty(L.lib().slotscan_gen_log_bytes(B, T, H, N) // 4, device=dev, dtype=f32) \
+            if any(ctx.needs_input_grad[:6]) else None
         rc = L.lib().slotscan_gen_fwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
                                       int(frt), L.ptr(temp_), B, T, H, N, DK, DV, G, float(eps), int(occ_bin),
                                       int(hard), int(pin), L.ptr(kbuf), L.ptr(vbuf), L.ptr(obuf), L.ptr(am),
-                                      L.ptr(wb), L.stream_of(dev))
+                                      L.ptr(wb), L.ptr(rlog), L.stream_of(dev))
         L.check(rc, "slotscan_gen_fwd")
-        ctx.save_for_backward(k_, q_, v_, g, fr_, temp_, kbuf, vbuf, obuf, am)
+        ctx.save_for_backward(k_, q_, v_, g, fr_, temp_, kbuf, vbuf, obuf, am, rlog)
         ctx.meta = (int(N), int(G), bool(hard), float(eps), bool(detach_addr), bool(occ_bin), frt, dt,
                     tuple(fr.shape), torch.is_tensor(temp), bool(pin))
         if return_w:
@@ -200,7 +203,7 @@ class _KVScanGenHip(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dkbuf, dvbuf, _dwb=None):
-        k_, q_, v_, g, fr_, temp_, kbuf, vbuf, obuf, am = ctx.saved_tensors
+        k_, q_, v_, g, fr_, temp_, kbuf, vbuf, obuf, am, rlog = ctx.saved_tensors
         N, G, hard, eps, detach_addr, occ_bin, frt, dt, fr_shape, temp_is_tensor, pin = ctx.meta
         B, T, H, DK = k_.shape
         DV = v_.shape[-1]
@@ -216,8 +219,8 @@ class _KVScanGenHip(torch.autograd.Function):
         rc = L.lib().slotscan_gen_bwd(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
                                       int(frt), L.ptr(temp_), B, T, H, N, DK, DV, G, float(eps), int(occ_bin),
                                       int(hard), int(detach_addr), int(pin), L.ptr(kbuf), L.ptr(vbuf),
-                                      L.ptr(obuf),
-                                      L.ptr(am), L.ptr(dkbuf), L.ptr(dvbuf), L.ptr(ws), L.ptr(dk), L.ptr(dq),
+                                      L.ptr(obuf), L.ptr(am), L.ptr(rlog), L.ptr(dkbuf), L.ptr(dvbuf), L.ptr(ws),
+                                      L.ptr(dk), L.ptr(dq),
                                       L.ptr(dv), L.ptr(dg), L.ptr(dfr), L.ptr(dtemp), L.stream_of(dev))
         L.check(rc, "slotscan_gen_bwd")
         dfr = dfr.reshape(fr_shape) if not frt else dfr

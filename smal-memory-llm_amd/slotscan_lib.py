@@ -43,10 +43,11 @@ SIGNATURES = {
     "slotscan_bwd_mem": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
                                 _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32] + [_vp] * 19),
     "slotscan_gen_fwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
-                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32] + [_vp] * 6),
+                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32] + [_vp] * 7),
+    "slotscan_gen_log_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "slotscan_gen_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "slotscan_gen_bwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
-                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32, _i32] + [_vp] * 14),
+                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32, _i32] + [_vp] * 15),
     "slotread_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "slotread_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _vp, _vp, _vp, _vp, _vp, _vp]),
