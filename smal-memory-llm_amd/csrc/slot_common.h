@@ -117,4 +117,18 @@ __device__ __forceinline__ float fkey_inv(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// LDS byte address of a __shared__ object (for m0)
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)reinterpret_cast<uintptr_t>((const lds_void*)p);
+}
+
+// One direct global -> LDS load: 16 bytes per active lane from g into LDS at lds + 16 * lane (lds
+// wave-uniform, in m0).  Issued as inline assembly, so the compiler does not track it: the caller waits for
+// it explicitly (a vmcnt wait) before the barrier that publishes the data.  It holds no data register.
+__device__ __forceinline__ void dma16(const void* g, unsigned lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off" : : "{m0}"(lds), "v"(g) : "memory");
+}
+
 }  // namespace slot

@@ -580,19 +580,34 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
         const int ns = min(t1 - t0, GL);
         if (t0 < sp.base) sp = load_steppar(a.gate, a.fr, a.frt, amlog, a.T, a.H, tok0, max(t1 - 64, 0), lane);
         // ---- the segment's logged row scalars (o, a_s, s, |K|), qinv, and key and query token rows of its
-        // first GL steps into LDS
+        // first GL steps into LDS.  Direct global -> LDS loads where the layouts allow (no data registers: the
+        // dK state is live here), waited for explicitly before the barrier.
         {
             const float* rec = rlog + (size_t)t0 * 4 * a.N;
-            for (int x = threadIdx.x; x < ns * 4 * NP; x += GEN_THREADS) {
-                const int st = x / (4 * NP), r = x - st * 4 * NP, f = r / NP, n = r - f * NP;
-                lsc[(st * 5 + f) * NP + n] = n < a.N ? rec[((size_t)st * 4 + f) * a.N + n] : 0.f;
+            if (full) {                       // a step's record (4 N floats) is N / 64 KB pieces, contiguous in lsc
+                const int pps = a.N / 64;
+                for (int k = w; k < ns * pps; k += GEN_WAVES) {
+                    const int st = k / pps, pc = k - st * pps;
+                    dma16((const char*)(rec + (size_t)st * 4 * a.N) + pc * 1024 + lane * 16,
+                          lds_addr(lsc + st * 5 * NP) + pc * 1024);
+                }
+            } else {
+                for (int x = threadIdx.x; x < ns * 4 * NP; x += GEN_THREADS) {
+                    const int st = x / (4 * NP), r = x - st * 4 * NP, f = r / NP, n = r - f * NP;
+                    lsc[(st * 5 + f) * NP + n] = n < a.N ? rec[((size_t)st * 4 + f) * a.N + n] : 0.f;
+                }
             }
             if (threadIdx.x < ns) lqinv[threadIdx.x] = qlog[t0 + threadIdx.x];
-            for (int x = threadIdx.x; x < ns * 2 * TU; x += GEN_THREADS) {
-                const int st = x / (2 * TU), wh = (x / TU) & 1, u = x % TU;
-                const char* row = (const char*)(wh ? a.q : a.k) + tok(t0 + st) * DK * sizeof(TI);
-                ltq[x] = reinterpret_cast<const uint4*>(row)[u];
+            {                                 // token rows (st, key / query): 1 KB of them per load instruction
+                constexpr int LPR = DK * (int)sizeof(TI) / 16;        // lanes per token row
+                constexpr int RPI = 64 / LPR;                          // rows per instruction
+                for (int k = w; k * RPI < 2 * ns; k += GEN_WAVES) {
+                    const int row = k * RPI + lane / LPR, st = row >> 1;
+                    const char* g = (const char*)((row & 1) ? a.q : a.k) + tok(t0 + st) * DK * sizeof(TI) + (lane % LPR) * 16;
+                    if (row < 2 * ns) dma16(g, lds_addr(ltq) + k * 1024);
+                }
             }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
         __syncthreads();                      // the replay reads the logged addresses of every row group
         // ---- replay the segment's keys from its emitted copy, keeping every step's pre-write state
@@ -698,7 +713,12 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             auto load_K = [&](float (&K)[RPL][DPK]) {
                 const int c = (s / SC::GC) * SC::GC;
                 ld_rows<RPL, DPK>(K, scr_k + (size_t)(c / SC::GC) * NP * DK, rk_off, true, RPL);
-                for (int u = c; u < s; u++) {
+                // at most GC - 1 updates, unrolled with a uniform test: a rolled loop rotated the 8 RPL key
+                // registers through copies at every iteration
+#pragma unroll
+                for (int uu = 0; uu < SC::GC - 1; uu++) {
+                    const int u = c + uu;
+                    if (u >= s) break;
                     float ku[DPK];
                     tokrow(0, u, t0 + u, ku);
                     const float gu = steppar_g(sp, t0 + u);
@@ -860,19 +880,19 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             pend_t = t;
             pend_qinv = qinv;
             par ^= 1;
-            // carry to the pre-write adjoint
+            // carry to the pre-write adjoint; attached: dK += c (temp qn - s kinv K), c = ds kinv (the second
+            // term dropped where |K| < 1e-6)
+            float tq[DPK];
+#pragma unroll
+            for (int i = 0; i < DPK; i++) tq[i] = temp * (qt[i] * qinv);
 #pragma unroll
             for (int j = 0; j < RPL; j++) {
                 const float omw = 1.f - wr[j];
                 if (!a.detach) {
                     const float c = ds[j] * kinv[j];
-                    const bool small = knr[j] < GEN_NORM_EPS;
+                    const float cs = knr[j] < GEN_NORM_EPS ? 0.f : c * (sr[j] * kinv[j]);
 #pragma unroll
-                    for (int i = 0; i < DPK; i++) {
-                        const float qn = qt[i] * qinv;
-                        const float m = small ? c * temp * qn : c * (temp * qn - sr[j] * K[j][i] * kinv[j]);
-                        dK[j][i] = fmaf(omw, dK[j][i], m);
-                    }
+                    for (int i = 0; i < DPK; i++) dK[j][i] = fmaf(-cs, K[j][i], fmaf(c, tq[i], omw * dK[j][i]));
                 } else {
 #pragma unroll
                     for (int i = 0; i < DPK; i++) dK[j][i] *= omw;
@@ -902,8 +922,10 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 }
             }
         }
-        __syncthreads();                      // the walk's reads are done before the next replay overwrites
+        __syncthreads();                      // the last walk step's posts are visible
         if (pend_t >= 0) { finish_q(pend_t, pend_t - t0, pend_qinv, p2[par ^ 1]); pend_t = -1; }
+        __syncthreads();                      // every read of this segment's LDS data is done before the next
+                                              // segment's staging overwrites it
     }
     if (w == 1 && lane == 0) {
         a.part[2 * chain] = dfr_acc;

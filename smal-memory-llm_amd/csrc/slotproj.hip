@@ -47,8 +47,6 @@ constexpr int STAGE = PT * PK * 2; // bytes of one operand's stage (16 KB)
 constexpr int PLD = STAGE / 1024 / (PTHREADS / 64);   // 1-KB load instructions per wave, operand and stage (4)
 constexpr int PXCD = 8;            // XCDs of an MI355X: consecutive workgroups go to consecutive XCDs
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 struct ProjArgs {
     const bf16_t* a; const bf16_t* w; const bf16_t* d; bf16_t* out;
     int M, N, K, mblocks, nblocks;
@@ -67,18 +65,10 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
 }
 
-// one direct global -> LDS load: 16 bytes per lane from g into LDS at lds + 16 * lane (lds wave-uniform, in m0).
-// Issued as inline assembly so that the compiler does not track it: its own tracking cannot tell the ring's
-// buffers apart and would drain every load in flight before each stage's first LDS read.  The kernel waits for
-// these loads itself (wait_vm before the barrier that publishes a stage), and issues no other vector-memory
-// load while any is in flight, so the compiler's counts for its own loads stay exact.
-__device__ __forceinline__ void dma16(const void* g, unsigned lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off" : : "{m0}"(lds), "v"(g) : "memory");
-}
-
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-    return (unsigned)reinterpret_cast<uintptr_t>((const lds_void*)p);
-}
+// The ring's direct global -> LDS loads (dma16) are not tracked by the compiler: its own tracking cannot tell
+// the ring's buffers apart and would drain every load in flight before each stage's first LDS read.  The kernel
+// waits for these loads itself (wait_vm before the barrier that publishes a stage), and issues no other
+// vector-memory load while any is in flight, so the compiler's counts for its own loads stay exact.
 
 // workgroup barrier that orders LDS for the compiler but adds no hardware wait for the direct loads still in
 // flight (those are waited for explicitly, per stage, before the barrier that publishes them)
