@@ -40,6 +40,8 @@
 // backward's replay needs none (the address comes from the log).  Each step of its walk needs one: the waves post the
 // address-gradient sums and their dk/dv partials; the previous step's dq/dfr/dtemp partials ride along on
 // the same exchange.  The scratch is written and read in 16-byte units, each row by its 16 dim-lanes.
+// The step is bound by its VALU instruction count (2 waves per SIMD), so the clamped inverse norms and the
+// softmax normaliser use the hardware v_rsq / v_rcp / v_sqrt (1 ulp) instead of IEEE division sequences.
 #include "slot_common.h"
 #include "slotscan.h"
 #include "slot_host.h"
@@ -269,7 +271,7 @@ __device__ __forceinline__ int gen_address(const float (&z)[RPL], const float (&
             for (int ww = 0; ww < st; ww++) sw[ww] += sw[ww + st];
         S += sw[0];
     }
-    const float rS = 1.f / S;
+    const float rS = __builtin_amdgcn_rcpf(S);
     const int row = hard ? (hard_row >= 0 ? hard_row : BI) : -1;
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
@@ -290,7 +292,7 @@ __device__ __forceinline__ void gen_scores(const float (&K)[RPL][DPK], const flo
 #pragma unroll
     for (int i = 0; i < DPK; i++) qq = fmaf(qt[i], qt[i], qq);
     qq = rowsum16(qq);
-    qinv = 1.f / fmaxf(sqrtf(qq), GEN_NORM_EPS);
+    qinv = __builtin_amdgcn_rsqf(fmaxf(qq, GEN_NORM_EPS * GEN_NORM_EPS));   // 1 / max(|q|, 1e-6)
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
         float d = 0.f, n2 = 0.f;
@@ -298,8 +300,8 @@ __device__ __forceinline__ void gen_scores(const float (&K)[RPL][DPK], const flo
         for (int i = 0; i < DPK; i++) { d = fmaf(K[j][i], qt[i], d); n2 = fmaf(K[j][i], K[j][i], n2); }
         d = rowsum16(d);
         n2 = rowsum16(n2);
-        kn[j] = sqrtf(n2);
-        const float kinv = 1.f / fmaxf(kn[j], GEN_NORM_EPS);
+        kn[j] = __builtin_amdgcn_sqrtf(n2);
+        const float kinv = __builtin_amdgcn_rsqf(fmaxf(n2, GEN_NORM_EPS * GEN_NORM_EPS));   // 1 / max(|K|, 1e-6)
         sr[j] = temp * (d * kinv * qinv);
         if (pin && kn[j] < GEN_NORM_EPS) sr[j] = 0.f;   // pinned: a (near-)zero row scores 0
         const float occ = occ_bin ? (o[j] >= eps ? 1.f : 0.f) : o[j];
@@ -561,7 +563,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
         for (int i = 0; i < DPK; i++) { pr = fmaf(qt[i] * qinv, dqn[i], pr); qq = fmaf(qt[i], qt[i], qq); }
         pr = rowsum16(pr);
         qq = rowsum16(qq);
-        const bool small = sqrtf(qq) < GEN_NORM_EPS;
+        const bool small = qq < GEN_NORM_EPS * GEN_NORM_EPS;
         if (rl == 0) {
             float r[DPK];
 #pragma unroll
@@ -853,7 +855,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             for (int j = 0; j < RPL; j++) {
                 dz[j] = as[j] * (g * dw[j] - SA);
                 ds[j] = (a.pin && knr[j] < GEN_NORM_EPS) ? 0.f : dz[j];
-                kinv[j] = 1.f / fmaxf(knr[j], GEN_NORM_EPS);
+                kinv[j] = __builtin_amdgcn_rcpf(fmaxf(knr[j], GEN_NORM_EPS));
                 const float occ = a.occ_bin ? (o[j] >= a.eps ? 1.f : 0.f) : o[j];
                 sfo = fmaf(occ, dz[j], sfo);
                 sds = fmaf(ds[j], sr[j], sds);
