@@ -233,6 +233,10 @@ struct ChainFwdArgs {
     int ts, te;                                          // steps [ts, te) of the T-long sequence; ts % G == 0
     // the writer-epilogue emission (all NULL: fp32 kbuf): bf16 key copies, kinv and valid per snapshot row
     bf16_t* kbm; float* kinvm; uint8_t* validm;
+    // chain (b, h) of k0 and kfin is slab b * k0bs + h (kfbs): H for (B*H, N, D) carries; NB * H where a chunk
+    // of the pipeline starts from (ends in) the key snapshot of its first (next) block.  skip0: that first
+    // snapshot is already written (by the previous chunk), so this chunk does not store it.
+    int k0bs, kfbs, skip0;
 };
 
 // Wave-local LDS ordering: lanes of one wave exchange data through LDS (DS instructions of a wave execute
@@ -410,7 +414,7 @@ void chain_fwd(ChainFwdArgs a) {
     const ChainRows<P> R(tid);
     const size_t sstride = (size_t)H * N * D;
     const size_t snap0 = ((size_t)b * a.NB + ts / G) * H + h;           // (b, ts / G, h): snapshot of block ts / G
-    float* kb = MB ? nullptr : a.kbuf + snap0 * N * D;
+    float* kb = MB ? nullptr : a.kbuf + snap0 * N * D + (a.skip0 ? sstride : 0);   // skip0: the first slab is written
     bf16_t* kbm = MB ? a.kbm + snap0 * N * D : nullptr;
     float* kinvm = MB ? a.kinvm + snap0 * N : nullptr;
     uint8_t* validm = MB ? a.validm + snap0 * N : nullptr;
@@ -425,7 +429,7 @@ void chain_fwd(ChainFwdArgs a) {
             float row[EPL];
 #pragma unroll
             for (int e = 0; e < EPL; e++) row[e] = 0.f;
-            if (a.k0 && n < N) ld_slice<EPL>(row, a.k0 + ((size_t)bh * N + n) * D, c);
+            if (a.k0 && n < N) ld_slice<EPL>(row, a.k0 + ((size_t)(b * a.k0bs + h) * N + n) * D, c);
             float kk = 0.f;
 #pragma unroll
             for (int e = 0; e < EPL; e++) { Kv[e][j] = row[e]; kk = fmaf(row[e], row[e], kk); }
@@ -528,7 +532,7 @@ void chain_fwd(ChainFwdArgs a) {
             uint4 r[CHAIN_WAVES];
 #pragma unroll
             for (int w = 0; w < CHAIN_WAVES; w++) r[w] = s_red[par][w];
-            if (gc == 0) {                                  // the PRE-write key state of block t / G:
+            if (gc == 0 && (MB || t != ts || !a.skip0)) {   // the PRE-write key state of block t / G:
                 u32 ro = roff;                              // every row group stores whole rows
                 int nvv = nvalid;
                 asm volatile("" : "+v"(ro), "+v"(nvv));     // per-snapshot offsets, not 16 live registers
@@ -611,7 +615,7 @@ void chain_fwd(ChainFwdArgs a) {
     for (int jr = 0; jr < P; jr++) {
         float row[EPL];
         row_of(jr, row);
-        if (jr < nvalid) st_slice_at<EPL, false>(a.kfin + (size_t)bh * N * D, roff + (u32)(jr * D * 4), row);
+        if (jr < nvalid) st_slice_at<EPL, false>(a.kfin + (size_t)(b * a.kfbs + h) * N * D, roff + (u32)(jr * D * 4), row);
     }
     if (valid_me && R.prim) a.ofin[(size_t)bh * N + R.n_me] = o_me;
 }
@@ -623,6 +627,7 @@ struct RowsFwdArgs {
     int T, H, N, G, NB;
     int ts, te;                                          // steps [ts, te); ts % G == 0
     bf16_t* vbm;                                         // the writer-epilogue emission (NULL: fp32 vbuf)
+    int v0bs, vfbs, skip0;                               // as ChainFwdArgs' k0bs, kfbs, skip0
 };
 
 // 512 lanes = 32 rows of one chain per workgroup; grid (B*H, ceil(N/32)).  Replays every row's value from
@@ -646,7 +651,7 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     float V[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; e++) V[e] = 0.f;
-    if (live && a.v0) ld_slice<EPL>(V, a.v0 + ((size_t)bh * N + n) * D, c);
+    if (live && a.v0) ld_slice<EPL>(V, a.v0 + ((size_t)(b * a.v0bs + h) * N + n) * D, c);
     const size_t vrow0 = (((size_t)b * a.NB + a.ts / G) * H + h) * N * D + (size_t)(live ? n : 0) * D;
     float* vb = MB ? nullptr : a.vbuf + vrow0;
     bf16_t* vbh = MB ? a.vbm + vrow0 : nullptr;
@@ -679,7 +684,10 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
                 ev &= ev - 1;
                 if ((sm >> i) & 1u) {
                     if constexpr (MB) { st_slice_bf_at<EPL>(vbh, 8u * (u32)c, V); vbh += sstride; }
-                    else { st_slice_nt<EPL>(vb, V, c); vb += sstride; }
+                    else {
+                        if (t0 + j0 + i != a.ts || !a.skip0) st_slice_nt<EPL>(vb, V, c);   // skip0: already written
+                        vb += sstride;
+                    }
                 }
                 if ((hm >> i) & 1u) {
                     const size_t ix = tok0 + (size_t)(t0 + j0 + i) * H;
@@ -693,7 +701,7 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
             }
         }
     }
-    if (live) st_slice<EPL>(a.vfin + ((size_t)bh * N + n) * D, V, c);
+    if (live) st_slice<EPL>(a.vfin + ((size_t)(b * a.vfbs + h) * N + n) * D, V, c);
 }
 
 // =========================================================================================== rows_bwd
@@ -2125,12 +2133,16 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
     const int NB = (int)((T + G - 1) / G);
     ChainFwdArgs ca{q, k, gate, fr, temp, k0, o0, kbuf, am, kold, oold, cslog, kfin, ofin,
                     (int)T, (int)H, (int)N, (int)G, NB, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0, 0, (int)T,
-                    kbm, kinvm, validm};
-    RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB, 0, (int)T, vbm};
+                    kbm, kinvm, validm, (int)H, (int)H, 0};
+    RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB, 0, (int)T, vbm,
+                   (int)H, (int)H, 0};
     // Long sequences run as a two-stream pipeline over step chunks of a multiple of G: the key chain of
     // chunk c + 1 (latency-bound, caller's stream) overlaps the value replay of chunk c (HBM-bound, the
-    // library's side stream).  Both kernels carry their state through kfin / ofin and vfin in place
-    // (every element is read at a chunk's start and written at its end by the same lane).
+    // library's side stream).  The state crosses an inner chunk boundary te as the snapshot of block te / G,
+    // which is exactly the state there: a chunk ends by writing it (it is its next block's PRE-write
+    // snapshot) and the next chunk starts from it without storing it again (fp32 contract; the bf16 copies
+    // of the fused contract cannot carry fp32 state, so there kfin and vfin carry it).  The occupancy
+    // crosses through ofin; the last chunk writes kfin, vfin, ofin.
     const int64_t len = T >= 512 ? ((std::max<int64_t>(128, T / 8) + G - 1) / G) * G : T;
     const int nch = (int)((T + len - 1) / len);
     hipStream_t side = nullptr;
@@ -2142,7 +2154,22 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
     for (int c = 0; c < nch; c++) {
         ca.ts = ra.ts = (int)(c * len);
         ca.te = ra.te = (int)std::min<int64_t>(T, (c + 1) * len);
-        if (c > 0) { ca.k0 = kfin; ca.o0 = ofin; ra.v0 = vfin; }
+        const bool inner_end = ca.te < T;
+        if (c > 0) {
+            ca.o0 = ofin;
+            if (mem) { ca.k0 = kfin; ra.v0 = vfin; }
+            else {                                       // from the snapshot slab of block ts / G
+                ca.k0 = kbuf + (size_t)(ca.ts / G) * H * N * D;
+                ra.v0 = vbuf + (size_t)(ra.ts / G) * H * N * D;
+                ca.k0bs = ra.v0bs = NB * (int)H;
+                ca.skip0 = ra.skip0 = 1;
+            }
+        }
+        if (!mem) {                                      // an inner chunk ends in the next block's slab
+            ca.kfin = inner_end ? kbuf + (size_t)(ca.te / G) * H * N * D : kfin;
+            ra.vfin = inner_end ? vbuf + (size_t)(ra.te / G) * H * N * D : vfin;
+            ca.kfbs = ra.vfbs = inner_end ? NB * (int)H : (int)H;
+        }
         {
             slothost::Scope sc(SLOTSCAN_K_CHAIN_FWD, st);
             if (D == 128) e = dtype == SLOTSCAN_BF16 ? launch_chain_fwd<128, bf16_t>(ca, (int)B, st) : launch_chain_fwd<128, float>(ca, (int)B, st);
