@@ -447,8 +447,8 @@ __host__ __device__ inline size_t gen_log_floats(int64_t BH, int64_t T, int64_t 
 }
 
 // Scratch per chain: for every segment step s the row scalar e - P = <v_t, D> - <V, D> (NP floats), then
-// the pre-write keys (NP, DK) of every GC-th step, the first included (a copy of the emitted one, so every
-// checkpoint has NP rows and is read without bounds tests).  NP = 32 * RPL.  The first GL steps of a
+// the pre-write keys (NP, DK) of every GC-th step after the first (the first step's are the emitted copy).
+// NP = 32 * RPL.  The first GL steps of a
 // segment keep their row scalars (the four logged ones and e - P), key and query token rows and qinv in
 // LDS instead (gen_bwd), so the walk reads them at LDS latency; later steps read the logged ones from the
 // log.  The walk rebuilds the keys of any step from the checkpoint at or before it with the updates in
@@ -458,7 +458,7 @@ template <int DK, int DV, int RPL>
 struct GenScr {
     static constexpr int NP = 32 * RPL;
     static constexpr int GC = 4;
-    __host__ __device__ static int64_t nck(int G) { return (G + GC - 1) / GC; }
+    __host__ __device__ static int64_t nck(int G) { return (G - 1) / GC; }
     __host__ __device__ static int64_t chain(int G) { return (int64_t)G * NP + nck(G) * NP * DK; }
 };
 
@@ -643,8 +643,8 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 const int s = t - t0;
                 float vt[DPV];
                 rv.cvt(vt);
-                if (s % SC::GC == 0) {                      // a key checkpoint
-                    char* sk = (char*)(scr_k + (size_t)(s / SC::GC) * NP * DK) + rk_off;
+                if (s > 0 && s % SC::GC == 0) {             // a key checkpoint
+                    char* sk = (char*)(scr_k + (size_t)(s / SC::GC - 1) * NP * DK) + rk_off;
 #pragma unroll
                     for (int j = 0; j < RPL; j++)
 #pragma unroll
@@ -714,7 +714,8 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             // one brought into the cache).
             auto load_K = [&](float (&K)[RPL][DPK]) {
                 const int c = (s / SC::GC) * SC::GC;
-                ld_rows<RPL, DPK>(K, scr_k + (size_t)(c / SC::GC) * NP * DK, rk_off, true, RPL);
+                if (c == 0) ld_rows<RPL, DPK>(K, a.kbuf + ((((size_t)b * a.NB + tb) * a.H + h) * a.N) * DK, rk_off, full, nv);
+                else ld_rows<RPL, DPK>(K, scr_k + (size_t)(c / SC::GC - 1) * NP * DK, rk_off, true, RPL);
                 // at most GC - 1 updates, unrolled with a uniform test: a rolled loop rotated the 8 RPL key
                 // registers through copies at every iteration
 #pragma unroll
@@ -976,7 +977,7 @@ static void dispatch(bool bwd, int64_t DK, int64_t DV, int rpl, dim3 grid, hipSt
 static int64_t scr_chain(int64_t DK, int64_t DV, int rpl, int64_t G) {
     const int64_t NP = 32 * rpl;
     (void)DV;
-    return G * NP + ((G + 3) / 4) * NP * DK;                           // GenScr<...>::chain
+    return G * NP + ((G - 1) / 4) * NP * DK;                           // GenScr<...>::chain
 }
 
 }  // namespace
