@@ -709,9 +709,9 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             const int s = t - t0;
             const size_t ti = tok(t);
             // The pre-write keys of step s: the checkpoint at or before it, then the replay's updates of the
-            // steps in between.  Built twice, before and after the step's barrier, rather than held across
-            // it: 8 * RPL fewer live registers through the exchange (the second build reads what the first
-            // one brought into the cache).
+            // steps in between.  Built once per step and held across the step's barrier (with the addresses
+            // held as scalar bases and lane offsets there is room for them; rebuilding them after the barrier
+            // cost more).
             auto load_K = [&](float (&K)[RPL][DPK]) {
                 const int c = (s / SC::GC) * SC::GC;
                 if (c == 0) ld_rows<RPL, DPK>(K, a.kbuf + ((((size_t)b * a.NB + tb) * a.H + h) * a.N) * DK, rk_off, full, nv);
@@ -745,7 +745,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                     }
                 }
             };
-            // the row scalars likewise: read where they are used, on each side of the barrier
+            // the row scalars: read where they are used, on each side of the barrier
             auto load_s = [&](float (&x)[RPL], int f) {
                 if (s < GL) {
 #pragma unroll
@@ -770,9 +770,10 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             // dw per row; dk_t, dv_t partials; the two address sums
             float dw[RPL], wr[RPL];
             float pg = 0.f, pa = 0.f;
-            {
-            float K[RPL][DPK], o[RPL], as[RPL], ad[RPL], ep[RPL];
+            float K[RPL][DPK];
             load_K(K);
+            {
+            float o[RPL], as[RPL], ad[RPL], ep[RPL];
             load_s(o, 0); load_s(as, 1); load_s(ep, 4);
             {
                 const int amt = a.hard ? steppar_am(sp, t) : -1;
@@ -846,8 +847,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 if (lane == 0) a.dg[ti] = SG;
             }
             // dz and the search-side partials
-            float K[RPL][DPK], o[RPL], as[RPL], sr[RPL], knr[RPL], qt[DPK];
-            load_K(K);
+            float o[RPL], as[RPL], sr[RPL], knr[RPL], qt[DPK];
             load_s(o, 0); load_s(as, 1); load_s(sr, 2); load_s(knr, 3);
             tokrow(1, s, t, qt);
             float dz[RPL], ds[RPL], kinv[RPL];      // ds: dz with the pinned rows' score path cut
