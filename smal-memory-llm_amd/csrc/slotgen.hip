@@ -186,6 +186,25 @@ __device__ __forceinline__ void lds_barrier() {
 // Sum over the 4 row-lanes (lanes c, c+16, c+32, c+48).
 __device__ __forceinline__ float rows4_sum(float x) { return sum4rows(x); }
 
+// Reduce-scatter of NV per-lane values over the 4 row-lanes: row-lane rl ends with the totals of values
+// rows4_rs_base<NV>(rl) .. + NV / 4 - 1.  The 16-lane swap first, then the 32-lane one, each adding its
+// two returned copies in the same order as sum4rows, so every total is bitwise sum4rows' result; 3 NV / 4
+// swaps instead of 2 NV.
+template <int NV> __device__ __forceinline__ void rows4_rs(const float (&x)[NV], float (&y)[NV / 4]) {
+    float a[NV / 2];
+#pragma unroll
+    for (int k = 0; k < NV / 2; k++) {   // rows 0, 2 keep values k, rows 1, 3 values NV / 2 + k
+        auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[k]), __float_as_uint(x[NV / 2 + k]), false, false);
+        a[k] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+#pragma unroll
+    for (int k = 0; k < NV / 4; k++) {   // the lower half keeps a[k], the upper half a[NV / 4 + k]
+        auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[k]), __float_as_uint(a[NV / 4 + k]), false, false);
+        y[k] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+}
+template <int NV> __device__ __forceinline__ int rows4_rs_base(int rl) { return (NV / 4) * (rl >> 1) + (NV / 2) * (rl & 1); }
+
 // One step's address over the chain: every lane gets its rows' soft address a_s, the address a used for the
 // write (a_s, or the one-hot of `hard_row`), and the winning row of the hard argmax.  xf is the workgroup
 // exchange slot of this step: [wave][8] = {softmax max, sum, first-free index, its z, best z, best index}.
@@ -796,14 +815,14 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             pg = rows4_sum(pg);
             pa = rows4_sum(pa);
             float* q1 = p1[par];
-            {
+            {   // the wave's dk, dv partials: summed over its rows, reduce-scattered over the row-lanes
                 float pk[DPK], pv[DPV];
 #pragma unroll
                 for (int i = 0; i < DPK; i++) {
                     float x = 0.f;
 #pragma unroll
                     for (int j = 0; j < RPL; j++) x = fmaf(wr[j], dK[j][i], x);
-                    pk[i] = rows4_sum(x);
+                    pk[i] = x;
                 }
 #pragma unroll
                 for (int i = 0; i < DPV; i += 4) {             // dV(t+) = cV D
@@ -814,16 +833,17 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                         const float4 d = *reinterpret_cast<const float4*>(dvr + j * DV + i);
                         x.x = fmaf(c, d.x, x.x); x.y = fmaf(c, d.y, x.y); x.z = fmaf(c, d.z, x.z); x.w = fmaf(c, d.w, x.w);
                     }
-                    pv[i] = rows4_sum(x.x); pv[i + 1] = rows4_sum(x.y); pv[i + 2] = rows4_sum(x.z); pv[i + 3] = rows4_sum(x.w);
+                    pv[i] = x.x; pv[i + 1] = x.y; pv[i + 2] = x.z; pv[i + 3] = x.w;
                 }
-                if (rl == 0) {
+                float yk[DPK / 4], yv[DPV / 4];
+                rows4_rs<DPK>(pk, yk);
+                rows4_rs<DPV>(pv, yv);
+                float* ok = q1 + w * P1W + dl * DPK + rows4_rs_base<DPK>(rl);
+                float* ov = q1 + w * P1W + DK + dl * DPV + rows4_rs_base<DPV>(rl);
 #pragma unroll
-                    for (int i = 0; i < DPK; i += 4)
-                        *reinterpret_cast<float4*>(q1 + w * P1W + dl * DPK + i) = make_float4(pk[i], pk[i + 1], pk[i + 2], pk[i + 3]);
+                for (int i = 0; i < DPK / 4; i++) ok[i] = yk[i];
 #pragma unroll
-                    for (int i = 0; i < DPV; i += 4)
-                        *reinterpret_cast<float4*>(q1 + w * P1W + DK + dl * DPV + i) = make_float4(pv[i], pv[i + 1], pv[i + 2], pv[i + 3]);
-                }
+                for (int i = 0; i < DPV / 4; i++) ov[i] = yv[i];
                 if (lane == 0) { q1[w * P1W + DK + DV] = pg; q1[w * P1W + DK + DV + 1] = pa; }
             }
             lds_barrier();
@@ -864,20 +884,20 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             sfo = rows4_sum(sfo);
             sds = rows4_sum(sds);
             float* q2 = p2[par];
-            {
+            {   // the wave's dqn partial, reduce-scattered over the row-lanes
                 float pq[DPK];
 #pragma unroll
                 for (int i = 0; i < DPK; i++) {
                     float x = 0.f;
 #pragma unroll
                     for (int j = 0; j < RPL; j++) x = fmaf(ds[j] * kinv[j], K[j][i], x);
-                    pq[i] = rows4_sum(temp * x);
+                    pq[i] = temp * x;
                 }
-                if (rl == 0) {
+                float yq[DPK / 4];
+                rows4_rs<DPK>(pq, yq);
+                float* oq = q2 + w * P2W + dl * DPK + rows4_rs_base<DPK>(rl);
 #pragma unroll
-                    for (int i = 0; i < DPK; i += 4)
-                        *reinterpret_cast<float4*>(q2 + w * P2W + dl * DPK + i) = make_float4(pq[i], pq[i + 1], pq[i + 2], pq[i + 3]);
-                }
+                for (int i = 0; i < DPK / 4; i++) oq[i] = yq[i];
                 if (lane == 0) { q2[w * P2W + DK] = sfo; q2[w * P2W + DK + 1] = sds; }
             }
             pend_t = t;
