@@ -583,14 +583,20 @@ void chain_fwd(ChainFwdArgs a) {
             if (amv >= R.rowbase && amv < R.rowbase + P) {  // this row group holds the written row
                 const int sl = amv & (P - 1);               // its register slot: the same in every lane
                 const float omw = 1.f - g;
-                float old[EPL], part = 0.f;
+                // the step's E row first: its LDS latency overlaps the row update
+                const f32x4* er = reinterpret_cast<const f32x4*>(&s_E[buf][j][0]);
+                f32x4 e4[CT / 4];
 #pragma unroll
-                for (int e = 0; e < EPL; e++) {
-                    old[e] = Kv[e][sl];
-                    const float nv = blend(old[e], kv[e], g, omw);
-                    Kv[e][sl] = nv;
-                    part = fmaf(nv, nv, part);
-                }
+                for (int q4 = 0; q4 < CT / 4; q4++) e4[q4] = er[q4];
+                float old[EPL], nv[EPL], part = 0.f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) old[e] = Kv[e][sl];
+#pragma unroll
+                for (int e = 0; e < EPL; e++) nv[e] = blend(old[e], kv[e], g, omw);
+#pragma unroll
+                for (int e = 0; e < EPL; e++) Kv[e][sl] = nv[e];
+#pragma unroll
+                for (int e = 0; e < EPL; e++) part = fmaf(nv[e], nv[e], part);
                 if (a.kold) st_slice<EPL>(a.kold + ix * D, old, c);
                 const float kk = rowsum16(part);
                 if (R.n_me == amv) {
@@ -599,13 +605,10 @@ void chain_fwd(ChainFwdArgs a) {
                     kinv_me = rsq_clamped(kk);
                     vld_me = kk > 1e-12f;
                     // all 16 entries: those at or before step j are never read again in this window
-                    const f32x4* er = reinterpret_cast<const f32x4*>(&s_E[buf][j][0]);
 #pragma unroll
-                    for (int q4 = 0; q4 < CT / 4; q4++) {
-                        const f32x4 e4 = er[q4];
+                    for (int q4 = 0; q4 < CT / 4; q4++)
 #pragma unroll
-                        for (int x = 0; x < 4; x++) Sr[4 * q4 + x] = fmaf(omw, Sr[4 * q4 + x], g * e4[x]);
-                    }
+                        for (int x = 0; x < 4; x++) Sr[4 * q4 + x] = fmaf(omw, Sr[4 * q4 + x], g * e4[q4][x]);
                 }
             }
         }
