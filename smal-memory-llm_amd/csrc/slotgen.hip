@@ -114,30 +114,36 @@ template <typename TI, int N> __device__ __forceinline__ void ldtok(const TI* p,
         }
     }
 }
-// Raw token bytes of a lane's N elements (16-byte pieces), loaded one step ahead and converted only where
-// used: a prefetch held as converted fp32 registers took twice the registers, and the compiler then
-// converted (and waited for) each load right after issuing it.  `base` is uniform, `off` the lane's byte
-// offset, so the loads use a scalar base with a 32-bit lane offset.
+// Raw token bytes of a lane's N elements (8 or a multiple of 16 bytes), loaded one step ahead and converted
+// only where used: a prefetch held as converted fp32 registers took twice the registers, and the compiler
+// then converted (and waited for) each load right after issuing it.  `base` is uniform, `off` the lane's
+// byte offset, so the loads use a scalar base with a 32-bit lane offset.
 template <typename TI, int N> struct RawTok {
-    static constexpr int U = N * (int)sizeof(TI) / 16;
-    uint4 r[U];
+    static constexpr int BYTES = N * (int)sizeof(TI);
+    static constexpr int NW = BYTES / 4;   // 32-bit words
+    static_assert(BYTES == 8 || BYTES % 16 == 0, "token slice must be 8 bytes or whole 16-byte pieces");
+    uint32_t w[NW];
     __device__ __forceinline__ void load(const void* base, uint32_t off) {
+        const char* p = (const char*)base + off;
+        if constexpr (BYTES == 8) {
+            const uint2 v = *reinterpret_cast<const uint2*>(p);
+            w[0] = v.x; w[1] = v.y;
+        } else {
 #pragma unroll
-        for (int u = 0; u < U; u++) r[u] = *reinterpret_cast<const uint4*>((const char*)base + off + 16 * u);
+            for (int u = 0; u < NW / 4; u++) {
+                const uint4 v = *reinterpret_cast<const uint4*>(p + 16 * u);
+                w[4 * u] = v.x; w[4 * u + 1] = v.y; w[4 * u + 2] = v.z; w[4 * u + 3] = v.w;
+            }
+        }
     }
     __device__ __forceinline__ void cvt(float* x) const {
 #pragma unroll
-        for (int u = 0; u < U; u++) {
+        for (int i = 0; i < NW; i++) {
             if constexpr (sizeof(TI) == 4) {
-                x[4 * u] = __uint_as_float(r[u].x); x[4 * u + 1] = __uint_as_float(r[u].y);
-                x[4 * u + 2] = __uint_as_float(r[u].z); x[4 * u + 3] = __uint_as_float(r[u].w);
+                x[i] = __uint_as_float(w[i]);
             } else {
-                const uint32_t w[4] = {r[u].x, r[u].y, r[u].z, r[u].w};
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    x[8 * u + 2 * k] = __uint_as_float(w[k] << 16);
-                    x[8 * u + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-                }
+                x[2 * i] = __uint_as_float(w[i] << 16);
+                x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
             }
         }
     }
@@ -533,8 +539,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
     auto tokrow = [&](int which, int s, int t, float* x) {
         if (s < GL) {
             RawTok<TI, DPK> r;
-#pragma unroll
-            for (int u = 0; u < RawTok<TI, DPK>::U; u++) r.r[u] = ltq[(s * 2 + which) * TU + dl * RawTok<TI, DPK>::U + u];
+            r.load(ltq + (s * 2 + which) * TU, (uint32_t)(dl * DPK * sizeof(TI)));
             r.cvt(x);
         } else {
             const TI* p = static_cast<const TI*>(which ? a.q : a.k);

@@ -133,8 +133,16 @@ def test_gen_scan_matches_oracle(case):
     run_case(*case)
 
 
-def test_gen_scan_bf16_tokens():
-    run_case(1, 48, 2, 64, 128, 128, 8, False, False, True, False, True, False, dtype=torch.bfloat16)
+BF16_CASES = [  # bf16 token rows: staged raw in LDS for a segment's first 8 steps, read from HBM after them
+    (1, 48, 2, 64, 128, 128, 8, False, False, True, False, True, False),    # 8-step segments, full row layout
+    (1, 70, 2, 100, 64, 128, 16, False, False, True, True, True, False),    # DK = 64 rows, 16-step segments, padded
+    (1, 40, 2, 192, 128, 64, 8, True, True, False, False, True, False),     # hard, detached, DK != DV, 192 rows
+]
+
+
+@pytest.mark.parametrize("case", BF16_CASES, ids=lambda c: "B{}T{}H{}N{}K{}V{}G{}h{}d{}f{}o{}q{}g{}".format(*c))
+def test_gen_scan_bf16_tokens(case):
+    run_case(*case, dtype=torch.bfloat16)
 
 
 def test_gen_scan_is_deterministic():
