@@ -392,7 +392,9 @@ def bench_window(args, W):
     view = lambda x: x.transpose(1, 2).requires_grad_()           # (B, T, H, D) viewed as (B, H, T, D)
     cq, ck, cv = view(rn(B, T, Hk, D)), view(rn(B, T, Hk, D)), view(rn(B, T, Hk, D))
     cq2 = view(rn(B, T, Hk * (NQ - 1), D))
-    do1, do2 = rn(B, Hk, T, D), rn(B, Hk * (NQ - 1), T, D)
+    # the upstream gradients arrive as the same kind of view: the caller transposes the window's output back
+    # and flattens it token-major (memlm_sh.py:485-486, 493-494)
+    do1, do2 = rn(B, T, Hk, D).transpose(1, 2), rn(B, T, Hk * (NQ - 1), D).transpose(1, 2)
     leaves = (cq, cq2, ck, cv)
 
     def step():

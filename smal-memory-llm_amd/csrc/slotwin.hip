@@ -17,12 +17,11 @@
 //             the score tile's D layout (the exponentials are rounded to bf16 unnormalised and the sum
 //             divides at the end).  V^T is gathered from value rows staged in LDS.  The log-sum-exp of
 //             every query is kept for the backward.
-//   dq        per query tile: S^T and dP^T = V dO^T as above, dS = P (dP - rowsum(dO o O)), dQ^T = K^T dS^T;
-//             it also stores rowsum(dO o O) for the key pass.
-//   dk, dv    per key tile, queries as the A rows: S and dP (queries x keys) for the two query tiles that
-//             see the keys, then dV^T = dO^T P and dK^T = Q^T dS, whose B operands are again the D layout.
-//             The query heads of a key/value head are summed in the kernel: no atomics, bitwise
-//             reproducible.
+//   backward  one pass per 128-key run: per key tile, queries as the A rows, S and dP (queries x keys) for
+//             the two query tiles that see the keys, dS = P (dP - rowsum(dO o O)), then dV^T = dO^T P and
+//             dK^T = Q^T dS, whose B operands are again the D layout; the dS tiles go through LDS transposed
+//             for dQ^T = K^T dS^T.  The query heads of a key/value head are summed in the kernel: no
+//             atomics, bitwise reproducible.
 #include "slot_common.h"
 #include "slotscan.h"
 #include "slotwin.h"
@@ -41,6 +40,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define WIN_THREADS (64 * WIN_WAVES)
 #define WIN_TILE (16 * WIN_WAVES)                    // query (or key) rows per workgroup
 #define WIN_STAGE (WIN_TILE + 16)                    // staged rows: the tile plus the 16 rows the band reaches
+#ifndef WIN_BWD_WAVES
+#define WIN_BWD_WAVES 8                              // backward: waves (16-key tiles) per workgroup
+#endif
 
 namespace {
 
@@ -90,11 +92,11 @@ struct WinArgs {
     float scale;
 };
 
-// stage rows [r0, r0 + WIN_STAGE) of head h of x (B, T, H, D) into s (zeros outside [0, T))
-template <int D, int ST>
+// stage rows [r0, r0 + NR) of head h of x (B, T, H, D) into s (zeros outside [0, T)), NT threads
+template <int D, int ST, int NR = WIN_STAGE, int NT = WIN_THREADS>
 __device__ __forceinline__ void stage_rows(bf16_t* s, const bf16_t* x, int b, int T, int H, int h, int r0, int tid) {
     constexpr int RU = D / 8;
-    for (int e = tid; e < WIN_STAGE * RU; e += WIN_THREADS) {
+    for (int e = tid; e < NR * RU; e += NT) {
         const int r = e / RU, cc = e - (e / RU) * RU, t = r0 + r;
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
         if (t >= 0 && t < T) v = ld16(x + (((size_t)b * T + t) * H + h) * D + cc * 8);
@@ -173,79 +175,37 @@ __global__ __launch_bounds__(WIN_THREADS) void win_fwd(WinArgs a) {
     if (qok && g == 0) a.lse_out[((size_t)b * Hq + hq) * T + tq] = mx + __logf(l);
 }
 
-// --------------------------------------------------------------------------------------- backward dq
-template <int D>
-__global__ __launch_bounds__(WIN_THREADS) void win_bwd_q(WinArgs a) {
-    constexpr int KK = D / 32, DT = D / 16, ST = D + 8;
-    __shared__ __align__(16) bf16_t sK[WIN_STAGE * ST];
-    const int T = a.T, Hq = a.Hq, Hk = a.Hk, W = a.W;
-    const int b = blockIdx.z, hq = blockIdx.y, hk = hq / (Hq / Hk);
-    const int t0 = blockIdx.x * WIN_TILE;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
-    stage_rows<D, ST>(sK, a.k, b, T, Hk, hk, t0 - 16, tid);
-    __syncthreads();
-    const int qt = t0 + 16 * w;
-    if (qt >= T) return;
-    const int tq = qt + c;
-    const bool qok = tq < T;
-    const size_t qrow = ((size_t)b * T + (qok ? tq : 0)) * Hq + hq;
-    uint4 qf[KK], df[KK];
-    float di = 0.f;                                    // rowsum(dO o O) of query tq, over this lane's dims
-#pragma unroll
-    for (int kk = 0; kk < KK; kk++) {
-        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-        qf[kk] = qok ? ld16(a.q + qrow * D + 32 * kk + 8 * g) : z;
-        df[kk] = qok ? ld16(a.dO + qrow * D + 32 * kk + 8 * g) : z;
-        di += dot8(df[kk], qok ? ld16(a.o + qrow * D + 32 * kk + 8 * g) : z);
-    }
-    di = sum4rows(di);
-    const float lq = qok ? a.lse[((size_t)b * Hq + hq) * T + tq] : 0.f;
-    uint2 dsf[2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int j = qt - 16 + 16 * u + c;
-        const bool jok = j >= 0 && j < T;
-        const size_t krow = ((size_t)b * T + (jok ? j : 0)) * Hk + hk;
-        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-            sa = mfma_k32(jok ? ld16(a.k + krow * D + 32 * kk + 8 * g) : z, qf[kk], sa);
-            pa = mfma_k32(jok ? ld16(a.v + krow * D + 32 * kk + 8 * g) : z, df[kk], pa);
-        }
-        float ds[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int jj = qt - 16 + 16 * u + 4 * g + i;
-            const float p = allowed(tq, jj, T, W) ? __expf(sa[i] * a.scale - lq) : 0.f;
-            ds[i] = p * (pa[i] - di);
-        }
-        dsf[u] = make_uint2(pack_bf16x2(ds[0], ds[1]), pack_bf16x2(ds[2], ds[3]));
-    }
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++) {
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < 2; u++) o = mfma_k16(gather4<ST>(sK, 16 * w + 16 * u + 4 * g, 16 * dt + c), dsf[u], o);
-        if (qok) st4bf(a.dq + qrow * D + 16 * dt + 4 * g, o[0] * a.scale, o[1] * a.scale, o[2] * a.scale, o[3] * a.scale);
-    }
-    if (qok && g == 0) a.dsum[((size_t)b * Hq + hq) * T + tq] = di;
-}
-
-// ----------------------------------------------------------------------------------- backward dk, dv
-template <int D>
-__global__ __launch_bounds__(WIN_THREADS) void win_bwd_kv(WinArgs a) {
-    constexpr int KK = D / 32, DT = D / 16, ST = D + 8;
-    __shared__ __align__(16) bf16_t sQ[WIN_STAGE * ST];
-    __shared__ __align__(16) bf16_t sD[WIN_STAGE * ST];
+// ------------------------------------------------------------------------------------ backward, one pass
+// One workgroup of NW waves per run of 16 NW keys [k0, k0 + 16 NW) of key/value head hk; wave w owns key tile
+// kt = k0 + 16 w and query tile kt (the same token rows).  Per query head of the group:
+//   stage   q and dout rows [k0, k0 + 16 NW + 16) (the query tiles kt and kt + 16 that see key tile kt), their
+//           log-sum-exp, and D = rowsum(dout o out), reduced across the 16-byte chunks of a row as the
+//           staging loads arrive;
+//   dk, dv  per wave and u in {0, 1}: S and dP (queries kt + 16 u x keys kt, queries as the A rows), P and
+//           dS, then dV^T += dO^T P and dK^T += Q^T dS (B operands = the D layout), summed over the heads;
+//   dq      every dS tile goes to LDS transposed (queries x keys, keys contiguous), so that dQ^T = K^T dS^T
+//           over key tiles kt - 16 and kt reads its B operand as one 8-byte load: wave w's own u = 0 tile
+//           and wave w - 1's u = 1 tile; wave 0 computes the pair (query tile k0, key tile k0 - 16) itself.
+// S and dP are computed once per (query tile, key tile) pair for all three gradients.
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
+    constexpr int NTH = 64 * NW, TILE = 16 * NW, STG = TILE + 16;   // threads, keys per workgroup, staged rows
+    constexpr int KK = D / 32, DT = D / 16, ST = D + 8, RU = D / 8;
+    constexpr int TS = 20;                             // transposed dS row (bf16): 10 dwords, 16 rows on 32 banks
+    __shared__ __align__(16) bf16_t sK[STG * ST];   // key rows [k0 - 16, k0 + 64)
+    __shared__ __align__(16) bf16_t sQ[STG * ST];   // query rows [k0, k0 + 80) of the current head
+    __shared__ __align__(16) bf16_t sD[STG * ST];   // dout rows, the same
+    __shared__ float sL[STG], sDs[STG];        // their log-sum-exp and rowsum(dout o out)
+    __shared__ __align__(16) bf16_t sT[NW + 1][2][16 * TS];   // dS tiles [query][key]; [WAVES] = wave 0's extra
     const int T = a.T, Hq = a.Hq, Hk = a.Hk, W = a.W, R = Hq / Hk;
     const int b = blockIdx.z, hk = blockIdx.y;
-    const int k0 = blockIdx.x * WIN_TILE;
+    const int k0 = blockIdx.x * TILE;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
-    const int kt = k0 + 16 * w;                        // this wave's key tile; lane column = key kt + c
-    const int j = kt + c;
+    const int kt = k0 + 16 * w;                        // this wave's key tile and query tile
+    const int j = kt + c;                              // lane column = key j (key/value pass)
     const bool jok = j < T;
     const size_t krow = ((size_t)b * T + (jok ? j : 0)) * Hk + hk;
+    stage_rows<D, ST, STG, NTH>(sK, a.k, b, T, Hk, hk, k0 - 16, tid);
     uint4 kb[KK], vb[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; kk++) {
@@ -256,18 +216,47 @@ __global__ __launch_bounds__(WIN_THREADS) void win_bwd_kv(WinArgs a) {
     f32x4 dkt[DT], dvt[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) dkt[dt] = dvt[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // the dS of query tile u (rows 4 g + i) against this lane's key column, into the transposed tile
+    auto put_ds = [&](bf16_t* tile, const float* ds) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) tile[(4 * g + i) * TS + c] = f2bf(ds[i]);
+    };
     for (int r = 0; r < R; r++) {
         const int hq = hk * R + r;
-        __syncthreads();                               // the previous head's staged rows are consumed
-        stage_rows<D, ST>(sQ, a.q, b, T, Hq, hq, k0, tid);
-        stage_rows<D, ST>(sD, a.dO, b, T, Hq, hq, k0, tid);
-        __syncthreads();
-        if (kt >= T) continue;
         const float* lse = a.lse + ((size_t)b * Hq + hq) * T;
-        const float* dsm = a.dsum + ((size_t)b * Hq + hq) * T;
+        __syncthreads();                               // the previous head's staged rows and dS tiles are consumed
+        stage_rows<D, ST, STG, NTH>(sQ, a.q, b, T, Hq, hq, k0, tid);
+        // dout rows, and D as they arrive: the RU chunks of a row are RU consecutive lanes of one DPP row, and
+        // every lane runs every pass (whole rows past the staged range only compute zeros)
+        constexpr int NIT = (STG * RU + NTH - 1) / NTH;
 #pragma unroll
-        for (int u = 0; u < 2; u++) {                  // query tile u: queries kt + 16 u + (0..15), A rows
-            const int rq = 16 * w + 16 * u;            // its first staged row
+        for (int it = 0; it < NIT; it++) {
+            const int e = tid + NTH * it;
+            const bool ev = e < STG * RU;
+            const int rr = e / RU, cc = e - (e / RU) * RU, t = k0 + rr;
+            uint4 dv = make_uint4(0u, 0u, 0u, 0u), ov = dv;
+            if (ev && t < T) {
+                const size_t x = (((size_t)b * T + t) * Hq + hq) * D + cc * 8;
+                dv = ld16(a.dO + x);
+                ov = ld16(a.o + x);
+            }
+            if (ev) *reinterpret_cast<uint4*>(sD + rr * ST + cc * 8) = dv;
+            float di = dot8(dv, ov);
+            di += dppf<SLOT_DPP_XOR1>(di);
+            di += dppf<SLOT_DPP_XOR2>(di);
+            di += dppf<SLOT_DPP_HMIR>(di);
+            if constexpr (RU == 16) di += dppf<SLOT_DPP_MIR>(di);
+            if (ev && cc == 0) {
+                sDs[rr] = di;
+                if (rr < TILE && t < T) a.dsum[((size_t)b * Hq + hq) * T + t] = di;
+            }
+        }
+        if (tid < STG) sL[tid] = k0 + tid < T ? lse[k0 + tid] : 0.f;
+        __syncthreads();
+        // ---- S, dP per (query tile kt + 16 u, key tile kt); dk, dv; dS tiles for dq
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int rq = 16 * w + 16 * u;            // the query tile's first staged row
             f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < KK; kk++) {
@@ -279,9 +268,8 @@ __global__ __launch_bounds__(WIN_THREADS) void win_bwd_kv(WinArgs a) {
             for (int i = 0; i < 4; i++) {              // query kt + 16 u + 4 g + i, key j
                 const int tq = kt + 16 * u + 4 * g + i;
                 const bool ok = allowed(tq, j, T, W);
-                const float lq = ok ? lse[tq] : 0.f, dq = ok ? dsm[tq] : 0.f;
-                p[i] = ok ? __expf(sa[i] * a.scale - lq) : 0.f;
-                ds[i] = p[i] * (pa[i] - dq);
+                p[i] = ok ? __expf(sa[i] * a.scale - sL[rq + 4 * g + i]) : 0.f;
+                ds[i] = p[i] * (pa[i] - sDs[rq + 4 * g + i]);
             }
             const uint2 pB = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
             const uint2 dB = make_uint2(pack_bf16x2(ds[0], ds[1]), pack_bf16x2(ds[2], ds[3]));
@@ -290,9 +278,48 @@ __global__ __launch_bounds__(WIN_THREADS) void win_bwd_kv(WinArgs a) {
                 dvt[dt] = mfma_k16(gather4<ST>(sD, rq + 4 * g, 16 * dt + c), pB, dvt[dt]);
                 dkt[dt] = mfma_k16(gather4<ST>(sQ, rq + 4 * g, 16 * dt + c), dB, dkt[dt]);
             }
+            put_ds(&sT[w][u][0], ds);
+        }
+        if (w == 0) {                                  // query tile k0 against key tile k0 - 16 (dq only)
+            const int jx = k0 - 16 + c;
+            const bool jxok = jx >= 0;
+            const size_t vrow = ((size_t)b * T + (jxok ? jx : 0)) * Hk + hk;
+            f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+                const uint4 kx = ld16(sK + c * ST + 32 * kk + 8 * g);   // staged rows 0..15 = keys k0 - 16..
+                const uint4 vx = jxok ? ld16(a.v + vrow * D + 32 * kk + 8 * g) : make_uint4(0u, 0u, 0u, 0u);
+                sa = mfma_k32(ld16(sQ + c * ST + 32 * kk + 8 * g), kx, sa);
+                pa = mfma_k32(ld16(sD + c * ST + 32 * kk + 8 * g), vx, pa);
+            }
+            float ds[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tq = k0 + 4 * g + i;
+                const bool ok = allowed(tq, jx, T, W);
+                const float p = ok ? __expf(sa[i] * a.scale - sL[4 * g + i]) : 0.f;
+                ds[i] = p * (pa[i] - sDs[4 * g + i]);
+            }
+            put_ds(&sT[NW][1][0], ds);
+        }
+        __syncthreads();
+        // ---- dQ^T (dims x queries of tile kt) = K^T dS^T over key tiles kt - 16 and kt
+        const int tq = kt + c;
+        const bool qok = tq < T;
+        const bf16_t* t0p = w > 0 ? &sT[w - 1][1][0] : &sT[NW][1][0];
+        const bf16_t* t1p = &sT[w][0][0];
+        const uint2 b0 = *reinterpret_cast<const uint2*>(t0p + c * TS + 4 * g);
+        const uint2 b1 = *reinterpret_cast<const uint2*>(t1p + c * TS + 4 * g);
+        const size_t qrow = ((size_t)b * T + (qok ? tq : 0)) * Hq + hq;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            f32x4 o = {0.f, 0.f, 0.f, 0.f};
+            o = mfma_k16(gather4<ST>(sK, 16 * w + 4 * g, 16 * dt + c), b0, o);
+            o = mfma_k16(gather4<ST>(sK, 16 * w + 16 + 4 * g, 16 * dt + c), b1, o);
+            if (qok) st4bf(a.dq + qrow * D + 16 * dt + 4 * g, o[0] * a.scale, o[1] * a.scale, o[2] * a.scale, o[3] * a.scale);
         }
     }
-    if (!jok || kt >= T) return;
+    if (!jok) return;
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) {
         st4bf(a.dk + krow * D + 16 * dt + 4 * g, dkt[dt][0] * a.scale, dkt[dt][1] * a.scale, dkt[dt][2] * a.scale,
@@ -346,20 +373,13 @@ extern "C" int slotwin_bwd(const void* q, const void* k, const void* v, const vo
     hipStream_t st = (hipStream_t)stream;
     WinArgs a{(const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, (const bf16_t*)out, lse, (const bf16_t*)dout,
               nullptr, nullptr, (bf16_t*)dq, (bf16_t*)dk, (bf16_t*)dv, dsum, (int)T, (int)Hq, (int)Hk, (int)W, scale};
-    const unsigned nt = (unsigned)((T + WIN_TILE - 1) / WIN_TILE);
+    const unsigned nt = (unsigned)((T + 16 * WIN_BWD_WAVES - 1) / (16 * WIN_BWD_WAVES));
     hipError_t e;
     {
         slothost::Scope sc(SLOTSCAN_K_WIN_BWD, st);
-        if (D == 128) slothost::launch(win_bwd_q<128>, dim3(nt, (unsigned)Hq, (unsigned)B), dim3(WIN_THREADS), 0, st, a);
-        else slothost::launch(win_bwd_q<64>, dim3(nt, (unsigned)Hq, (unsigned)B), dim3(WIN_THREADS), 0, st, a);
+        if (D == 128) slothost::launch(win_bwd<128, WIN_BWD_WAVES>, dim3(nt, (unsigned)Hk, (unsigned)B), dim3(64 * WIN_BWD_WAVES), 0, st, a);
+        else slothost::launch(win_bwd<64, WIN_BWD_WAVES>, dim3(nt, (unsigned)Hk, (unsigned)B), dim3(64 * WIN_BWD_WAVES), 0, st, a);
         e = hipGetLastError();
     }
-    if (e != hipSuccess) return hip_fail(e, "win_bwd_q launch");
-    {
-        slothost::Scope sc(SLOTSCAN_K_WIN_BWD, st);
-        if (D == 128) slothost::launch(win_bwd_kv<128>, dim3(nt, (unsigned)Hk, (unsigned)B), dim3(WIN_THREADS), 0, st, a);
-        else slothost::launch(win_bwd_kv<64>, dim3(nt, (unsigned)Hk, (unsigned)B), dim3(WIN_THREADS), 0, st, a);
-        e = hipGetLastError();
-    }
-    return e == hipSuccess ? 0 : hip_fail(e, "win_bwd_kv launch");
+    return e == hipSuccess ? 0 : hip_fail(e, "win_bwd launch");
 }
