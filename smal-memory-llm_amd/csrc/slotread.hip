@@ -423,7 +423,8 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
             __builtin_amdgcn_sched_barrier(0);                    // bound the operand prefetch window
         }
         // scores in the log2 domain, u = raw * kinv * scale * log2(e) (+ -inf for an invalid slot), so that
-        // exp(s - max s) = exp2(u - max u): 9 VALU operations per score
+        // exp(s - max s) = exp2(u - max u) is one v_exp_f32 (the library exp2f adds a range fix-up of five
+        // more VALU operations for results below 2^-126, far below what the bf16 output resolves)
         float sc[WIDE_NP / 16][4];
         float mx = -INFINITY;
         const float scl2 = scl * LOG2E_F;
@@ -447,7 +448,7 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
         for (int nt = 0; nt < WIDE_NP / 16; nt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float e = exp2f(sc[nt][i] - mxs);
+                const float e = __builtin_amdgcn_exp2f(sc[nt][i] - mxs);
                 sc[nt][i] = e;
                 sum += e;
             }
