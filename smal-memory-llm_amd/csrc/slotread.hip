@@ -90,7 +90,7 @@ struct ReadSmem {
 };
 
 template <int D>
-__global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
+__global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void read_fwd(ReadFwdArgs a) {
     constexpr int KK = D / 32;
     constexpr int DT = D / 16;
     constexpr int VST = ReadSmem<D>::VST;
@@ -118,6 +118,22 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
     const bf16_t* Vb = a.vb + (size_t)slab * N * D;
     const float* KI = a.kinv + (size_t)slab * N;
     const uint8_t* VA = a.valid + (size_t)slab * N;
+
+    // the first query tile's B operand and sharpness, issued before the slab's loads so that its latency
+    // overlaps theirs (a block's queries usually fit one tile)
+    auto load_q = [&](int m0, uint4* qf, float& scl) {
+        const int m = m0 + c;
+        const bool mok = m < mhi;
+        size_t qrow = 0;
+        if (mok) qrow = (((size_t)b * a.T + t0 + m / a.NQ) * a.H + h) * a.NQ + (m % a.NQ);
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++)
+            qf[kk] = mok ? *reinterpret_cast<const uint4*>(a.q + qrow * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
+        scl = mok ? a.scale[qrow] : 0.f;
+    };
+    uint4 qn[KK];
+    float scn;
+    load_q(mlo, qn, scn);
 
     // ---- this wave's keys (A operand of the score product), kinv and validity, values (A of the output)
     uint4 kf[READ_TPW][KK];
@@ -147,24 +163,26 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
     }
     bf16_t* sV = reinterpret_cast<bf16_t*>(s_big) + w * (READ_TPW * 16 * VST);
     {
-        // fixed trip count, fully unrolled: all of this wave's value loads are in flight together
-        constexpr int CH = READ_TPW * 16 * (D / 8) / 64;            // 16-byte chunks per lane
+        // this wave's value rows straight into its LDS rows (direct global -> LDS loads, no data registers):
+        // 16-byte chunk L of the padded region is row L / CPR, chunk L % CPR; the pad chunk is not written,
+        // and rows past N or past this wave's tiles get zeros from an ordinary LDS store (the V^T tiles read
+        // all READ_TPW tiles)
+        constexpr int CPR = VST * 2 / 16;                           // 16-byte chunks per padded row
+        constexpr int NI = (READ_TPW * 16 * CPR + 63) / 64;         // load instructions for the whole region
         const int nbase = w * TPW * 16;
         const int rows = TPW * 16;
-        uint4 x[CH];
+        const unsigned l0 = lds_addr(sV);
 #pragma unroll
-        for (int it = 0; it < CH; it++) {
+        for (int it = 0; it < NI; it++) {
             const int e = lane + 64 * it;
-            const int r = e / (D / 8), cc = e % (D / 8);
+            const int r = e / CPR, cc = e - (e / CPR) * CPR;
             const int n = nbase + r;
-            x[it] = (r < rows && n < N) ? *reinterpret_cast<const uint4*>(Vb + (size_t)n * D + cc * 8) : make_uint4(0, 0, 0, 0);
+            if (r < READ_TPW * 16 && cc < D / 8) {
+                if (r < rows && n < N) dma16(Vb + (size_t)n * D + cc * 8, l0 + 1024u * it);
+                else *reinterpret_cast<uint4*>(sV + r * VST + cc * 8) = make_uint4(0, 0, 0, 0);
+            }
         }
-#pragma unroll
-        for (int it = 0; it < CH; it++) {
-            const int e = lane + 64 * it;
-            const int r = e / (D / 8), cc = e % (D / 8);
-            *reinterpret_cast<uint4*>(sV + r * VST + cc * 8) = x[it];
-        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");           // the direct loads are not tracked
     }
     wave_lds_sync();
     uint2 vf[READ_TPW][DT];                                      // V^T tile: row = dim 16dt + c, k = slot 4g + i
@@ -179,16 +197,12 @@ __global__ __launch_bounds__(READ_THREADS) void read_fwd(ReadFwdArgs a) {
 
     float* sO = reinterpret_cast<float*>(s_big);
     for (int m0 = mlo; m0 < mhi; m0 += 16) {
-        // ---- queries of this tile: B operand, lane column = query m0 + c
-        const int m = m0 + c;
-        const bool mok = m < mhi;
-        size_t qrow = 0;
-        if (mok) qrow = (((size_t)b * a.T + t0 + m / a.NQ) * a.H + h) * a.NQ + (m % a.NQ);
+        // ---- queries of this tile: B operand, lane column = query m0 + c (the next tile's in flight)
         uint4 qf[KK];
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++)
-            qf[kk] = mok ? *reinterpret_cast<const uint4*>(a.q + qrow * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
-        const float scl = mok ? a.scale[qrow] : 0.f;
+        for (int kk = 0; kk < KK; kk++) qf[kk] = qn[kk];
+        const float scl = scn;
+        if (m0 + 16 < mhi) load_q(m0 + 16, qn, scn);
 
         f32x4 acc[READ_TPW];
 #pragma unroll
