@@ -117,26 +117,31 @@ __global__ __launch_bounds__(WIN_THREADS) void win_fwd(WinArgs a) {
     const int b = blockIdx.z, hq = blockIdx.y, hk = hq / (Hq / Hk);
     const int t0 = blockIdx.x * WIN_TILE;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
-    stage_rows<D, ST>(sV, a.v, b, T, Hk, hk, t0 - 16, tid);
-    __syncthreads();
+    // this wave's query and key operands first, so that their latency overlaps the value staging's
     const int qt = t0 + 16 * w;
-    if (qt >= T) return;                              // no barrier follows
     const int tq = qt + c;                            // this lane's query column
     const bool qok = tq < T;
     const bf16_t* qrow = a.q + (((size_t)b * T + (qok ? tq : 0)) * Hq + hq) * D;
-    uint4 qf[KK];
+    uint4 qf[KK], kf[2][KK];
 #pragma unroll
     for (int kk = 0; kk < KK; kk++) qf[kk] = qok ? ld16(qrow + 32 * kk + 8 * g) : make_uint4(0u, 0u, 0u, 0u);
-    f32x4 acc[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {                      // key tile u: keys qt - 16 + 16 u + (0..15)
         const int j = qt - 16 + 16 * u + c;
         const bool jok = j >= 0 && j < T;
         const bf16_t* krow = a.k + (((size_t)b * T + (jok ? j : 0)) * Hk + hk) * D;
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) kf[u][kk] = jok ? ld16(krow + 32 * kk + 8 * g) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    stage_rows<D, ST>(sV, a.v, b, T, Hk, hk, t0 - 16, tid);
+    __syncthreads();
+    if (qt >= T) return;                              // no barrier follows
+    f32x4 acc[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
         acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++)
-            acc[u] = mfma_k32(jok ? ld16(krow + 32 * kk + 8 * g) : make_uint4(0u, 0u, 0u, 0u), qf[kk], acc[u]);
+        for (int kk = 0; kk < KK; kk++) acc[u] = mfma_k32(kf[u][kk], qf[kk], acc[u]);
     }
     // band softmax of query column tq: lane (c, g) holds keys qt - 16 + 16 u + 4 g + i
     float s[2][4];
