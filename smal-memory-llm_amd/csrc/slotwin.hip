@@ -10,13 +10,15 @@
 // from (memlm_sh.py:482-484).  W <= 16, so a 16-query tile sees at most two 16-key tiles.
 //
 // gfx950 mapping.  One wave per 16-row tile, 4 waves per workgroup:
-//   forward   S^T (keys x queries) = K Q^T with v_mfma_f32_16x16x32_bf16 (keys as the A rows, queries as
-//             the B columns, D/32 k-steps) for the two key tiles; the D layout puts one query column in
-//             every lane (4 keys per lane per tile), so the band softmax is 8 values per lane and one
-//             cross-row reduction; O^T = V^T P^T with v_mfma_f32_16x16x16_bf16, whose B operand is exactly
-//             the score tile's D layout (the exponentials are rounded to bf16 unnormalised and the sum
-//             divides at the end).  V^T is gathered from value rows staged in LDS.  The log-sum-exp of
-//             every query is kept for the backward.
+//   forward   per 64-token tile and key/value head, the staged values and each wave's key operands serve
+//             every query head of the group; S^T (keys x queries) = K Q^T with v_mfma_f32_16x16x32_bf16
+//             (keys as the A rows, queries as the B columns, D/32 k-steps) for the two key tiles; the D
+//             layout puts one query column in every lane (4 keys per lane per tile), so the band softmax
+//             is 8 values per lane and one cross-row reduction; O^T = V^T P^T with
+//             v_mfma_f32_16x16x16_bf16, whose B operand is exactly the score tile's D layout (the
+//             exponentials are rounded to bf16 unnormalised and the sum divides at the end).  V^T is
+//             gathered from value rows staged in LDS.  The log-sum-exp of every query is kept for the
+//             backward.
 //   backward  one pass per 128-key run: per key tile, queries as the A rows, S and dP (queries x keys) for
 //             the two query tiles that see the keys, dS = P (dP - rowsum(dO o O)), then dV^T = dO^T P and
 //             dK^T = Q^T dS, whose B operands are again the D layout; the dS tiles go through LDS transposed
@@ -113,18 +115,22 @@ template <int D>
 __global__ __launch_bounds__(WIN_THREADS) void win_fwd(WinArgs a) {
     constexpr int KK = D / 32, DT = D / 16, ST = D + 8;
     __shared__ __align__(16) bf16_t sV[WIN_STAGE * ST];
-    const int T = a.T, Hq = a.Hq, Hk = a.Hk, W = a.W;
-    const int b = blockIdx.z, hq = blockIdx.y, hk = hq / (Hq / Hk);
+    const int T = a.T, Hq = a.Hq, Hk = a.Hk, W = a.W, R = Hq / Hk;
+    const int b = blockIdx.z, hk = blockIdx.y;        // every query head of key/value head hk
     const int t0 = blockIdx.x * WIN_TILE;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
-    // this wave's query and key operands first, so that their latency overlaps the value staging's
+    // this wave's first query and key operands first, so that their latency overlaps the value staging's;
+    // the keys and staged values serve every query head of the group
     const int qt = t0 + 16 * w;
     const int tq = qt + c;                            // this lane's query column
     const bool qok = tq < T;
-    const bf16_t* qrow = a.q + (((size_t)b * T + (qok ? tq : 0)) * Hq + hq) * D;
-    uint4 qf[KK], kf[2][KK];
+    const size_t qrow0 = ((size_t)b * T + (qok ? tq : 0)) * Hq + hk * R;    // (b, tq, first head of the group)
+    auto load_q = [&](int r, uint4* qf) {
 #pragma unroll
-    for (int kk = 0; kk < KK; kk++) qf[kk] = qok ? ld16(qrow + 32 * kk + 8 * g) : make_uint4(0u, 0u, 0u, 0u);
+        for (int kk = 0; kk < KK; kk++) qf[kk] = qok ? ld16(a.q + (qrow0 + r) * D + 32 * kk + 8 * g) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    uint4 qn[KK], kf[2][KK];
+    load_q(0, qn);
 #pragma unroll
     for (int u = 0; u < 2; u++) {                      // key tile u: keys qt - 16 + 16 u + (0..15)
         const int j = qt - 16 + 16 * u + c;
@@ -136,48 +142,55 @@ __global__ __launch_bounds__(WIN_THREADS) void win_fwd(WinArgs a) {
     stage_rows<D, ST>(sV, a.v, b, T, Hk, hk, t0 - 16, tid);
     __syncthreads();
     if (qt >= T) return;                              // no barrier follows
-    f32x4 acc[2];
+    for (int r = 0; r < R; r++) {
+        const int hq = hk * R + r;
+        uint4 qf[KK];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-        acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < KK; kk++) qf[kk] = qn[kk];
+        if (r + 1 < R) load_q(r + 1, qn);             // the next head's queries in flight
+        f32x4 acc[2];
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) acc[u] = mfma_k32(kf[u][kk], qf[kk], acc[u]);
-    }
-    // band softmax of query column tq: lane (c, g) holds keys qt - 16 + 16 u + 4 g + i
-    float s[2][4];
-    float mx = -INFINITY;
+        for (int u = 0; u < 2; u++) {
+            acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 2; u++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int j = qt - 16 + 16 * u + 4 * g + i;
-            s[u][i] = allowed(tq, j, T, W) ? acc[u][i] * a.scale : -INFINITY;
-            mx = fmaxf(mx, s[u][i]);
+            for (int kk = 0; kk < KK; kk++) acc[u] = mfma_k32(kf[u][kk], qf[kk], acc[u]);
         }
-    mx = max4rows(mx);
-    float l = 0.f;
+        // band softmax of query column tq: lane (c, g) holds keys qt - 16 + 16 u + 4 g + i
+        float s[2][4];
+        float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 2; u++)
+        for (int u = 0; u < 2; u++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float e = s[u][i] == -INFINITY ? 0.f : __expf(s[u][i] - mx);
-            s[u][i] = e;
-            l += e;
+            for (int i = 0; i < 4; i++) {
+                const int j = qt - 16 + 16 * u + 4 * g + i;
+                s[u][i] = allowed(tq, j, T, W) ? acc[u][i] * a.scale : -INFINITY;
+                mx = fmaxf(mx, s[u][i]);
+            }
+        mx = max4rows(mx);
+        float l = 0.f;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float e = s[u][i] == -INFINITY ? 0.f : __expf(s[u][i] - mx);
+                s[u][i] = e;
+                l += e;
+            }
+        l = sum4rows(l);
+        uint2 pf[2];                                   // bf16 exponentials: the B operand (k = key, col = query)
+#pragma unroll
+        for (int u = 0; u < 2; u++) pf[u] = make_uint2(pack_bf16x2(s[u][0], s[u][1]), pack_bf16x2(s[u][2], s[u][3]));
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        bf16_t* orow = a.out + (qrow0 + r) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 2; u++) o = mfma_k16(gather4<ST>(sV, 16 * w + 16 * u + 4 * g, 16 * dt + c), pf[u], o);
+            if (qok) st4bf(orow + 16 * dt + 4 * g, o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
         }
-    l = sum4rows(l);
-    uint2 pf[2];                                       // bf16 exponentials: the B operand (k = key, col = query)
-#pragma unroll
-    for (int u = 0; u < 2; u++) pf[u] = make_uint2(pack_bf16x2(s[u][0], s[u][1]), pack_bf16x2(s[u][2], s[u][3]));
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    bf16_t* orow = a.out + (((size_t)b * T + (qok ? tq : 0)) * Hq + hq) * D;
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++) {
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < 2; u++) o = mfma_k16(gather4<ST>(sV, 16 * w + 16 * u + 4 * g, 16 * dt + c), pf[u], o);
-        if (qok) st4bf(orow + 16 * dt + 4 * g, o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+        if (qok && g == 0) a.lse_out[((size_t)b * Hq + hq) * T + tq] = mx + __logf(l);
     }
-    if (qok && g == 0) a.lse_out[((size_t)b * Hq + hq) * T + tq] = mx + __logf(l);
 }
 
 // ------------------------------------------------------------------------------------ backward, one pass
@@ -355,7 +368,7 @@ extern "C" int slotwin_fwd(const void* q, const void* k, const void* v, int64_t 
     hipStream_t st = (hipStream_t)stream;
     WinArgs a{(const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, nullptr, nullptr, nullptr,
               (bf16_t*)out, lse, nullptr, nullptr, nullptr, nullptr, (int)T, (int)Hq, (int)Hk, (int)W, scale};
-    const dim3 grid((unsigned)((T + WIN_TILE - 1) / WIN_TILE), (unsigned)Hq, (unsigned)B), block(WIN_THREADS);
+    const dim3 grid((unsigned)((T + WIN_TILE - 1) / WIN_TILE), (unsigned)Hk, (unsigned)B), block(WIN_THREADS);
     hipError_t e;
     {
         slothost::Scope sc(SLOTSCAN_K_WIN_FWD, st);
