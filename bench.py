@@ -600,6 +600,8 @@ def bench_read(args, W):
         "roofline": {"bound": "hbm", "kernel": "read_fwd", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic(args.workload).get("read_fwd"),
+                     "traffic_source": f"profiles/hbm_traffic_{args.workload}.md: committed rocprofv3 FETCH_SIZE and "
+                                       "WRITE_SIZE passes, not measured in this run",
                      "algorithmic_bytes_per_launch": by, "avg_launch_ms": round(kms, 4),
                      "mfma_tflops": round(fl / (kms * 1e-3) / 1e12, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
                      "mfma_frac": round(fl / (kms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
@@ -741,6 +743,8 @@ def main():
                            ", occ_bin, per-token fr", "tokens_per_step": tokens},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "traffic_source": (f"profiles/hbm_traffic_{args.workload}.md: committed rocprofv3 FETCH_SIZE and "
+                                        "WRITE_SIZE passes, not measured in this run") if traffic else None,
                      "algorithmic_bytes_per_launch": launch_bytes[dom],
                      "avg_launch_ms": round(dom_ms, 4), "timed_launches": dom_cnt},
         "step_roofline": {"algorithmic_bytes": step_bytes,
