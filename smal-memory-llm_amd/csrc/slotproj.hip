@@ -215,7 +215,7 @@ __global__ __launch_bounds__(PTHREADS) void proj_gemm(ProjArgs p) {
     stage_barrier();
     auto epilogue = [&](auto with_delta) {
         constexpr int CH = PT * PT * 2 / 16 / PTHREADS;   // 16-byte chunks per thread (32)
-        constexpr int BATCH = 8;
+        constexpr int BATCH = 16;
 #pragma unroll
         for (int b0 = 0; b0 < CH; b0 += BATCH) {
             uint4 dv[BATCH];
