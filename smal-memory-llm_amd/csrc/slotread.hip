@@ -552,7 +552,7 @@ __device__ __forceinline__ uint2 gather4(const bf16_t* p, int stride) {
 }
 
 template <int D, bool ACC>
-__global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
+__global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(ACC ? 1 : 3))) void read_bwd(ReadBwdArgs a) {
     constexpr int KK = D / 32;
     constexpr int DT = D / 16;
     constexpr int TST = ReadBwdSmem<D>::TST;
@@ -609,6 +609,39 @@ __global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) { acc_dk[u][dt] = f32x4{0.f, 0.f, 0.f, 0.f}; acc_dv[u][dt] = f32x4{0.f, 0.f, 0.f, 0.f}; }
     }
+
+    // The dK / dV output rows of this wave's slots, one matrix and PD dims per pass (64 at D = 128, 32 at
+    // D = 64: what the wave's rows of s_part hold): the D layout of a (slot tile u, dim tile dt) fragment
+    // (row dim 16dt + 4g + i, column slot 16nt + c, so 4 consecutive dims of one slot per lane) goes to LDS as
+    // row-major bf16, PD * 2 bytes per slot with the 8-byte pieces XOR-swizzled by the row, and comes back as
+    // whole 16-byte pieces of each row, so that the stores fill whole lines (8-byte stores of 16 rows per
+    // instruction had cost half the kernel).  frag(u, dt) gives the fragment; the caller owns s_part.
+    constexpr int PD = READ_TPW * 16 * 128 <= 16 * OST * 4 ? 64 : 32;
+    constexpr int RB = 2 * PD, S8 = RB / 8, C16 = RB / 16;   // row bytes, 8-byte slots, 16-byte chunks
+    static_assert(READ_TPW * 16 * RB <= 16 * OST * 4, "a pass fits the wave's partial rows");
+    unsigned char* tw = reinterpret_cast<unsigned char*>(s_part + w * 16 * OST);
+    auto emit_rows = [&](bf16_t* dst, int hf, auto frag) {
+#pragma unroll
+        for (int dd = 0; dd < PD / 16; dd++) {
+#pragma unroll
+            for (int u = 0; u < READ_TPW; u++) {              // tiles past N carry zero draw and P
+                const f32x4 r = frag(u, (PD / 16) * hf + dd);
+                const int row = u * 16 + c, s8 = 4 * dd + g;
+                *reinterpret_cast<uint2*>(tw + row * RB + 8 * (s8 ^ (row & (S8 - 1)))) =
+                    make_uint2(pack2(r[0], r[1]), pack2(r[2], r[3]));
+            }
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int k = 0; k < READ_TPW * 16 * C16 / 64; k++) {
+            const int idx = 64 * k + lane, row = idx / C16, ch = idx % C16, x = row & (S8 - 1);
+            uint4 v = *reinterpret_cast<const uint4*>(tw + row * RB + 16 * (ch ^ (x >> 1)));
+            if (x & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+            const int n = w * TPW * 16 + row;
+            if (row < TPW * 16 && n < N) *reinterpret_cast<uint4*>(dst + (size_t)n * D + PD * hf + 8 * ch) = v;
+        }
+        wave_lds_sync();                                      // the reads are done before the next pass writes
+    };
 
     for (int m0 = 0; m0 < Mblk; m0 += 16) {
         // ---- (a) the 16-query tile of Q and dO, and the multipliers, into LDS
@@ -760,30 +793,31 @@ __global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
             for (int i = 0; i < 4; i++) s_dsc[w][4 * g + i] = dsl[i];
         }
         // ---- (d) dK^T = Q^T draw and dV^T = dO^T P, per (slot tile, dim tile)
+        if constexpr (ACC) {
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            const uint2 qT = gather4(s_q + (4 * g) * TST + dt * 16 + c, TST);    // A: row dim 16dt + c, k = query 4g + i
-            const uint2 dT = gather4(s_do + (4 * g) * TST + dt * 16 + c, TST);
+            for (int dt = 0; dt < DT; dt++) {
+                const uint2 qT = gather4(s_q + (4 * g) * TST + dt * 16 + c, TST);    // A: row dim 16dt + c, k = query 4g + i
+                const uint2 dT = gather4(s_do + (4 * g) * TST + dt * 16 + c, TST);
 #pragma unroll
-            for (int u = 0; u < READ_TPW; u++) {                // tiles past N carry zero draw and P
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                if constexpr (ACC) {
+                for (int u = 0; u < READ_TPW; u++) {            // tiles past N carry zero draw and P
                     acc_dk[u][dt] = mfma_k16(qT, drB[u], acc_dk[u][dt]);
                     acc_dv[u][dt] = mfma_k16(dT, pB[u], acc_dv[u][dt]);
-                } else {
-                    const f32x4 gk = mfma_k16(qT, drB[u], z);
-                    const f32x4 gv = mfma_k16(dT, pB[u], z);
-                    // D layout: row dim 16dt + 4g + i, column slot 16 nt + c -> 4 consecutive dims of one slot
-                    const int n = (w * TPW + u) * 16 + c;
-                    if (tile[u] && n < N) {
-                        uint2 xk, xv;
-                        xk.x = pack2(gk[0], gk[1]); xk.y = pack2(gk[2], gk[3]);
-                        xv.x = pack2(gv[0], gv[1]); xv.y = pack2(gv[2], gv[3]);
-                        *reinterpret_cast<uint2*>(dKb + (size_t)n * D + dt * 16 + 4 * g) = xk;
-                        *reinterpret_cast<uint2*>(dVb + (size_t)n * D + dt * 16 + 4 * g) = xv;
-                    }
                 }
             }
+        } else {
+            // one matrix and PD dims per pass through the wave's rows of s_part (free until (e))
+#pragma unroll
+            for (int hf = 0; hf < D / PD; hf++)
+                emit_rows(dKb, hf, [&](int u, int dt) {
+                    const uint2 aT = gather4(s_q + (4 * g) * TST + dt * 16 + c, TST);   // A: row dim 16dt + c, k = query
+                    return mfma_k16(aT, drB[u], f32x4{0.f, 0.f, 0.f, 0.f});
+                });
+#pragma unroll
+            for (int hf = 0; hf < D / PD; hf++)
+                emit_rows(dVb, hf, [&](int u, int dt) {
+                    const uint2 aT = gather4(s_do + (4 * g) * TST + dt * 16 + c, TST);
+                    return mfma_k16(aT, pB[u], f32x4{0.f, 0.f, 0.f, 0.f});
+                });
         }
         // ---- (e) dQ^T partial = K^T draw^T over this wave's slots
         bf16_t* dr_t = s_dr[w];
@@ -876,19 +910,11 @@ __global__ __launch_bounds__(READ_THREADS) void read_bwd(ReadBwdArgs a) {
         if (tile[u] && g == 0 && n < N) a.dkinv[(size_t)slab * N + n] = v;
     }
     if constexpr (ACC) {
+        __syncthreads();                                      // every wave's reads of the last partials are done
 #pragma unroll
-        for (int u = 0; u < READ_TPW; u++) {
-            const int n = (w * TPW + u) * 16 + c;
-            if (!tile[u] || n >= N) continue;
+        for (int hf = 0; hf < D / PD; hf++) emit_rows(dKb, hf, [&](int u, int dt) { return acc_dk[u][dt]; });
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                uint2 xk, xv;
-                xk.x = pack2(acc_dk[u][dt][0], acc_dk[u][dt][1]); xk.y = pack2(acc_dk[u][dt][2], acc_dk[u][dt][3]);
-                xv.x = pack2(acc_dv[u][dt][0], acc_dv[u][dt][1]); xv.y = pack2(acc_dv[u][dt][2], acc_dv[u][dt][3]);
-                *reinterpret_cast<uint2*>(dKb + (size_t)n * D + dt * 16 + 4 * g) = xk;
-                *reinterpret_cast<uint2*>(dVb + (size_t)n * D + dt * 16 + 4 * g) = xv;
-            }
-        }
+        for (int hf = 0; hf < D / PD; hf++) emit_rows(dVb, hf, [&](int u, int dt) { return acc_dv[u][dt]; });
     }
 }
 
