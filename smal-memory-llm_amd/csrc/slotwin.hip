@@ -73,8 +73,37 @@ __device__ __forceinline__ uint2 gather4(const bf16_t* s, int r, int col) {
     x.y = (uint32_t)p[2 * ST] | ((uint32_t)p[3 * ST] << 16);
     return x;
 }
-__device__ __forceinline__ void st4bf(bf16_t* p, float a0, float a1, float a2, float a3) {
-    *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(a0, a1), pack_bf16x2(a2, a3));
+// Wave-local LDS ordering (DS instructions of a wave execute in order; the fences keep the compiler from
+// moving the accesses across)
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+// 16 rows of D bf16 from a wave's MFMA D-layout fragments (lane (c, g) holds dims 16 dt + 4 g .. + 3 of row c:
+// frag(dt)) through 32 D bytes of the wave's LDS (row-major, 8-byte pieces XOR-swizzled by the row), stored as
+// whole 16-byte pieces of each row (rowp(r): the row's address, or nullptr to skip it), so that a store
+// instruction writes 4 whole rows instead of 32 bytes of each of 16 rows
+template <int D, class F, class R>
+__device__ __forceinline__ void emit_rows16(unsigned char* lw, int lane, F frag, R rowp) {
+    constexpr int RBY = 2 * D, C16 = RBY / 16;           // row bytes, 16-byte chunks per row
+    const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; dt++) {
+        const f32x4 o = frag(dt);
+        const int s8 = 4 * dt + g;                        // the 8-byte piece of row c
+        *reinterpret_cast<uint2*>(lw + c * RBY + 8 * (s8 ^ c)) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < 16 * C16 / 64; k++) {
+        const int idx = 64 * k + lane, r = idx / C16, ch = idx % C16;
+        uint4 v = *reinterpret_cast<const uint4*>(lw + r * RBY + 16 * (ch ^ (r >> 1)));
+        if (r & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        bf16_t* q = rowp(r);
+        if (q) *reinterpret_cast<uint4*>(q + 8 * ch) = v;
+    }
+    wave_lds_sync();                                      // the reads are done before the region is reused
 }
 __device__ __forceinline__ float dot8(uint4 x, uint4 y) {     // <x, y> of 8 bf16 pairs, fp32
     const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {y.x, y.y, y.z, y.w};
@@ -115,6 +144,7 @@ template <int D>
 __global__ __launch_bounds__(WIN_THREADS) void win_fwd(WinArgs a) {
     constexpr int KK = D / 32, DT = D / 16, ST = D + 8;
     __shared__ __align__(16) bf16_t sV[WIN_STAGE * ST];
+    __shared__ __align__(16) unsigned char sO[WIN_WAVES][32 * D];   // a wave's output rows on their way out
     const int T = a.T, Hq = a.Hq, Hk = a.Hk, W = a.W, R = Hq / Hk;
     const int b = blockIdx.z, hk = blockIdx.y;        // every query head of key/value head hk
     const int t0 = blockIdx.x * WIN_TILE;
@@ -181,14 +211,12 @@ __global__ __launch_bounds__(WIN_THREADS) void win_fwd(WinArgs a) {
 #pragma unroll
         for (int u = 0; u < 2; u++) pf[u] = make_uint2(pack_bf16x2(s[u][0], s[u][1]), pack_bf16x2(s[u][2], s[u][3]));
         const float inv = l > 0.f ? 1.f / l : 0.f;
-        bf16_t* orow = a.out + (qrow0 + r) * D;
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
+        emit_rows16<D>(sO[w], lane, [&](int dt) {
             f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < 2; u++) o = mfma_k16(gather4<ST>(sV, 16 * w + 16 * u + 4 * g, 16 * dt + c), pf[u], o);
-            if (qok) st4bf(orow + 16 * dt + 4 * g, o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
-        }
+            return f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+        }, [&](int rr) { return qt + rr < T ? a.out + ((((size_t)b * T + qt + rr) * Hq + hq) * D) : (bf16_t*)nullptr; });
         if (qok && g == 0) a.lse_out[((size_t)b * Hq + hq) * T + tq] = mx + __logf(l);
     }
 }
@@ -220,6 +248,8 @@ __global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
     const int k0 = blockIdx.x * TILE;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
     const int kt = k0 + 16 * w;                        // this wave's key tile and query tile
+    unsigned char* ow = reinterpret_cast<unsigned char*>(sQ) + w * 32 * D;   // output rows, once sQ is read
+    static_assert(NW * 32 * D <= STG * ST * 2, "every wave's output rows fit in sQ");
     const int j = kt + c;                              // lane column = key j (key/value pass)
     const bool jok = j < T;
     const size_t krow = ((size_t)b * T + (jok ? j : 0)) * Hk + hk;
@@ -322,28 +352,23 @@ __global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
         }
         __syncthreads();
         // ---- dQ^T (dims x queries of tile kt) = K^T dS^T over key tiles kt - 16 and kt
-        const int tq = kt + c;
-        const bool qok = tq < T;
         const bf16_t* t0p = w > 0 ? &sT[w - 1][1][0] : &sT[NW][1][0];
         const bf16_t* t1p = &sT[w][0][0];
         const uint2 b0 = *reinterpret_cast<const uint2*>(t0p + c * TS + 4 * g);
         const uint2 b1 = *reinterpret_cast<const uint2*>(t1p + c * TS + 4 * g);
-        const size_t qrow = ((size_t)b * T + (qok ? tq : 0)) * Hq + hq;
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
+        // the rows go out through this wave's slice of sQ: every wave's reads of the head's q rows are done
+        emit_rows16<D>(ow, lane, [&](int dt) {
             f32x4 o = {0.f, 0.f, 0.f, 0.f};
             o = mfma_k16(gather4<ST>(sK, 16 * w + 4 * g, 16 * dt + c), b0, o);
             o = mfma_k16(gather4<ST>(sK, 16 * w + 16 + 4 * g, 16 * dt + c), b1, o);
-            if (qok) st4bf(a.dq + qrow * D + 16 * dt + 4 * g, o[0] * a.scale, o[1] * a.scale, o[2] * a.scale, o[3] * a.scale);
-        }
+            return f32x4{o[0] * a.scale, o[1] * a.scale, o[2] * a.scale, o[3] * a.scale};
+        }, [&](int rr) { return kt + rr < T ? a.dq + ((((size_t)b * T + kt + rr) * Hq + hq) * D) : (bf16_t*)nullptr; });
     }
-    if (!jok) return;
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++) {
-        st4bf(a.dk + krow * D + 16 * dt + 4 * g, dkt[dt][0] * a.scale, dkt[dt][1] * a.scale, dkt[dt][2] * a.scale,
-              dkt[dt][3] * a.scale);
-        st4bf(a.dv + krow * D + 16 * dt + 4 * g, dvt[dt][0], dvt[dt][1], dvt[dt][2], dvt[dt][3]);
-    }
+    auto krowp = [&](bf16_t* base, int rr) { return kt + rr < T ? base + ((((size_t)b * T + kt + rr) * Hk + hk) * D) : (bf16_t*)nullptr; };
+    emit_rows16<D>(ow, lane, [&](int dt) {
+        return f32x4{dkt[dt][0] * a.scale, dkt[dt][1] * a.scale, dkt[dt][2] * a.scale, dkt[dt][3] * a.scale};
+    }, [&](int rr) { return krowp(a.dk, rr); });
+    emit_rows16<D>(ow, lane, [&](int dt) { return dvt[dt]; }, [&](int rr) { return krowp(a.dv, rr); });
 }
 
 }  // namespace
