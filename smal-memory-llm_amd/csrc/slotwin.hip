@@ -123,16 +123,36 @@ struct WinArgs {
     float scale;
 };
 
-// stage rows [r0, r0 + NR) of head h of x (B, T, H, D) into s (zeros outside [0, T)), NT threads
+// Rows [r0, r0 + NR) of head h of x (B, T, H, D), staged by NT threads into s (row stride ST, zeros outside
+// [0, T)).  load() issues every piece of a lane back to back, unconditionally, from in-range addresses (a
+// piece past the rows or outside [0, T) reads row clamp(t)), so they are in flight together and nothing
+// waits for them before store(), which zeroes those pieces and writes the rest to LDS.  A load per piece
+// behind a branch, or a select right after it, would wait for each piece in turn.
+template <int D, int ST, int NR = WIN_STAGE, int NT = WIN_THREADS>
+struct StagedRows {
+    static constexpr int RU = D / 8, NE = NR * RU, NI = (NE + NT - 1) / NT;
+    uint4 v[NI];
+    __device__ __forceinline__ void load(const bf16_t* x, int b, int T, int H, int h, int r0, int tid) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int e = tid + NT * i, r = e / RU, cc = e - (e / RU) * RU;
+            const int tc = min(max(r0 + r, 0), T - 1);
+            v[i] = ld16(x + (((size_t)b * T + tc) * H + h) * D + cc * 8);
+        }
+    }
+    __device__ __forceinline__ void store(bf16_t* s, int T, int r0, int tid) const {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int e = tid + NT * i, r = e / RU, cc = e - (e / RU) * RU, t = r0 + r;
+            if (e < NE) *reinterpret_cast<uint4*>(s + r * ST + cc * 8) = (t >= 0 && t < T) ? v[i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+};
 template <int D, int ST, int NR = WIN_STAGE, int NT = WIN_THREADS>
 __device__ __forceinline__ void stage_rows(bf16_t* s, const bf16_t* x, int b, int T, int H, int h, int r0, int tid) {
-    constexpr int RU = D / 8;
-    for (int e = tid; e < NR * RU; e += NT) {
-        const int r = e / RU, cc = e - (e / RU) * RU, t = r0 + r;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (t >= 0 && t < T) v = ld16(x + (((size_t)b * T + t) * H + h) * D + cc * 8);
-        *reinterpret_cast<uint4*>(s + r * ST + cc * 8) = v;
-    }
+    StagedRows<D, ST, NR, NT> rows;
+    rows.load(x, b, T, H, h, r0, tid);
+    rows.store(s, T, r0, tid);
 }
 
 __device__ __forceinline__ bool allowed(int tq, int j, int T, int W) {
@@ -241,6 +261,7 @@ __global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
     __shared__ __align__(16) bf16_t sK[STG * ST];   // key rows [k0 - 16, k0 + 64)
     __shared__ __align__(16) bf16_t sQ[STG * ST];   // query rows [k0, k0 + 80) of the current head
     __shared__ __align__(16) bf16_t sD[STG * ST];   // dout rows, the same
+    __shared__ __align__(16) bf16_t sVx[16 * ST];   // value rows [k0 - 16, k0)
     __shared__ float sL[STG], sDs[STG];        // their log-sum-exp and rowsum(dout o out)
     __shared__ __align__(16) bf16_t sT[NW + 1][2][16 * TS];   // dS tiles [query][key]; [WAVES] = wave 0's extra
     const int T = a.T, Hq = a.Hq, Hk = a.Hk, W = a.W, R = Hq / Hk;
@@ -253,7 +274,10 @@ __global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
     const int j = kt + c;                              // lane column = key j (key/value pass)
     const bool jok = j < T;
     const size_t krow = ((size_t)b * T + (jok ? j : 0)) * Hk + hk;
-    stage_rows<D, ST, STG, NTH>(sK, a.k, b, T, Hk, hk, k0 - 16, tid);
+    StagedRows<D, ST, STG, NTH> krows;                 // key rows [k0 - 16, k0 + 16 NW)
+    krows.load(a.k, b, T, Hk, hk, k0 - 16, tid);
+    StagedRows<D, ST, 16, NTH> vxrows;                 // value rows [k0 - 16, k0): wave 0's extra tile
+    vxrows.load(a.v, b, T, Hk, hk, k0 - 16, tid);
     uint4 kb[KK], vb[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; kk++) {
@@ -269,27 +293,57 @@ __global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) tile[(4 * g + i) * TS + c] = f2bf(ds[i]);
     };
+    // A head's rows [k0, k0 + 16 NW + 16) (the query tiles kt and kt + 16 that see key tile kt) are loaded one
+    // head ahead, during the previous head's dq pass: the q rows and the log-sum-exp into registers, the dout
+    // rows straight into sD by direct global -> LDS loads (its last reads are done by then; sQ is still the
+    // dq rows' way out).  Pieces past T are zero.  The out rows, needed only for D = rowsum(dout o out), are
+    // loaded in one batch when the head starts.
+    constexpr int CPR = ST / 8;                         // 16-byte chunks of a padded row (the pad is not loaded)
+    constexpr int NDI = (STG * CPR + NTH - 1) / NTH;    // direct loads per lane for the dout rows
+    constexpr int NIT = (STG * RU + NTH - 1) / NTH;
+    StagedRows<D, ST, STG, NTH> qrows;
+    float lsev = 0.f;
+    const unsigned sD0 = lds_addr(sD);
+    // Every per-head index is derived from an opaque copy of the thread index, so the compiler does not hoist
+    // dozens of loop-invariant 64-bit lane addresses and masks out of the head loop (they spilled)
+    auto opaque_tid = [&]() { int x = tid; asm volatile("" : "+v"(x)); return x; };
+    auto load_head = [&](int hq) {
+        const int tl = opaque_tid();
+        qrows.load(a.q, b, T, Hq, hq, k0, tl);
+#pragma unroll
+        for (int it = 0; it < NDI; it++) {
+            const int L = NTH * it + tl, r = L / CPR, cc = L - (L / CPR) * CPR, t = k0 + r;
+            if (r < STG && cc < RU) {                   // chunk L of sD: row r, 16-byte piece cc
+                if (t < T) dma16(a.dO + (((size_t)b * T + t) * Hq + hq) * D + cc * 8, sD0 + 16u * (NTH * it + 64 * w));
+                else *reinterpret_cast<uint4*>(sD + r * ST + cc * 8) = make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+        lsev = a.lse[((size_t)b * Hq + hq) * T + min(k0 + min(tl, STG - 1), T - 1)];   // zeroed past T when stored
+    };
+    load_head(hk * R);
+    krows.store(sK, T, k0 - 16, tid);
+    vxrows.store(sVx, T, k0 - 16, tid);
     for (int r = 0; r < R; r++) {
         const int hq = hk * R + r;
-        const float* lse = a.lse + ((size_t)b * Hq + hq) * T;
-        __syncthreads();                               // the previous head's staged rows and dS tiles are consumed
-        stage_rows<D, ST, STG, NTH>(sQ, a.q, b, T, Hq, hq, k0, tid);
-        // dout rows, and D as they arrive: the RU chunks of a row are RU consecutive lanes of one DPP row, and
-        // every lane runs every pass (whole rows past the staged range only compute zeros)
-        constexpr int NIT = (STG * RU + NTH - 1) / NTH;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this lane's direct loads into sD have landed
+        __syncthreads();                               // sD complete; the previous head's dq rows are out of sQ
+        const int tl = opaque_tid();
+        uint4 orows[NIT];                              // out rows, in the order of the D reduction below
 #pragma unroll
         for (int it = 0; it < NIT; it++) {
-            const int e = tid + NTH * it;
+            const int e = tl + NTH * it, rr = e / RU, cc = e - (e / RU) * RU, t = k0 + rr;
+            const uint4 ov = ld16(a.o + (((size_t)b * T + min(t, T - 1)) * Hq + hq) * D + cc * 8);
+            orows[it] = (e < STG * RU && t < T) ? ov : make_uint4(0u, 0u, 0u, 0u);
+        }
+        qrows.store(sQ, T, k0, tl);
+        if (tl < STG) sL[tl] = k0 + tl < T ? lsev : 0.f;
+        // D: the RU chunks of a row are RU consecutive lanes of one DPP row
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int e = tl + NTH * it;
             const bool ev = e < STG * RU;
-            const int rr = e / RU, cc = e - (e / RU) * RU, t = k0 + rr;
-            uint4 dv = make_uint4(0u, 0u, 0u, 0u), ov = dv;
-            if (ev && t < T) {
-                const size_t x = (((size_t)b * T + t) * Hq + hq) * D + cc * 8;
-                dv = ld16(a.dO + x);
-                ov = ld16(a.o + x);
-            }
-            if (ev) *reinterpret_cast<uint4*>(sD + rr * ST + cc * 8) = dv;
-            float di = dot8(dv, ov);
+            const int rr = min(e / RU, STG - 1), cc = e - (e / RU) * RU, t = k0 + rr;
+            float di = dot8(ld16(sD + rr * ST + cc * 8), orows[it]);
             di += dppf<SLOT_DPP_XOR1>(di);
             di += dppf<SLOT_DPP_XOR2>(di);
             di += dppf<SLOT_DPP_HMIR>(di);
@@ -299,7 +353,6 @@ __global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
                 if (rr < TILE && t < T) a.dsum[((size_t)b * Hq + hq) * T + t] = di;
             }
         }
-        if (tid < STG) sL[tid] = k0 + tid < T ? lse[k0 + tid] : 0.f;
         __syncthreads();
         // ---- S, dP per (query tile kt + 16 u, key tile kt); dk, dv; dS tiles for dq
 #pragma unroll
@@ -330,15 +383,12 @@ __global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
         }
         if (w == 0) {                                  // query tile k0 against key tile k0 - 16 (dq only)
             const int jx = k0 - 16 + c;
-            const bool jxok = jx >= 0;
-            const size_t vrow = ((size_t)b * T + (jxok ? jx : 0)) * Hk + hk;
             f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < KK; kk++) {
                 const uint4 kx = ld16(sK + c * ST + 32 * kk + 8 * g);   // staged rows 0..15 = keys k0 - 16..
-                const uint4 vx = jxok ? ld16(a.v + vrow * D + 32 * kk + 8 * g) : make_uint4(0u, 0u, 0u, 0u);
                 sa = mfma_k32(ld16(sQ + c * ST + 32 * kk + 8 * g), kx, sa);
-                pa = mfma_k32(ld16(sD + c * ST + 32 * kk + 8 * g), vx, pa);
+                pa = mfma_k32(ld16(sD + c * ST + 32 * kk + 8 * g), ld16(sVx + c * ST + 32 * kk + 8 * g), pa);
             }
             float ds[4];
 #pragma unroll
@@ -351,6 +401,7 @@ __global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
             put_ds(&sT[NW][1][0], ds);
         }
         __syncthreads();
+        if (r + 1 < R) load_head(hq + 1);              // the next head's rows in flight during the dq pass
         // ---- dQ^T (dims x queries of tile kt) = K^T dS^T over key tiles kt - 16 and kt
         const bf16_t* t0p = w > 0 ? &sT[w - 1][1][0] : &sT[NW][1][0];
         const bf16_t* t1p = &sT[w][0][0];
