@@ -136,6 +136,9 @@ __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(3)
     load_q(mlo, qn, scn);
 
     // ---- this wave's keys (A operand of the score product), kinv and validity, values (A of the output)
+    // Every load is issued unconditionally from a clamped in-range address and masked by a select, in
+    // straight-line code: a load behind a branch waits for itself (and the next load reused its address
+    // registers, so the 24 validity and kinv loads went out one at a time)
     uint4 kf[READ_TPW][KK];
     float kv[READ_TPW][4];
     uint32_t vmask = 0;
@@ -145,18 +148,16 @@ __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(3)
         const bool tile = u < TPW && nt < NT16;
         const int nr = nt * 16 + c;                              // A-operand row of this lane
 #pragma unroll
-        for (int kk = 0; kk < KK; kk++) {                        // clamped address, then select: no branch
+        for (int kk = 0; kk < KK; kk++) {
             const uint4 x = *reinterpret_cast<const uint4*>(Kb + (size_t)min(nr, N - 1) * D + kk * 32 + 8 * g);
             kf[u][kk] = (tile && nr < N) ? x : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            // both loads issued unconditionally (in range): no load waits on another's result
             const int n = nt * 16 + 4 * g + i;                     // D-layout row of item i
-            const bool in = tile && n < N;
-            const uint8_t va = in ? VA[n] : (uint8_t)0;
-            const float ki = in ? KI[n] : 0.f;
-            const bool ok = va != 0;
+            const uint8_t va = VA[min(n, N - 1)];
+            const float ki = KI[min(n, N - 1)];
+            const bool ok = tile && n < N && va != 0;
             kv[u][i] = ok ? ki : 0.f;
             vmask |= (ok ? 1u : 0u) << (u * 4 + i);
         }
@@ -551,6 +552,12 @@ __device__ __forceinline__ uint2 gather4(const bf16_t* p, int stride) {
     return r;
 }
 
+// read_bwd's score and datt products load their key and value operands RBWD_KBATCH k-steps at a time per
+// operand before the MFMAs that use them: 2 keeps the non-accumulating form within 168 VGPRs (3 workgroups
+// per CU) without spills, where one load pair per k-step made every MFMA wait for its own loads
+#ifndef RBWD_KBATCH
+#define RBWD_KBATCH 2
+#endif
 template <int D, bool ACC>
 __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(ACC ? 1 : 3))) void read_bwd(ReadBwdArgs a) {
     constexpr int KK = D / 32;
@@ -584,22 +591,21 @@ __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(AC
     bf16_t* dKb = a.dkb + (size_t)slab * N * D;
     bf16_t* dVb = a.dvb + (size_t)slab * N * D;
 
-    // this lane's slot column in the S layout: n = 16 nt + c
+    // this lane's slot column in the S layout: n = 16 nt + c.  Validity and kinv are loaded unconditionally
+    // from clamped rows and masked where first used (after the query tile's barrier), so no load here waits
     float kvc[READ_TPW];
-    uint32_t vmask = 0;
+    uint32_t vraw[READ_TPW];
     bool tile[READ_TPW];
 #pragma unroll
     for (int u = 0; u < READ_TPW; u++) {
         const int nt = w * TPW + u;
         tile[u] = u < TPW && nt < NT16;
-        const int n = nt * 16 + c;
-        const bool in = tile[u] && n < N;
-        const uint8_t va = in ? VA[n] : (uint8_t)0;
-        const float ki = in ? KI[n] : 0.f;
-        const bool ok = va != 0;
-        kvc[u] = ok ? ki : 0.f;
-        vmask |= (ok ? 1u : 0u) << u;
+        const int n = min(nt * 16 + c, N - 1);
+        vraw[u] = VA[n];
+        kvc[u] = KI[n];
     }
+    uint32_t vmask = 0;
+    bool masked = false;
     float dkinv_acc[READ_TPW] = {};
     f32x4 acc_dk[ACC ? READ_TPW : 1][ACC ? DT : 1];
     f32x4 acc_dv[ACC ? READ_TPW : 1][ACC ? DT : 1];
@@ -664,6 +670,15 @@ __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(AC
             s_scl[threadIdx.x] = sv;
         }
         __syncthreads();
+        if (!masked) {                                     // once: the slot masks of the raw loads above
+            masked = true;
+#pragma unroll
+            for (int u = 0; u < READ_TPW; u++) {
+                const bool ok = tile[u] && (w * TPW + u) * 16 + c < N && vraw[u] != 0u;
+                kvc[u] = ok ? kvc[u] : 0.f;
+                vmask |= (ok ? 1u : 0u) << u;
+            }
+        }
         float scl[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) scl[i] = s_scl[4 * g + i];
@@ -684,12 +699,20 @@ __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(AC
                 const int n = (w * TPW + u) * 16 + c;
                 const bool in = tile[u] && n < N;
                 const size_t nc = (size_t)min(n, N - 1) * D;          // clamped address, then select
+                constexpr int KB = RBWD_KBATCH < KK ? RBWD_KBATCH : KK;   // loads per batch, per operand
 #pragma unroll
-                for (int kk = 0; kk < KK; kk++) {
-                    const uint4 kx = *reinterpret_cast<const uint4*>(Kb + nc + kk * 32 + 8 * g);
-                    const uint4 vx = *reinterpret_cast<const uint4*>(Vb + nc + kk * 32 + 8 * g);
-                    sacc[u] = mfma_k32(qa[kk], in ? kx : make_uint4(0, 0, 0, 0), sacc[u]);
-                    dacc[u] = mfma_k32(da[kk], in ? vx : make_uint4(0, 0, 0, 0), dacc[u]);
+                for (int k0 = 0; k0 < KK; k0 += KB) {
+                    uint4 kx[KB], vx[KB];
+#pragma unroll
+                    for (int kk = 0; kk < KB; kk++) {
+                        kx[kk] = *reinterpret_cast<const uint4*>(Kb + nc + (k0 + kk) * 32 + 8 * g);
+                        vx[kk] = *reinterpret_cast<const uint4*>(Vb + nc + (k0 + kk) * 32 + 8 * g);
+                    }
+#pragma unroll
+                    for (int kk = 0; kk < KB; kk++) {
+                        sacc[u] = mfma_k32(qa[k0 + kk], in ? kx[kk] : make_uint4(0, 0, 0, 0), sacc[u]);
+                        dacc[u] = mfma_k32(da[k0 + kk], in ? vx[kk] : make_uint4(0, 0, 0, 0), dacc[u]);
+                    }
                 }
             }
         }
