@@ -336,7 +336,13 @@ void chain_fwd(ChainFwdArgs a) {
 
     if (wave == CHAIN_WAVES) {                          // the producer wave
         uint4 rq[UPT];
-        float rs = 0.f;
+        float rs = 0.f;                                 // lanes < CT: the gate of step lane; CT.. 2 CT: fr
+        bool rsok = false;                              // rs is live (else 0 is staged)
+        // the step scalars come from one of two uniform pointers, chosen per lane; the value is masked when it
+        // is staged, so nothing waits for the load here (indexing the argument block per lane had fetched the
+        // pointer with a vector load and waited for every load in flight)
+        const float* const gate_p = a.gate;
+        const float* const fr_p = a.frt ? a.fr : a.gate;
         auto load_chunk = [&](int ch) {
 #pragma unroll
             for (int m = 0; m < UPT; m++) {
@@ -348,11 +354,10 @@ void chain_fwd(ChainFwdArgs a) {
                     if (t < te) rq[m] = reinterpret_cast<const uint4*>((arr ? kp : qp) + (tok0 + (size_t)t * H) * D)[w];
                 }
             }
-            if (lane < 2 * CT) {
-                const int t = ts + ch * CT + (lane & (CT - 1));
-                rs = 0.f;
-                if (t < te) rs = (lane < CT) ? a.gate[tok0 + (size_t)t * H] : (a.frt ? a.fr[tok0 + (size_t)t * H] : 0.f);
-            }
+            const int t = ts + ch * CT + (lane & (CT - 1));
+            const float* sp = lane < CT ? gate_p : fr_p;
+            rs = sp[tok0 + (size_t)min(t, te - 1) * H];
+            rsok = lane < 2 * CT && t < te && (lane < CT || a.frt);
         };
         auto store_chunk = [&](int bf) {
 #pragma unroll
@@ -363,8 +368,9 @@ void chain_fwd(ChainFwdArgs a) {
                     stage_store(arr ? &s_k[bf][j][w * EPU] : &s_q[bf][j][w * EPU], rq[m], BF);
                 }
             }
-            if (lane < CT) s_g[bf][lane] = rs;
-            else if (lane < 2 * CT) s_fr[bf][lane - CT] = rs;
+            const float rv = rsok ? rs : 0.f;
+            if (lane < CT) s_g[bf][lane] = rv;
+            else if (lane < 2 * CT) s_fr[bf][lane - CT] = rv;
         };
         // E[s][u] = <k_s, q_u> (A = key tokens, B = query tokens; lane l, reg r -> E[4 ag + r][m16]) and
         // 1 / max(|q_u|, 1e-6) (four lanes per query, dims split in quarters)
@@ -422,17 +428,33 @@ void chain_fwd(ChainFwdArgs a) {
     float o_me = 0.f, kinv_me;
     bool vld_me;                                        // |K_me|^2 > 1e-12 (the epilogue's `valid`)
     {
+        // the P rows' loads go out together (from row min(n, N - 1), unconditionally) and rows past N are
+        // zeroed afterwards: a load per row behind a branch, used right away, waited for each row in turn
+        const float* k0r = a.k0 ? a.k0 + (size_t)(b * a.k0bs + h) * N * D : nullptr;
+        if (k0r) {
+#pragma unroll
+            for (int j = 0; j < P; j++) {
+                float row[EPL];
+                ld_slice<EPL>(row, k0r + (size_t)min(R.row(j), N - 1) * D, c);
+#pragma unroll
+                for (int e = 0; e < EPL; e++) Kv[e][j] = row[e];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < P; j++)
+#pragma unroll
+                for (int e = 0; e < EPL; e++) Kv[e][j] = 0.f;
+        }
         float x[P];
 #pragma unroll
         for (int j = 0; j < P; j++) {
-            const int n = R.row(j);
-            float row[EPL];
-#pragma unroll
-            for (int e = 0; e < EPL; e++) row[e] = 0.f;
-            if (a.k0 && n < N) ld_slice<EPL>(row, a.k0 + ((size_t)(b * a.k0bs + h) * N + n) * D, c);
+            const bool in = R.row(j) < N;
             float kk = 0.f;
 #pragma unroll
-            for (int e = 0; e < EPL; e++) { Kv[e][j] = row[e]; kk = fmaf(row[e], row[e], kk); }
+            for (int e = 0; e < EPL; e++) {
+                Kv[e][j] = in ? Kv[e][j] : 0.f;
+                kk = fmaf(Kv[e][j], Kv[e][j], kk);
+            }
             x[j] = kk;
         }
         const float nsq0 = rs_reduce<P>(x, c);
