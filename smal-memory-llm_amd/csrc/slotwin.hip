@@ -43,8 +43,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define WIN_TILE (16 * WIN_WAVES)                    // query (or key) rows per workgroup
 #define WIN_STAGE (WIN_TILE + 16)                    // staged rows: the tile plus the 16 rows the band reaches
 #ifndef WIN_BWD_WAVES
-#define WIN_BWD_WAVES 8                              // backward: waves (16-key tiles) per workgroup
-#endif
+#define WIN_BWD_WAVES 4                              // backward: waves (16-key tiles) per workgroup; 4 fits two
+#endif                                               // workgroups (75 KB of LDS each) on a CU
 
 namespace {
 
@@ -254,7 +254,8 @@ __global__ __launch_bounds__(WIN_THREADS) void win_fwd(WinArgs a) {
 //           and wave w - 1's u = 1 tile; wave 0 computes the pair (query tile k0, key tile k0 - 16) itself.
 // S and dP are computed once per (query tile, key tile) pair for all three gradients.
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void win_bwd(WinArgs a) {
+// At most 256 VGPRs (2 waves per SIMD): two 4-wave workgroups share a CU, one staging while the other computes
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void win_bwd(WinArgs a) {
     constexpr int NTH = 64 * NW, TILE = 16 * NW, STG = TILE + 16;   // threads, keys per workgroup, staged rows
     constexpr int KK = D / 32, DT = D / 16, ST = D + 8, RU = D / 8;
     constexpr int TS = 20;                             // transposed dS row (bf16): 10 dwords, 16 rows on 32 banks
