@@ -56,7 +56,7 @@ WORKLOADS = {
     # frozen-store read fan-out: 6 reader layers, one block (NB = 1: G = T), one query per head and token
     "config4": dict(kind="read", B=64, T=1024, H=6, N=192, D=128, G=1024, NQ=1, layers=6),
     # long-context streaming: 128 chunks of 1024 tokens, state carried, int8 + per-row fp32 scale emission
-    "config5": dict(kind="stream", B=8, T=131072, H=6, N=192, D=128, G=8, chunk=1024),
+    "config5": dict(kind="stream", B=8, T=131072, H=6, N=192, D=128, G=8, chunk=1024, seed=4),
     # config 4 with each reader layer's output projection into the residual (memlm_sh.py:499-501): the read,
     # then wo_tk (d_model 2048, bias-free) added to the window output, forward only
     "config4_wo": dict(kind="read_out", B=64, T=1024, H=6, N=192, D=128, G=1024, NQ=1, layers=6, DM=2048),
@@ -89,6 +89,24 @@ def scan_workload_inputs(W, dev):
     dkb = rn(B, NB, H, N, D).to(torch.bfloat16).float()
     dvb = rn(B, NB, H, N, D).to(torch.bfloat16).float()
     return k, q, v, gate, fr, temp, dkb, dvb, rn
+
+
+def stream_workload_inputs(W, T, dev):
+    """The streaming workload's synthetic tokens (config 5), T of them per batch row, drawn on the GPU from
+    the workload's seeded generator (seed 4) in a fixed order: k, q, v bf16 N(0,1) with k and q L2-normalised,
+    gate = sigmoid(N(0,1.5)) bf16, fr ~ U[0,2) bf16 -- config 2's distributions.  The parity test of the
+    carried-state stream draws its 3,072 tokens per row the same way."""
+    import torch
+    B, H, D = W["B"], W["H"], W["D"]
+    gen = torch.Generator(device=dev).manual_seed(W.get("seed", 4))
+    rn = lambda *s: torch.randn(*s, device=dev, generator=gen)
+    unit = lambda x: x / x.norm(dim=-1, keepdim=True)
+    k = unit(rn(B, T, H, D)).to(torch.bfloat16)
+    q = unit(rn(B, T, H, D)).to(torch.bfloat16)
+    v = rn(B, T, H, D).to(torch.bfloat16)
+    gate = torch.sigmoid(rn(B, T, H) * 1.5).to(torch.bfloat16)
+    fr = (torch.rand(B, T, H, device=dev, generator=gen) * 2).to(torch.bfloat16)
+    return k, q, v, gate, fr
 
 
 def algorithmic_bytes(B, T, H, N, D, G, mem=False, soft=False):
@@ -298,8 +316,10 @@ def cpu_baseline_read(W, seed=3):
 def bench_stream(args, W):
     """Config 5: forward-only streaming scan, 1024-token chunks with the slot state carried, every chunk's
     snapshot copies emitted as int8 codes + one fp32 scale per row (the storage quantiser, bits 8, group D).
-    The emission of chunk c runs on a second stream while chunk c+1 scans: the scan keeps only B*H = 48
-    workgroups busy, so the quantiser passes fill otherwise idle CUs.  One step = the whole T-token stream."""
+    Each chunk is one kv_scan_stream_q call, the fused path (slotscan_fwd_codes): the chain stores no
+    snapshots and the row replay emits both copies' codes, beside the next chain chunk.  The line also times
+    the two-pass path on the same stream (kv_scan_stream's fp32 snapshots, then fq_codes on a second stream)
+    as `two_pass_ms_per_step`.  One step = the whole T-token stream."""
     import torch
     import slotkern_hip as KH
     import slotmem_hip as MH
@@ -307,23 +327,27 @@ def bench_stream(args, W):
 
     B, T, H, N, D, G, C = (W[x] for x in ("B", "T", "H", "N", "D", "G", "chunk"))
     dev = torch.device("cuda:0")
-    gen = torch.Generator(device=dev).manual_seed(4)
-    rn = lambda *s: torch.randn(*s, device=dev, generator=gen)
-    unit = lambda x: x / x.norm(dim=-1, keepdim=True)
-    k = unit(rn(B, T, H, D)).to(torch.bfloat16)
-    q = unit(rn(B, T, H, D)).to(torch.bfloat16)
-    v = rn(B, T, H, D).to(torch.bfloat16)
-    gate = torch.sigmoid(rn(B, T, H) * 1.5).to(torch.bfloat16)
-    fr = (torch.rand(B, T, H, device=dev, generator=gen) * 2).to(torch.bfloat16)
+    k, q, v, gate, fr = stream_workload_inputs(W, T, dev)
+    temp = torch.tensor(16.0, device=dev)                   # resident: no host copy per call
     side = torch.cuda.Stream(device=dev)                  # default priority
     main = torch.cuda.current_stream(dev)
 
     def stream_pass():
         st = None
+        out = None
+        for t0 in range(0, T, C):
+            sl = slice(t0, t0 + C)
+            kq, vq, st = KH.kv_scan_stream_q(k[:, sl], v[:, sl], gate[:, sl], fr[:, sl], N, temp, G=G, q=q[:, sl],
+                                             occ_bin=True, state=st, bits=8)
+            out = (kq, vq)
+        return st, out
+
+    def stream_pass_two():
+        st = None
         pending = None
         for t0 in range(0, T, C):
             sl = slice(t0, t0 + C)
-            kb, vb, st = KH.kv_scan_stream(k[:, sl], v[:, sl], gate[:, sl], fr[:, sl], N, 16.0, G=G, q=q[:, sl],
+            kb, vb, st = KH.kv_scan_stream(k[:, sl], v[:, sl], gate[:, sl], fr[:, sl], N, temp, G=G, q=q[:, sl],
                                            occ_bin=True, state=st)
             ev = torch.cuda.Event()
             ev.record(main)
@@ -336,6 +360,12 @@ def bench_stream(args, W):
         main.wait_stream(side)
         return st, pending
 
+    stream_pass_two()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    stream_pass_two()
+    torch.cuda.synchronize()
+    two_ms = (time.perf_counter() - t0) * 1e3
     for _ in range(args.warmup):
         stream_pass()
     torch.cuda.synchronize()
@@ -365,6 +395,7 @@ def bench_stream(args, W):
                           "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
         "kernels_ms": {n: round(x / c, 4) for n, (x, c) in prof.items()},
         "kernels_total_ms": {n: round(x / args.steps, 3) for n, (x, c) in prof.items()},
+        "two_pass_ms_per_step": round(two_ms, 3),
     }
     print(json.dumps(out), flush=True)
 

@@ -148,6 +148,60 @@ int slotscan_bwd_mem(const void* k, const void* q, const void* v, int dtype,
                      void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
                      void* stream);
 
+/* Forward scan with the writer epilogue and the storage quantiser fused in.  Replaces kv_scan_g followed by
+ * the quantised epilogue of the writer layer (memlm_sh.py:453-456 then :468-471, _quantize_mem :231-234):
+ *     kq = _fq(kbuf, bits, group);  nsq = kq.pow(2).sum(-1)
+ *     mem = (kq.to(bf16), _fq(vbuf, bits, group).to(bf16), rsqrt(nsq.clamp_min(1e-12)), nsq > 1e-12)
+ * with _fq the midrise quantiser (memlm_sh.py:221-229; bits 2..8, one fp32 scale per `group` channels, a
+ * power of two in [4, D]); bits = 0 emits the plain values (the same outputs as slotscan_fwd_mem).  The
+ * chain kernel stores no key snapshots: the row replay rebuilds every key and value row from the address
+ * log (bitwise the chain's state) and emits both copies.  run_sh25.sh:224 trains the last 20 % of its steps
+ * this way (--qat_bits 3 --sh_qgroup 16).
+ *   kcarry  (B*H, N, D) fp32 scratch in which the key replay carries its state across the forward
+ *           pipeline's inner chunk boundaries: slotscan_fwd_carry_bytes(B, T, H, N, D, G) bytes, NULL when
+ *           that is 0 (one chunk)
+ * Every other argument is as in slotscan_fwd_mem. */
+size_t slotscan_fwd_carry_bytes(int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G);
+int slotscan_fwd_memq(const void* k, const void* q, const void* v, int dtype,
+                      const float* gate, const float* fr, int fr_per_token, const float* temp,
+                      int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                      float eps, int occ_bin, int bits, int64_t group,
+                      const float* k0, const float* v0, const float* o0,
+                      void* kb, void* vb, float* kinv, uint8_t* valid, int32_t* am,
+                      float* kold, float* vold, float* oold, float* cslog,
+                      float* kfin, float* vfin, float* ofin, float* kcarry, void* stream);
+
+/* Backward of slotscan_fwd_memq: as slotscan_bwd_mem, with K in dkbuf = dkb + 2 K dnsq the quantised key
+ * _fq(K, bits, group) that kinv was taken from, and the quantiser's own gradient the identity
+ * (straight-through, memlm_sh.py:229). */
+int slotscan_bwd_memq(const void* k, const void* q, const void* v, int dtype,
+                      const float* gate, const float* fr, int fr_per_token, const float* temp,
+                      int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                      float eps, int occ_bin, int bits, int64_t group,
+                      const int32_t* am, const float* kold, const float* vold, const float* oold,
+                      const float* cslog, const float* kfin, const float* vfin, const float* ofin,
+                      const void* dkb, const void* dvb, const float* dkinv, void* workspace,
+                      void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
+                      void* stream);
+
+/* Forward-only scan emitting both copies in the storage quantiser's integer form: the streaming scan of
+ * BASELINE config 5 (int8 values with one fp32 absmax scale per row: bits = 8, group = D).  Replaces
+ * kv_scan_g followed by _fq (memlm_sh.py:221-228) kept as codes:
+ *     codes = clamp(floor(x / s), -2^(bits-1), 2^(bits-1) - 1) int8,  s = max(absmax / 2^(bits-1), 1e-30)
+ * per group, scale = s (0 for an all-zero group), so (code + 0.5) * scale is _fq's value.
+ *   kcode, vcode    (B, ceil(T/G), H, N, D) int8, 16-byte aligned
+ *   kscale, vscale  (B, ceil(T/G), H, N, D / group) fp32
+ *   k0, v0, o0 / kfin, vfin, ofin  the carried state in / out, as in slotscan_fwd (the stream's chunks)
+ *   kcarry          as in slotscan_fwd_memq
+ * No undo log is written (no backward follows).  The chain stores no snapshots; the row replay emits them. */
+int slotscan_fwd_codes(const void* k, const void* q, const void* v, int dtype,
+                       const float* gate, const float* fr, int fr_per_token, const float* temp,
+                       int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                       float eps, int occ_bin, int bits, int64_t group,
+                       const float* k0, const float* v0, const float* o0,
+                       int8_t* kcode, float* kscale, int8_t* vcode, float* vscale, int32_t* am,
+                       float* kfin, float* vfin, float* ofin, float* kcarry, void* stream);
+
 /* General-mode scan: every mode the row-sparse kernels above do not cover -- soft write addresses
  * (hard = 0), the attached address gradient (detach_addr = 0), DK != DV -- as the reference runs them on its
  * general Triton scan (gqa25/slotkern_cuda.py:539-542 -> gqa25/slotkern_kvg.py:257-265; forward

@@ -302,10 +302,17 @@ __device__ __forceinline__ u32 wavemax_key(u32 v) {
 // which the owner lane applies to its row's scores (rounded once per term, re-derived from the keys at
 // the next window).  The row norm of the written row is recomputed from its new elements.  The per-step
 // work left is the score, the argmax, and the one-row update.
+//
+// EM selects the key emission: CF_F32 the fp32 snapshots (kbuf); CF_BF the writer epilogue's bf16 copies with
+// kinv and valid; CF_NONE no key snapshots at all -- the row replay (rows_fwd with RF_CODES / RF_MEMQ) rebuilds
+// every key row bitwise from the address log and emits both copies, so the latency-bound chain carries no
+// snapshot bursts.
 #define FWD_THREADS (CHAIN_THREADS + 64)
-template <int D, int P, typename TI, bool MB>
+enum { CF_F32 = 0, CF_BF = 1, CF_NONE = 2 };
+template <int D, int P, typename TI, int EM>
 __global__ __attribute__((amdgpu_flat_work_group_size(FWD_THREADS, FWD_THREADS), amdgpu_waves_per_eu(2)))
 void chain_fwd(ChainFwdArgs a) {
+    constexpr bool MB = EM == CF_BF;
     constexpr int EPL = D / 16;
     constexpr int DP = D + 4;                           // padded LDS row: 16 rows at stride DP hit 16 bank groups
     constexpr int EPU = 16 / (int)sizeof(TI);          // token elements per uint4
@@ -420,7 +427,7 @@ void chain_fwd(ChainFwdArgs a) {
     const ChainRows<P> R(tid);
     const size_t sstride = (size_t)H * N * D;
     const size_t snap0 = ((size_t)b * a.NB + ts / G) * H + h;           // (b, ts / G, h): snapshot of block ts / G
-    float* kb = MB ? nullptr : a.kbuf + snap0 * N * D + (a.skip0 ? sstride : 0);   // skip0: the first slab is written
+    float* kb = EM == CF_F32 ? a.kbuf + snap0 * N * D + (a.skip0 ? sstride : 0) : nullptr;   // skip0: the first slab is written
     bf16_t* kbm = MB ? a.kbm + snap0 * N * D : nullptr;
     float* kinvm = MB ? a.kinvm + snap0 * N : nullptr;
     uint8_t* validm = MB ? a.validm + snap0 * N : nullptr;
@@ -554,7 +561,7 @@ void chain_fwd(ChainFwdArgs a) {
             uint4 r[CHAIN_WAVES];
 #pragma unroll
             for (int w = 0; w < CHAIN_WAVES; w++) r[w] = s_red[par][w];
-            if (gc == 0 && (MB || t != ts || !a.skip0)) {   // the PRE-write key state of block t / G:
+            if (EM != CF_NONE && gc == 0 && (MB || t != ts || !a.skip0)) {   // the PRE-write key state of block t / G:
                 u32 ro = roff;                              // every row group stores whole rows
                 int nvv = nvalid;
                 asm volatile("" : "+v"(ro), "+v"(nvv));     // per-snapshot offsets, not 16 live registers
@@ -653,16 +660,90 @@ struct RowsFwdArgs {
     int ts, te;                                          // steps [ts, te); ts % G == 0
     bf16_t* vbm;                                         // the writer-epilogue emission (NULL: fp32 vbuf)
     int v0bs, vfbs, skip0;                               // as ChainFwdArgs' k0bs, kfbs, skip0
+    // RF_CODES / RF_MEMQ: the key replay (tokens k, start state k0 (B*H, N, D) or NULL, end state kfin) and the
+    // emission of both copies -- integer codes + per-group scales (RF_CODES), or the quantiser's values (bits
+    // 0: the plain values) as bf16 with kinv and valid of the emitted keys (RF_MEMQ, into kbm, vbm, kinvm,
+    // validm)
+    const void* k; const float* k0; float* kfin;
+    int bits, group;
+    bf16_t* kbm; float* kinvm; uint8_t* validm;
+    int8_t* kcode; float* kscale; int8_t* vcode; float* vscale;
 };
+
+// The storage quantiser _fq (memlm_sh.py:221-228) over a row slice held the row-group way: EPL / 4 pieces of
+// 4 consecutive channels, piece jj at channels 64 jj + 4 c, the row's 16 lanes c one DPP row.  A group of
+// `group` channels is group / 4 consecutive lanes of one piece (group <= 64), or the whole row (group 128,
+// D = 128).  Per element: a = the group's absmax, s = max(a / 2^(bits-1), 1e-30), code = clamp(floor(x / s),
+// -2^(bits-1), 2^(bits-1) - 1) (IEEE division), value x + (q - x) with q = (code + 0.5) s, or 0 where a == 0
+// -- the expressions of the two-pass quantiser (slotmem.hip), so codes, scales and values are bitwise its own.
+// scl[jj]: the scale of piece jj's group (0 for an all-zero group).
+template <int EPL>
+__device__ __forceinline__ void fq_slice(const float* x, int bits, int group, float* val, float* code, float* scl) {
+    constexpr int NP = EPL / 4;
+    const float half = (float)(1 << (bits - 1));
+    float am[NP];
+#pragma unroll
+    for (int jj = 0; jj < NP; jj++) {
+        float m = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) m = fmaxf(m, fabsf(x[4 * jj + e]));
+        am[jj] = m;
+    }
+    if (NP == 2 && group > 64) {                         // one group per row of 128 channels
+        const float m = rowmax16(fmaxf(am[0], am[NP - 1]));
+#pragma unroll
+        for (int jj = 0; jj < NP; jj++) am[jj] = m;
+    } else {
+#pragma unroll
+        for (int jj = 0; jj < NP; jj++) {
+            float m = am[jj];
+            if (group >= 8) m = fmaxf(m, dppf<SLOT_DPP_XOR1>(m));
+            if (group >= 16) m = fmaxf(m, dppf<SLOT_DPP_XOR2>(m));
+            if (group >= 32) m = fmaxf(m, dppf<SLOT_DPP_HMIR>(m));
+            if (group >= 64) m = fmaxf(m, dppf<SLOT_DPP_MIR>(m));
+            am[jj] = m;
+        }
+    }
+#pragma unroll
+    for (int jj = 0; jj < NP; jj++) {
+        const float ag = am[jj];
+        const float sc = fmaxf(ag / half, 1e-30f);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float xe = x[4 * jj + e];
+            const float cd = fminf(fmaxf(floorf(xe / sc), -half), half - 1.f);
+            float q = (cd + 0.5f) * sc;
+            q = ag > 0.f ? q : 0.f;
+            val[4 * jj + e] = xe + (q - xe);
+            code[4 * jj + e] = cd;
+        }
+        scl[jj] = ag > 0.f ? sc : 0.f;
+    }
+}
+
+// codes of one piece (4 floats holding integers in [-128, 127]) packed as 4 bytes, channel order
+__device__ __forceinline__ u32 pack_codes4(const float* cd) {
+    return ((u32)(int)cd[0] & 0xffu) | (((u32)(int)cd[1] & 0xffu) << 8) | (((u32)(int)cd[2] & 0xffu) << 16) |
+           (((u32)(int)cd[3] & 0xffu) << 24);
+}
 
 // 512 lanes = 32 rows of one chain per workgroup; grid (B*H, ceil(N/32)).  Replays every row's value from
 // the address log and emits the value snapshots with full-row non-temporal stores.  A row changes only at
 // its own writes, so the replay visits events, not steps: per 16-step piece of the staged address log a
 // lane forms the mask of steps that wrote its row (4 LDS reads) and, with the piece's G-aligned snapshot
 // steps, walks the set bits in step order (snapshot first: it is the PRE-write state).
-template <int D, typename TI, bool MB>
+// EM: RF_F32 fp32 value snapshots; RF_BF bf16 value copies; RF_CODES / RF_MEMQ also replay the KEY rows (the
+// chain's own blend on the same staged token values, so bitwise the chain's keys) and emit both copies in
+// the storage quantiser's integer form (RF_CODES) or as the writer epilogue's bf16 values with kinv and
+// valid (RF_MEMQ).  The key state crosses the forward pipeline's inner chunk boundaries through kfin (each
+// chunk's replay ends by writing it and the next starts from it), apart from the chain's own carry.
+enum { RF_F32 = 0, RF_BF = 1, RF_CODES = 2, RF_MEMQ = 3 };
+template <int D, typename TI, int EM>
 ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     constexpr int EPL = D / 16;
+    constexpr int NP = EPL / 4;
+    constexpr bool MB = EM == RF_BF;
+    constexpr bool KR = EM >= RF_CODES;                  // the key rows are replayed too
     constexpr int TC = 256;                              // staged steps: 2 KB of LDS, so the replay blocks fit beside two chain blocks on a CU
     __shared__ __align__(16) int s_am[TC];
     __shared__ float s_g[TC];
@@ -672,15 +753,59 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
     const int n = blockIdx.y * 32 + rg;
     const bool live = n < N;
     const TI* __restrict__ vp = (const TI*)a.v;
+    const TI* __restrict__ kp = (const TI*)a.k;
     const size_t tok0 = (size_t)b * T * H + h;
-    float V[EPL];
+    float V[EPL], K[EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; e++) V[e] = 0.f;
+    for (int e = 0; e < EPL; e++) { V[e] = 0.f; K[e] = 0.f; }
     if (live && a.v0) ld_slice<EPL>(V, a.v0 + ((size_t)(b * a.v0bs + h) * N + n) * D, c);
+    if (KR && live && a.k0) ld_slice<EPL>(K, a.k0 + ((size_t)bh * N + n) * D, c);
     const size_t vrow0 = (((size_t)b * a.NB + a.ts / G) * H + h) * N * D + (size_t)(live ? n : 0) * D;
-    float* vb = MB ? nullptr : a.vbuf + vrow0;
+    float* vb = EM == RF_F32 ? a.vbuf + vrow0 : nullptr;
     bf16_t* vbh = MB ? a.vbm + vrow0 : nullptr;
     const size_t sstride = (size_t)H * N * D;
+    // RF_CODES / RF_MEMQ outputs: the row's snapshot index advances by one (b, nb, h) slab per snapshot
+    size_t srow = (((size_t)b * a.NB + a.ts / G) * H + h) * N + (size_t)(live ? n : 0);
+    const int gpr = KR && EM == RF_CODES ? D / a.group : 0;   // scales per row
+    auto emit = [&]() {
+        if constexpr (EM == RF_CODES) {
+            float kv[EPL], kc[EPL], ks[NP], vv[EPL], vc[EPL], vs[NP];
+            fq_slice<EPL>(K, a.bits, a.group, kv, kc, ks);
+            fq_slice<EPL>(V, a.bits, a.group, vv, vc, vs);
+            int8_t* kcr = a.kcode + srow * D;
+            int8_t* vcr = a.vcode + srow * D;
+#pragma unroll
+            for (int jj = 0; jj < NP; jj++) {
+                __builtin_nontemporal_store(pack_codes4(kc + 4 * jj), reinterpret_cast<u32*>(kcr + 64 * jj + 4 * c));
+                __builtin_nontemporal_store(pack_codes4(vc + 4 * jj), reinterpret_cast<u32*>(vcr + 64 * jj + 4 * c));
+                const int ch = 64 * jj + 4 * c;          // the group's first lane stores its scale
+                if (ch % a.group == 0) {
+                    a.kscale[srow * gpr + ch / a.group] = ks[jj];
+                    a.vscale[srow * gpr + ch / a.group] = vs[jj];
+                }
+            }
+        } else if constexpr (EM == RF_MEMQ) {
+            float kv[EPL], vv[EPL];
+            if (a.bits) {
+                float cd[EPL], sc[NP];
+                fq_slice<EPL>(K, a.bits, a.group, kv, cd, sc);
+                fq_slice<EPL>(V, a.bits, a.group, vv, cd, sc);
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; e++) { kv[e] = K[e]; vv[e] = V[e]; }
+            }
+            float sq = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) sq = fmaf(kv[e], kv[e], sq);
+            const float nsq = rowsum16(sq);
+            st_slice_bf_at<EPL>(a.kbm + srow * D, 8u * (u32)c, kv);
+            st_slice_bf_at<EPL>(a.vbm + srow * D, 8u * (u32)c, vv);
+            if (c == 0) {                                // kinv and valid of the emitted (quantised) keys
+                a.kinvm[srow] = rsqrtf(fmaxf(nsq, 1e-12f));
+                a.validm[srow] = nsq > 1e-12f ? 1 : 0;
+            }
+        }
+    };
     for (int t0 = a.ts; t0 < a.te; t0 += TC) {
         const int tn = min(TC, a.te - t0);
         __syncthreads();
@@ -709,9 +834,12 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
                 ev &= ev - 1;
                 if ((sm >> i) & 1u) {
                     if constexpr (MB) { st_slice_bf_at<EPL>(vbh, 8u * (u32)c, V); vbh += sstride; }
-                    else {
+                    else if constexpr (EM == RF_F32) {
                         if (t0 + j0 + i != a.ts || !a.skip0) st_slice_nt<EPL>(vb, V, c);   // skip0: already written
                         vb += sstride;
+                    } else {
+                        emit();
+                        srow += (size_t)H * N;
                     }
                 }
                 if ((hm >> i) & 1u) {
@@ -722,11 +850,18 @@ ROWS_ATTR void rows_fwd(RowsFwdArgs a) {
                     if (a.vold) st_slice<EPL>(a.vold + ix * D, V, c);
 #pragma unroll
                     for (int e = 0; e < EPL; e++) V[e] = blend(V[e], vv[e], g, omw);
+                    if constexpr (KR) {
+                        float kk[EPL];
+                        ld_slice<EPL>(kk, kp + ix * D, c);
+#pragma unroll
+                        for (int e = 0; e < EPL; e++) K[e] = blend(K[e], kk[e], g, omw);
+                    }
                 }
             }
         }
     }
     if (live) st_slice<EPL>(a.vfin + ((size_t)(b * a.vfbs + h) * N + n) * D, V, c);
+    if (KR && live && a.kfin) st_slice<EPL>(a.kfin + ((size_t)bh * N + n) * D, K, c);   // the key carry (inner chunks)
 }
 
 // =========================================================================================== rows_bwd
@@ -736,8 +871,11 @@ struct RowsBwdArgs {
     const float* dkbuf; const float* dvbuf;
     void* dk; void* dv; float* dn;
     int T, H, N, G, NB;
-    // the writer-epilogue contract upstream (rows_bwd<..., MB = true>): the bf16 copies' gradients and dkinv
+    // the writer-epilogue contract upstream (rows_bwd<..., MB = true>): the bf16 copies' gradients and dkinv;
+    // qbits > 0: the copies were the storage quantiser's values (qbits, qgroup), whose gradient is straight
+    // through, while kinv came from the quantised keys
     const bf16_t* dkbm; const bf16_t* dvbm; const float* dkinvm;
+    int qbits, qgroup;
 };
 
 // 512 lanes = 32 rows per workgroup, grid (B*H, ceil(N/32)); reverse in t, in 16-step chunks aligned to
@@ -998,16 +1136,26 @@ ROWS_ATTR void rows_bwd(RowsBwdArgs a) {
         }
     };
     // MB: the writer epilogue's key gradient at this snapshot, d kbuf = d kb + 2 K dnsq with
-    // dnsq = -0.5 kinv^3 dkinv where |K|^2 >= 1e-12 (slotmem.hip's backward); K is the snapshot's value
+    // dnsq = -0.5 kinv^3 dkinv where |K|^2 >= 1e-12 (slotmem.hip's backward); K is the snapshot's value, or
+    // with the storage quantiser its quantised value (memlm_sh.py:231-234: kinv is taken from _fq(kbuf), and
+    // _fq passes the gradient straight through)
     auto combine = [&](float* pk, float dki) {
+        float kq[EPL];
+        if (a.qbits) {
+            float cd[EPL], sc[NQ];
+            fq_slice<EPL>(K, a.qbits, a.qgroup, kq, cd, sc);
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) kq[e] = K[e];
+        }
         float nsq = 0.f;
 #pragma unroll
-        for (int e = 0; e < EPL; e++) nsq = fmaf(K[e], K[e], nsq);
+        for (int e = 0; e < EPL; e++) nsq = fmaf(kq[e], kq[e], nsq);
         nsq = rowsum16(nsq);
         const float ki = rsq_clamped(nsq);
         const float coef = nsq >= 1e-12f ? -(ki * ki * ki) * dki : 0.f;
 #pragma unroll
-        for (int e = 0; e < EPL; e++) pk[e] = fmaf(coef, K[e], pk[e]);
+        for (int e = 0; e < EPL; e++) pk[e] = fmaf(coef, kq[e], pk[e]);
     };
     auto enter_mb = [&](const u32x2* hk, const u32x2* hv, float hki) {
         float pk[EPL], pv[EPL];
@@ -1964,8 +2112,9 @@ template <int D, typename TI>
 hipError_t launch_chain_fwd(const ChainFwdArgs& a, int B, hipStream_t st) {
     dim3 grid(B * a.H), block(FWD_THREADS);
 #define SLOT_CF(PP) if (a.N <= 4 * CHAIN_WAVES * PP) { \
-        if (a.kbm) slothost::launch((chain_fwd<D, PP, TI, true>), grid, block, 0, st, a); \
-        else slothost::launch((chain_fwd<D, PP, TI, false>), grid, block, 0, st, a); \
+        if (a.kbm) slothost::launch((chain_fwd<D, PP, TI, CF_BF>), grid, block, 0, st, a); \
+        else if (a.kbuf) slothost::launch((chain_fwd<D, PP, TI, CF_F32>), grid, block, 0, st, a); \
+        else slothost::launch((chain_fwd<D, PP, TI, CF_NONE>), grid, block, 0, st, a); \
         return hipGetLastError(); }
     SLOT_CF(1) SLOT_CF(2) SLOT_CF(4) SLOT_CF(8) SLOT_CF(16)
 #undef SLOT_CF
@@ -2132,44 +2281,77 @@ static int check_common(int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, i
     return 0;
 }
 
-// The forward of both contracts: fp32 snapshots (kbuf, vbuf) or, when kbm is set, the writer epilogue's
-// bf16 copies with kinv and valid (kbm, vbm, kinvm, validm).
+// What one forward call emits.  FE_F32: fp32 snapshots (kbuf, vbuf).  FE_MEM: the writer epilogue's bf16
+// copies with kinv and valid, the keys from the chain (kbm, vbm, kinvm, validm).  FE_MEMQ: the same outputs
+// with the storage quantiser applied (bits > 0; bits 0 = plain values), both copies from the row replay.
+// FE_CODES: the quantiser's integer codes and per-group scales of both copies, from the row replay.
+enum { FE_F32 = 0, FE_MEM = 1, FE_MEMQ = 2, FE_CODES = 3 };
+struct FwdOut {
+    int mode;
+    float* kbuf; float* vbuf;
+    bf16_t* kbm; bf16_t* vbm; float* kinvm; uint8_t* validm;
+    int8_t* kcode; float* kscale; int8_t* vcode; float* vscale;
+    int bits, group;
+    float* kcarry;                                       // FE_MEMQ / FE_CODES: the key replay's chunk carry
+};
+
+// chunk length of the forward pipeline (a multiple of G); T < 512 runs as one chunk
+static int64_t fwd_chunk_len(int64_t T, int64_t G) {
+    return T >= 512 ? ((std::max<int64_t>(128, T / 8) + G - 1) / G) * G : T;
+}
+
+static int check_q(int bits, int64_t group, int64_t D, bool codes) {
+    if (codes ? (bits < 2 || bits > 8) : (bits != 0 && (bits < 2 || bits > 8)))
+        return fail(SLOTSCAN_ERR_SHAPE, codes ? "bits must be 2..8" : "bits must be 0 or 2..8");
+    if (bits != 0 && (group < 4 || group > D || (group & (group - 1)) != 0))
+        return fail(SLOTSCAN_ERR_SHAPE, "group must be a power of two in [4, D]");
+    return 0;
+}
+
+// The forward of every contract.
 static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
                     const float* gate, const float* fr, int fr_per_token, const float* temp,
                     int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
                     float eps, int occ_bin,
-                    const float* k0, const float* v0, const float* o0,
-                    float* kbuf, float* vbuf, bf16_t* kbm, bf16_t* vbm, float* kinvm, uint8_t* validm,
+                    const float* k0, const float* v0, const float* o0, FwdOut o,
                     int32_t* am, float* kold, float* vold, float* oold, float* cslog,
                     float* kfin, float* vfin, float* ofin, void* stream) {
     if (int r = check_common(B, T, H, N, D, G, dtype)) return r;
-    const bool mem = kbm != nullptr;
+    const int mode = o.mode;
+    const bool kr = mode == FE_MEMQ || mode == FE_CODES;         // the row replay emits the keys
+    const int64_t len = fwd_chunk_len(T, G);
+    const int nch = (int)((T + len - 1) / len);
     if (!k || !q || !v || !gate || !fr || !temp || !am || !kfin || !vfin || !ofin ||
-        (mem ? (!vbm || !kinvm || !validm) : (!kbuf || !vbuf)))
+        (mode == FE_F32 && (!o.kbuf || !o.vbuf)) ||
+        ((mode == FE_MEM || mode == FE_MEMQ) && (!o.kbm || !o.vbm || !o.kinvm || !o.validm)) ||
+        (mode == FE_CODES && (!o.kcode || !o.kscale || !o.vcode || !o.vscale)) || (kr && nch > 1 && !o.kcarry))
         return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd: a required pointer is NULL");
-    if (mem) { kbuf = vbuf = nullptr; }
+    if (kr)
+        if (int r = check_q(o.bits, o.group, D, mode == FE_CODES)) return r;
     if ((kold == nullptr) != (oold == nullptr) || (kold == nullptr) != (vold == nullptr) ||
         (kold == nullptr) != (cslog == nullptr))
         return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd: kold, vold, oold and cslog must be all set or all NULL");
-    if (!al16(k) || !al16(q) || !al16(v) || !al16(kbuf) || !al16(vbuf) || !al16(kbm) || !al16(vbm) ||
+    if (!al16(k) || !al16(q) || !al16(v) || !al16(o.kbuf) || !al16(o.vbuf) || !al16(o.kbm) || !al16(o.vbm) ||
+        !al16(o.kcode) || !al16(o.vcode) || !al16(o.kcarry) ||
         !al16(kfin) || !al16(vfin) || (kold && (!al16(kold) || !al16(vold))) || (k0 && !al16(k0)) || (v0 && !al16(v0)))
         return fail(SLOTSCAN_ERR_ALIGN, "slotscan_fwd: row buffers must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     const int NB = (int)((T + G - 1) / G);
-    ChainFwdArgs ca{q, k, gate, fr, temp, k0, o0, kbuf, am, kold, oold, cslog, kfin, ofin,
+    const bool f32 = mode == FE_F32;
+    ChainFwdArgs ca{q, k, gate, fr, temp, k0, o0, f32 ? o.kbuf : nullptr, am, kold, oold, cslog, kfin, ofin,
                     (int)T, (int)H, (int)N, (int)G, NB, eps, fr_per_token ? 1 : 0, occ_bin ? 1 : 0, 0, (int)T,
-                    kbm, kinvm, validm, (int)H, (int)H, 0};
-    RowsFwdArgs ra{v, gate, am, v0, vbuf, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB, 0, (int)T, vbm,
-                   (int)H, (int)H, 0};
+                    mode == FE_MEM ? o.kbm : nullptr, o.kinvm, o.validm, (int)H, (int)H, 0};
+    RowsFwdArgs ra{v, gate, am, v0, f32 ? o.vbuf : nullptr, vold, vfin, (int)T, (int)H, (int)N, (int)G, NB, 0,
+                   (int)T, o.vbm, (int)H, (int)H, 0,
+                   k, k0, nullptr, o.bits, o.group, o.kbm, o.kinvm, o.validm, o.kcode, o.kscale, o.vcode, o.vscale};
     // Long sequences run as a two-stream pipeline over step chunks of a multiple of G: the key chain of
-    // chunk c + 1 (latency-bound, caller's stream) overlaps the value replay of chunk c (HBM-bound, the
-    // library's side stream).  The state crosses an inner chunk boundary te as the snapshot of block te / G,
-    // which is exactly the state there: a chunk ends by writing it (it is its next block's PRE-write
-    // snapshot) and the next chunk starts from it without storing it again (fp32 contract; the bf16 copies
-    // of the fused contract cannot carry fp32 state, so there kfin and vfin carry it).  The occupancy
-    // crosses through ofin; the last chunk writes kfin, vfin, ofin.
-    const int64_t len = T >= 512 ? ((std::max<int64_t>(128, T / 8) + G - 1) / G) * G : T;
-    const int nch = (int)((T + len - 1) / len);
+    // chunk c + 1 (latency-bound, caller's stream) overlaps the row replay of chunk c (HBM-bound, the
+    // library's side stream).  fp32 contract: the state crosses an inner chunk boundary te as the snapshot
+    // of block te / G, which is exactly the state there -- a chunk ends by writing it (it is its next block's
+    // PRE-write snapshot) and the next chunk starts from it without storing it again.  The other contracts
+    // emit no fp32 state, so the chain carries its keys in kfin, the value replay its values in vfin, and a
+    // key replay its keys in kcarry (the chain may already be overwriting kfin while the replay of an
+    // earlier chunk runs).  The occupancy crosses through ofin; the last chunk writes kfin, vfin, ofin.
     hipStream_t side = nullptr;
     hipEvent_t* ev = nullptr;
     if (nch > 1)
@@ -2182,17 +2364,21 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
         const bool inner_end = ca.te < T;
         if (c > 0) {
             ca.o0 = ofin;
-            if (mem) { ca.k0 = kfin; ra.v0 = vfin; }
-            else {                                       // from the snapshot slab of block ts / G
-                ca.k0 = kbuf + (size_t)(ca.ts / G) * H * N * D;
-                ra.v0 = vbuf + (size_t)(ra.ts / G) * H * N * D;
+            if (!f32) {
+                ca.k0 = kfin;
+                ra.v0 = vfin;
+                if (kr) ra.k0 = o.kcarry;
+            } else {                                     // from the snapshot slab of block ts / G
+                ca.k0 = o.kbuf + (size_t)(ca.ts / G) * H * N * D;
+                ra.v0 = o.vbuf + (size_t)(ra.ts / G) * H * N * D;
                 ca.k0bs = ra.v0bs = NB * (int)H;
                 ca.skip0 = ra.skip0 = 1;
             }
         }
-        if (!mem) {                                      // an inner chunk ends in the next block's slab
-            ca.kfin = inner_end ? kbuf + (size_t)(ca.te / G) * H * N * D : kfin;
-            ra.vfin = inner_end ? vbuf + (size_t)(ra.te / G) * H * N * D : vfin;
+        if (kr) ra.kfin = inner_end ? o.kcarry : nullptr;
+        if (f32) {                                       // an inner chunk ends in the next block's slab
+            ca.kfin = inner_end ? o.kbuf + (size_t)(ca.te / G) * H * N * D : kfin;
+            ra.vfin = inner_end ? o.vbuf + (size_t)(ra.te / G) * H * N * D : vfin;
             ca.kfbs = ra.vfbs = inner_end ? NB * (int)H : (int)H;
         }
         {
@@ -2209,8 +2395,10 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
         }
         {
             slothost::Scope sc(SLOTSCAN_K_ROWS_FWD, rs);
-#define SLOT_RF(DD, TT) { if (mem) slothost::launch((rows_fwd<DD, TT, true>), grid, block, 0, rs, ra); \
-                          else slothost::launch((rows_fwd<DD, TT, false>), grid, block, 0, rs, ra); }
+#define SLOT_RF(DD, TT) { if (mode == FE_MEM) slothost::launch((rows_fwd<DD, TT, RF_BF>), grid, block, 0, rs, ra); \
+                          else if (mode == FE_MEMQ) slothost::launch((rows_fwd<DD, TT, RF_MEMQ>), grid, block, 0, rs, ra); \
+                          else if (mode == FE_CODES) slothost::launch((rows_fwd<DD, TT, RF_CODES>), grid, block, 0, rs, ra); \
+                          else slothost::launch((rows_fwd<DD, TT, RF_F32>), grid, block, 0, rs, ra); }
             if (D == 128) {
                 if (dtype == SLOTSCAN_BF16) SLOT_RF(128, bf16_t) else SLOT_RF(128, float)
             } else {
@@ -2236,10 +2424,10 @@ extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dty
                             float* kbuf, float* vbuf, int32_t* am,
                             float* kold, float* vold, float* oold, float* cslog,
                             float* kfin, float* vfin, float* ofin, void* stream) {
-    if (!kbuf || !vbuf) return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd: a required pointer is NULL");
+    FwdOut o{};
+    o.mode = FE_F32; o.kbuf = kbuf; o.vbuf = vbuf;
     return scan_fwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, k0, v0, o0,
-                    kbuf, vbuf, nullptr, nullptr, nullptr, nullptr, am, kold, vold, oold, cslog,
-                    kfin, vfin, ofin, stream);
+                    o, am, kold, vold, oold, cslog, kfin, vfin, ofin, stream);
 }
 
 extern "C" int slotscan_fwd_mem(const void* k, const void* q, const void* v, int dtype,
@@ -2250,10 +2438,44 @@ extern "C" int slotscan_fwd_mem(const void* k, const void* q, const void* v, int
                                 void* kb, void* vb, float* kinv, uint8_t* valid, int32_t* am,
                                 float* kold, float* vold, float* oold, float* cslog,
                                 float* kfin, float* vfin, float* ofin, void* stream) {
-    if (!kb || !vb || !kinv || !valid) return fail(SLOTSCAN_ERR_NULL, "slotscan_fwd_mem: a required pointer is NULL");
+    FwdOut o{};
+    o.mode = FE_MEM; o.kbm = (bf16_t*)kb; o.vbm = (bf16_t*)vb; o.kinvm = kinv; o.validm = valid;
     return scan_fwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, k0, v0, o0,
-                    nullptr, nullptr, (bf16_t*)kb, (bf16_t*)vb, kinv, valid, am, kold, vold, oold, cslog,
-                    kfin, vfin, ofin, stream);
+                    o, am, kold, vold, oold, cslog, kfin, vfin, ofin, stream);
+}
+
+extern "C" size_t slotscan_fwd_carry_bytes(int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G) {
+    if (B < 1 || T < 1 || H < 1 || N < 1 || D < 1 || G < 1) return 0;
+    return fwd_chunk_len(T, G) < T ? (size_t)B * H * N * D * sizeof(float) : 0;
+}
+
+extern "C" int slotscan_fwd_memq(const void* k, const void* q, const void* v, int dtype,
+                                 const float* gate, const float* fr, int fr_per_token, const float* temp,
+                                 int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                                 float eps, int occ_bin, int bits, int64_t group,
+                                 const float* k0, const float* v0, const float* o0,
+                                 void* kb, void* vb, float* kinv, uint8_t* valid, int32_t* am,
+                                 float* kold, float* vold, float* oold, float* cslog,
+                                 float* kfin, float* vfin, float* ofin, float* kcarry, void* stream) {
+    FwdOut o{};
+    o.mode = FE_MEMQ; o.kbm = (bf16_t*)kb; o.vbm = (bf16_t*)vb; o.kinvm = kinv; o.validm = valid;
+    o.bits = bits; o.group = (int)group; o.kcarry = kcarry;
+    return scan_fwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, k0, v0, o0,
+                    o, am, kold, vold, oold, cslog, kfin, vfin, ofin, stream);
+}
+
+extern "C" int slotscan_fwd_codes(const void* k, const void* q, const void* v, int dtype,
+                                  const float* gate, const float* fr, int fr_per_token, const float* temp,
+                                  int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                                  float eps, int occ_bin, int bits, int64_t group,
+                                  const float* k0, const float* v0, const float* o0,
+                                  int8_t* kcode, float* kscale, int8_t* vcode, float* vscale, int32_t* am,
+                                  float* kfin, float* vfin, float* ofin, float* kcarry, void* stream) {
+    FwdOut o{};
+    o.mode = FE_CODES; o.kcode = kcode; o.kscale = kscale; o.vcode = vcode; o.vscale = vscale;
+    o.bits = bits; o.group = (int)group; o.kcarry = kcarry;
+    return scan_fwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, k0, v0, o0,
+                    o, am, nullptr, nullptr, nullptr, nullptr, kfin, vfin, ofin, stream);
 }
 
 // The untracked G = 8 row kernel (rows_bwd<.., G8 = true, ..>) needs two snapshot boundaries at fixed
@@ -2289,11 +2511,13 @@ static int scan_bwd(const void* k, const void* q, const void* v, int dtype,
                     const int32_t* am, const float* kold, const float* vold, const float* oold,
                     const float* cslog, const float* kfin, const float* vfin, const float* ofin,
                     const float* dkbuf, const float* dvbuf, const bf16_t* dkbm, const bf16_t* dvbm,
-                    const float* dkinvm, void* workspace,
+                    const float* dkinvm, int qbits, int qgroup, void* workspace,
                     void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
                     void* stream) {
     if (int r = check_common(B, T, H, N, D, G, dtype)) return r;
     const bool mem = dkbm != nullptr;
+    if (mem && qbits)
+        if (int r = check_q(qbits, qgroup, D, false)) return r;
     if (!k || !q || !v || !gate || !fr || !temp || !am || !kold || !vold || !oold || !cslog || !kfin || !vfin || !ofin ||
         (mem ? (!dvbm || !dkinvm) : (!dkbuf || !dvbuf)) || !workspace || !dk || !dq || !dv || !dgate || !dfr || !dtemp)
         return fail(SLOTSCAN_ERR_NULL, "slotscan_bwd: a required pointer is NULL");
@@ -2308,7 +2532,7 @@ static int scan_bwd(const void* k, const void* q, const void* v, int dtype,
     const size_t dnb = (size_t)B * H * N * T * sizeof(float);
     float* part = (float*)((char*)workspace + ((dnb + 255) & ~(size_t)255));
     RowsBwdArgs ra{k, v, gate, am, kold, vold, kfin, vfin, dkbuf, dvbuf, dk, dv, dn,
-                   (int)T, (int)H, (int)N, (int)G, NB, dkbm, dvbm, dkinvm};
+                   (int)T, (int)H, (int)N, (int)G, NB, dkbm, dvbm, dkinvm, mem ? qbits : 0, qgroup};
     dim3 grid((unsigned)(B * H), (unsigned)((N + 31) / 32)), block(512);
     hipError_t e;
     {
@@ -2358,7 +2582,7 @@ extern "C" int slotscan_bwd(const void* k, const void* q, const void* v, int dty
                             void* stream) {
     if (!dkbuf || !dvbuf) return fail(SLOTSCAN_ERR_NULL, "slotscan_bwd: a required pointer is NULL");
     return scan_bwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, am, kold, vold,
-                    oold, cslog, kfin, vfin, ofin, dkbuf, dvbuf, nullptr, nullptr, nullptr, workspace,
+                    oold, cslog, kfin, vfin, ofin, dkbuf, dvbuf, nullptr, nullptr, nullptr, 0, 0, workspace,
                     dk, dq, dv, dgate, dfr, dtemp, stream);
 }
 
@@ -2408,7 +2632,7 @@ extern "C" int slotscan_bwd_noalloc(const void* k, const void* q, const void* v,
     void* ws = nullptr;
     if (int r = scratch_ptr(&ws)) return r;
     return scan_bwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, am, kold, vold,
-                    oold, cslog, kfin, vfin, ofin, dkbuf, dvbuf, nullptr, nullptr, nullptr, ws,
+                    oold, cslog, kfin, vfin, ofin, dkbuf, dvbuf, nullptr, nullptr, nullptr, 0, 0, ws,
                     dk, dq, dv, dgate, dfr, dtemp, stream);
 }
 
@@ -2424,5 +2648,20 @@ extern "C" int slotscan_bwd_mem(const void* k, const void* q, const void* v, int
     if (!dkb || !dvb || !dkinv) return fail(SLOTSCAN_ERR_NULL, "slotscan_bwd_mem: a required pointer is NULL");
     return scan_bwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, am, kold, vold,
                     oold, cslog, kfin, vfin, ofin, nullptr, nullptr, (const bf16_t*)dkb, (const bf16_t*)dvb, dkinv,
-                    workspace, dk, dq, dv, dgate, dfr, dtemp, stream);
+                    0, 0, workspace, dk, dq, dv, dgate, dfr, dtemp, stream);
+}
+
+extern "C" int slotscan_bwd_memq(const void* k, const void* q, const void* v, int dtype,
+                                 const float* gate, const float* fr, int fr_per_token, const float* temp,
+                                 int64_t B, int64_t T, int64_t H, int64_t N, int64_t D, int64_t G,
+                                 float eps, int occ_bin, int bits, int64_t group,
+                                 const int32_t* am, const float* kold, const float* vold, const float* oold,
+                                 const float* cslog, const float* kfin, const float* vfin, const float* ofin,
+                                 const void* dkb, const void* dvb, const float* dkinv, void* workspace,
+                                 void* dk, void* dq, void* dv, float* dgate, float* dfr, float* dtemp,
+                                 void* stream) {
+    if (!dkb || !dvb || !dkinv) return fail(SLOTSCAN_ERR_NULL, "slotscan_bwd_memq: a required pointer is NULL");
+    return scan_bwd(k, q, v, dtype, gate, fr, fr_per_token, temp, B, T, H, N, D, G, eps, occ_bin, am, kold, vold,
+                    oold, cslog, kfin, vfin, ofin, nullptr, nullptr, (const bf16_t*)dkb, (const bf16_t*)dvb, dkinv,
+                    bits, (int)group, workspace, dk, dq, dv, dgate, dfr, dtemp, stream);
 }

@@ -80,9 +80,26 @@ def _prep(k, q, v, gate, fr, temp, hard_gate):
     return dt, k_, q_, v_, g, fr_, frt, temp_
 
 
-def _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, state=None, mem=False):
+def _state_in(state, B, H, N, D):
+    if state is None:
+        return None, None, None
+    k0, v0, o0 = (x.contiguous().to(torch.float32) for x in state)
+    if k0.shape != (B * H, N, D) or v0.shape != (B * H, N, D) or o0.shape != (B * H, N):
+        raise ValueError("state must be (K (B*H,N,D), V (B*H,N,D), o (B*H,N))")
+    return k0, v0, o0
+
+
+def _carry(B, T, H, N, D, G, dev):
+    """The key replay's chunk carry (slotscan_fwd_carry_bytes), or None when the forward runs as one chunk."""
+    nb = L.lib().slotscan_fwd_carry_bytes(B, T, H, N, D, G)
+    return torch.empty(nb // 4, device=dev, dtype=torch.float32) if nb else None
+
+
+def _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, state=None, mem=False, bits=0, group=16):
     """One forward launch.  mem=False: returns (kbuf, vbuf, am, logs..., final state).  mem=True: the writer
-    epilogue is fused in, and the first two results are replaced by the four (kb, vb, kinv, valid)."""
+    epilogue is fused in, and the first two results are replaced by the four (kb, vb, kinv, valid); with
+    bits > 0 it is the quantised epilogue (slotscan_fwd_memq: the storage quantiser's values, kinv and valid
+    of the quantised keys)."""
     B, T, H, D = k_.shape
     NB = (T + G - 1) // G
     dev = k_.device
@@ -98,15 +115,19 @@ def _fwd(k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, state=Non
     if logs:
         kold, vold, oold, cslog = e(B, T, H, D), e(B, T, H, D), e(B, T, H), e(B * H, T, N)
     kfin, vfin, ofin = e(B * H, N, D), e(B * H, N, D), e(B * H, N)
-    k0 = v0 = o0 = None
-    if state is not None:
-        k0, v0, o0 = (x.contiguous().to(f32) for x in state)
-        if k0.shape != (B * H, N, D) or v0.shape != (B * H, N, D) or o0.shape != (B * H, N):
-            raise ValueError("state must be (K (B*H,N,D), V (B*H,N,D), o (B*H,N))")
-    head = (L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_), int(frt), L.ptr(temp_),
-            B, T, H, N, D, G, float(eps), int(bool(occ_bin)), L.ptr(k0), L.ptr(v0), L.ptr(o0))
+    k0, v0, o0 = _state_in(state, B, H, N, D)
+    pre = (L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_), int(frt), L.ptr(temp_),
+           B, T, H, N, D, G, float(eps), int(bool(occ_bin)))
+    head = pre + (L.ptr(k0), L.ptr(v0), L.ptr(o0))
     tail = (L.ptr(am), L.ptr(kold), L.ptr(vold), L.ptr(oold), L.ptr(cslog), L.ptr(kfin), L.ptr(vfin),
-            L.ptr(ofin), L.stream_of(dev))
+            L.ptr(ofin))
+    if mem and bits:
+        kc = _carry(B, T, H, N, D, G, dev)
+        rc = L.lib().slotscan_fwd_memq(*pre, int(bits), int(group), L.ptr(k0), L.ptr(v0), L.ptr(o0), L.ptr(kbuf),
+                                       L.ptr(vbuf), L.ptr(kinv), L.ptr(valid), *tail, L.ptr(kc), L.stream_of(dev))
+        L.check(rc, "slotscan_fwd_memq")
+        return (kbuf, vbuf, kinv, valid), am, kold, vold, oold, cslog, kfin, vfin, ofin
+    tail = tail + (L.stream_of(dev),)
     if mem:
         rc = L.lib().slotscan_fwd_mem(*head, L.ptr(kbuf), L.ptr(vbuf), L.ptr(kinv), L.ptr(valid), *tail)
         L.check(rc, "slotscan_fwd_mem")
@@ -143,9 +164,9 @@ class _KVScanHip(torch.autograd.Function):
         return _bwd(ctx, (dkbuf, dvbuf), mem=False) + (None,) * 5
 
 
-def _bwd(ctx, grads, mem):
-    """One backward launch: grads = (dkbuf, dvbuf) fp32, or (dkb, dvb bf16, dkinv fp32) with mem=True.
-    Returns the gradients of (k, q, v, gate, fr, temp)."""
+def _bwd(ctx, grads, mem, bits=0, group=16):
+    """One backward launch: grads = (dkbuf, dvbuf) fp32, or (dkb, dvb bf16, dkinv fp32) with mem=True (and
+    the quantised epilogue's backward with bits > 0).  Returns the gradients of (k, q, v, gate, fr, temp)."""
     k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, cslog, kfin, vfin, ofin = ctx.saved_tensors
     N, G, frt, eps, occ_bin, dt, fr_shape, temp_is_tensor = ctx.meta
     B, T, H, D = k_.shape
@@ -156,11 +177,12 @@ def _bwd(ctx, grads, mem):
     dg = torch.empty(B, T, H, device=dev, dtype=f32)
     dfr = torch.empty_like(fr_)
     dtemp = torch.empty(1, device=dev, dtype=f32)
+    qa = (int(bits), int(group)) if mem and bits else ()
     args = (L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_), int(frt), L.ptr(temp_),
-            B, T, H, N, D, G, float(eps), int(occ_bin), L.ptr(am), L.ptr(kold), L.ptr(vold), L.ptr(oold),
+            B, T, H, N, D, G, float(eps), int(occ_bin)) + qa + (L.ptr(am), L.ptr(kold), L.ptr(vold), L.ptr(oold),
             L.ptr(cslog), L.ptr(kfin), L.ptr(vfin), L.ptr(ofin)) + tuple(L.ptr(x) for x in grads) + \
         (L.ptr(ws), L.ptr(dk), L.ptr(dq), L.ptr(dv), L.ptr(dg), L.ptr(dfr), L.ptr(dtemp), L.stream_of(dev))
-    name = "slotscan_bwd_mem" if mem else "slotscan_bwd"
+    name = ("slotscan_bwd_memq" if qa else "slotscan_bwd_mem") if mem else "slotscan_bwd"
     L.check(getattr(L.lib(), name)(*args), name)
     dfr = dfr.reshape(fr_shape) if not frt else dfr
     dtemp = dtemp.reshape(()) if temp_is_tensor else None
@@ -232,17 +254,18 @@ class _KVScanMemHip(torch.autograd.Function):
     """The scan with the writer epilogue fused in: forward returns (kb, vb, kinv, valid) directly."""
 
     @staticmethod
-    def forward(ctx, k, q, v, gate, fr, temp, N, G, hard_gate, eps, occ_bin):
+    def forward(ctx, k, q, v, gate, fr, temp, N, G, hard_gate, eps, occ_bin, bits=0, group=16):
         D = k.shape[-1]
         if v.shape[-1] != D:
             raise ValueError("the HIP scan needs DK == DV")
         dt, k_, q_, v_, g, fr_, frt, temp_ = _prep(k, q, v, gate, fr, temp, hard_gate)
         logs = any(ctx.needs_input_grad[:6])
         (kb, vb, kinv, valid), am, kold, vold, oold, cslog, kfin, vfin, ofin = _fwd(
-            k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, mem=True)
+            k_, q_, v_, g, fr_, frt, temp_, N, G, eps, occ_bin, dt, logs, mem=True, bits=bits, group=group)
         if logs:
             ctx.save_for_backward(k_, q_, v_, g, fr_, temp_, am, kold, vold, oold, cslog, kfin, vfin, ofin)
         ctx.meta = (int(N), int(G), frt, float(eps), bool(occ_bin), dt, tuple(fr.shape), torch.is_tensor(temp))
+        ctx.q = (int(bits), int(group))
         ctx.mark_non_differentiable(valid)
         return kb, vb, kinv, valid
 
@@ -257,7 +280,7 @@ class _KVScanMemHip(torch.autograd.Function):
         dvb = torch.zeros(B, NB, H, N, D, device=dev, dtype=bf) if dvb is None else dvb.contiguous().to(bf)
         dkinv = torch.zeros(B, NB, H, N, device=dev, dtype=torch.float32) if dkinv is None \
             else dkinv.contiguous().to(torch.float32)
-        return _bwd(ctx, (dkb, dvb, dkinv), mem=True) + (None,) * 5
+        return _bwd(ctx, (dkb, dvb, dkinv), mem=True, bits=ctx.q[0], group=ctx.q[1]) + (None,) * 7
 
 
 def kv_scan_c(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
@@ -276,25 +299,32 @@ def kv_scan_c(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e
 
 
 def kv_scan_mem(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
-                occ_bin=False, dtype=torch.bfloat16):
-    """kv_scan_g followed by the writer layer's full-precision epilogue, in one forward and one backward
-    (memlm_sh.py:453-456 then :473-475): returns (kb, vb, kinv, valid) with kb, vb the snapshots in bf16,
-    kinv = rsqrt(max(|K|^2, 1e-12)) fp32 and valid = |K|^2 > 1e-12 (bool), each (B, ceil(T/G), H, N[, D]).
+                occ_bin=False, dtype=torch.bfloat16, bits=0, group=16):
+    """kv_scan_g followed by the writer layer's epilogue, in one forward and one backward (memlm_sh.py:453-456
+    then :466-475): returns (kb, vb, kinv, valid), each (B, ceil(T/G), H, N[, D]).
+    bits = 0: the full-precision epilogue (:473-475) -- kb, vb the snapshots in bf16, kinv =
+    rsqrt(max(|K|^2, 1e-12)) fp32, valid = |K|^2 > 1e-12 (bool).
+    bits > 0: the storage quantiser (:468-471, _quantize_mem :231-234), the setting sh25 trains its last 20 %
+    in (run_sh25.sh:224, bits 3, group 16): kb, vb = _fq(snapshot, bits, group) in bf16 with a
+    straight-through gradient, kinv and valid from the quantised keys.
     In the row-sparse mode (hard, detached address, DK == DV) the fp32 snapshots are never materialised.
     Every other mode runs the general-mode scan and then the epilogue kernels (two passes, the same
     outputs and autograd).  Only the bf16 copies (the activation dtype of training) are emitted."""
     if dtype != torch.bfloat16:
         raise NotImplementedError("the fused scan + epilogue emits bf16 copies only; use kv_scan_g and "
                                   "writer_epilogue for another dtype")
+    MH._check_q(int(bits), int(group), k.shape[-1])
     if _unsupported(hard, detach_addr, k.shape[-1], v.shape[-1], N) is not None:
         why = _unsupported_gen(k.shape[-1], v.shape[-1], N)
         if why:
             raise NotImplementedError(why)
         kbuf, vbuf = kv_scan_c(k, v, gate, fr, N, temp, G=G, hard=hard, hard_gate=hard_gate, eps=eps,
                                detach_addr=detach_addr, q=q, occ_bin=occ_bin)
+        if bits:
+            return MH.quantize_mem(kbuf, vbuf, int(bits), int(group), dtype=dtype)
         return MH.writer_epilogue(kbuf, vbuf, dtype=dtype)
     return _KVScanMemHip.apply(k, k if q is None else q, v, gate, fr, temp, N, int(G), bool(hard_gate), eps,
-                               bool(occ_bin))
+                               bool(occ_bin), int(bits), int(group))
 
 
 def kv_scan_g(k, v, gate, fr, N, temp, G=16, hard=False, hard_gate=False, eps=1e-4, detach_addr=False, q=None,
@@ -364,10 +394,34 @@ def kv_scan_stream(k, v, gate, fr, N, temp, G=8, hard_gate=False, eps=1e-4, q=No
 @torch.no_grad()
 def kv_scan_stream_q(k, v, gate, fr, N, temp, G=8, hard_gate=False, eps=1e-4, q=None, occ_bin=False, state=None,
                      bits=8, group=None):
-    """kv_scan_stream with the emitted copies in the storage quantiser's integer form (memlm_sh.py:221-228):
-    returns ((kcodes, kscales), (vcodes, vscales), state_out), codes int8 (B, NB, H, N, D) and fp32 scales
-    (B, NB, H, N, D // group).  bits = 8 with group = D (the default) is one fp32 absmax scale per row."""
-    kbuf, vbuf, st = kv_scan_stream(k, v, gate, fr, N, temp, G=G, hard_gate=hard_gate, eps=eps, q=q,
-                                    occ_bin=occ_bin, state=state)
-    grp = k.shape[-1] if group is None else int(group)
-    return MH.fq_codes(kbuf, bits, grp), MH.fq_codes(vbuf, bits, grp), st
+    """kv_scan_stream with the emitted copies in the storage quantiser's integer form (memlm_sh.py:221-228),
+    in one fused forward (slotscan_fwd_codes: the chain stores no snapshots, the row replay rebuilds every key
+    and value row and emits its codes): returns ((kcodes, kscales), (vcodes, vscales), state_out), codes int8
+    (B, NB, H, N, D) and fp32 scales (B, NB, H, N, D // group), bitwise the codes of kv_scan_stream's fp32
+    snapshots.  bits = 8 with group = D (the default) is one fp32 absmax scale per row."""
+    why = _unsupported(True, True, k.shape[-1], v.shape[-1], N)
+    if why:
+        raise NotImplementedError(why)
+    qq = k if q is None else q
+    dt, k_, q_, v_, g, fr_, frt, temp_ = _prep(k, qq, v, gate, fr, temp, hard_gate)
+    B, T, H, D = k_.shape
+    grp = D if group is None else int(group)
+    MH._check_q(int(bits), grp, D)
+    if not bits:
+        raise ValueError("kv_scan_stream_q needs bits in 2..8")
+    NB = (T + G - 1) // G
+    dev = k_.device
+    e = lambda *s_, dtype=torch.float32: torch.empty(*s_, device=dev, dtype=dtype)
+    kc, vc = e(B, NB, H, N, D, dtype=torch.int8), e(B, NB, H, N, D, dtype=torch.int8)
+    ks, vs = e(B, NB, H, N, D // grp), e(B, NB, H, N, D // grp)
+    am = e(B, T, H, dtype=torch.int32)
+    kfin, vfin, ofin = e(B * H, N, D), e(B * H, N, D), e(B * H, N)
+    k0, v0, o0 = _state_in(state, B, H, N, D)
+    kcar = _carry(B, T, H, N, D, int(G), dev)
+    rc = L.lib().slotscan_fwd_codes(L.ptr(k_), L.ptr(q_), L.ptr(v_), L.dtype_code(dt), L.ptr(g), L.ptr(fr_),
+                                    int(frt), L.ptr(temp_), B, T, H, int(N), D, int(G), float(eps),
+                                    int(bool(occ_bin)), int(bits), grp, L.ptr(k0), L.ptr(v0), L.ptr(o0),
+                                    L.ptr(kc), L.ptr(ks), L.ptr(vc), L.ptr(vs), L.ptr(am), L.ptr(kfin),
+                                    L.ptr(vfin), L.ptr(ofin), L.ptr(kcar), L.stream_of(dev))
+    L.check(rc, "slotscan_fwd_codes")
+    return (kc, ks), (vc, vs), (kfin, vfin, ofin)

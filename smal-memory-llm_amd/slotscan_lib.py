@@ -30,6 +30,13 @@ SIGNATURES = {
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "slotscan_fwd_mem": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
                                 _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32] + [_vp] * 16),
+    "slotscan_fwd_carry_bytes": (_sz, [_i64] * 6),
+    "slotscan_fwd_memq": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
+                                 _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i64] + [_vp] * 17),
+    "slotscan_bwd_memq": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
+                                 _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i64] + [_vp] * 19),
+    "slotscan_fwd_codes": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp,
+                                  _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i64] + [_vp] * 13),
     "slotscan_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64]),
     "slotscan_bwd_plan": (_i32, [_i64, _i64, _i64, _i64, _i64, _i32]),
     "slotscan_profile": (_i32, [_i32]),

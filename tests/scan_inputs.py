@@ -38,3 +38,16 @@ def upstream(shape, seed):
 
 def np64(x):
     return None if x is None else x.detach().double().cpu().numpy()
+
+
+def assert_no_flips(info):
+    """Slot addresses bit-exact: the GPU's row equals the fp64 oracle's own argmax at every step (the
+    reference's acceptance is "rows differing == 0", kvu/test_cuda.py:62).  On failure the message gives the
+    count and the worst fp64 margin z(argmax) - z(GPU row), so a genuine near-tie on a new seed (|margin|
+    far below what fp32 scores resolve) can be told apart from a wrong address."""
+    bad = ~info["agree"]
+    n = int(bad.sum())
+    if n:
+        worst = float(np.abs(info["margin"][bad]).max())
+        raise AssertionError(f"{n} address disagreements with the fp64 oracle, worst fp64 margin {worst:.3e}")
+    return n

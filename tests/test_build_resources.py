@@ -19,3 +19,17 @@ def test_untracked_rows_kernels_use_no_scratch():
         assert d["ScratchSize [bytes/lane]"] == "0", f"{name} uses scratch: {d}"
         assert d["VGPRs Spill"] == "0", f"{name} spills: {d}"
         assert d["Dynamic Stack"] == "False", name
+
+
+def test_proj_gemm_uses_no_scratch():
+    """proj_gemm fills its LDS ring with direct global -> LDS loads issued through inline asm (untracked by the
+    compiler) and waits for each stage with a counted `s_waitcnt vmcnt(n)` (csrc/slotproj.hip).  A scratch
+    spill or reload in the k loop would be one more vector-memory operation on the same counter, so a stage
+    could be published before its loads land.  The counts hold only while the kernel has no scratch."""
+    rep = build.resource_report("slotproj.hip")
+    kern = {n: d for n, d in rep.items() if n.startswith("proj_gemm") or "proj_gemm<" in n}
+    assert kern, sorted(rep)
+    for name, d in kern.items():
+        assert d["ScratchSize [bytes/lane]"] == "0", f"{name} uses scratch: {d}"
+        assert d["VGPRs Spill"] == "0", f"{name} spills: {d}"
+        assert d["Dynamic Stack"] == "False", name

@@ -16,7 +16,7 @@ import torch
 
 from oracle import read_oracle as RO
 from oracle import scan_oracle as SO
-from scan_inputs import np64, scan_inputs, upstream
+from scan_inputs import assert_no_flips, np64, scan_inputs, upstream
 
 pytestmark = pytest.mark.gpu
 
@@ -112,8 +112,7 @@ def _check(B, T, H, N, D, G, frt, occb, sep_q, hardg, seed, dtype=torch.float32,
     # ---- against the oracle
     am = _am(k, q, v, g, fr, N, G, occb, hardg)
     okb, info, ogr = _oracle_grads(k, q, v, g, fr, N, G, occb, hardg, am, wk, wv, wi)
-    bad = ~info["agree"]
-    assert bad.sum() == 0 or np.abs(info["margin"][bad]).max() < 1e-4
+    assert_no_flips(info)
     _, ova = RO.writer_epilogue(okb)
     assert np.array_equal(valid.cpu().numpy(), ova)
     assert _rel(kb.float().cpu(), okb) < 2 ** -8
@@ -160,3 +159,97 @@ def test_scan_mem_refuses_other_copy_dtypes():
         KH.kv_scan_mem(k, v, g, fr, 16, TEMP, G=8, hard=True, detach_addr=True, q=q, dtype=torch.float32)
     with pytest.raises(NotImplementedError):
         KH.kv_scan_mem(k, v, g, fr, 16, TEMP, G=8, hard=False, detach_addr=True, q=q, dtype=torch.float16)
+
+
+# ---------------------------------------------------------------- the quantised epilogue (sh25's QAT phase)
+def _run_q(fused, k, q, v, g, fr, N, G, occb, hardg, wk, wv, wi, bits, group):
+    """As _run, with the storage quantiser: fused = kv_scan_mem(bits, group) (slotscan_fwd_memq /
+    slotscan_bwd_memq), unfused = kv_scan_c then quantize_mem (the two-pass path, memlm_sh.py:453-456 then
+    :468-471).  Also returns the unfused path's fp32 snapshots."""
+    kk, qq, vv, gg, ff, tp = _leaves(k, q, v, g, fr)
+    kw = dict(G=G, hard=True, hard_gate=hardg, detach_addr=True, q=qq, occ_bin=occb)
+    snaps = None
+    if fused:
+        kb, vb, kinv, valid = KH.kv_scan_mem(kk, vv, gg, ff, N, tp, bits=bits, group=group, **kw)
+    else:
+        kbuf, vbuf = KH.kv_scan_c(kk, vv, gg, ff, N, tp, **kw)
+        kb, vb, kinv, valid = MH.quantize_mem(kbuf, vbuf, bits, group, dtype=torch.bfloat16)
+        snaps = (kbuf.detach(), vbuf.detach())
+    loss = (kb.float() * wk.to(DEV)).sum() + (vb.float() * wv.to(DEV)).sum() + (kinv * wi.to(DEV)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    grads = dict(dk=kk.grad, dv=vv.grad, dgate=gg.grad, dfr=ff.grad, dtemp=tp.grad,
+                 dq=None if qq is None else qq.grad)
+    return (kb.detach(), vb.detach(), kinv.detach(), valid), grads, snaps
+
+
+def _check_q(B, T, H, N, D, G, frt, occb, sep_q, hardg, bits, group, seed, dtype=torch.float32):
+    print(f"memq case B{B} T{T} H{H} N{N} D{D} G{G} bits={bits} group={group} frt={frt} occb={occb} q={sep_q} "
+          f"hardg={hardg} {dtype}", flush=True)
+    k, q, v, g, fr = scan_inputs(B, T, H, D, seed, sep_q=sep_q, frt=frt, dtype=dtype)
+    NB = (T + G - 1) // G
+    wk, wv = upstream((B, NB, H, N, D), seed + 1000)
+    wi = torch.randn(B, NB, H, N, generator=torch.Generator().manual_seed(seed + 2000))
+    (kb, vb, kinv, valid), gf, _ = _run_q(True, k, q, v, g, fr, N, G, occb, hardg, wk, wv, wi, bits, group)
+    (kb0, vb0, kinv0, valid0), gu, (kbuf, vbuf) = _run_q(False, k, q, v, g, fr, N, G, occb, hardg, wk, wv, wi,
+                                                         bits, group)
+    # ---- forward against the two-pass path: the same quantiser values, bitwise
+    assert kb.dtype == torch.bfloat16 and kb.shape == (B, NB, H, N, D) and kinv.shape == (B, NB, H, N)
+    assert torch.equal(kb, kb0) and torch.equal(vb, vb0)
+    assert torch.equal(valid, valid0)
+    np.testing.assert_allclose(kinv.cpu().numpy(), kinv0.cpu().numpy(), rtol=2e-6)
+    # ---- the quantiser against the oracle on the same fp32 snapshots (bitwise), the snapshots against the
+    # fp64 oracle teacher-forced on the GPU's addresses
+    okq, ovq, okinv, ova = RO.quantize_mem(kbuf.cpu().numpy(), vbuf.cpu().numpy(), bits, group)
+    np.testing.assert_array_equal(kb.float().cpu().numpy(), RO.bf16_round(okq))
+    np.testing.assert_array_equal(vb.float().cpu().numpy(), RO.bf16_round(ovq))
+    assert np.array_equal(valid.cpu().numpy(), ova)
+    np.testing.assert_allclose(kinv.cpu().numpy(), okinv, rtol=2e-6)
+    am = _am(k, q, v, g, fr, N, G, occb, hardg)
+    kn, qn, vn, gn, frn = np64(k), np64(q), np64(v), np64(g), np64(fr)
+    okb, ovb, info = SO.scan_forward(kn, vn, gn, frn, N, TEMP, G=G, hard=True, hard_gate=hardg, eps=1e-4,
+                                     detach_addr=True, q=qn, occ_bin=occb, teacher=am)
+    assert_no_flips(info)
+    assert _rel(kbuf.cpu(), okb) < 1e-5 and _rel(vbuf.cpu(), ovb) < 1e-5
+    # ---- gradients: against the two-pass path, and against the oracle with the quantised epilogue's
+    # autograd folded into the snapshot upstream (straight-through: dkbuf = dkb + 2 kq dnsq, kq = _fq(K))
+    names = ["dk", "dv", "dgate", "dfr", "dtemp"] + (["dq"] if sep_q else [])
+    tol_u = 5e-5 if dtype == torch.float32 else 1e-2
+    for n in names:
+        a, b = gf[n].double().cpu().numpy(), gu[n].double().cpu().numpy()
+        assert _rel(a, b) < tol_u, f"{n} fused vs two-pass rel err {_rel(a, b):.3e}"
+    kq = okq.astype(np.float64)
+    nsq = (kq * kq).sum(-1)
+    kiq = 1.0 / np.sqrt(np.maximum(nsq, 1e-12))
+    dnsq = np.where(nsq >= 1e-12, -0.5 * kiq ** 3 * np64(wi), 0.0)
+    dkb = np64(wk.to(torch.bfloat16)) + 2.0 * kq * dnsq[..., None]
+    ogr = SO.scan_backward(kn, vn, gn, frn, N, TEMP, okb, ovb, info, dkb, np64(wv.to(torch.bfloat16)), G=G,
+                           hard=True, hard_gate=hardg, eps=1e-4, detach_addr=True, q=qn, occ_bin=occb)
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    worst = {}
+    for n in names:
+        ref = ogr[n] if (n != "dk" or sep_q) else ogr["dk"] + ogr["dq"]
+        worst[n] = _rel(gf[n].double().cpu().numpy().reshape(np.shape(ref)), ref)
+    print("   rel err vs oracle:", {kk: f"{x:.1e}" for kk, x in worst.items()}, flush=True)
+    for n, x in worst.items():
+        assert x < tol, f"{n} rel err {x:.3e} >= {tol}"
+
+
+MEMQ_CASES = [  # B, T, H, N, D, G, frt, occb, sep_q, hardg, bits, group
+    (2, 256, 2, 192, 128, 8, True, True, True, False, 3, 16),      # sh25's QAT setting (run_sh25.sh:224)
+    (2, 200, 2, 96, 128, 8, True, True, True, False, 3, 16),       # T % 16 != 0: the general row kernel
+    (2, 250, 3, 192, 64, 8, True, True, True, False, 4, 8),        # D = 64, group 8 (two lanes)
+    (1, 600, 2, 96, 128, 8, True, True, True, False, 3, 16),       # chunked forward: the key replay's carry
+    (1, 300, 3, 50, 128, 7, False, True, True, True, 8, 128),      # one scale per row, G = 7, hard gate
+    (1, 300, 2, 40, 64, 16, False, False, False, False, 2, 64),    # q = k, scalar fr, group = D = 64
+    (1, 5, 2, 20, 128, 8, True, True, True, False, 5, 32),         # T < G, group 32
+]
+
+
+@pytest.mark.parametrize("case", MEMQ_CASES, ids=lambda c: "B{}T{}H{}N{}D{}G{}f{}o{}q{}h{}b{}g{}".format(*c))
+def test_scan_memq_matches_two_pass_and_oracle(case):
+    _check_q(*case, seed=37)
+
+
+def test_scan_memq_bf16_tokens():
+    _check_q(2, 256, 2, 192, 128, 8, True, True, True, False, 3, 16, seed=39, dtype=torch.bfloat16)

@@ -143,3 +143,37 @@ def test_proj_validation_rejects_before_launch(M, N, K, code):
     an error code and message, before any GPU call (so this runs without a GPU)."""
     assert L.lib().slotproj_fwd(None, None, None, M, N, K, None, None) == code
     assert L.lib().slotscan_last_error()
+
+
+def _codes_call(**over):
+    a = dict(B=1, T=8, H=1, N=16, D=64, G=8, bits=8, group=64, kcode=1 << 20, kscale=1 << 20, vcode=1 << 20,
+             vscale=1 << 20, kcarry=None)
+    a.update(over)
+    vp = lambda x: None if x is None else ctypes.c_void_p(x)
+    p = vp(1 << 20)
+    return L.lib().slotscan_fwd_codes(p, p, p, 0, p, p, 1, p, a["B"], a["T"], a["H"], a["N"], a["D"], a["G"], 1e-4,
+                                      1, a["bits"], a["group"], None, None, None, vp(a["kcode"]), vp(a["kscale"]),
+                                      vp(a["vcode"]), vp(a["vscale"]), p, p, p, p, vp(a["kcarry"]), None)
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(bits=1), 1), (dict(bits=9), 1), (dict(group=3), 1), (dict(group=128), 1), (dict(group=2), 1),
+    (dict(kcode=None), 3), (dict(vscale=None), 3),
+    (dict(T=1024), 3),                        # a multi-chunk forward needs the key replay's carry
+    (dict(kcode=(1 << 20) + 4), 4),
+])
+def test_codes_validation_rejects_before_launch(over, code):
+    """slotscan_fwd_codes refuses bad quantiser parameters (bits 2..8, group a power of two in [4, D]), NULL
+    outputs, a missing key carry where the forward runs as a pipeline, and misaligned codes, before any GPU
+    call."""
+    assert _codes_call(**over) == code
+    assert L.lib().slotscan_last_error()
+
+
+@pytest.mark.parametrize("B,T,H,N,D,G,nbytes", [
+    (8, 1024, 6, 192, 128, 8, 8 * 6 * 192 * 128 * 4),   # config 5's calls: the 8-chunk pipeline
+    (2, 511, 2, 64, 64, 8, 0),                          # one chunk: no carry
+    (1, 512, 1, 16, 64, 8, 16 * 64 * 4),
+])
+def test_fwd_carry_bytes(B, T, H, N, D, G, nbytes):
+    assert L.lib().slotscan_fwd_carry_bytes(B, T, H, N, D, G) == nbytes
