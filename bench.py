@@ -48,6 +48,9 @@ WORKLOADS = {
     "config2": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8),
     # the writer layer's scan with its epilogue fused in (bf16 copies, kinv, valid), against the two-pass path
     "config2_mem": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8, mem=True),
+    # the same with sh25's storage quantiser in training (run_sh25.sh:224: 3 bits, one scale per 16 channels),
+    # fused (kv_scan_mem(bits, group)) against the two-pass path (kv_scan_c, then quantize_mem)
+    "config2_mem_q": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8, mem=True, qbits=3, qgroup=16),
     "config2_soft": dict(kind="scan", B=64, T=1024, H=6, N=192, D=128, G=8, soft=True),
     "config3": dict(kind="scan", B=64, T=1024, H=6, N=96, D=128, G=8, seed=2),
     "config3_t512": dict(kind="scan", B=128, T=512, H=6, N=96, D=128, G=8, seed=2),
@@ -60,6 +63,10 @@ WORKLOADS = {
     # config 4 with each reader layer's output projection into the residual (memlm_sh.py:499-501): the read,
     # then wo_tk (d_model 2048, bias-free) added to the window output, forward only
     "config4_wo": dict(kind="read_out", B=64, T=1024, H=6, N=192, D=128, G=1024, NQ=1, layers=6, DM=2048),
+    # one reader layer of training at the sh25 shape (G = 8, NQ = 2, d_model 2048): the read and wo_tk into
+    # the residual, forward + backward (the projection's backward on the library's GEMMs, slotproj_bwd)
+    "read_out_train": dict(kind="read_out", B=64, T=1024, H=6, N=192, D=128, G=8, NQ=2, layers=1, DM=2048,
+                           backward=True),
     # one reader layer of training at the config-2 memory: G = 8 tokens per block, NQ = 2, forward + backward
     "read_train": dict(kind="read", B=64, T=1024, H=6, N=192, D=128, G=8, NQ=2, layers=1, backward=True),
     # one layer's 16-token window at the training shape (run_sh25.sh:223): 4 K/V heads x 128, kv_nq 4 (the
@@ -109,14 +116,15 @@ def stream_workload_inputs(W, T, dev):
     return k, q, v, gate, fr
 
 
-def algorithmic_bytes(B, T, H, N, D, G, mem=False, soft=False):
+def algorithmic_bytes(B, T, H, N, D, G, mem=False, soft=False, memq=False):
     """Per-kernel and per-step algorithmic HBM bytes (inputs read once, outputs written once; logs, Dn and
     staging are implementation choices and are not counted).  Token tensors bf16, snapshots fp32, gate and
     fr bf16 as the caller holds them (the kernels read the fp32 copies the wrapper makes: 4 B each).
     mem: the fused writer epilogue -- bf16 snapshot copies, plus kinv (fp32) and valid (1 B) per key row
     out and dkinv (fp32) per key row in.  soft: the general-mode kernels, whose forward also emits the
     occupancy snapshot (fp32 per row) and whose backward reads the three snapshots back (the replay
-    scratch is an implementation choice and is not counted)."""
+    scratch is an implementation choice and is not counted).  memq: the quantised epilogue, whose copies the
+    row replay emits (it reads the key tokens too) and the chain none."""
     tok = B * T * H
     NB = (T + G - 1) // G
     rows = B * NB * H * N
@@ -136,6 +144,9 @@ def algorithmic_bytes(B, T, H, N, D, G, mem=False, soft=False):
         "rows_bwd": 2 * snap + kx_b + 2 * row + tok * 4 + 2 * row,  # dkbuf, dvbuf (dkinv), k, v, gate in; dk, dv out
         "chain_bwd": row + 2 * tok * 4 + row + 2 * tok * 4,        # q, gate, fr in; dq, dgate, dfr out
     }
+    if memq:
+        per_kernel["chain_fwd"] = 2 * row + 2 * tok * 4              # q, k, gate, fr in
+        per_kernel["rows_fwd"] = 2 * row + tok * 4 + 2 * snap + kx_f  # k, v, gate in; kb, vb, kinv, valid out
     step = (3 * row + 2 * tok * 2 + 2 * snap + kx_f) + \
         (2 * snap + kx_b + 3 * row + 2 * tok * 2 + 3 * row + 2 * tok * 2)
     return per_kernel, step
@@ -502,7 +513,20 @@ def bench_read_out(args, W):
     wos = [(rn(DM, KD) / KD ** 0.5).to(bf) for _ in range(layers)]
     deltas = [rn(B, T, DM).to(bf) for _ in range(layers)]
 
+    bwd = W.get("backward", False)
+    if bwd:
+        for t_ in [K, V, kinv] + qs + scs + wos + deltas:
+            t_.requires_grad_()
+        douts = [rn(B, T, DM).to(bf) for _ in range(layers)]
+
     def step():
+        if bwd:
+            for t_ in [K, V, kinv] + qs + scs + wos + deltas:
+                t_.grad = None                                  # time the op, not a gradient accumulation
+            outs = [RH.slot_read_out(qs[i], K, V, kinv, valid, scs[i], G, wos[i], delta=deltas[i])
+                    for i in range(layers)]
+            torch.autograd.backward(outs, douts)
+            return outs
         with torch.no_grad():
             return [RH.slot_read_out(qs[i], K, V, kinv, valid, scs[i], G, wos[i], delta=deltas[i])
                     for i in range(layers)]
@@ -534,6 +558,19 @@ def bench_read_out(args, W):
     e1.record()
     torch.cuda.synchronize()
     gemm_ms = e0.elapsed_time(e1) / reps
+    bwd_lib_ms = None
+    if bwd:     # the projection's backward products as library GEMMs (torch.mm, hipBLASLt), same operands
+        g2 = douts[0].reshape(B * T, DM)
+        w0 = wos[0].detach()
+        lib = lambda: (torch.mm(g2, w0), torch.mm(g2.t(), x))
+        for _ in range(3):
+            lib()
+        e0.record()
+        for _ in range(reps):
+            lib()
+        e1.record()
+        torch.cuda.synchronize()
+        bwd_lib_ms = e0.elapsed_time(e1) / reps
     tot, cnt = prof["read_fwd"]
     rms = tot / cnt
     ptot, pcnt = prof["proj"]
@@ -566,6 +603,20 @@ def bench_read_out(args, W):
                          "layer_total": round(ms / layers, 4)},
         "kernels_ms": {n: round(x / c, 4) for n, (x, c) in prof.items()},
     }
+    if bwd:
+        kb_ = {n: prof[n][0] / prof[n][1] for n in ("proj_drd", "proj_dwo", "proj_reduce")}
+        bms = sum(kb_.values())
+        bfl = 2 * gfl                                               # drd and dwo, each the forward's flops
+        out["metric"] = (f"slot-read + wo_tk training tokens/s (one reader layer, B{B} T{T} H{H} S{N} d{D} G{G} "
+                         f"NQ{NQ}, d_model {DM}, forward + backward)")
+        out["proj_bwd_roofline"] = {"bound": "mfma", "kernel": "slotproj_bwd (weight transpose, proj_gemm for drd, "
+                                    "projt_gemm + proj_reduce for dwo)", "flops_per_launch": bfl,
+                                    "achieved": round(bfl / (bms * 1e-3) / 1e12, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                                    "unit": "TFLOP/s", "frac": round(bfl / (bms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                                    "avg_launch_ms": round(bms, 4), "kernels_ms": {n: round(x, 4) for n, x in kb_.items()},
+                                    "library_gemms_ms": round(bwd_lib_ms, 4)}
+        out["per_layer_ms"]["proj_bwd"] = round(bms, 4)
+        out["per_layer_ms"]["library_bwd_gemms"] = round(bwd_lib_ms, 4)
     print(json.dumps(out), flush=True)
 
 
@@ -689,6 +740,7 @@ def main():
     inputs = (k, q, v, gate, fr, temp)
     mem = W.get("mem", False)
     soft = W.get("soft", False)
+    qb, qg = W.get("qbits", 0), W.get("qgroup", 16)
     kw = dict(G=G, hard=not soft, hard_gate=False, detach_addr=not soft, q=q, occ_bin=True)
 
     if mem:
@@ -697,12 +749,15 @@ def main():
         dki = rn(B, NB, H, N)
 
         def step():
-            kb, vb, kinv, _valid = KH.kv_scan_mem(k, v, gate, fr, N, temp, **kw)
+            kb, vb, kinv, _valid = KH.kv_scan_mem(k, v, gate, fr, N, temp, bits=qb, group=qg, **kw)
             return torch.autograd.grad((kb, vb, kinv), inputs, (dkb, dvb, dki))
 
         def step_two_pass():                 # the same outputs through the scan, then the epilogue
             kbuf, vbuf = KH.kv_scan_c(k, v, gate, fr, N, temp, **kw)
-            kb, vb, kinv, _valid = MH.writer_epilogue(kbuf, vbuf, dtype=torch.bfloat16)
+            if qb:
+                kb, vb, kinv, _valid = MH.quantize_mem(kbuf, vbuf, qb, qg, dtype=torch.bfloat16)
+            else:
+                kb, vb, kinv, _valid = MH.writer_epilogue(kbuf, vbuf, dtype=torch.bfloat16)
             return torch.autograd.grad((kb, vb, kinv), inputs, (dkb, dvb, dki))
     else:
         def step():
@@ -718,7 +773,7 @@ def main():
     torch.cuda.synchronize()
     L.profile(False)
     warm = L.profile_read()
-    per_kernel_bytes, step_bytes = algorithmic_bytes(B, T, H, N, D, G, mem=mem, soft=soft)
+    per_kernel_bytes, step_bytes = algorithmic_bytes(B, T, H, N, D, G, mem=mem, soft=soft, memq=bool(qb))
     dom = max((n for n in warm if n in per_kernel_bytes), key=lambda n: warm[n][0] / warm[n][1], default=None)
     L.profile(True, kernels=None if dom is None else [dom])
     t0 = time.perf_counter()
@@ -755,7 +810,8 @@ def main():
     ach = launch_bytes[dom] / (dom_ms * 1e-3) / 1e9
     traffic = measured_traffic(args.workload).get(dom)
     out = {
-        "metric": (f"slot-scan + writer epilogue fwd+bwd tokens/s at B{B} T{T} H{H} S{N} d{D}" if mem else
+        "metric": (f"slot-scan + writer epilogue{f' (storage quantiser, {qb} bits, group {qg})' if qb else ''} "
+                   f"fwd+bwd tokens/s at B{B} T{T} H{H} S{N} d{D}" if mem else
                    "slot-scan fwd+bwd tokens/s at B64 T1024 H6 S192 d128; % HBM/MFMA roofline"
                    if args.workload == "config2" else f"slot-scan fwd+bwd tokens/s at B{B} T{T} H{H} S{N} d{D}"),
         "value": round(tokens / (ms * 1e-3), 1),

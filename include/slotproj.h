@@ -20,6 +20,19 @@ extern "C" {
 int slotproj_fwd(const void* rd, const void* wo, const void* delta, int64_t M, int64_t N, int64_t K, void* out,
                  void* stream);
 
+/* The projection's backward, the two products autograd forms for wo_tk (memlm_sh.py:500) from the upstream
+ * gradient dout (M, N) of out:
+ *     drd (M, K) = dout wo            dwo (N, K) = dout^T rd
+ * each a bf16 product with fp32 accumulation rounded to bf16 once, as the reference's bf16 matmuls are (the
+ * gradient of delta is dout itself and needs no kernel).  drd runs on the forward's GEMM kernel with the
+ * transposed weight; dwo on a GEMM that reads both token-major operands through gfx950's transposing LDS
+ * read, split over the tokens, then a fixed-order sum of the splits (no atomics: bitwise reproducible).
+ * N and K multiples of 256, M any.  workspace: slotproj_bwd_workspace(M, N, K) bytes, 256-byte aligned (the
+ * transposed weight and the splits' fp32 partials).  Other pointers 16-byte aligned. */
+size_t slotproj_bwd_workspace(int64_t M, int64_t N, int64_t K);
+int slotproj_bwd(const void* dout, const void* rd, const void* wo, int64_t M, int64_t N, int64_t K, void* drd,
+                 void* dwo, void* workspace, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -260,7 +260,10 @@ int slotscan_gen_bwd(const void* k, const void* q, const void* v, int dtype, con
 #define SLOTSCAN_K_GEN_FWD 11
 #define SLOTSCAN_K_GEN_BWD 12
 #define SLOTSCAN_K_PROJ 13
-#define SLOTSCAN_NK 14
+#define SLOTSCAN_K_PROJ_DRD 14
+#define SLOTSCAN_K_PROJ_DWO 15
+#define SLOTSCAN_K_PROJ_RED 16
+#define SLOTSCAN_NK 17
 int slotscan_profile(int enable);
 int slotscan_profile_read(double* total_ms, int64_t* count, int nk);
 

@@ -23,6 +23,7 @@
 // cover 256 bytes of distinct banks: rows r, r + 4, r + 8, r + 12 share banks modulo 256 bytes and the XOR puts
 // their chunk in 4 different places (a swizzle in place of padding, which a direct load cannot leave).  Workgroup order is XCD-aware: the 8 column tiles of a row block run on
 // one XCD (workgroup i goes to XCD i mod 8), so that block's read rows are fetched into one L2 once.
+#include <algorithm>
 #include <type_traits>
 
 #include "slot_common.h"
@@ -38,6 +39,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32;
 
 constexpr int PT = 256;            // output tile edge (rows and columns)
 constexpr int PK = 32;             // K per stage: 64-byte LDS rows
@@ -246,7 +248,288 @@ __global__ __launch_bounds__(PTHREADS) void proj_gemm(ProjArgs p) {
     else epilogue(std::false_type{});
 }
 
+// ------------------------------------------------------------------------------------ the backward's GEMMs
+// dWo = dDelta^T rd: C (N, K) = A^T B with A = dDelta (M, N) and B = rd (M, K), both token-major, the tokens
+// the reduction.  The same 256 x 256 tile, 4 waves and 4-stage ring of direct global -> LDS loads as
+// proj_gemm, a stage now being 32 TOKEN rows of the tile's 256 columns of each operand (512-byte LDS rows,
+// the 16-byte chunk c of row t at chunk position c ^ 2 (t & 3)).  The MFMA operands need 8 consecutive
+// tokens of one column per lane, which gfx950's transposing LDS read delivers: ds_read_b64_tr_b16 lets each
+// 16-lane group read a 4 x 16 block of 16-bit values -- lane l supplying the address of 4 consecutive
+// elements of row (l >> 2) & 3 -- and hands lane l the 4 rows of column l; two such reads (tokens t..t+3,
+// t+4..t+7) are one operand.  The chunk swizzle puts the 4 rows x 2 chunks of one group's read on 8 distinct
+// 16-byte bank groups.  The tokens are split over `splits` workgroups per output tile (24 tiles at
+// d_model 2048 and K 768 would not fill 256 CUs); each writes its fp32 partial tile and proj_reduce sums the
+// partials in split order and rounds the sum to bf16 once (the bf16 matmul's one rounding of its fp32
+// accumulation) -- fixed order, no atomics.
+struct ProjTArgs {
+    const bf16_t* a; const bf16_t* b; float* part;
+    int M, N, K, nblocks, kblocks, tps;                   // tps: tokens per split (a multiple of PK)
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ uint2 ld_tr(const unsigned char* p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const lds_void*)p));
+    return __builtin_bit_cast(uint2, v);
+}
+
+__global__ __launch_bounds__(PTHREADS) void projt_gemm(ProjTArgs p) {
+    __shared__ __align__(1024) unsigned char smem[2 * NST * STAGE];
+    unsigned char* const sA = smem;
+    unsigned char* const sB = smem + NST * STAGE;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tiles = p.nblocks * p.kblocks;
+    const int split = blockIdx.x / tiles, tile = blockIdx.x % tiles;
+    const int nb = tile / p.kblocks, kb = tile % p.kblocks;
+    const int n0 = nb * PT, k0 = kb * PT;
+    const int m_lo = split * p.tps, m_hi = min(p.M, m_lo + p.tps);
+    const int KT = (m_hi - m_lo) / PK;                    // full stages (the pipelined loop)
+    const int tail = (m_hi - m_lo) - KT * PK;             // tokens of a last partial stage (0 .. 31)
+
+    // direct loads: instruction i of wave w fills token rows 2 (4 i + w) and + 1 of a stage (lane L: row
+    // + (L >> 5), chunk position L & 31, global chunk (L & 31) ^ 2 (row & 3))
+    const bf16_t* ga[PLD];
+    const bf16_t* gb[PLD];
+#pragma unroll
+    for (int i = 0; i < PLD; i++) {
+        const int r = 2 * (PLD * i + wave) + (lane >> 5);
+        const int c = (lane & 31) ^ (2 * (r & 3));
+        ga[i] = p.a + (size_t)(m_lo + r) * p.N + n0 + 8 * c;
+        gb[i] = p.b + (size_t)(m_lo + r) * p.K + k0 + 8 * c;
+    }
+    auto dma = [&](int kt, int q) {
+        const int buf = kt % NST;
+        if (q < PLD) dma16(ga[q] + (size_t)kt * PK * p.N, lds_addr(sA + buf * STAGE + (PLD * q + wave) * 1024));
+        else dma16(gb[q - PLD] + (size_t)kt * PK * p.K, lds_addr(sB + buf * STAGE + (PLD * (q - PLD) + wave) * 1024));
+    };
+
+    const int wm = wave >> 1, wn = wave & 1;
+    // this lane's part of a transposed read: token row 8 (g >> 1) + ((l >> 2) & 3) (+ 16 ks + 4 half), chunk
+    // 2 (g & 1) + ((l & 3) >> 1) of the operand tile's 32 columns, byte 8 (l & 1) of the chunk; g = l >> 4
+    const int g4 = lane >> 4, rq = (lane >> 2) & 3;
+    const int rowb = (8 * (g4 >> 1) + rq) * 512, cl = 2 * (g4 & 1) + ((lane & 3) >> 1), hb = 8 * (lane & 1);
+    int offA[4], offB[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        offA[t] = rowb + 16 * ((16 * wm + 4 * t + cl) ^ (2 * rq)) + hb;
+        offB[t] = rowb + 16 * ((16 * wn + 4 * t + cl) ^ (2 * rq)) + hb;
+    }
+    // op[ks][t]: A operand of n tile t (dDelta), op[ks][4 + t]: B operand of k tile t (rd); groups of 4 reads
+    // as in proj_gemm (A ks 0, B ks 0, A ks 1, B ks 1)
+    auto read_ops_at = [&](const unsigned char* bufA, const unsigned char* bufB, uint4 (&op)[2][8], int r) {
+        const int ks = r >> 1;
+        const unsigned char* base = (r & 1) ? bufB : bufA;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const unsigned char* q0 = base + ((r & 1) ? offB[t] : offA[t]) + 16 * ks * 512;
+            const uint2 lo = ld_tr(q0), hi = ld_tr(q0 + 4 * 512);
+            op[ks][4 * (r & 1) + t] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+    };
+    auto read_ops = [&](int kt, uint4 (&op)[2][8], int r) {
+        const int buf = kt % NST;
+        read_ops_at(sA + buf * STAGE, sB + buf * STAGE, op, r);
+    };
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    // the k loop of proj_gemm (same load trickle, counted waits and barrier placement), with the A operand
+    // the n tile i and the B operand the k tile j
+    constexpr int PER = 2 * PLD;
+    auto stage = [&](int kt, uint4 (&cur)[2][8], uint4 (&nxt)[2][8]) {
+        const bool more = kt + 1 < KT, pre = kt + 3 < KT;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const int ks = g >> 2, i = g & 3;
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = mfma32(cur[ks][i], cur[ks][4 + j], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (pre) dma(kt + 3, g);
+            if (g == 4 && more) {
+                if (pre) wait_vm<PER + 5>();
+                else if (kt + 2 < KT) wait_vm<PER>();
+                else wait_vm<0>();
+                wait_lgkm0();
+                stage_barrier();
+            }
+            if (g >= 4 && more) read_ops(kt + 1, nxt, g - 4);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    uint4 opA[2][8], opB[2][8];
+    // (not wrapped in a test of KT > 0: with no full stage nothing is loaded, the operand reads below read
+    // whatever the ring holds and no MFMA uses them; a branch here made the compiler spill the accumulators)
+#pragma unroll
+    for (int st = 0; st < NST - 1; st++)
+        if (st < KT)
+#pragma unroll
+            for (int q = 0; q < PER; q++) dma(st, q);
+    if (KT > 2) wait_vm<2 * PER>();
+    else if (KT > 1) wait_vm<PER>();
+    else wait_vm<0>();
+    stage_barrier();
+#pragma unroll
+    for (int r = 0; r < 4; r++) read_ops(0, opA, r);
+    int kt = 0;
+    for (; kt + 1 < KT; kt += 2) {
+        stage(kt, opA, opB);
+        stage(kt + 1, opB, opA);
+    }
+    if (kt < KT) stage(kt, opA, opB);
+    if (tail) {
+        // the last, partial stage: plain loads of the valid token rows (zeros past them, so they add
+        // nothing), written to ring buffer 0 in the swizzled layout, then one stage of MFMAs
+        wait_lgkm0();
+        stage_barrier();                                   // every wave is done reading the ring
+        const int t0 = m_lo + KT * PK;
+#pragma unroll
+        for (int i = 0; i < PLD; i++) {
+            const int r = 2 * (PLD * i + wave) + (lane >> 5);
+            const int c = (lane & 31) ^ (2 * (r & 3));
+            const int m = min(t0 + r, p.M - 1);
+            uint4 va = *reinterpret_cast<const uint4*>(p.a + (size_t)m * p.N + n0 + 8 * c);
+            uint4 vb = *reinterpret_cast<const uint4*>(p.b + (size_t)m * p.K + k0 + 8 * c);
+            if (r >= tail) va = vb = make_uint4(0u, 0u, 0u, 0u);
+            *reinterpret_cast<uint4*>(sA + (PLD * i + wave) * 1024 + 16 * lane) = va;
+            *reinterpret_cast<uint4*>(sB + (PLD * i + wave) * 1024 + 16 * lane) = vb;
+        }
+        wait_lgkm0();
+        stage_barrier();
+#pragma unroll
+        for (int r = 0; r < 4; r++) read_ops_at(sA, sB, opA, r);
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const int ks = g >> 2, i = g & 3;
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = mfma32(opA[ks][i], opA[ks][4 + j], acc[i][j]);
+        }
+    }
+    // epilogue: acc[i][j] lane l, register r holds C[n][k] with n = 128 wm + 32 i + 8 (r >> 2) + 4 (l >> 5) +
+    // (r & 3) and k = 128 wn + 32 j + (l & 31): 32 lanes store 128 contiguous bytes of one partial row
+    // (a wave-uniform base and one 32-bit lane offset: no per-element 64-bit addresses; the lane id is formed
+    // anew with mbcnt, so that nothing computed before the k loop has to stay live across it)
+    const int ln = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const float* out0 = p.part + (size_t)split * p.N * p.K + (size_t)(n0 + 128 * wm) * p.K + k0 + 128 * wn;
+    const u32 loff = (u32)((4 * (ln >> 5)) * p.K + (ln & 31)) * 4u;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+            char* rowp = (char*)(out0 + (size_t)dr * p.K);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                __builtin_nontemporal_store(acc[i][j][r], reinterpret_cast<float*>(rowp + loff + 128 * j));
+        }
+}
+
+// dWo = bf16(sum over the splits, in split order, of the fp32 partials): 4 elements per thread
+__global__ __launch_bounds__(256) void proj_reduce(const float* __restrict__ part, int splits, int64_t nk,
+                                                   bf16_t* __restrict__ out) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= nk) return;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 s = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(part + i));
+    for (int q = 1; q < splits; q++) {
+        const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(part + (size_t)q * nk + i));
+        s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+    }
+    uint2 r;
+    r.x = pack_bf16x2(s.x, s.y);
+    r.y = pack_bf16x2(s.z, s.w);
+    *reinterpret_cast<uint2*>(out + i) = r;
+}
+
+// woT (K, N) = wo (N, K)^T, bf16, 64 x 64 tiles through LDS (the 2 x 64 x 64 staging reads / writes whole
+// 128-byte rows on both sides)
+__global__ __launch_bounds__(256) void proj_transpose(const bf16_t* __restrict__ w, int N, int K,
+                                                      bf16_t* __restrict__ wt) {
+    __shared__ bf16_t t[64][66];
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64, tid = threadIdx.x;
+    for (int u = tid; u < 64 * 64; u += 256) {
+        const int r = u >> 6, c = u & 63;
+        if (r0 + r < N && c0 + c < K) t[r][c] = w[(size_t)(r0 + r) * K + c0 + c];
+    }
+    __syncthreads();
+    for (int u = tid; u < 64 * 64; u += 256) {
+        const int c = u >> 6, r = u & 63;
+        if (r0 + r < N && c0 + c < K) wt[(size_t)(c0 + c) * N + r0 + r] = t[r][c];
+    }
+}
+
+// the token splits of projt_gemm for an (N, K) output: about two rounds of workgroups on 256 CUs, each split
+// a multiple of the 32-token stage
+static void projt_plan(int64_t M, int64_t N, int64_t K, int* splits, int* tps) {
+    const int64_t tiles = (N / PT) * (K / PT);
+    int64_t s = std::max<int64_t>(1, (512 + tiles - 1) / tiles);
+    int64_t t = ((M + s - 1) / s + PK - 1) / PK * PK;
+    s = (M + t - 1) / t;
+    *splits = (int)s;
+    *tps = (int)t;
+}
+
 }  // namespace
+
+extern "C" size_t slotproj_bwd_workspace(int64_t M, int64_t N, int64_t K) {
+    if (M < 1 || N < 1 || K < 1) return 0;
+    int splits = 0, tps = 0;
+    projt_plan(M, N, K, &splits, &tps);
+    const size_t wt = ((size_t)N * K * 2 + 255) & ~(size_t)255;
+    return wt + (size_t)splits * N * K * 4;
+}
+
+extern "C" int slotproj_bwd(const void* dout, const void* rd, const void* wo, int64_t M, int64_t N, int64_t K,
+                            void* drd, void* dwo, void* workspace, void* stream) {
+    if (M < 1 || N < 1 || K < 1) return fail(SLOTSCAN_ERR_SHAPE, "slotproj_bwd: M, N and K must be >= 1");
+    if (N % PT != 0 || K % PT != 0)
+        return fail(SLOTSCAN_ERR_SHAPE, "slotproj_bwd: N and K must be multiples of 256");
+    if (M > 0x7fffffffLL || N * K > 0x7fffffffLL || M * N > ((int64_t)1 << 40) || M * K > ((int64_t)1 << 40))
+        return fail(SLOTSCAN_ERR_SHAPE, "slotproj_bwd: shape too large");
+    if (!dout || !rd || !wo || !drd || !dwo || !workspace)
+        return fail(SLOTSCAN_ERR_NULL, "slotproj_bwd: a required pointer is NULL");
+    if (!slothost::al16(dout) || !slothost::al16(rd) || !slothost::al16(wo) || !slothost::al16(drd) ||
+        !slothost::al16(dwo) || ((uintptr_t)workspace & 255u))
+        return fail(SLOTSCAN_ERR_ALIGN, "slotproj_bwd: operands 16-byte, workspace 256-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    bf16_t* wt = (bf16_t*)workspace;
+    float* part = (float*)((char*)workspace + (((size_t)N * K * 2 + 255) & ~(size_t)255));
+    // dRD (M, K) = dout (M, N) wo (N, K): proj_gemm with the transposed weight as its (K, N) operand
+    slothost::launch(proj_transpose, dim3((unsigned)((K + 63) / 64), (unsigned)((N + 63) / 64)), dim3(256), 0, st,
+                     (const bf16_t*)wo, (int)N, (int)K, wt);
+    {
+        slothost::Scope sc(SLOTSCAN_K_PROJ_DRD, st);
+        ProjArgs a{(const bf16_t*)dout, wt, nullptr, (bf16_t*)drd, (int)M, (int)K, (int)N,
+                   (int)((M + PT - 1) / PT), (int)(K / PT)};
+        const int groups = (a.mblocks + PXCD - 1) / PXCD;
+        slothost::launch(proj_gemm, dim3((unsigned)(groups * PXCD * a.nblocks)), dim3(PTHREADS), 0, st, a);
+    }
+    // dWo (N, K) = dout^T rd: the transposing GEMM over token splits, then the fixed-order reduction
+    int splits = 0, tps = 0;
+    projt_plan(M, N, K, &splits, &tps);
+    {
+        slothost::Scope sc(SLOTSCAN_K_PROJ_DWO, st);
+        ProjTArgs t{(const bf16_t*)dout, (const bf16_t*)rd, part, (int)M, (int)N, (int)K, (int)(N / PT), (int)(K / PT),
+                    tps};
+        slothost::launch(projt_gemm, dim3((unsigned)(splits * t.nblocks * t.kblocks)), dim3(PTHREADS), 0, st, t);
+    }
+    {
+        slothost::Scope sc(SLOTSCAN_K_PROJ_RED, st);
+        const int64_t nk = N * K;
+        slothost::launch(proj_reduce, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, st, (const float*)part,
+                         splits, nk, (bf16_t*)dwo);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "slotproj_bwd launch");
+    return 0;
+}
 
 extern "C" int slotproj_fwd(const void* rd, const void* wo, const void* delta, int64_t M, int64_t N, int64_t K,
                             void* out, void* stream) {

@@ -110,18 +110,37 @@ def shared_read(q, kbuf, buf, kinv, valid, log_rsel, G, s=None, rsharp=None):
 
 def _proj(x, w, d2):
     """delta + x @ w^T for x (M, K), w (N, K), d2 (M, N) or None, all bf16 on one GPU: the library's gfx950 GEMM
-    with the add in its epilogue (slotproj_fwd) when N is a multiple of 256 and K of 32, else one library GEMM
-    (torch.addmm / linear: hipBLASLt) for the shapes that kernel does not tile."""
+    with the add in its epilogue (slotproj_fwd).  Its tiles need N a multiple of 256 and K of 32; other shapes
+    raise NotImplementedError (there is no second GEMM backend here)."""
     M, K = x.shape
     N = w.shape[0]
-    if N % 256 == 0 and K % 32 == 0:
-        w_ = w.contiguous()
-        out = torch.empty(M, N, device=x.device, dtype=x.dtype)
-        rc = L.lib().slotproj_fwd(L.ptr(x), L.ptr(w_), None if d2 is None else L.ptr(d2), M, N, K, L.ptr(out),
-                                  L.stream_of(x.device))
-        L.check(rc, "slotproj_fwd")
-        return out
-    return torch.nn.functional.linear(x, w) if d2 is None else torch.addmm(d2, x, w.t())
+    if N % 256 or K % 32:
+        raise NotImplementedError(f"the HIP read-out projection tiles d_model in multiples of 256 and H*NQ*dv in "
+                                  f"multiples of 32 (got d_model={N}, H*NQ*dv={K})")
+    w_ = w.contiguous()
+    out = torch.empty(M, N, device=x.device, dtype=x.dtype)
+    rc = L.lib().slotproj_fwd(L.ptr(x), L.ptr(w_), None if d2 is None else L.ptr(d2), M, N, K, L.ptr(out),
+                              L.stream_of(x.device))
+    L.check(rc, "slotproj_fwd")
+    return out
+
+
+def _proj_bwd(g, x, w):
+    """(dx, dw) = (g w, g^T x) for the projection out = x w^T: g (M, N), x (M, K), w (N, K), bf16, on the
+    library's GEMMs (slotproj_bwd).  N and K multiples of 256."""
+    M, N = g.shape
+    K = x.shape[1]
+    if N % 256 or K % 256:
+        raise NotImplementedError(f"the HIP read-out projection's backward tiles d_model and H*NQ*dv in multiples "
+                                  f"of 256 (got d_model={N}, H*NQ*dv={K})")
+    g_, x_, w_ = g.contiguous(), x.contiguous(), w.contiguous()
+    dx = torch.empty(M, K, device=g.device, dtype=torch.bfloat16)
+    dw = torch.empty(N, K, device=g.device, dtype=torch.bfloat16)
+    ws = torch.empty(L.lib().slotproj_bwd_workspace(M, N, K), device=g.device, dtype=torch.uint8)
+    rc = L.lib().slotproj_bwd(L.ptr(g_), L.ptr(x_), L.ptr(w_), M, N, K, L.ptr(dx), L.ptr(dw), L.ptr(ws),
+                              L.stream_of(g.device))
+    L.check(rc, "slotproj_bwd")
+    return dx, dw
 
 
 class _ReadOutHip(torch.autograd.Function):
@@ -130,7 +149,8 @@ class _ReadOutHip(torch.autograd.Function):
     (slotproj_fwd: fp32 accumulation rounded to bf16, then added to delta and rounded again, the reference's
     bf16 Linear output and bf16 residual add), and rd -- written by the read kernel already in
     the GEMM's row-major (B*T, H*NQ*D) layout -- is kept in bf16 for dwo, as the reference's autograd keeps it
-    for wo_tk.  The backward's two products (dRD = dDelta Wo, dWo = dDelta^T rd) are plain library GEMMs."""
+    for wo_tk.  The backward's two products (dRD = dDelta Wo, dWo = dDelta^T rd) run on the library's own GEMMs
+    (slotproj_bwd), each rounded to bf16 once, as the reference's bf16 matmuls round."""
 
     @staticmethod
     def forward(ctx, q, kbuf, buf, kinv, valid, scale, wo, delta, G):
@@ -158,8 +178,9 @@ class _ReadOutHip(torch.autograd.Function):
         B, T, H, NQ, D = q_.shape
         _, NB, _, N, _ = kb_.shape
         g = dout.reshape(B * T, -1).to(rd.dtype)
-        drd = torch.mm(g, w).reshape(B, T, H, NQ, D)             # dRD = dDelta Wo
-        dwo = torch.mm(g.t(), rd.reshape(B * T, -1)).to(wo_dtype)  # dWo = dDelta^T rd
+        drd, dwo = _proj_bwd(g, rd.reshape(B * T, -1), w)        # dRD = dDelta Wo, dWo = dDelta^T rd
+        drd = drd.reshape(B, T, H, NQ, D)
+        dwo = dwo.to(wo_dtype)
         dq = torch.empty_like(q_)
         dkb = torch.empty_like(kb_)
         dvb = torch.empty_like(vb_)

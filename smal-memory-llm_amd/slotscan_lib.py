@@ -62,6 +62,8 @@ SIGNATURES = {
     "slotmem_epilogue_bwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i64, _i32, _vp, _vp, _vp]),
     "slotmem_codes": (_i32, [_vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp]),
     "slotproj_fwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "slotproj_bwd_workspace": (_sz, [_i64, _i64, _i64]),
+    "slotproj_bwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "slotwin_fwd": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp]),
     "slotwin_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                            _vp, _vp, _vp, _vp, _vp]),
@@ -110,7 +112,8 @@ def dtype_code(dt):
 
 
 KERNEL_NAMES = ("chain_fwd", "rows_fwd", "rows_bwd", "chain_bwd", "reduce_parts", "read_fwd", "read_bwd", "mem_fwd",
-                "mem_bwd", "win_fwd", "win_bwd", "gen_fwd", "gen_bwd", "proj")
+                "mem_bwd", "win_fwd", "win_bwd", "gen_fwd", "gen_bwd", "proj", "proj_drd", "proj_dwo",
+                "proj_reduce")
 
 
 def profile(enable, kernels=None):

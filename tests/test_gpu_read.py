@@ -294,7 +294,7 @@ def _bf16_ulp(x):
 
 @pytest.mark.parametrize("M,N,K,with_delta", [(1, 256, 32, True), (300, 512, 768, True), (513, 2048, 64, False),
                                               (256, 256, 800, False), (70, 512, 96, True), (200, 256, 128, True),
-                                              (257, 256, 800, True)])
+                                              (257, 256, 800, True), (100, 256, 32, False)])
 def test_proj_gemm_matches_fp64(M, N, K, with_delta):
     """slotproj_fwd, the reader's wo_tk projection with the residual add in the GEMM epilogue, against an fp64
     GEMM of the same bf16 operands.  The kernel rounds as the reference does: the product (fp32 accumulation)
@@ -302,8 +302,8 @@ def test_proj_gemm_matches_fp64(M, N, K, with_delta):
     again -- the bf16 residual add, :501.  So |out - exact| <= 1/2 bf16 ulp of the result, plus 1/2 bf16 ulp
     of the product when there is a delta, plus the fp32 accumulation error (2^-20 * sum |rd||wo|).  Ragged M
     (1, 300, 513) covers partial row tiles; rows past M of a larger buffer are checked untouched; K = 800 is
-    25 k stages (an odd count; the loop runs stages in pairs); K = 96 and 128 are 3 and 4 stages, either
-    side of where delta starts to be fetched during the k loop (4 stages or more)."""
+    25 k stages (an odd count; the loop runs stages in pairs); K = 32, 64, 96 and 128 are 1-4 stages, the
+    short-loop paths of the ring's prologue and counted waits (delta is read in the epilogue only)."""
     gen = torch.Generator().manual_seed(M * 7 + K)
     a = torch.randn(M, K, generator=gen).to(torch.bfloat16)
     w = (torch.randn(N, K, generator=gen) / K ** 0.5).to(torch.bfloat16)
@@ -349,3 +349,57 @@ def test_read_out_projection_runs_the_library_gemm():
         L.profile(False)
     prof = L.profile_read()
     assert prof.get("proj", (0.0, 0))[1] == 2 and prof.get("read_fwd", (0.0, 0))[1] == 2
+
+
+def test_proj_gemm_in_place_residual_add():
+    """slotproj.h allows delta to alias out (the residual updated in place): with a ragged M the result equals the
+    out-of-place call bitwise, and the rows past M are untouched."""
+    M, N, K = 300, 512, 256
+    gen = torch.Generator().manual_seed(5)
+    a = torch.randn(M, K, generator=gen).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, K, generator=gen) / K ** 0.5).to(torch.bfloat16).to(DEV)
+    buf = torch.full((M + 3, N), 7.0, dtype=torch.bfloat16, device=DEV)
+    buf[:M] = torch.randn(M, N, generator=gen).to(torch.bfloat16).to(DEV)
+    ref = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    L.check(L.lib().slotproj_fwd(L.ptr(a), L.ptr(w), L.ptr(buf), M, N, K, L.ptr(ref), L.stream_of(a.device)), "fwd")
+    L.check(L.lib().slotproj_fwd(L.ptr(a), L.ptr(w), L.ptr(buf), M, N, K, L.ptr(buf), L.stream_of(a.device)), "fwd")
+    torch.cuda.synchronize()
+    assert torch.equal(buf[:M], ref)
+    assert (buf[M:].float() == 7.0).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 256), (122, 256, 768), (300, 512, 768), (1000, 256, 512),
+                                   (8192, 2048, 768)])
+def test_proj_bwd_matches_fp64(M, N, K):
+    """slotproj_bwd, the backward of the read-out projection (drd = dout wo, dwo = dout^T rd), against fp64
+    products of the same bf16 operands.  Each output is one fp32 accumulation rounded to bf16 (the reference's
+    bf16 matmuls), so |got - exact| <= 1/2 bf16 ulp of the result + 2^-20 * sum |a||b| (fp32 accumulation; for
+    dwo also the fp32 sum of the token splits).  M = 1, 122, 300, 1000 leave a partial 32-token stage (and
+    splits with no full stage); 8192 x 2048 x 768 is config4_wo's weight shape (about 22 splits of 12 stages).
+    Run twice: bitwise the same (fixed-order split sum, no atomics)."""
+    gen = torch.Generator().manual_seed(M + N + K)
+    g = torch.randn(M, N, generator=gen).to(torch.bfloat16)
+    x = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=gen) / K ** 0.5).to(torch.bfloat16)
+    print(f"   proj bwd M={M} N={N} K={K}", flush=True)
+    gd, xd, wd = g.to(DEV), x.to(DEV), w.to(DEV)
+    outs = [RH._proj_bwd(gd, xd, wd) for _ in range(2)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    G_, X, W = g.double().numpy(), x.double().numpy(), w.double().numpy()
+    for name, got, ref, mag in (("drd", outs[0][0], G_ @ W, np.abs(G_) @ np.abs(W)),
+                                ("dwo", outs[0][1], G_.T @ X, np.abs(G_).T @ np.abs(X))):
+        bound = 0.5 * _bf16_ulp(ref) + 2.0 ** -20 * mag
+        err = np.abs(got.double().cpu().numpy() - ref)
+        print(f"   {name}: max err / bound {np.max(err / bound):.3f}", flush=True)
+        assert (err <= bound).all(), name
+
+
+def test_proj_bwd_refuses_untiled_shapes():
+    """The backward tiles d_model and H*NQ*dv in multiples of 256; other shapes raise (no second GEMM backend)."""
+    g = torch.zeros(4, 256, dtype=torch.bfloat16, device=DEV)
+    x = torch.zeros(4, 96, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(NotImplementedError):
+        RH._proj_bwd(g, x, torch.zeros(256, 96, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(NotImplementedError):
+        RH._proj(x, torch.zeros(200, 96, dtype=torch.bfloat16, device=DEV), None)

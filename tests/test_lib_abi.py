@@ -177,3 +177,13 @@ def test_codes_validation_rejects_before_launch(over, code):
 ])
 def test_fwd_carry_bytes(B, T, H, N, D, G, nbytes):
     assert L.lib().slotscan_fwd_carry_bytes(B, T, H, N, D, G) == nbytes
+
+
+@pytest.mark.parametrize("M,N,K,code", [(0, 256, 256, 1), (8, 300, 256, 1), (8, 256, 96, 1), (8, 256, 256, 3)])
+def test_proj_bwd_validation_rejects_before_launch(M, N, K, code):
+    """slotproj_bwd refuses shapes its tiles do not cover (N and K multiples of 256) and NULL operands before
+    any GPU call; its workspace holds the transposed weight and the token splits' fp32 partials."""
+    assert L.lib().slotproj_bwd(None, None, None, M, N, K, None, None, None, None) == code
+    assert L.lib().slotscan_last_error()
+    ws = L.lib().slotproj_bwd_workspace(65536, 2048, 768)
+    assert ws >= 2048 * 768 * 2 + 2048 * 768 * 4 and (ws - ((2048 * 768 * 2 + 255) & ~255)) % (2048 * 768 * 4) == 0
