@@ -9,7 +9,8 @@
  * Conventions: every tensor is bf16 (uint16 bit patterns) and token-major, (B, T, H, D) contiguous with
  * H = Hq for q, out, dout, dq and H = Hk for k, v, dk, dv -- the reference's (B, H, T, D) operands are
  * transposed views of this layout (memlm_sh.py:482-484).  D is 64 or 128, 1 <= W <= 16.  Pointers are device
- * pointers; q, k, v, out (backward), dout 16-byte aligned.  Error codes as in slotscan.h. */
+ * pointers; q, k, v, out, dout, dq, dk, dv 16-byte aligned (the outputs are written in 16-byte row pieces).
+ * Error codes as in slotscan.h. */
 #ifndef SLOTWIN_H
 #define SLOTWIN_H
 #include <stddef.h>

@@ -440,8 +440,8 @@ extern "C" int slotwin_fwd(const void* q, const void* k, const void* v, int64_t 
                            int64_t Hk, int64_t D, int64_t W, float scale, void* out, float* lse, void* stream) {
     if (int r = check_win(B, T, Hq, Hk, D, W)) return r;
     if (!q || !k || !v || !out || !lse) return fail(SLOTSCAN_ERR_NULL, "slotwin_fwd: a required pointer is NULL");
-    if (!al16(q) || !al16(k) || !al16(v) || ((uintptr_t)out & 7u))
-        return fail(SLOTSCAN_ERR_ALIGN, "slotwin_fwd: q, k, v must be 16-byte aligned, out 8-byte");
+    if (!al16(q) || !al16(k) || !al16(v) || !al16(out))                // out is written in 16-byte row pieces
+        return fail(SLOTSCAN_ERR_ALIGN, "slotwin_fwd: q, k, v and out must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     WinArgs a{(const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, nullptr, nullptr, nullptr,
               (bf16_t*)out, lse, nullptr, nullptr, nullptr, nullptr, (int)T, (int)Hq, (int)Hk, (int)W, scale};
@@ -462,9 +462,8 @@ extern "C" int slotwin_bwd(const void* q, const void* k, const void* v, const vo
     if (int r = check_win(B, T, Hq, Hk, D, W)) return r;
     if (!q || !k || !v || !out || !lse || !dout || !dsum || !dq || !dk || !dv)
         return fail(SLOTSCAN_ERR_NULL, "slotwin_bwd: a required pointer is NULL");
-    if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(dout) || ((uintptr_t)dq & 7u) ||
-        ((uintptr_t)dk & 7u) || ((uintptr_t)dv & 7u))
-        return fail(SLOTSCAN_ERR_ALIGN, "slotwin_bwd: q, k, v, out, dout must be 16-byte aligned, dq, dk, dv 8-byte");
+    if (!al16(q) || !al16(k) || !al16(v) || !al16(out) || !al16(dout) || !al16(dq) || !al16(dk) || !al16(dv))
+        return fail(SLOTSCAN_ERR_ALIGN, "slotwin_bwd: q, k, v, out, dout, dq, dk and dv must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     WinArgs a{(const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, (const bf16_t*)out, lse, (const bf16_t*)dout,
               nullptr, nullptr, (bf16_t*)dq, (bf16_t*)dk, (bf16_t*)dv, dsum, (int)T, (int)Hq, (int)Hk, (int)W, scale};

@@ -187,3 +187,18 @@ def test_proj_bwd_validation_rejects_before_launch(M, N, K, code):
     assert L.lib().slotscan_last_error()
     ws = L.lib().slotproj_bwd_workspace(65536, 2048, 768)
     assert ws >= 2048 * 768 * 2 + 2048 * 768 * 4 and (ws - ((2048 * 768 * 2 + 255) & ~255)) % (2048 * 768 * 4) == 0
+
+
+@pytest.mark.parametrize("which", ["out", "dq", "dk", "dv"])
+def test_window_refuses_8_byte_aligned_outputs(which):
+    """win_fwd / win_bwd write out, dq, dk and dv as 16-byte row pieces: an 8-byte-aligned output pointer is
+    refused with SLOTSCAN_ERR_ALIGN before any GPU call."""
+    good, bad = ctypes.c_void_p(1 << 20), ctypes.c_void_p((1 << 20) + 8)
+    if which == "out":
+        rc = L.lib().slotwin_fwd(good, good, good, 1, 16, 2, 2, 64, 16, 0.125, bad, good, None)
+    else:
+        o = {n: (bad if n == which else good) for n in ("dq", "dk", "dv")}
+        rc = L.lib().slotwin_bwd(good, good, good, good, good, good, 1, 16, 2, 2, 64, 16, 0.125, good, o["dq"], o["dk"],
+                                 o["dv"], None)
+    assert rc == 4
+    assert b"16-byte" in L.lib().slotscan_last_error()
