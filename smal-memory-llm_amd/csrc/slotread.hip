@@ -22,6 +22,8 @@
 //   reduce   the 4 waves' partial O (their slot ranges) are summed in a fixed order through LDS and
 //            written as bf16, 16 contiguous bytes per lane, in token-major order.
 // Three workgroup barriers per 16-query tile; no atomics, so the result is bitwise reproducible.
+#include <algorithm>
+
 #include "slot_common.h"
 #include "slotscan.h"
 #include "slotread.h"
@@ -77,7 +79,8 @@ struct ReadFwdArgs {
     const uint8_t* valid;
     const float* scale;
     bf16_t* rd;
-    int T, H, NQ, N, G, NB, MC;   // MC: query rows per workgroup (multiple of 16)
+    int T, H, NQ, N, G, NB, MC;   // MC: query rows per workgroup / work unit (multiple of 16)
+    int slabs, parts;             // read_fwd_wide: the work units are (slab, part of MC queries)
 };
 
 template <int D>
@@ -289,222 +292,318 @@ __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(3)
 
 // ------------------------------------------------------------------------------------ wide query blocks
 // Blocks with many queries (the frozen-store fan-out: one block of T*NQ queries per head) invert the split:
-// the workgroup stages the block's keys (row-major) and values (TRANSPOSED, slot-contiguous) in LDS once,
-// and each of its 16 waves owns whole 16-query tiles against ALL slots, so the softmax is wave-local (no
-// workgroup barrier after staging).  Per tile and wave:
+// the workgroup stages the block's keys and values in LDS once, and each of its 8 waves owns whole pairs of
+// 16-query tiles against ALL slots, so the softmax is wave-local; every key and value operand read from LDS
+// feeds one MFMA of each tile of the pair (half the LDS reads per query of one tile per wave, at 2 waves per
+// SIMD and up to 256 registers).  Per tile and wave:
 //   S^T = K Q^T     12 x D/32 MFMA 16x16x32, A = key rows from LDS (16 B per lane), B = queries from HBM
-//                   (loaded one tile ahead);
+//                   (loaded one pair ahead, across unit boundaries);
 //   softmax         48 scores per lane (its query column), cross-row permlane max / sum;
 //   O^T = V^T P^T   D/16 x 6 MFMA 16x16x32: B = the probabilities straight from the score tiles (slots
 //                   4g+i of tile 2c and 16+4g+i of tile 2c+1 as the 8 k-slots of lane group g), A = the
-//                   same 8 slots of one value dimension, two 8-byte reads from the transposed LDS copy;
+//                   same 8 slots of one value dimension, read TRANSPOSED from the row-major value rows by two
+//                   ds_read_b64_tr_b16 (a 16-lane group reads 4 slot rows x 16 dims; lane l receives dim l);
 //   store           4 consecutive dims of one query per lane and tile (8 bytes), token-major.
-#define WIDE_WAVES 16
+// The grid is persistent: one workgroup per CU walks the work units (a block's query range, about 3 per
+// workgroup) so that staging overlaps compute.  Keys are staged in two ping-pong buffers: the NEXT unit's
+// keys are fetched by direct global -> LDS loads (no registers) during the current unit, after its first
+// tile's softmax.  Values are staged row-major (as the keys: no transposition, so they too are direct loads)
+// into one buffer, fetched when every wave is done with the current unit's values; the next unit's first
+// tile waits for them only before its value product, behind its scores and softmax.  147 KB of LDS at
+// D = 128.  The 16-byte chunks
+// of a staged row are XOR-swizzled (kpos, vpos) so that the key operand reads (16 consecutive rows at one
+// chunk) and the transposed value reads (4 rows x 2 chunks per 16-lane group) hit distinct banks.
+// Rows past N are copies of row N - 1 with kinv 0 and mask -inf: their probability is exactly 0.
+#define WIDE_WAVES 8
 #define WIDE_THREADS (64 * WIDE_WAVES)
-#define WIDE_NP 192                              // staged slots (N rounded up to 32, at most 192)
+#define WIDE_NP 192                              // staged slots (N <= 192)
 
 template <int D>
 struct WideSmem {
-    static constexpr int KST = D + 8;            // key row stride (bf16)
-    // Transposed value row stride (bf16): 98 dwords, 2 mod 32 banks, so the 16 rows one 8-byte read
-    // instruction touches (lanes c = 0..15 of a group) fall on 32 distinct banks.
-    static constexpr int VTS = WIDE_NP + 4;
+    static constexpr int ROWB = 2 * D;           // bytes of a staged key / value row
+    static constexpr int OPB = WIDE_NP * ROWB;   // bytes of one staged operand (48 KB at D = 128)
+    static constexpr int NDMA = OPB / 1024;      // 1-KB direct loads per operand
+    static constexpr int PWD = NDMA / WIDE_WAVES;   // direct loads per wave and operand (6 at D = 128)
+    static constexpr int CH = D / 8;             // 16-byte chunks per row
+    static constexpr int RP = 256 / ROWB;        // rows per 256 bytes (64 banks)
+    static_assert(NDMA % WIDE_WAVES == 0 && PWD < 16, "direct-load split");
 };
+// chunk position of logical 16-byte chunk c of staged key row r / value row s (XOR: its own inverse)
+template <int D> __device__ __forceinline__ int kpos(int r, int c) {
+    return c ^ ((r / WideSmem<D>::RP) & (WideSmem<D>::CH - 1));
+}
+template <int D> __device__ __forceinline__ int vpos(int r, int c) {
+    return c ^ (2 * ((r / WideSmem<D>::RP) & (WideSmem<D>::CH / 2 - 1)));
+}
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+__device__ __forceinline__ uint2 ld_tr16(const unsigned char* p) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const lds_void*)p)));
+}
+// wait until at most n of this wave's vector-memory operations are outstanding.  The direct loads are not
+// tracked by the compiler; the kernel's other vector-memory operations -- query loads, output stores, any
+// scratch access -- are tracked by it or younger, so they can only make these waits longer, never shorter.
+template <int n> __device__ __forceinline__ void wide_wait_vm() {
+    static_assert(n >= 0 && n < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | n);
+}
 
 template <int D>
 __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
+    using S = WideSmem<D>;
     constexpr int KK = D / 32;
     constexpr int DT = D / 16;
-    constexpr int KST = WideSmem<D>::KST;
-    constexpr int VTS = WideSmem<D>::VTS;
-    __shared__ __align__(16) bf16_t sK[WIDE_NP * KST];
-    __shared__ __align__(16) bf16_t sVt[D * VTS];
-    __shared__ __align__(16) float sKV[WIDE_NP];          // kinv of a valid slot, 0 otherwise
-    __shared__ __align__(16) float sMK[WIDE_NP];          // 0 for a valid slot, -inf otherwise
+    constexpr int NT = WIDE_NP / 16;                       // slot tiles
+    __shared__ __align__(1024) unsigned char sKb[2][S::OPB];
+    __shared__ __align__(1024) unsigned char sVb[S::OPB];
+    __shared__ __align__(16) float sKV[2][WIDE_NP];       // kinv of a valid slot, 0 otherwise
+    __shared__ __align__(16) float sMK[2][WIDE_NP];       // 0 for a valid slot, -inf otherwise
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int slab = blockIdx.x;
-    const int h = slab % a.H;
-    const int j = (slab / a.H) % a.NB;
-    const int b = slab / (a.H * a.NB);
-    const int t0 = j * a.G;
-    const int Mblk = min(a.G, a.T - t0) * a.NQ;
-    const int mlo = blockIdx.y * a.MC;
-    const int mhi = min(Mblk, mlo + a.MC);
-    if (mlo >= mhi) return;
     const int N = a.N;
-    const bf16_t* Kb = a.kb + (size_t)slab * N * D;
-    const bf16_t* Vb = a.vb + (size_t)slab * N * D;
+    const int nunits = a.slabs * a.parts;
+    const int TPW = (a.MC / 32 + WIDE_WAVES - 1) / WIDE_WAVES;   // 32-query tile pairs per wave and unit
 
-    // ---- stage keys, transposed values and kinv/valid (rows >= N are zero / invalid)
-    {
-        constexpr int KTOT = WIDE_NP * (D / 8);
-        constexpr int KCH = (KTOT + WIDE_THREADS - 1) / WIDE_THREADS;  // 16-byte key chunks per thread
-        uint4 xk[KCH];
+    struct Unit { int slab, b, h, t0, mlo, mhi; };
+    auto unit = [&](int u) {
+        Unit x;                                            // (every field wave-uniform: scalar registers)
+        u = __builtin_amdgcn_readfirstlane(u);
+        x.slab = u / a.parts;
+        const int part = u - x.slab * a.parts;
+        x.h = x.slab % a.H;
+        const int j = (x.slab / a.H) % a.NB;
+        x.b = x.slab / (a.H * a.NB);
+        x.t0 = j * a.G;
+        const int Mblk = min(a.G, a.T - x.t0) * a.NQ;
+        x.mlo = part * a.MC;
+        x.mhi = min(Mblk, x.mlo + a.MC);
+        x.slab = __builtin_amdgcn_readfirstlane(x.slab); x.b = __builtin_amdgcn_readfirstlane(x.b);
+        x.h = __builtin_amdgcn_readfirstlane(x.h); x.t0 = __builtin_amdgcn_readfirstlane(x.t0);
+        x.mlo = __builtin_amdgcn_readfirstlane(x.mlo); x.mhi = __builtin_amdgcn_readfirstlane(x.mhi);
+        return x;
+    };
+    // this wave's direct loads of one staged operand (keys: kpos, values: vpos): lane L of block b fills LDS
+    // bytes 1024 b + 16 L, i.e. row (1024 b + 16 L) / ROWB at chunk position p, from the chunk stored there
+    auto stage = [&](const bf16_t* src, unsigned char* dst, bool val) {
 #pragma unroll
-        for (int it = 0; it < KCH; it++) {
-            const int e = min(threadIdx.x + WIDE_THREADS * it, KTOT - 1);
-            const int n = e / (D / 8), cc = e % (D / 8);
-            xk[it] = n < N ? *reinterpret_cast<const uint4*>(Kb + (size_t)n * D + cc * 8) : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < S::PWD; i++) {
+            const int blk = w * S::PWD + i, byte = blk * 1024 + 16 * lane;
+            const int r = byte / S::ROWB, p = (byte % S::ROWB) / 16;
+            const int cc = val ? vpos<D>(r, p) : kpos<D>(r, p);
+            dma16(src + (size_t)min(r, N - 1) * D + 8 * cc, lds_addr(dst + blk * 1024));
         }
-        // row pairs x 8-dim chunks per thread; the row pair varies fastest across lanes so that the
-        // transposed 4-byte LDS writes of a wave land in consecutive banks
-        constexpr int VTOT = (WIDE_NP / 2) * (D / 8);
-        constexpr int VCH = (VTOT + WIDE_THREADS - 1) / WIDE_THREADS;
-        uint4 v0[VCH], v1[VCH];
-#pragma unroll
-        for (int it = 0; it < VCH; it++) {
-            const int e = min(threadIdx.x + WIDE_THREADS * it, VTOT - 1);
-            const int p = e % (WIDE_NP / 2), cc = e / (WIDE_NP / 2);
-            const int n = 2 * p;
-            v0[it] = n < N ? *reinterpret_cast<const uint4*>(Vb + (size_t)n * D + cc * 8) : make_uint4(0, 0, 0, 0);
-            v1[it] = n + 1 < N ? *reinterpret_cast<const uint4*>(Vb + (size_t)(n + 1) * D + cc * 8) : make_uint4(0, 0, 0, 0);
-        }
+    };
+    auto load_kv = [&](const Unit& x, float& ki, uint32_t& va) {
+        const int nc = min((int)threadIdx.x, N - 1);
+        ki = a.kinv[(size_t)x.slab * N + nc];
+        va = a.valid[(size_t)x.slab * N + nc];
+    };
+    auto publish_kv = [&](int buf, float ki, uint32_t va) {
         if (threadIdx.x < WIDE_NP) {
-            const int n = threadIdx.x;
-            const int nc = min(n, N - 1);
-            const uint8_t va = a.valid[(size_t)slab * N + nc];
-            const float ki = a.kinv[(size_t)slab * N + nc];
-            const bool ok = n < N && va != 0;
-            sKV[n] = ok ? ki : 0.f;
-            sMK[n] = ok ? 0.f : -INFINITY;
+            const bool ok = (int)threadIdx.x < N && va != 0;
+            sKV[buf][threadIdx.x] = ok ? ki : 0.f;
+            sMK[buf][threadIdx.x] = ok ? 0.f : -INFINITY;
         }
-#pragma unroll
-        for (int it = 0; it < KCH; it++) {
-            const int e = threadIdx.x + WIDE_THREADS * it;
-            if (e >= KTOT) break;
-            const int n = e / (D / 8), cc = e % (D / 8);
-            *reinterpret_cast<uint4*>(sK + n * KST + cc * 8) = xk[it];
-        }
-#pragma unroll
-        for (int it = 0; it < VCH; it++) {
-            const int e = threadIdx.x + WIDE_THREADS * it;
-            if (e >= VTOT) break;
-            const int p = e % (WIDE_NP / 2), cc = e / (WIDE_NP / 2);
-            const uint32_t a0[4] = {v0[it].x, v0[it].y, v0[it].z, v0[it].w};
-            const uint32_t a1[4] = {v1[it].x, v1[it].y, v1[it].z, v1[it].w};
-#pragma unroll
-            for (int q = 0; q < 4; q++) {                 // dims 8cc + 2q, 8cc + 2q + 1: slots (2p, 2p+1) packed
-                const uint32_t lo = (a0[q] & 0xffffu) | (a1[q] << 16);
-                const uint32_t hi = (a0[q] >> 16) | (a1[q] & 0xffff0000u);
-                *reinterpret_cast<uint32_t*>(sVt + (8 * cc + 2 * q) * VTS + 2 * p) = lo;
-                *reinterpret_cast<uint32_t*>(sVt + (8 * cc + 2 * q + 1) * VTS + 2 * p) = hi;
-            }
-        }
-    }
-    __syncthreads();
-
-    auto load_q = [&](int m0, uint4* qf, float& scl) {
+    };
+    // the queries of the 16-query tile at m0: lane column m0 + c, dims kk * 32 + 8 g
+    auto load_q = [&](const Unit& x, int m0, uint4* qf, float& scl) {
         const int m = m0 + c;
-        const bool mok = m < mhi;
+        const bool mok = m < x.mhi;
         size_t qrow = 0;
-        if (mok) qrow = (((size_t)b * a.T + t0 + m / a.NQ) * a.H + h) * a.NQ + (m % a.NQ);
+        if (mok) qrow = (((size_t)x.b * a.T + x.t0 + m / a.NQ) * a.H + x.h) * a.NQ + (m % a.NQ);
 #pragma unroll
         for (int kk = 0; kk < KK; kk++)
             qf[kk] = mok ? *reinterpret_cast<const uint4*>(a.q + qrow * D + kk * 32 + 8 * g) : make_uint4(0, 0, 0, 0);
         scl = mok ? a.scale[qrow] : 0.f;
     };
-    int m0 = mlo + 16 * w;
-    uint4 qn[KK];
-    float scn = 0.f;
-    if (m0 < mhi) load_q(m0, qn, scn);
-    for (; m0 < mhi; m0 += 16 * WIDE_WAVES) {
-        // an opaque zero offset for the LDS operand reads: keeps the compiler from hoisting all 96 invariant
-        // key / value fragments out of the loop (they would need 384 registers)
-        int lo0 = 0;
-        asm volatile("" : "+v"(lo0));
-        uint4 qf[KK];
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++) qf[kk] = qn[kk];
-        const float scl = scn;
-        if (m0 + 16 * WIDE_WAVES < mhi) load_q(m0 + 16 * WIDE_WAVES, qn, scn);
+    auto load_pair = [&](const Unit& x, int m0, uint4 (&qf)[2][KK], float (&scl)[2]) {
+        load_q(x, m0, qf[0], scl[0]);
+        load_q(x, m0 + 16, qf[1], scl[1]);
+    };
 
-        // ---- scores S^T for all slot tiles: lane column = query m0 + c, items = slots 16nt + 4g + i
-        // k-step outer, slot tile inner: 12 independent accumulation chains keep the MFMA pipe full
-        f32x4 acc[WIDE_NP / 16];
+    // per-lane swizzles: key operand rows nt * 16 + c; value rows (tile) 4 g + ((c >> 2) & 3) (+ 32 cc, + 16)
+    const int ksw = (c / S::RP) & (S::CH - 1);
+    const int rq = (c >> 2) & 3;
+    const int vsw = 2 * (((4 * g + rq) / S::RP) & (S::CH / 2 - 1));
+    const int vch = (c & 3) >> 1, vhb = 8 * (c & 1);
+
+    // ---- prologue: the first unit's keys, values, kinv / valid and first query tile pair
+    int u = blockIdx.x;
+    Unit cur = unit(u);
+    stage(a.kb + (size_t)cur.slab * N * D, sKb[0], false);
+    stage(a.vb + (size_t)cur.slab * N * D, sVb, true);
+    {
+        float ki;
+        uint32_t va;
+        load_kv(cur, ki, va);
+        publish_kv(0, ki, va);
+    }
+    uint4 qn[2][KK];
+    float scn[2] = {0.f, 0.f};
+    load_pair(cur, cur.mlo + 32 * w, qn, scn);
+    wide_wait_vm<0>();
+    __syncthreads();
+    int kb = 0;
+    for (;;) {
+        const int un = u + gridDim.x;
+        const bool hasn = un < nunits;
+        Unit nx = cur;
+        float kin = 0.f;
+        uint32_t van = 0;
+        if (hasn) nx = unit(un);
+        const unsigned char* Kc = sKb[kb];
+        for (int t = 0; t < TPW; t++) {
+            // a pair of 16-query tiles, A = [m0, m0 + 16) and B = [m0 + 16, m0 + 32): every key and value operand
+            // read from LDS feeds one MFMA of each
+            const int m0 = cur.mlo + 32 * (w + WIDE_WAVES * t);
+            const bool live = m0 < cur.mhi;
+            int lo0 = 0;                                   // opaque zero: no hoisting of the invariant key reads
+            asm volatile("" : "+v"(lo0));
+            uint4 qf[2][KK];
+            float scl[2];
 #pragma unroll
-        for (int nt = 0; nt < WIDE_NP / 16; nt++) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int e = 0; e < 2; e++) {
 #pragma unroll
-        for (int ng = 0; ng < WIDE_NP / 64; ng++) {               // 3 groups of 4 slot tiles
+                for (int kk = 0; kk < KK; kk++) qf[e][kk] = qn[e][kk];
+                scl[e] = scn[e];
+            }
+            if (t + 1 < TPW) load_pair(cur, m0 + 32 * WIDE_WAVES, qn, scn);
+            else if (hasn) load_pair(nx, nx.mlo + 32 * w, qn, scn);
+
+            f32x4 acc[2][NT];
+            uint4 pB[2][WIDE_NP / 32];
+            if (live) {
+                // ---- scores S^T for all slot tiles: lane column = query m0 (+16) + c, items = slots 16 nt + 4 g + i
 #pragma unroll
-            for (int kk = 0; kk < KK; kk++)
+                for (int e = 0; e < 2; e++)
 #pragma unroll
-                for (int nt = 4 * ng; nt < 4 * ng + 4; nt++) {
-                    // all 192 staged slots, branch-free: rows >= N are zero and marked invalid
-                    const uint4 ka = *reinterpret_cast<const uint4*>(sK + lo0 + (nt * 16 + c) * KST + kk * 32 + 8 * g);
-                    acc[nt] = mfma_k32(ka, qf[kk], acc[nt]);
+                    for (int nt = 0; nt < NT; nt++) acc[e][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ng = 0; ng < NT / 4; ng++) {                      // 3 groups of 4 slot tiles
+#pragma unroll
+                    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+                        for (int nt = 4 * ng; nt < 4 * ng + 4; nt++) {
+                            const uint4 ka = *reinterpret_cast<const uint4*>(
+                                Kc + lo0 + (nt * 16 + c) * S::ROWB + 16 * ((4 * kk + g) ^ ksw));
+                            acc[0][nt] = mfma_k32(ka, qf[0][kk], acc[0][nt]);
+                            acc[1][nt] = mfma_k32(ka, qf[1][kk], acc[1][nt]);
+                        }
+                    __builtin_amdgcn_sched_barrier(0);                    // bound the operand prefetch window
                 }
-            __builtin_amdgcn_sched_barrier(0);                    // bound the operand prefetch window
-        }
-        // scores in the log2 domain, u = raw * kinv * scale * log2(e) (+ -inf for an invalid slot), so that
-        // exp(s - max s) = exp2(u - max u) is one v_exp_f32 (the library exp2f adds a range fix-up of five
-        // more VALU operations for results below 2^-126, far below what the bf16 output resolves)
-        float sc[WIDE_NP / 16][4];
-        float mx = -INFINITY;
-        const float scl2 = scl * LOG2E_F;
+                // v = raw * kinv (+ -inf for an invalid slot), raw the bf16-rounded dot product; with the
+                // per-query scale s > 0 the softmax is exp(s (v - max v)) = exp2(fma(v, s log2(e), -max v s log2(e))):
+                // the shift rides in the fma, one v_exp_f32 per score
+                float mxt[2][NT];                                         // per slot tile, then a tree
 #pragma unroll
-        for (int nt = 0; nt < WIDE_NP / 16; nt++) {
-            const float4 kv = *reinterpret_cast<const float4*>(sKV + lo0 + nt * 16 + 4 * g);
-            const float4 mk = *reinterpret_cast<const float4*>(sMK + lo0 + nt * 16 + 4 * g);
-            const float kvs[4] = {kv.x, kv.y, kv.z, kv.w};
-            const float mks[4] = {mk.x, mk.y, mk.z, mk.w};
+                for (int nt = 0; nt < NT; nt++) {                          // kinv and mask read once per pair
+                    const float4 kv = *reinterpret_cast<const float4*>(&sKV[kb][lo0 + nt * 16 + 4 * g]);
+                    const float4 mk = *reinterpret_cast<const float4*>(&sMK[kb][lo0 + nt * 16 + 4 * g]);
+                    const float kvs[4] = {kv.x, kv.y, kv.z, kv.w};
+                    const float mks[4] = {mk.x, mk.y, mk.z, mk.w};
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float u = fmaf(bf16r(acc[nt][i]) * kvs[i], scl2, mks[i]);
-                sc[nt][i] = u;
-                mx = fmaxf(mx, u);
+                    for (int e = 0; e < 2; e++) {
+                        const uint32_t r01 = pack2(acc[e][nt][0], acc[e][nt][1]);
+                        const uint32_t r23 = pack2(acc[e][nt][2], acc[e][nt][3]);
+                        const float raw[4] = {__uint_as_float(r01 << 16), __uint_as_float(r01 & 0xffff0000u),
+                                              __uint_as_float(r23 << 16), __uint_as_float(r23 & 0xffff0000u)};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[e][nt][i] = fmaf(raw[i], kvs[i], mks[i]);
+                        mxt[e][nt] = fmaxf(fmaxf(acc[e][nt][0], acc[e][nt][1]), fmaxf(acc[e][nt][2], acc[e][nt][3]));
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+#pragma unroll
+                    for (int st = 1; st < NT; st *= 2)                     // pairwise tree over the slot tiles
+#pragma unroll
+                        for (int nt = 0; nt + st < NT; nt += 2 * st) mxt[e][nt] = fmaxf(mxt[e][nt], mxt[e][nt + st]);
+                    const float mx = max4rows(mxt[e][0]);
+                    const float s2 = scl[e] * LOG2E_F;
+                    const float sh = mx == -INFINITY ? 0.f : -mx * s2;    // no valid slot: every term exp2(-inf) = 0
+                    float st4[NT];
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[e][nt][i] = __builtin_amdgcn_exp2f(fmaf(acc[e][nt][i], s2, sh));
+                        st4[nt] = (acc[e][nt][0] + acc[e][nt][1]) + (acc[e][nt][2] + acc[e][nt][3]);
+                    }
+#pragma unroll
+                    for (int st = 1; st < NT; st *= 2)
+#pragma unroll
+                        for (int nt = 0; nt + st < NT; nt += 2 * st) st4[nt] += st4[nt + st];
+                    const float sum = sum4rows(st4[0]);
+                    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+#pragma unroll
+                    for (int cc = 0; cc < WIDE_NP / 32; cc++) {
+                        pB[e][cc].x = pack2(acc[e][2 * cc][0] * inv, acc[e][2 * cc][1] * inv);
+                        pB[e][cc].y = pack2(acc[e][2 * cc][2] * inv, acc[e][2 * cc][3] * inv);
+                        pB[e][cc].z = pack2(acc[e][2 * cc + 1][0] * inv, acc[e][2 * cc + 1][1] * inv);
+                        pB[e][cc].w = pack2(acc[e][2 * cc + 1][2] * inv, acc[e][2 * cc + 1][3] * inv);
+                    }
+                }
+            }
+            if (t == 0) {
+                // this unit's values (their loads went out at the end of the previous unit, behind its last
+                // tile): wait for everything this wave issued, then the next unit's keys and kinv / valid go out,
+                // behind the rest of this unit
+                wide_wait_vm<0>();
+                __syncthreads();
+                if (hasn) {
+                    stage(a.kb + (size_t)nx.slab * N * D, sKb[kb ^ 1], false);
+                    load_kv(nx, kin, van);
+                }
+            }
+            // the unit's last pair: wait here for everything this wave has issued -- the next unit's keys and
+            // kinv / valid among it, long done -- so that no wait is needed after this pair's output stores
+            // (gfx9 counts stores on the same counter: a wait behind them would wait for their round trip)
+            if (t == TPW - 1) wide_wait_vm<0>();
+            if (live) {
+                // ---- O^T = V^T P^T, one 16-dim tile at a time (both query tiles per value operand), stored as 4
+                // dims x 1 query per lane
+                f32x4 o[2][DT];
+#pragma unroll
+                for (int e = 0; e < 2; e++)
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++) o[e][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int cc = 0; cc < WIDE_NP / 32; cc++) {
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++) {
+                        const unsigned char* vr = sVb + (cc * 32 + 4 * g + rq) * S::ROWB + 16 * ((2 * dt + vch) ^ vsw) + vhb;
+                        const uint2 lo = ld_tr16(vr);
+                        const uint2 hi = ld_tr16(vr + 16 * S::ROWB);
+                        const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                        o[0][dt] = mfma_k32(va, pB[0][cc], o[0][dt]);
+                        o[1][dt] = mfma_k32(va, pB[1][cc], o[1][dt]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const int m = m0 + 16 * e + c;
+                    if (m < cur.mhi) {
+                        bf16_t* dst = a.rd + ((((size_t)cur.b * a.T + cur.t0 + m / a.NQ) * a.H + cur.h) * a.NQ + (m % a.NQ)) * D;
+#pragma unroll
+                        for (int dt = 0; dt < DT; dt++) {
+                            uint2 x;
+                            x.x = pack2(o[e][dt][0], o[e][dt][1]);
+                            x.y = pack2(o[e][dt][2], o[e][dt][3]);
+                            *reinterpret_cast<uint2*>(dst + dt * 16 + 4 * g) = x;
+                        }
+                    }
+                }
             }
         }
-        mx = max4rows(mx);
-        const float mxs = mx == -INFINITY ? 0.f : mx;              // no valid slot: every term is exp2(-inf) = 0
-        float sum = 0.f;
-#pragma unroll
-        for (int nt = 0; nt < WIDE_NP / 16; nt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float e = __builtin_amdgcn_exp2f(sc[nt][i] - mxs);
-                sc[nt][i] = e;
-                sum += e;
-            }
-        sum = sum4rows(sum);
-        const float inv = sum > 0.f ? 1.f / sum : 0.f;
-        uint4 pB[WIDE_NP / 32];
-#pragma unroll
-        for (int cc = 0; cc < WIDE_NP / 32; cc++) {
-            pB[cc].x = pack2(sc[2 * cc][0] * inv, sc[2 * cc][1] * inv);
-            pB[cc].y = pack2(sc[2 * cc][2] * inv, sc[2 * cc][3] * inv);
-            pB[cc].z = pack2(sc[2 * cc + 1][0] * inv, sc[2 * cc + 1][1] * inv);
-            pB[cc].w = pack2(sc[2 * cc + 1][2] * inv, sc[2 * cc + 1][3] * inv);
-        }
-        // ---- O^T = V^T P^T, one 16-dim tile at a time, stored as 4 dims x 1 query per lane
-        const int m = m0 + c;
-        const bool mok = m < mhi;
-        bf16_t* dst = nullptr;
-        if (mok) dst = a.rd + ((((size_t)b * a.T + t0 + m / a.NQ) * a.H + h) * a.NQ + (m % a.NQ)) * D;
-        f32x4 o[DT];
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int cc = 0; cc < WIDE_NP / 32; cc++) {
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                const bf16_t* vr = sVt + lo0 + (dt * 16 + c) * VTS + cc * 32 + 4 * g;
-                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-                o[dt] = mfma_k32(make_uint4(lo.x, lo.y, hi.x, hi.y), pB[cc], o[dt]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (mok) {
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                uint2 x;
-                x.x = pack2(o[dt][0], o[dt][1]);
-                x.y = pack2(o[dt][2], o[dt][3]);
-                *reinterpret_cast<uint2*>(dst + dt * 16 + 4 * g) = x;
-            }
-        }
+        __syncthreads();                                     // every wave is done with this unit's keys and values
+        if (!hasn) break;
+        stage(a.vb + (size_t)nx.slab * N * D, sVb, true);     // the next unit's values
+        publish_kv(kb ^ 1, kin, van);                        // (its keys landed before the last pair's stores)
+        __syncthreads();
+        u = un;
+        cur = nx;
+        kb ^= 1;
     }
 }
 
@@ -975,6 +1074,19 @@ static int read_rows_per_wg(int64_t slabs, int64_t Mfull) {
     return (int)(per * 16);
 }
 
+// compute units of the current device (cached per device)
+static int cu_count() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cache[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
 extern "C" int slotread_fwd(const void* q, const void* kbuf, const void* vbuf, const float* kinv,
                             const uint8_t* valid, const float* scale, int64_t B, int64_t T, int64_t H, int64_t NQ,
                             int64_t N, int64_t D, int64_t G, void* rd, void* stream) {
@@ -989,7 +1101,7 @@ extern "C" int slotread_fwd(const void* q, const void* kbuf, const void* vbuf, c
     const int MC = read_rows_per_wg(slabs, G * NQ);
     const int64_t ysplit = (G * NQ + MC - 1) / MC;
     ReadFwdArgs ra{(const bf16_t*)q, (const bf16_t*)kbuf, (const bf16_t*)vbuf, kinv, valid, scale, (bf16_t*)rd,
-                   (int)T, (int)H, (int)NQ, (int)N, (int)G, (int)NB, MC};
+                   (int)T, (int)H, (int)NQ, (int)N, (int)G, (int)NB, MC, (int)slabs, 1};
     dim3 grid((unsigned)slabs, (unsigned)ysplit), block(READ_THREADS);
     hipError_t e;
     {
@@ -1001,7 +1113,11 @@ extern "C" int slotread_fwd(const void* q, const void* kbuf, const void* vbuf, c
             if (split > (tiles + WIDE_WAVES - 1) / WIDE_WAVES) split = (tiles + WIDE_WAVES - 1) / WIDE_WAVES;
             if (split < 1) split = 1;
             ra.MC = (int)(((tiles + split - 1) / split) * 16);
-            dim3 wgrid((unsigned)slabs, (unsigned)((G * NQ + ra.MC - 1) / ra.MC)), wblock(WIDE_THREADS);
+            ra.MC = (ra.MC + 31) / 32 * 32;                   // whole 32-query tile pairs
+            ra.parts = (int)((G * NQ + ra.MC - 1) / ra.MC);
+            // persistent: one workgroup per CU (the 147 KB of LDS hold one), each walking about 3 units
+            const int64_t units = slabs * ra.parts;
+            dim3 wgrid((unsigned)std::min<int64_t>(units, cu_count())), wblock(WIDE_THREADS);
             if (D == 128) slothost::launch(read_fwd_wide<128>, wgrid, wblock, 0, st, ra);
             else slothost::launch(read_fwd_wide<64>, wgrid, wblock, 0, st, ra);
         } else {
