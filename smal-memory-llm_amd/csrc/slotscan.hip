@@ -1628,13 +1628,15 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 // `wpc` 16-step windows, one workgroup each (grid (B*H, chunks)): the state at a chunk's end t_end is exact
 // from the undo log -- row n holds kold (oold) of its first write at or after t_end, or kfin (ofin) when no
 // later step writes it -- so the chunks run concurrently.  A workgroup of NW = D / 16 waves walks its windows
-// in reverse:
-//   S1  publish the prefetched window: cosines and Dn step-major, kold and query rows, the step scalars;
-//   S2  |kold_i|^2 of each write (one wave: lane = (write, part)), and per write the next write to the same row
-//       inside the window and whether it is the row's first;
+// in reverse, three barriers per window (B1 after S1, B2 after S4, B3 after S7):
+//   S1  publish the prefetched window (Dn transposed to step-major, kold and query rows, the step scalars) and
+//       derive from registers alone what the window's writes need: 1 / |kold_i| and 1 / |q_t| (lane sums over
+//       each row's prefetch lanes), and from the step scalars, which every wave loads, each wave's share of the
+//       occupancy masks (bit s of row n = row n occupied at step s) and per write the next write to the same
+//       row inside the window and whether it is the row's first;
 //   S4  the softmax adjoints of all 16 steps at once: step s is a group of NC = NT / 16 lanes (one or two DPP
-//       rows), each lane RPC consecutive slot rows.  The occupancy at s follows from the window-end occupancy
-//       and the window's later writes; the exponentials are shifted by the largest z over the eligible rows
+//       rows), each lane RPC slot rows strided by NC, its cosines straight from its prefetch registers.  The
+//       exponentials are shifted by the largest z over the eligible rows
 //       (the occupied ones and the lowest free one, a step-group max); SS and sum e dw are step-group sums;
 //       W[s][n] = temp dz_n goes to LDS; dgate = Dn of the written row; dfr in closed form over the occupied
 //       rows; dtemp accumulates sum dz cs;
@@ -1645,11 +1647,15 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 //   S7  the undo, every write at once: x_i = Kh(kold_i); the key after write i is Kh(kold_j) of the next write
 //       j to the same row in the window, else the window-end key; delta_i = x_i - after_i.  Then each row the
 //       window wrote takes x of its FIRST write: the keys at the window start;
-//   S8  the rewritten rows' correction, sum_{s >= t} W[t][a_s] delta_s, as a 16 x 16 x 16 MFMA;
+//   S8  the rewritten rows' correction, sum_{s >= t} W[t][a_s] delta_s, as a 16 x 16 x 16 MFMA (S6 and S8 produce
+//       dqn transposed, so each lane holds four consecutive dims of one step and stores them at once);
 //   S9  dq = qinv (dqn - qhat <qhat, dqn>) (qinv dqn where |q| < 1e-6), one LDS exchange for the dot products.
-// Every Kh value is an element times rsq_clamped(|row|^2), |row|^2 summed in one fixed order (a lane's part
-// of 4-element pieces, then sum4rows) wherever a key is normalised, so a chunk starts from bitwise the keys
-// the reverse walk of the whole chain would hold there: the results do not depend on the chunking.
+// What S8 and S9 need from LDS that the next window's S1 and S4 overwrite is read into registers before B3, and
+// the undo deltas have their own buffer, so no barrier closes a window.
+// Every Kh value is an element times rsq_clamped(|row|^2), |row|^2 summed in one fixed order (sq4 of each
+// lane's 4-element piece, then lanesum over the row's D / 4 lanes) wherever a key is normalised, so a chunk
+// starts from bitwise the keys the reverse walk of the whole chain would hold there: the results do not depend
+// on the chunking.
 #define WIN 16
 
 // Reductions over the NC lanes of one step in the softmax phase: one DPP row (NC = 16) or two (NC = 32, the
@@ -1707,48 +1713,79 @@ template <int NC> __device__ __forceinline__ void step_argmin(int& i, float& x, 
     }
 }
 
+// Sum over aligned groups of L consecutive lanes (L = 8, 16 or 32), the bitwise-same result at every lane of a
+// group: each stage adds the same two partial sums (IEEE addition is commutative).
+template <int L> __device__ __forceinline__ float lanesum(float v) {
+    static_assert(L == 8 || L == 16 || L == 32, "lane group");
+    v += dppf<SLOT_DPP_XOR1>(v);
+    v += dppf<SLOT_DPP_XOR2>(v);
+    v += dppf<SLOT_DPP_HMIR>(v);
+    if constexpr (L >= 16) v += dppf<SLOT_DPP_MIR>(v);
+    if constexpr (L == 32) {
+        auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    return v;
+}
+// An empty use of values in vector registers: the loads that produce them are issued before it on every path,
+// so a group of LDS reads is issued together and waited on once (the compiler otherwise sinks each read into
+// the branch of the select that consumes it, one wait per read).
+__device__ __forceinline__ void keep() {}
+template <typename T, typename... Ts> __device__ __forceinline__ void keep(T& v, Ts&... r) {
+    asm volatile("" : "+v"(v));
+    keep(r...);
+}
+// The squares of a 4-element key piece, summed in one fixed order (the first term of every key norm).
+__device__ __forceinline__ float sq4(float4 x) { return fmaf(x.w, x.w, fmaf(x.z, x.z, fmaf(x.y, x.y, x.x * x.x))); }
+
 template <int D, int RPL, typename TI>
 __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
-    constexpr int NW = D / 16;                          // waves: wave w owns dims [16 w, 16 w + 16)
+    constexpr int NW = D / 16;                          // waves: wave w owns dims [16 w, 16 w + 16) in S6, S8, S9
     constexpr int NT = 64 * NW;
     constexpr int NR = 64 * RPL;                        // slot-row capacity
     constexpr int KK = NR / 4;                          // MFMA k-steps over the rows
-    constexpr int P = NR + 4;                           // transposed key stride: 4 mod 32 banks
+    constexpr int P = NR + 4;                           // transposed key stride: 4 mod 64 banks
     constexpr int SW = NR + 4;                          // W row stride, likewise
-    constexpr int SC = NR + 2;                          // cosine / Dn row stride (step-major): 2 mod 32 banks, so
-                                                        // the Dn publish (16 steps x 2 rows per 32-lane pass of
-                                                        // 4-byte accesses) hits 32 distinct banks
-    constexpr int KOS = D + 4;                          // kold / query row stride
+    constexpr int SD = NR + 4;                          // Dn row stride (step-major), likewise: the transposing
+                                                        // publish (16 steps x 4 rows per store) hits 64 banks
     constexpr int NC = NT / WIN;                        // lanes per step in the softmax phase
-    constexpr int RPC = NR / NC;                        // slot rows per lane in the softmax phase
+    constexpr int RPC = NR / NC;                        // slot rows per lane there: r, r + NC, r + 2 NC, ...
+    constexpr int KOS = D + NC;                         // kold row stride, NC mod 64 banks: the undo's writes of one
+                                                        // wave (2 or 4, NC dims each) read disjoint banks
+    constexpr int QS = D + 4;                           // query row stride: S9's four steps per wave on distinct banks
     constexpr int DPT = D / NC;                         // dims per lane in the undo (4), strided by NC
-    constexpr int DEL = D + 16;                         // undo-delta row stride: 2 steps x 16 dims per 32-lane pass
-                                                        // of 4-byte reads on distinct banks
-    constexpr int EPU = 16 / (int)sizeof(TI);
-    constexpr int UCS = (WIN * NR + NT - 1) / NT;       // per-lane prefetch: cosines, Dn
-    constexpr int UKO = (WIN * D / 4 + NT - 1) / NT;    // kold rows (uint4)
-    constexpr int UQ = (WIN * D / EPU + NT - 1) / NT;   // query rows (uint4)
+    constexpr int DEL = D + 16;                         // undo-delta row stride
+    constexpr int EPU = 16 / (int)sizeof(TI);           // query elements per 16-byte piece
+    constexpr int KLR = D / 4;                          // lanes per kold row in the prefetch (one float4 each)
+    constexpr int QLR = D / EPU;                        // lanes per query row in the prefetch (one 16-byte piece)
+    constexpr int UDN = (4 * NR + NT - 1) / NT;         // Dn float4 pieces per lane in the prefetch (4 per row)
+    constexpr int Q4 = RPC / 4, R2 = (RPC % 4) / 2;     // softmax lane rows: Q4 groups of 4, then R2 pairs
     constexpr bool BF = sizeof(TI) == 2;
-    static_assert(DPT == 4 && RPC % 2 == 0 && (KK / 4) % 2 == 0, "layout assumptions");
+    static_assert(DPT == 4 && (KK / 4) % 2 == 0 && WIN * KLR == NT && WIN * QLR <= NT && (WIN * QLR) % 64 == 0 &&
+                  RPC == 4 * Q4 + 2 * R2 && (4 * NR) % 64 == 0 && RPL + 1 <= NW, "layout assumptions");
     __shared__ __align__(16) float sKT[D * P];          // normalised keys, transposed
-    __shared__ __align__(16) float sW[WIN * SW];
-    constexpr int CSN = WIN * SC > WIN * DEL ? WIN * SC : WIN * DEL;
-    __shared__ __align__(16) float sCS[CSN];            // cosines [step][row]; the undo deltas [step][D] after S4
-    __shared__ __align__(16) float sDN[WIN * SC];       // Dn [step][row]
+    __shared__ __align__(16) float sW[WIN * SW];        // W = temp dz [step][row]
+    __shared__ __align__(16) float sDN[WIN * SD];       // Dn [step][row]
+    __shared__ __align__(16) float sDel[WIN * DEL];     // undo deltas [write][dim]
     __shared__ __align__(16) float sKO[WIN * KOS];      // kold rows of the window's writes
-    __shared__ __align__(16) float sQ[WIN * KOS];       // query rows
+    __shared__ __align__(16) float sQ[WIN * QS];        // query rows
     __shared__ float sO[NR];                            // occupancy at the window end
     __shared__ u32 s_tkm[NR];                           // per row: bit s = occupied at window step s
-    __shared__ __align__(16) int s_am[WIN];
-    __shared__ __align__(16) float s_oo[WIN];
+    __shared__ u32 s_scw[RPL + 1][4 * WIN];             // step scalars (address, oold, gate, fr; 16 each), one
+                                                        // copy per mask wave; wave 0's serves the whole block
+    u32* s_sc = s_scw[0];
+    __shared__ float s_kil[WIN], s_qi[WIN], s_pr[WIN];
+    __shared__ float s_dgf[2][WIN];                     // per step: dgate and the per-token dfr, stored by wave 0
     __shared__ int s_nx[WIN], s_first[WIN];
-    __shared__ float s_g[WIN], s_fr[WIN], s_kil[WIN], s_qi[WIN], s_pr[WIN];
     __shared__ float s_fin[2][NW];
-    float* sDel = sCS;
+    const int* s_am = reinterpret_cast<const int*>(s_sc);
+    const float* s_oo = reinterpret_cast<const float*>(s_sc + WIN);
+    const float* s_g = reinterpret_cast<const float*>(s_sc + 2 * WIN);
+    const float* s_fr = reinterpret_cast<const float*>(s_sc + 3 * WIN);
 
     const int T = a.T, H = a.H, N = a.N;
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, grp = lane >> 4;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const TI* __restrict__ qp = (const TI*)a.q;
     const size_t tok0 = (size_t)b * T * H + h;
     const float temp = a.temp[0];
@@ -1767,25 +1804,32 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     __syncthreads();
     for (int t = t_end + tid; t < T; t += NT) atomicMin(&s_fw[min(max(a.am[tok0 + (size_t)t * H], 0), NR - 1)], t);
     __syncthreads();
-    // the keys at t_end (kold of the row's first later write, else kfin), normalised, transposed into sKT;
-    // lane (row r0 + c, part grp): 4-element pieces grp, grp + 4, grp + 8, ... of the row
-    for (int r0 = 16 * wave; r0 < NR; r0 += 16 * NW) {
-        const int row = r0 + c;
-        const int fw = row < N ? s_fw[row] : T;
-        float x[D / 4];
-        float ss = 0.f;
-        const float* src = fw < T ? a.kold + (tok0 + (size_t)fw * H) * D : a.kfin + ((size_t)bh * N + min(row, N - 1)) * D;
+    // the keys at t_end (kold of the row's first later write, else kfin), normalised, transposed into sKT.
+    // KLR lanes per row, lane l holding elements 4 l .. 4 l + 3: sq4 per lane, then lanesum<KLR>, the one order
+    // of every key norm in this kernel
+    {
+        constexpr int NP = NR / (NT / KLR);              // row passes; every pass's piece is loaded first
+        const int l = tid % KLR;
+        float4 xs[NP];
 #pragma unroll
-        for (int u = 0; u < D / 16; u++) {
-            const float4 v = row < N ? ld4(src + 4 * (grp + 4 * u)) : make_float4(0.f, 0.f, 0.f, 0.f);
-            x[4 * u] = v.x; x[4 * u + 1] = v.y; x[4 * u + 2] = v.z; x[4 * u + 3] = v.w;
-            ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+        for (int p = 0; p < NP; p++) {
+            const int row = (NT / KLR) * p + tid / KLR;
+            xs[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (row < N) {
+                const int fw = s_fw[row];
+                const float* src = fw < T ? a.kold + (tok0 + (size_t)fw * H) * D : a.kfin + ((size_t)bh * N + row) * D;
+                xs[p] = ld4(src + 4 * l);
+            }
         }
-        const float ki = rsq_clamped(sum4rows(ss));
 #pragma unroll
-        for (int u = 0; u < D / 16; u++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) sKT[(4 * (grp + 4 * u) + e) * P + row] = x[4 * u + e] * ki;
+        for (int p = 0; p < NP; p++) {
+            const int row = (NT / KLR) * p + tid / KLR;
+            const float ki = rsq_clamped(lanesum<KLR>(sq4(xs[p])));
+            sKT[(4 * l + 0) * P + row] = xs[p].x * ki;
+            sKT[(4 * l + 1) * P + row] = xs[p].y * ki;
+            sKT[(4 * l + 2) * P + row] = xs[p].z * ki;
+            sKT[(4 * l + 3) * P + row] = xs[p].w * ki;
+        }
     }
     for (int n = tid; n < NR; n += NT) {                // the occupancy at t_end, likewise
         const int fw = n < N ? s_fw[n] : T;
@@ -1793,163 +1837,211 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     }
     __syncthreads();
 
-    // ---- window prefetch into registers: every load is a per-window base plus a 32-bit element offset computed
-    // once (the step index of each is kept to mask the last window's missing steps)
-    float ncs[UCS], ndn[UCS];
-    uint4 nko[UKO], nq[UQ];
-    float nsc = 0.f;
-    u32 ocs[UCS], odn[UCS], oko[UKO], oq[UQ];
-    int ics[UCS], idn[UCS], iko[UKO], iq[UQ];
-#pragma unroll
-    for (int u2 = 0; u2 < UCS; u2++) {
-        const int u = tid + NT * u2;
-        const int i = u / NR, n = u % NR;                          // step-major: rows consecutive across lanes
-        ics[u2] = (u < WIN * NR && n < N) ? i : WIN;
-        ocs[u2] = (u32)(i * N + n);
-        const int n2 = u / WIN, i2 = u % WIN;                      // row-major: 16 steps of a row consecutive
-        idn[u2] = (u < WIN * NR && n2 < N) ? i2 : WIN;
-        odn[u2] = (u32)(n2 * T + i2);
-    }
-#pragma unroll
-    for (int u2 = 0; u2 < UKO; u2++) {
-        const int u = tid + NT * u2, i = u / (D / 4);
-        iko[u2] = u < WIN * D / 4 ? i : WIN;
-        oko[u2] = (u32)(i * H * D + 4 * (u % (D / 4)));
-    }
-#pragma unroll
-    for (int u2 = 0; u2 < UQ; u2++) {
-        const int u = tid + NT * u2, i = u / (D / EPU);
-        iq[u2] = u < WIN * D / EPU ? i : WIN;
-        oq[u2] = (u32)(i * H * D + EPU * (u % (D / EPU)));
-    }
-    auto load_win = [&](int m) {
+    // ---- window prefetch into registers, 16 bytes per lane wherever the layout allows (the address unit takes
+    // about as long per load instruction whatever its width): the cosines as the softmax phase's lanes hold them
+    // (step tid / NC; rows 4 (r + NC k) .. + 3 for k < Q4, then 4 NC Q4 + 2 r, + 1); Dn in 4-step pieces of a row
+    // (its 16 steps are 64 contiguous bytes), transposed through LDS; one float4 of a kold row and one 16-byte piece
+    // of a query row per lane; the step scalars in lanes 16 k + i (k: address, oold, gate, fr) of the waves that
+    // derive the occupancy masks and same-row links from them.  Rows whose pieces are not 16-byte aligned (N or T
+    // not a multiple of 4) or cross the end take scalar loads.  Each value is loaded under one condition into a
+    // register zeroed beforehand (address: -1), so the load is an exec-masked instruction whose result nothing
+    // waits for until the consumer.
+    const int s4 = tid / NC, r4 = tid % NC;
+    const bool n4 = (N & 3) == 0, n2 = (N & 1) == 0, t4 = (T & 3) == 0;
+    float ncs[RPC];
+    float4 ndn[UDN];
+    float4 nko;
+    uint4 nq = make_uint4(0u, 0u, 0u, 0u);
+    u32 nsc = 0u;
+    // A window's loads come in NPART parts, issued between the next window's MFMA groups (all at once, the
+    // loads of the eight waves queue in the address unit for longer than the matrix phase lasts).
+    constexpr int NPART = 5;
+    auto load_part = [&](int m, int part) {
         const int t0 = m * WIN, nt = min(WIN, T - t0);
-        const float* csb = a.cslog + ((size_t)bh * T + t0) * N;
-        const float* dnb = a.dn + (size_t)bh * N * T + t0;
-        const float* kob = a.kold + (tok0 + (size_t)t0 * H) * D;
-        const TI* qb = qp + (tok0 + (size_t)t0 * H) * D;
+        if (part == 3 || part == 4) {                   // the cosines: the groups of 4, then the pair
+            const float* csb = a.cslog + ((size_t)bh * T + t0) * N + (u32)(s4 * N);
+            const bool sok = s4 < nt;
+            if (part == 3) {
 #pragma unroll
-        for (int u2 = 0; u2 < UCS; u2++) {
-            ncs[u2] = ics[u2] < nt ? csb[ocs[u2]] : 0.f;
-            ndn[u2] = idn[u2] < nt ? dnb[odn[u2]] : 0.f;
+                for (int k = 0; k < Q4; k++) {
+                    const int n = 4 * (r4 + NC * k);
+                    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (sok && n4 && n + 3 < N) x = ld4(csb + n);
+                    else if (sok && !(n4 && n + 3 < N)) {
+                        if (n < N) x.x = csb[n];
+                        if (n + 1 < N) x.y = csb[n + 1];
+                        if (n + 2 < N) x.z = csb[n + 2];
+                        if (n + 3 < N) x.w = csb[n + 3];
+                    }
+                    ncs[4 * k] = x.x; ncs[4 * k + 1] = x.y; ncs[4 * k + 2] = x.z; ncs[4 * k + 3] = x.w;
+                }
+            } else if (R2) {
+                const int n = 4 * NC * Q4 + 2 * r4;
+                float2 x = make_float2(0.f, 0.f);
+                if (sok && n2 && n + 1 < N) x = *reinterpret_cast<const float2*>(csb + n);
+                else if (sok && !(n2 && n + 1 < N)) {
+                    if (n < N) x.x = csb[n];
+                    if (n + 1 < N) x.y = csb[n + 1];
+                }
+                ncs[4 * Q4] = x.x; ncs[4 * Q4 + 1] = x.y;
+            }
         }
+        if (part == 1 || part == 2) {                   // Dn: piece u = 4 n + q holds steps 4 q .. 4 q + 3 of row n
+            const float* dnb = a.dn + (size_t)bh * N * T + t0;
 #pragma unroll
-        for (int u2 = 0; u2 < UKO; u2++)
-            nko[u2] = iko[u2] < nt ? *reinterpret_cast<const uint4*>(kob + oko[u2]) : make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-        for (int u2 = 0; u2 < UQ; u2++)
-            nq[u2] = iq[u2] < nt ? *reinterpret_cast<const uint4*>(qb + oq[u2]) : make_uint4(0u, 0u, 0u, 0u);
-        if (tid < 4 * WIN) {
-            const int kind = tid / WIN, i = tid % WIN;
-            nsc = kind == 0 ? __int_as_float(-1) : 0.f;
+            for (int u2 = part == 1 ? 0 : (UDN + 1) / 2; u2 < (part == 1 ? (UDN + 1) / 2 : UDN); u2++) {
+                const int u = tid + NT * u2, n = u >> 2, i = 4 * (u & 3);
+                const bool live = u < 4 * NR && n < N;
+                const float* src = dnb + (size_t)n * T + i;
+                float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (live && t4 && i + 3 < nt) x = ld4(src);
+                else if (live && !(t4 && i + 3 < nt)) {
+                    if (i < nt) x.x = src[0];
+                    if (i + 1 < nt) x.y = src[1];
+                    if (i + 2 < nt) x.z = src[2];
+                    if (i + 3 < nt) x.w = src[3];
+                }
+                ndn[u2] = x;
+            }
+        }
+        if (part != 0) return;
+        {
+            const int i = tid / KLR;
+            nko = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < nt) nko = ld4(a.kold + (tok0 + (size_t)(t0 + i) * H) * D + 4 * (tid % KLR));
+        }
+        if (tid < WIN * QLR) {                          // whole waves
+            const int i = tid / QLR;
+            nq = make_uint4(0u, 0u, 0u, 0u);
+            if (i < nt) nq = *reinterpret_cast<const uint4*>(qp + (tok0 + (size_t)(t0 + i) * H) * D + EPU * (tid % QLR));
+        }
+        if (tid < 64 * (RPL + 1)) {                     // the mask and link waves; one load per 16-lane kind (a
+            const int kind = lane >> 4, i = lane & 15;  // per-lane choice of base pointer compiles to a load of it)
+            const size_t ix = tok0 + (size_t)(t0 + i) * H;
+            nsc = kind == 0 ? 0xffffffffu : 0u;
             if (i < nt) {
-                const size_t ix = tok0 + (size_t)(t0 + i) * H;
-                nsc = kind == 0 ? __int_as_float(a.am[ix]) : kind == 1 ? a.gate[ix]
-                    : kind == 2 ? (frt ? a.fr[ix] : 0.f) : a.oold[ix];
+                if (kind == 0) nsc = (u32)a.am[ix];
+                else if (kind == 1) nsc = __float_as_uint(a.oold[ix]);
+                else if (kind == 2) nsc = __float_as_uint(a.gate[ix]);
+                else if (frt) nsc = __float_as_uint(a.fr[ix]);
             }
         }
     };
 
     float dtemp_acc = 0.f, dfr_acc = 0.f;
-    load_win(m_hi - 1);
+#pragma unroll
+    for (int pp = 0; pp < NPART; pp++) load_part(m_hi - 1, pp);
     for (int m = m_hi - 1; m >= m_lo; m--) {
         const int t0 = m * WIN, nt = min(WIN, T - t0);
         // lane indices re-derived from an opaque copy every window: comparisons on them are then not loop
         // invariant, so the compiler does not hoist dozens of 64-bit lane masks into (spilled) scalar registers
-        const int tidw = tid;
-        const int lanew = tidw & 63, cw = lanew & 15, grpw = lanew >> 4;
-        // S1: publish
+        u32 tidw;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(tidw) : "v"(tid));
+        const int lanew = (int)(tidw & 63u), cw = lanew & 15, grpw = lanew >> 4;
+        // S1: publish the window, with everything about its writes that needs no other wave's data
 #pragma unroll
-        for (int u2 = 0; u2 < UCS; u2++) {
-            const int u = tidw + NT * u2;
-            if (u < WIN * NR) {
-                sCS[(u / NR) * SC + u % NR] = ncs[u2];
-                sDN[(u % WIN) * SC + u / WIN] = ndn[u2];
+        for (int u2 = 0; u2 < UDN; u2++) {
+            const u32 u = tidw + NT * u2;
+            if (u < 4 * NR) {                            // whole waves
+                const u32 n = u >> 2, i = 4 * (u & 3);
+                sDN[(i + 0) * SD + n] = ndn[u2].x;
+                sDN[(i + 1) * SD + n] = ndn[u2].y;
+                sDN[(i + 2) * SD + n] = ndn[u2].z;
+                sDN[(i + 3) * SD + n] = ndn[u2].w;
             }
         }
-#pragma unroll
-        for (int u2 = 0; u2 < UKO; u2++) {
-            const int u = tidw + NT * u2;
-            if (u < WIN * D / 4) *reinterpret_cast<uint4*>(&sKO[(u / (D / 4)) * KOS + 4 * (u % (D / 4))]) = nko[u2];
+        {                                                // kold rows and 1 / |kold_i|
+            const int i = (int)(tidw / KLR), l = (int)(tidw % KLR);
+            *reinterpret_cast<float4*>(&sKO[i * KOS + 4 * l]) = nko;
+            const float ki = rsq_clamped(lanesum<KLR>(sq4(nko)));
+            if (l == 0) s_kil[i] = ki;
         }
+        if (tidw < WIN * QLR) {                          // query rows and 1 / max(|q_t|, 1e-6), signed: negative
+            const int i = (int)(tidw / QLR), l = (int)(tidw % QLR);   // where |q_t|^2 < 1e-12 (no projection)
+            stage_store(&sQ[i * QS + EPU * l], nq, BF);
+            float qq;
+            if constexpr (BF) {
+                const u32 w4[4] = {nq.x, nq.y, nq.z, nq.w};
+                qq = 0.f;
 #pragma unroll
-        for (int u2 = 0; u2 < UQ; u2++) {
-            const int u = tidw + NT * u2;
-            if (u < WIN * D / EPU) stage_store(&sQ[(u / (D / EPU)) * KOS + EPU * (u % (D / EPU))], nq[u2], BF);
+                for (int k = 0; k < 4; k++) {
+                    const float lo = __uint_as_float(w4[k] << 16), hi = __uint_as_float(w4[k] & 0xffff0000u);
+                    qq = fmaf(lo, lo, qq);
+                    qq = fmaf(hi, hi, qq);
+                }
+            } else {
+                qq = sq4(make_float4(__uint_as_float(nq.x), __uint_as_float(nq.y), __uint_as_float(nq.z),
+                                     __uint_as_float(nq.w)));
+            }
+            qq = lanesum<QLR>(qq);
+            if (l == 0) s_qi[i] = qq < 1e-12f ? -rsq_clamped(qq) : rsq_clamped(qq);
         }
-        if (tidw < 4 * WIN) {
-            const int kind = tidw / WIN, i = tidw % WIN;
-            if (kind == 0) s_am[i] = __float_as_int(nsc);
-            else if (kind == 1) s_g[i] = nsc;
-            else if (kind == 2) s_fr[i] = nsc;
-            else s_oo[i] = nsc;
+        if (tidw < 64 * (RPL + 1)) {                     // waves 0 .. RPL (whole waves): each publishes its copy of
+            const int wv = (int)(tidw >> 6);             // the step scalars and reads it back as broadcasts (its own
+            s_scw[wv][lanew] = nsc;                      // writes, in order: a wave barrier suffices)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            int ai[WIN];
+            float oi[WIN];
+#pragma unroll
+            for (int k = 0; k < WIN / 4; k++) {
+                const int4 x = *reinterpret_cast<const int4*>(&s_scw[wv][4 * k]);
+                const float4 y = *reinterpret_cast<const float4*>(&s_scw[wv][WIN + 4 * k]);
+                ai[4 * k] = x.x; ai[4 * k + 1] = x.y; ai[4 * k + 2] = x.z; ai[4 * k + 3] = x.w;
+                oi[4 * k] = y.x; oi[4 * k + 1] = y.y; oi[4 * k + 2] = y.z; oi[4 * k + 3] = y.w;
+            }
+            if (wv < RPL) {                              // occupancy masks, row 64 wave + lane: over the window's 16
+                const int n = 64 * wv + lanew;           // steps backwards from the window-end occupancy, o becomes
+                float o = sO[n];                         // the pre-write occupancy at each write to the row
+                u32 mk = 0u;
+#pragma unroll
+                for (int i = WIN - 1; i >= 0; i--) {
+                    o = ai[i] == n ? oi[i] : o;
+                    mk |= (n < N && o >= eps ? 1u : 0u) << i;
+                }
+                s_tkm[n] = mk;
+            } else if (lanew < WIN) {                    // per write: the next write to the same row inside the
+                const int i = lanew, me = (int)nsc;      // window, and whether it is the row's first
+                int nx = -1;
+                bool first = true;
+#pragma unroll
+                for (int j = WIN - 1; j >= 0; j--) {
+                    if (j > i && ai[j] == me) nx = j;    // ends at the smallest such j
+                    if (j < i && ai[j] == me) first = false;
+                }
+                s_nx[i] = i < nt ? nx : -1;
+                s_first[i] = (i < nt && first) ? 1 : 0;
+            }
         }
         __syncthreads();                                                      // B1
-        // S2: |kold_i|^2 (lane = (write c, part grp), the order of the chunk start) and the same-row links
-        if (wave == 0) {
-            float ss = 0.f;
-#pragma unroll
-            for (int u = 0; u < D / 16; u++) {
-                const float4 x = ld4(&sKO[cw * KOS + 4 * (grpw + 4 * u)]);
-                ss = fmaf(x.x, x.x, ss); ss = fmaf(x.y, x.y, ss); ss = fmaf(x.z, x.z, ss); ss = fmaf(x.w, x.w, ss);
-            }
-            const float kn = sum4rows(ss);
-            if (grpw == 0) s_kil[cw] = rsq_clamped(kn);
-        } else if (wave == 1 && lanew < WIN) {
-            const int i = lanew, ai = s_am[i];
-            int nx = -1;
-            bool first = true;
-#pragma unroll
-            for (int j = WIN - 1; j >= 0; j--) {
-                const int aj = s_am[j];
-                if (j > i && aj == ai) nx = j;                // ends at the smallest such j
-                if (j < i && aj == ai) first = false;
-            }
-            s_nx[i] = i < nt ? nx : -1;
-            s_first[i] = (i < nt && first) ? 1 : 0;
-        } else if (wave == 2) {                            // 1 / max(|q_t|, 1e-6), 0 where |q_t|^2 < 1e-12
-            float qq = 0.f;
-#pragma unroll
-            for (int u = 0; u < D / 16; u++) {
-                const float4 x = ld4(&sQ[cw * KOS + 4 * (grpw + 4 * u)]);
-                qq = fmaf(x.x, x.x, qq); qq = fmaf(x.y, x.y, qq); qq = fmaf(x.z, x.z, qq); qq = fmaf(x.w, x.w, qq);
-            }
-            qq = sum4rows(qq);
-            if (grpw == 0) s_qi[cw] = qq < 1e-12f ? -rsq_clamped(qq) : rsq_clamped(qq);   // sign: no projection
-        }
-        if (NT - 1 - tidw < NR) {                          // occupancy masks, on the last NR lanes: row n over the
-            const int n = NT - 1 - tidw;                   // window's 16 steps
-            float o = sO[n];
-            u32 mk = 0u;
-#pragma unroll
-            for (int i = WIN - 1; i >= 0; i--) {           // backwards: o becomes the pre-write occupancy at i
-                o = s_am[i] == n ? s_oo[i] : o;
-                mk |= (n < N && o >= eps ? 1u : 0u) << i;
-            }
-            s_tkm[n] = mk;
-        }
-        __syncthreads();                                                      // B1b
-        // S4: the softmax adjoint of every step: step s = lanes [NC s, NC s + NC), rows n0 .. n0 + RPC - 1
+        // S4: the softmax adjoint of every step: step s = lanes [NC s, NC s + NC), rows as in the prefetch
         {
-            const int s = tidw / NC, r = tidw % NC, n0 = r * RPC;
+            const int s = (int)(tidw / NC), r = (int)(tidw % NC);
             const bool live = s < nt;
             const float g = s_g[s], frv = frt ? s_fr[s] : fr_s;
-            float cs[RPC], dw[RPC];
+            auto rowof = [&](int j) { return j < 4 * Q4 ? 4 * (r + NC * (j >> 2)) + (j & 3) : 4 * NC * Q4 + 2 * r + j - 4 * Q4; };
+            float dw[RPC];
+            u32 tkm[RPC];
 #pragma unroll
-            for (int j = 0; j < RPC; j += 2) {
-                const float2 x = *reinterpret_cast<const float2*>(&sCS[s * SC + n0 + j]);
-                const float2 y = *reinterpret_cast<const float2*>(&sDN[s * SC + n0 + j]);
-                cs[j] = x.x; cs[j + 1] = x.y; dw[j] = y.x; dw[j + 1] = y.y;
+            for (int k = 0; k < Q4; k++) {
+                const float4 x = ld4(&sDN[s * SD + rowof(4 * k)]);
+                const uint4 y = *reinterpret_cast<const uint4*>(&s_tkm[rowof(4 * k)]);
+                dw[4 * k] = x.x; dw[4 * k + 1] = x.y; dw[4 * k + 2] = x.z; dw[4 * k + 3] = x.w;
+                tkm[4 * k] = y.x; tkm[4 * k + 1] = y.y; tkm[4 * k + 2] = y.z; tkm[4 * k + 3] = y.w;
             }
-            u32 tk = 0u, rows = 0u;                            // occupied at step s; below N
+            if constexpr (R2 > 0) {
+                const float2 x = *reinterpret_cast<const float2*>(&sDN[s * SD + rowof(4 * Q4)]);
+                const uint2 y = *reinterpret_cast<const uint2*>(&s_tkm[rowof(4 * Q4)]);
+                dw[4 * Q4] = x.x; dw[4 * Q4 + 1] = x.y; tkm[4 * Q4] = y.x; tkm[4 * Q4 + 1] = y.y;
+            }
+            u32 tk = 0u, rows = 0u;                      // occupied at step s; below N
 #pragma unroll
-            for (int j = 0; j < RPC; j += 2) {
-                const uint2 m2 = *reinterpret_cast<const uint2*>(&s_tkm[n0 + j]);
-                tk |= ((m2.x >> s) & 1u) << j;
-                tk |= ((m2.y >> s) & 1u) << (j + 1);
-                rows |= (n0 + j < N ? 1u : 0u) << j;
-                rows |= (n0 + j + 1 < N ? 1u : 0u) << (j + 1);
+            for (int j = 0; j < RPC; j++) {
+                tk |= ((tkm[j] >> s) & 1u) << j;
+                rows |= (rowof(j) < N ? 1u : 0u) << j;
             }
+            const float* cs = ncs;
             // the lowest free row of the step with its z and Dn, and the largest z over the occupied rows
             const u32 fm = rows & ~tk;
             const int jf = fm ? (int)__builtin_ctz(fm) : 0;
@@ -1960,7 +2052,9 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
                 FD = j == jf ? dw[j] : FD;
                 if ((tk >> j) & 1u) mz = fmaxf(mz, fmaf(temp, cs[j], -frv));
             }
-            int ff = fm ? n0 + jf : INT_MAX;
+            int ff = INT_MAX;                            // rows increase with j: the first free j is the lowest
+#pragma unroll
+            for (int j = RPC - 1; j >= 0; j--) ff = j == jf && fm ? rowof(j) : ff;
             step_argmin<NC>(ff, zf, FD);
             mz = step_max<NC>(mz);
             const bool hasf = ff < N;
@@ -1978,103 +2072,151 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             const float ef = hasf ? __expf(zf - M) : 0.f;
             const float SS = SSt + ef, SSD = fmaf(ef, FD, SSDt);
             const float rss = live ? __builtin_amdgcn_rcpf(SS) : 0.f, sa = (g * SSD) * rss;
-            float dt = 0.f;
+            float dt = 0.f, wv[RPC];
 #pragma unroll
-            for (int j = 0; j < RPC; j += 2) {
-                float wv[2];
-#pragma unroll
-                for (int jj = 0; jj < 2; jj++) {
-                    const int n = n0 + j + jj;
-                    const float as = ((tk >> (j + jj)) & 1u) ? ev[j + jj] * rss : (n == ff ? ef * rss : 0.f);
-                    const float dz = as * (g * dw[j + jj] - sa);
-                    dt = fmaf(dz, cs[j + jj], dt);
-                    wv[jj] = temp * dz;
-                }
-                *reinterpret_cast<float2*>(&sW[s * SW + n0 + j]) = make_float2(wv[0], wv[1]);
+            for (int j = 0; j < RPC; j++) {
+                const float as = ((tk >> j) & 1u) ? ev[j] * rss : (rowof(j) == ff ? ef * rss : 0.f);
+                const float dz = as * (g * dw[j] - sa);
+                dt = fmaf(dz, cs[j], dt);
+                wv[j] = temp * dz;
             }
+#pragma unroll
+            for (int k = 0; k < Q4; k++)
+                *reinterpret_cast<float4*>(&sW[s * SW + rowof(4 * k)]) = make_float4(wv[4 * k], wv[4 * k + 1], wv[4 * k + 2], wv[4 * k + 3]);
+            if constexpr (R2 > 0) *reinterpret_cast<float2*>(&sW[s * SW + rowof(4 * Q4)]) = make_float2(wv[4 * Q4], wv[4 * Q4 + 1]);
             dtemp_acc += dt;
             const float pstep = temp * step_sum<NC>(dt);        // <qhat_s, dqn_s> = temp sum_n dz_n cs_n
-            if (r == 0) s_pr[s] = pstep;
-            if (r == 0 && live) {
-                const size_t ix = tok0 + (size_t)(t0 + s) * H;
+            if (r == 0) {
                 const float dfl = -(g * SSDt - sa * SSt) * rss;
-                a.dg[ix] = sDN[s * SC + s_am[s]];              // dgate of the written row: its Dn entry
-                if (frt) a.dfr[ix] = dfl;
-                else dfr_acc += dfl;
+                s_pr[s] = pstep;
+                s_dgf[0][s] = sDN[s * SD + max(s_am[s], 0)];   // dgate of the written row: its Dn entry
+                s_dgf[1][s] = dfl;
+                if (live && !frt) dfr_acc += dfl;
             }
         }
         __syncthreads();                                                      // B2
         if (tidw < WIN && s_first[tidw]) sO[s_am[tidw]] = s_oo[tidw];            // occupancy at the window start
-        // S5: prefetch the next (earlier) window while the matrix cores run
-        if (m > m_lo) load_win(m - 1);
-        float av8[4];                                      // S8's A operand: W[c][a_s] for s = 4 kc + grp >= c
-#pragma unroll
-        for (int kc = 0; kc < 4; kc++) {
-            const int s = 4 * kc + grp;
-            av8[kc] = (s < nt && s >= c) ? sW[c * SW + s_am[s]] : 0.f;
+        if (tidw < 2 * WIN) {                            // the steps' dgate (and per-token dfr): one store each
+            const int i = lanew & 15, k = lanew >> 4;
+            const size_t ix = tok0 + (size_t)(t0 + i) * H;
+            const float v = s_dgf[k][i];
+            if (i < nt && k == 0) a.dg[ix] = v;
+            if (i < nt && k == 1 && frt) a.dfr[ix] = v;
         }
-        // S6: dqn = W Kh over every row for this wave's dims, two accumulation chains
+        // S8's B operand, W[c][a_s] for s = 4 kc + grp >= c, and S9's operands (the query of step c at this lane's
+        // four dims), read before B3: past it the next window's publish may overwrite them
+        float av8[4], qsv, prv;
+        float4 qv;
+        {
+            int as8[4];
+#pragma unroll
+            for (int kc = 0; kc < 4; kc++) as8[kc] = s_am[4 * kc + grpw];
+            qv = ld4(&sQ[cw * QS + d0 + 4 * grpw]);
+            qsv = s_qi[cw];
+            prv = s_pr[cw];
+            keep(as8[0], as8[1], as8[2], as8[3]);
+#pragma unroll
+            for (int kc = 0; kc < 4; kc++) av8[kc] = sW[cw * SW + min(max(as8[kc], 0), NR - 1)];
+            keep(av8[0], av8[1], av8[2], av8[3]);
+#pragma unroll
+            for (int kc = 0; kc < 4; kc++) {
+                const int s = 4 * kc + grpw;
+                av8[kc] = (s < nt && s >= cw) ? av8[kc] : 0.f;
+            }
+        }
+        // S6: dqn^T = Kh^T W^T over every row for this wave's dims (keys as the A operand, so lane (c, g) ends with
+        // dims 4 g .. 4 g + 3 of step c), two accumulation chains, each group's LDS reads issued one group ahead.
+        // S5, the prefetch of the next (earlier) window, is issued part by part between the MFMA groups
         f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+        const bool pf = m > m_lo;
+        const float* wrow = &sW[cw * SW + KK * grpw];
+        const float* krow = &sKT[(d0 + cw) * P + KK * grpw];
+        float4 av = ld4(wrow), bv = ld4(krow), av2 = ld4(wrow + 4), bv2 = ld4(krow + 4);
 #pragma unroll
         for (int k4 = 0; k4 < KK / 4; k4 += 2) {
-            const float4 av = ld4(&sW[cw * SW + KK * grpw + 4 * k4]);
-            const float4 bv = ld4(&sKT[(d0 + cw) * P + KK * grpw + 4 * k4]);
-            const float4 av2 = ld4(&sW[cw * SW + KK * grpw + 4 * k4 + 4]);
-            const float4 bv2 = ld4(&sKT[(d0 + cw) * P + KK * grpw + 4 * k4 + 4]);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av2.x, bv2.x, acc2, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av2.y, bv2.y, acc2, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av2.z, bv2.z, acc2, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av2.w, bv2.w, acc2, 0, 0, 0);
+            float4 na = av, nb = bv, na2 = av2, nb2 = bv2;
+            if (k4 + 2 < KK / 4) {
+                na = ld4(wrow + 4 * k4 + 8);
+                nb = ld4(krow + 4 * k4 + 8);
+                na2 = ld4(wrow + 4 * k4 + 12);
+                nb2 = ld4(krow + 4 * k4 + 12);
+            }
+            if (pf && k4 / 2 < NPART) load_part(m - 1, k4 / 2);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bv.x, av.x, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv2.x, av2.x, acc2, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bv.y, av.y, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv2.y, av2.y, acc2, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bv.z, av.z, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv2.z, av2.z, acc2, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bv.w, av.w, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv2.w, av2.w, acc2, 0, 0, 0);
+            av = na; bv = nb; av2 = na2; bv2 = nb2;
         }
+#pragma unroll
+        for (int pp = KK / 8; pp < NPART; pp++)
+            if (pf) load_part(m - 1, pp);
         // S7: the undo of every write at once: write i = lanes [NC i, NC i + NC), dims ud + NC e.  Dims strided
         // across lanes, so the column accesses of the transposed keys (stride P per dim) spread over the banks
-        const int ui = tidw / NC, ud = tidw % NC;
+        // (both candidates for the key after each write are read, unconditionally, and selected)
+        const int ui = (int)(tidw / NC), ud = (int)(tidw % NC);
         const bool uev = ui < nt;
-        const int uai = min(max(s_am[ui], 0), NR - 1);
+        int uam = s_am[ui], unx = s_nx[ui], ufi = s_first[ui];
+        float ki = s_kil[ui];
+        keep(uam, unx, ufi, ki);
+        const int uai = min(max(uam, 0), NR - 1), nxc = max(unx, 0);
+        const bool ufirst = uev && ufi != 0;
         float ux[DPT];
         {
-            const float ki = s_kil[ui];
-            const int nx = s_nx[ui];
-            const float kn = nx >= 0 ? s_kil[nx] : 0.f;
+            float kn = s_kil[nxc], ko[DPT], kx[DPT], kt[DPT];
 #pragma unroll
             for (int e = 0; e < DPT; e++) {
                 const int d = ud + NC * e;
-                ux[e] = sKO[ui * KOS + d] * ki;
-                const float af = nx >= 0 ? sKO[nx * KOS + d] * kn : sKT[d * P + uai];
-                sDel[ui * DEL + d] = uev ? ux[e] - af : 0.f;
+                ko[e] = sKO[ui * KOS + d];
+                kx[e] = sKO[nxc * KOS + d];
+                kt[e] = sKT[d * P + uai];
+            }
+            keep(kn, ko[0], ko[1], ko[2], ko[3], kx[0], kx[1], kx[2], kx[3], kt[0], kt[1], kt[2], kt[3]);
+#pragma unroll
+            for (int e = 0; e < DPT; e++) {
+                ux[e] = ko[e] * ki;
+                const float af = unx >= 0 ? kx[e] * kn : kt[e];
+                sDel[ui * DEL + ud + NC * e] = uev ? ux[e] - af : 0.f;
             }
         }
         __syncthreads();                                                      // B3: every read of the window-end keys done
-        if (uev && s_first[ui]) {
+        if (ufirst) {
 #pragma unroll
             for (int e = 0; e < DPT; e++) sKT[(ud + NC * e) * P + uai] = ux[e];
         }
-        // S8: the rewritten rows' correction, sum_{s >= t} W[t][a_s] delta_s
+        // S8: the rewritten rows' correction, sum_{s >= t} W[t][a_s] delta_s (rows of steps past the chain end
+        // are zero deltas)
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[r] += acc2[r];
+        float bv8[4];
 #pragma unroll
-        for (int kc = 0; kc < 4; kc++) {
-            const int s = 4 * kc + grpw;
-            const float bv = s < nt ? sDel[s * DEL + d0 + cw] : 0.f;
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av8[kc], bv, acc, 0, 0, 0);
-        }
+        for (int kc = 0; kc < 4; kc++) bv8[kc] = sDel[(4 * kc + grpw) * DEL + d0 + cw];
+        keep(bv8[0], bv8[1], bv8[2], bv8[3]);
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bv8[kc], av8[kc], acc, 0, 0, 0);
         // S9: dq = qinv (dqn - qhat <qhat, dqn>), or qinv dqn where |q| < 1e-6.  <qhat, dqn> = sum_n W_n <qhat, Kh_n>
-        // and <qhat_t, Kh_n(t)> is the cosine the forward logged, so the projection needs no sum over the dims
+        // and <qhat_t, Kh_n(t)> is the cosine the forward logged, so the projection needs no sum over the dims.
+        // Lane (c, g) stores dims 4 g .. 4 g + 3 of step c in one 8-byte (bf16) or 16-byte store
+        if (cw < nt) {
+            const float qi = fabsf(qsv), qd[4] = {qv.x, qv.y, qv.z, qv.w};
+            float rr[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int st = 4 * grpw + r;
-            if (st < nt) {
-                const float qs = s_qi[st], qi = fabsf(qs), pr = s_pr[st];
-                const float dqn = acc[r];
-                const float rr = qs < 0.f ? qi * dqn : qi * (dqn - (sQ[st * KOS + d0 + cw] * qi) * pr);
-                st1<TI>((TI*)a.dq + (tok0 + (size_t)(t0 + st) * H) * D + d0 + cw, rr);
+            for (int r = 0; r < 4; r++) rr[r] = qsv < 0.f ? qi * acc[r] : qi * (acc[r] - (qd[r] * qi) * prv);
+            const size_t off = (tok0 + (size_t)(t0 + cw) * H) * D + d0 + 4 * grpw;
+            if constexpr (BF) {
+                const uint2 pk = make_uint2((u32)f2bf(rr[0]) | ((u32)f2bf(rr[1]) << 16),
+                                            (u32)f2bf(rr[2]) | ((u32)f2bf(rr[3]) << 16));
+                *reinterpret_cast<uint2*>((bf16_t*)a.dq + off) = pk;
+            } else {
+                *reinterpret_cast<float4*>((float*)a.dq + off) = make_float4(rr[0], rr[1], rr[2], rr[3]);
             }
         }
-        __syncthreads();                                                      // B5: the window's LDS is free
+        // no barrier here: what the next window's S1 and S4 overwrite was read before B3, and S7's next deltas
+        // are written only after the next B2
     }
     dtemp_acc = wavesum(dtemp_acc);
     dfr_acc = wavesum(dfr_acc);
