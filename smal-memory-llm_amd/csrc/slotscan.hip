@@ -1744,22 +1744,25 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     constexpr int NT = 64 * NW;
     constexpr int NR = 64 * RPL;                        // slot-row capacity
     constexpr int KK = NR / 4;                          // MFMA k-steps over the rows
-    constexpr int P = NR + 4;                           // transposed key stride: 4 mod 64 banks
-    constexpr int SW = NR + 4;                          // W row stride, likewise
-    constexpr int SD = NR + 4;                          // Dn row stride (step-major), likewise: the transposing
-                                                        // publish (16 steps x 4 rows per store) hits 64 banks
+    // LDS: 32 banks of 4 bytes; 4-byte accesses are served 32 lanes per pass, 16-byte accesses 8 lanes per pass
+    constexpr int P = NR + 4;                           // transposed key stride, 4 mod 32: the 8 lanes of a 16-byte
+    constexpr int SW = NR + 4;                          // pass (8 dims / steps) read 8 disjoint 4-bank groups; W
+    constexpr int SD = NR + 4;                          // and Dn likewise (Dn's columns swizzled, dnc below)
     constexpr int NC = NT / WIN;                        // lanes per step in the softmax phase
-    constexpr int RPC = NR / NC;                        // slot rows per lane there: r, r + NC, r + 2 NC, ...
-    constexpr int KOS = D + NC;                         // kold row stride, NC mod 64 banks: the undo's writes of one
-                                                        // wave (2 or 4, NC dims each) read disjoint banks
+    constexpr int RPC = NR / NC;                        // slot rows per lane there (groups of 4, then a pair)
+    constexpr int KOS = D + 8;                          // kold and undo-delta row strides, 8 mod 32: a 4-byte pass of
+    constexpr int DEL = D + 8;                          // the undo (4 writes x 8 dims) hits 32 distinct banks
     constexpr int QS = D + 4;                           // query row stride: S9's four steps per wave on distinct banks
-    constexpr int DPT = D / NC;                         // dims per lane in the undo (4), strided by NC
-    constexpr int DEL = D + 16;                         // undo-delta row stride
+    constexpr int DPT = D / NC;                         // dims per lane in the undo (4)
     constexpr int EPU = 16 / (int)sizeof(TI);           // query elements per 16-byte piece
     constexpr int KLR = D / 4;                          // lanes per kold row in the prefetch (one float4 each)
     constexpr int QLR = D / EPU;                        // lanes per query row in the prefetch (one 16-byte piece)
     constexpr int UDN = (4 * NR + NT - 1) / NT;         // Dn float4 pieces per lane in the prefetch (4 per row)
     constexpr int Q4 = RPC / 4, R2 = (RPC % 4) / 2;     // softmax lane rows: Q4 groups of 4, then R2 pairs
+    // Dn column swizzle: row n of step s sits at column n ^ 8 [s & 8].  The transposing publish stores rows n .. n + 7
+    // at steps i, i + 4, i + 8, i + 12 in one pass: without it steps i and i + 8 share banks (2-way); the XOR
+    // moves whole 4-row groups, so the softmax phase's 16-byte reads of 4 rows stay contiguous
+    auto dnc = [](int s, int n) { return n ^ (s & 8); };
     constexpr bool BF = sizeof(TI) == 2;
     static_assert(DPT == 4 && (KK / 4) % 2 == 0 && WIN * KLR == NT && WIN * QLR <= NT && (WIN * QLR) % 64 == 0 &&
                   RPC == 4 * Q4 + 2 * R2 && (4 * NR) % 64 == 0 && RPL + 1 <= NW, "layout assumptions");
@@ -1944,10 +1947,10 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             const u32 u = tidw + NT * u2;
             if (u < 4 * NR) {                            // whole waves
                 const u32 n = u >> 2, i = 4 * (u & 3);
-                sDN[(i + 0) * SD + n] = ndn[u2].x;
-                sDN[(i + 1) * SD + n] = ndn[u2].y;
-                sDN[(i + 2) * SD + n] = ndn[u2].z;
-                sDN[(i + 3) * SD + n] = ndn[u2].w;
+                sDN[(i + 0) * SD + dnc(i + 0, n)] = ndn[u2].x;
+                sDN[(i + 1) * SD + dnc(i + 1, n)] = ndn[u2].y;
+                sDN[(i + 2) * SD + dnc(i + 2, n)] = ndn[u2].z;
+                sDN[(i + 3) * SD + dnc(i + 3, n)] = ndn[u2].w;
             }
         }
         {                                                // kold rows and 1 / |kold_i|
@@ -2025,13 +2028,13 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             u32 tkm[RPC];
 #pragma unroll
             for (int k = 0; k < Q4; k++) {
-                const float4 x = ld4(&sDN[s * SD + rowof(4 * k)]);
+                const float4 x = ld4(&sDN[s * SD + dnc(s, rowof(4 * k))]);
                 const uint4 y = *reinterpret_cast<const uint4*>(&s_tkm[rowof(4 * k)]);
                 dw[4 * k] = x.x; dw[4 * k + 1] = x.y; dw[4 * k + 2] = x.z; dw[4 * k + 3] = x.w;
                 tkm[4 * k] = y.x; tkm[4 * k + 1] = y.y; tkm[4 * k + 2] = y.z; tkm[4 * k + 3] = y.w;
             }
             if constexpr (R2 > 0) {
-                const float2 x = *reinterpret_cast<const float2*>(&sDN[s * SD + rowof(4 * Q4)]);
+                const float2 x = *reinterpret_cast<const float2*>(&sDN[s * SD + dnc(s, rowof(4 * Q4))]);
                 const uint2 y = *reinterpret_cast<const uint2*>(&s_tkm[rowof(4 * Q4)]);
                 dw[4 * Q4] = x.x; dw[4 * Q4 + 1] = x.y; tkm[4 * Q4] = y.x; tkm[4 * Q4 + 1] = y.y;
             }
@@ -2089,7 +2092,7 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             if (r == 0) {
                 const float dfl = -(g * SSDt - sa * SSt) * rss;
                 s_pr[s] = pstep;
-                s_dgf[0][s] = sDN[s * SD + max(s_am[s], 0)];   // dgate of the written row: its Dn entry
+                s_dgf[0][s] = sDN[s * SD + dnc(s, max(s_am[s], 0))];   // dgate of the written row: its Dn entry
                 s_dgf[1][s] = dfl;
                 if (live && !frt) dfr_acc += dfl;
             }
@@ -2155,10 +2158,12 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
 #pragma unroll
         for (int pp = KK / 8; pp < NPART; pp++)
             if (pf) load_part(m - 1, pp);
-        // S7: the undo of every write at once: write i = lanes [NC i, NC i + NC), dims ud + NC e.  Dims strided
-        // across lanes, so the column accesses of the transposed keys (stride P per dim) spread over the banks
+        // S7: the undo of every write at once: lane 128 w4 + 8 ui + g takes write ui, dims g + 8 (w4 + (D / 32) e).
+        // A 4-byte pass is 4 writes x 8 dims: the column accesses of the transposed keys (stride P per dim) land on
+        // 8 bank groups per write, offset by the writes' (different) rows; the kold and delta rows on 32 banks
         // (both candidates for the key after each write are read, unconditionally, and selected)
-        const int ui = (int)(tidw / NC), ud = (int)(tidw % NC);
+        const int ui = (int)((tidw >> 3) & 15), ud = (int)(tidw & 7) + 8 * (int)(tidw >> 7);
+        auto udim = [&](int e) { return ud + 8 * (D / 32) * e; };
         const bool uev = ui < nt;
         int uam = s_am[ui], unx = s_nx[ui], ufi = s_first[ui];
         float ki = s_kil[ui];
@@ -2170,7 +2175,7 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             float kn = s_kil[nxc], ko[DPT], kx[DPT], kt[DPT];
 #pragma unroll
             for (int e = 0; e < DPT; e++) {
-                const int d = ud + NC * e;
+                const int d = udim(e);
                 ko[e] = sKO[ui * KOS + d];
                 kx[e] = sKO[nxc * KOS + d];
                 kt[e] = sKT[d * P + uai];
@@ -2180,13 +2185,13 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             for (int e = 0; e < DPT; e++) {
                 ux[e] = ko[e] * ki;
                 const float af = unx >= 0 ? kx[e] * kn : kt[e];
-                sDel[ui * DEL + ud + NC * e] = uev ? ux[e] - af : 0.f;
+                sDel[ui * DEL + udim(e)] = uev ? ux[e] - af : 0.f;
             }
         }
         __syncthreads();                                                      // B3: every read of the window-end keys done
         if (ufirst) {
 #pragma unroll
-            for (int e = 0; e < DPT; e++) sKT[(ud + NC * e) * P + uai] = ux[e];
+            for (int e = 0; e < DPT; e++) sKT[udim(e) * P + uai] = ux[e];
         }
         // S8: the rewritten rows' correction, sum_{s >= t} W[t][a_s] delta_s (rows of steps past the chain end
         // are zero deltas)
