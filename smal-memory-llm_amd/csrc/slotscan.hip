@@ -1640,10 +1640,11 @@ CHAIN_ATTR void chain_bwd(ChainBwdArgs a) {
 //       (the occupied ones and the lowest free one, a step-group max); SS and sum e dw are step-group sums;
 //       W[s][n] = temp dz_n goes to LDS; dgate = Dn of the written row; dfr in closed form over the occupied
 //       rows; dtemp accumulates sum dz cs;
-//   S6  dqn = W Kh as fp32 MFMA (v_mfma_f32_16x16x4f32), wave w owning dims [16 w, 16 w + 16).  The normalised
-//       keys stay in LDS TRANSPOSED (dim-major, row stride P = NR + 4): k-step kk contracts rows KK g + kk for
-//       lane group g, so four consecutive k-steps of a lane's B operand are one 16-byte read, and so are its
-//       A operand's from W (the reference's order: normalise, then contract, slotkern_kvt.py:86-90);
+//   S6  dqn = W Kh on bf16 MFMA (v_mfma_f32_16x16x32_bf16) over operands split into two bf16 terms (hi*hi +
+//       hi*lo + lo*hi, within about 2^-16 of the fp32 products), wave w owning dims [16 w, 16 w + 16).  The
+//       normalised keys stay in LDS TRANSPOSED (dim-major hi and lo planes, row stride P = NR + 8): a lane's
+//       8 consecutive rows of a k-block are one 16-byte read per plane, and so are its W operand's (the
+//       reference's order: normalise, then contract, slotkern_kvt.py:86-90);
 //   S7  the undo, every write at once: x_i = Kh(kold_i); the key after write i is Kh(kold_j) of the next write
 //       j to the same row in the window, else the window-end key; delta_i = x_i - after_i.  Then each row the
 //       window wrote takes x of its FIRST write: the keys at the window start;
@@ -1738,16 +1739,36 @@ template <typename T, typename... Ts> __device__ __forceinline__ void keep(T& v,
 // The squares of a 4-element key piece, summed in one fixed order (the first term of every key norm).
 __device__ __forceinline__ float sq4(float4 x) { return fmaf(x.w, x.w, fmaf(x.z, x.z, fmaf(x.y, x.y, x.x * x.x))); }
 
+// Two-term bfloat16 split of fp32 operands: x = hi + lo + r with hi = bf16(x), lo = bf16(x - hi) (x - hi is exact
+// in fp32), |r| <= 2^-18 |x|.  hi*hi + hi*lo + lo*hi on bf16 MFMAs then carries a product to within about
+// 3 * 2^-18 of its fp32 value (the dropped lo*lo is below 2^-18), at 3 bf16 MFMAs of 16 cycles per 32-deep
+// k-block where fp32 MFMAs take 8 of 32 cycles.  Pairs are packed element 0 in bits 0-15.  The inputs pass an
+// empty asm first: x is then the rounded fp32 value on every path (a product feeding x - hi would otherwise be
+// contracted into an fma on some paths and not on others, and the same key would split differently).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ void split_bf2(float x0, float x1, u32& hi, u32& lo) {
+    asm volatile("" : "+v"(x0), "+v"(x1));
+    hi = pack_bf16x2(x0, x1);
+    lo = pack_bf16x2(x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u));
+}
+__device__ __forceinline__ float join_bf(bf16_t hi, bf16_t lo) { return bf2f(hi) + bf2f(lo); }
+__device__ __forceinline__ f32x4 mfma_bf32(const uint4& a, const uint4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+}
+
 template <int D, int RPL, typename TI>
 __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     constexpr int NW = D / 16;                          // waves: wave w owns dims [16 w, 16 w + 16) in S6, S8, S9
     constexpr int NT = 64 * NW;
     constexpr int NR = 64 * RPL;                        // slot-row capacity
-    constexpr int KK = NR / 4;                          // MFMA k-steps over the rows
-    // LDS: 32 banks of 4 bytes; 4-byte accesses are served 32 lanes per pass, 16-byte accesses 8 lanes per pass
-    constexpr int P = NR + 4;                           // transposed key stride, 4 mod 32: the 8 lanes of a 16-byte
-    constexpr int SW = NR + 4;                          // pass (8 dims / steps) read 8 disjoint 4-bank groups; W
-    constexpr int SD = NR + 4;                          // and Dn likewise (Dn's columns swizzled, dnc below)
+    constexpr int KG = NR / 4;                          // S6: rows per MFMA lane group (k = 8 g .. 8 g + 7 of a block)
+    constexpr int KB = NR / 32;                         // S6: 32-deep bf16 k-blocks over the rows
+    // LDS: 4-byte accesses are served 32 lanes per pass over 32 banks, 16-byte accesses 16 lanes per pass over 64
+    constexpr int P = NR + 8;                           // transposed key planes' stride (bf16), 400 B = 144 mod 256 at
+    constexpr int SW = NR + 8;                          // NR 192: S6's 16 dims / steps per 16-byte pass on 16 distinct
+                                                        // 16-byte bank groups; W's planes likewise
+    constexpr int SD = NR + 4;                          // Dn stride (fp32; its columns swizzled, dnc below)
     constexpr int NC = NT / WIN;                        // lanes per step in the softmax phase
     constexpr int RPC = NR / NC;                        // slot rows per lane there (groups of 4, then a pair)
     constexpr int KOS = D + 8;                          // kold and undo-delta row strides, 8 mod 32: a 4-byte pass of
@@ -1764,10 +1785,10 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     // moves whole 4-row groups, so the softmax phase's 16-byte reads of 4 rows stay contiguous
     auto dnc = [](int s, int n) { return n ^ (s & 8); };
     constexpr bool BF = sizeof(TI) == 2;
-    static_assert(DPT == 4 && (KK / 4) % 2 == 0 && WIN * KLR == NT && WIN * QLR <= NT && (WIN * QLR) % 64 == 0 &&
+    static_assert(DPT == 4 && NR % 32 == 0 && WIN * KLR == NT && WIN * QLR <= NT && (WIN * QLR) % 64 == 0 &&
                   RPC == 4 * Q4 + 2 * R2 && (4 * NR) % 64 == 0 && RPL + 1 <= NW, "layout assumptions");
-    __shared__ __align__(16) float sKT[D * P];          // normalised keys, transposed
-    __shared__ __align__(16) float sW[WIN * SW];        // W = temp dz [step][row]
+    __shared__ __align__(16) bf16_t sKT[2][D * P];      // normalised keys, transposed, split: [0] hi, [1] lo
+    __shared__ __align__(16) bf16_t sW[2][WIN * SW];    // W = temp dz [step][row], split likewise
     __shared__ __align__(16) float sDN[WIN * SD];       // Dn [step][row]
     __shared__ __align__(16) float sDel[WIN * DEL];     // undo deltas [write][dim]
     __shared__ __align__(16) float sKO[WIN * KOS];      // kold rows of the window's writes
@@ -1802,7 +1823,12 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     const int nwin = (T + WIN - 1) / WIN;
     const int m_lo = blockIdx.y * a.wpc, m_hi = min(nwin, m_lo + a.wpc);
     const int t_end = min(m_hi * WIN, T);
-    int* s_fw = reinterpret_cast<int*>(sW);
+    // element (dim d, row n) of the split transposed keys, from the low 16 bits of each half
+    auto st_kt = [&](int d, int n, u32 hi, u32 lo) {
+        sKT[0][d * P + n] = (bf16_t)hi;
+        sKT[1][d * P + n] = (bf16_t)lo;
+    };
+    int* s_fw = reinterpret_cast<int*>(&sW[0][0]);
     for (int n = tid; n < NR; n += NT) s_fw[n] = T;
     __syncthreads();
     for (int t = t_end + tid; t < T; t += NT) atomicMin(&s_fw[min(max(a.am[tok0 + (size_t)t * H], 0), NR - 1)], t);
@@ -1828,10 +1854,13 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
         for (int p = 0; p < NP; p++) {
             const int row = (NT / KLR) * p + tid / KLR;
             const float ki = rsq_clamped(lanesum<KLR>(sq4(xs[p])));
-            sKT[(4 * l + 0) * P + row] = xs[p].x * ki;
-            sKT[(4 * l + 1) * P + row] = xs[p].y * ki;
-            sKT[(4 * l + 2) * P + row] = xs[p].z * ki;
-            sKT[(4 * l + 3) * P + row] = xs[p].w * ki;
+            u32 h01, l01, h23, l23;
+            split_bf2(xs[p].x * ki, xs[p].y * ki, h01, l01);
+            split_bf2(xs[p].z * ki, xs[p].w * ki, h23, l23);
+            st_kt(4 * l + 0, row, h01, l01);
+            st_kt(4 * l + 1, row, h01 >> 16, l01 >> 16);
+            st_kt(4 * l + 2, row, h23, l23);
+            st_kt(4 * l + 3, row, h23 >> 16, l23 >> 16);
         }
     }
     for (int n = tid; n < NR; n += NT) {                // the occupancy at t_end, likewise
@@ -2084,9 +2113,19 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
                 wv[j] = temp * dz;
             }
 #pragma unroll
-            for (int k = 0; k < Q4; k++)
-                *reinterpret_cast<float4*>(&sW[s * SW + rowof(4 * k)]) = make_float4(wv[4 * k], wv[4 * k + 1], wv[4 * k + 2], wv[4 * k + 3]);
-            if constexpr (R2 > 0) *reinterpret_cast<float2*>(&sW[s * SW + rowof(4 * Q4)]) = make_float2(wv[4 * Q4], wv[4 * Q4 + 1]);
+            for (int k = 0; k < Q4; k++) {
+                uint2 hi, lo;
+                split_bf2(wv[4 * k], wv[4 * k + 1], hi.x, lo.x);
+                split_bf2(wv[4 * k + 2], wv[4 * k + 3], hi.y, lo.y);
+                *reinterpret_cast<uint2*>(&sW[0][s * SW + rowof(4 * k)]) = hi;
+                *reinterpret_cast<uint2*>(&sW[1][s * SW + rowof(4 * k)]) = lo;
+            }
+            if constexpr (R2 > 0) {
+                u32 hi, lo;
+                split_bf2(wv[4 * Q4], wv[4 * Q4 + 1], hi, lo);
+                *reinterpret_cast<u32*>(&sW[0][s * SW + rowof(4 * Q4)]) = hi;
+                *reinterpret_cast<u32*>(&sW[1][s * SW + rowof(4 * Q4)]) = lo;
+            }
             dtemp_acc += dt;
             const float pstep = temp * step_sum<NC>(dt);        // <qhat_s, dqn_s> = temp sum_n dz_n cs_n
             if (r == 0) {
@@ -2119,7 +2158,10 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             prv = s_pr[cw];
             keep(as8[0], as8[1], as8[2], as8[3]);
 #pragma unroll
-            for (int kc = 0; kc < 4; kc++) av8[kc] = sW[cw * SW + min(max(as8[kc], 0), NR - 1)];
+            for (int kc = 0; kc < 4; kc++) {
+                const int o = cw * SW + min(max(as8[kc], 0), NR - 1);
+                av8[kc] = join_bf(sW[0][o], sW[1][o]);
+            }
             keep(av8[0], av8[1], av8[2], av8[3]);
 #pragma unroll
             for (int kc = 0; kc < 4; kc++) {
@@ -2128,40 +2170,40 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             }
         }
         // S6: dqn^T = Kh^T W^T over every row for this wave's dims (keys as the A operand, so lane (c, g) ends with
-        // dims 4 g .. 4 g + 3 of step c), two accumulation chains, each group's LDS reads issued one group ahead.
-        // S5, the prefetch of the next (earlier) window, is issued part by part between the MFMA groups
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+        // dims 4 g .. 4 g + 3 of step c) on split bf16 operands: hi*hi, hi*lo and lo*hi in three accumulation
+        // chains, k-block j of lane group g = rows KG g + 8 j .. + 7, one 16-byte read per operand plane, each
+        // block's reads issued one block ahead.  S5, the prefetch of the next (earlier) window, is issued part by
+        // part between the MFMA blocks
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f}, acc3 = {0.f, 0.f, 0.f, 0.f};
         const bool pf = m > m_lo;
-        const float* wrow = &sW[cw * SW + KK * grpw];
-        const float* krow = &sKT[(d0 + cw) * P + KK * grpw];
-        float4 av = ld4(wrow), bv = ld4(krow), av2 = ld4(wrow + 4), bv2 = ld4(krow + 4);
+        const bf16_t* wh = &sW[0][cw * SW + KG * grpw];
+        const bf16_t* wl = &sW[1][cw * SW + KG * grpw];
+        const bf16_t* kh = &sKT[0][(d0 + cw) * P + KG * grpw];
+        const bf16_t* kl = &sKT[1][(d0 + cw) * P + KG * grpw];
+        auto ld8 = [](const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); };
+        uint4 ah = ld8(kh), al = ld8(kl), bh = ld8(wh), bl = ld8(wl);
 #pragma unroll
-        for (int k4 = 0; k4 < KK / 4; k4 += 2) {
-            float4 na = av, nb = bv, na2 = av2, nb2 = bv2;
-            if (k4 + 2 < KK / 4) {
-                na = ld4(wrow + 4 * k4 + 8);
-                nb = ld4(krow + 4 * k4 + 8);
-                na2 = ld4(wrow + 4 * k4 + 12);
-                nb2 = ld4(krow + 4 * k4 + 12);
+        for (int j = 0; j < KB; j++) {
+            uint4 nah = ah, nal = al, nbh = bh, nbl = bl;
+            if (j + 1 < KB) {
+                nah = ld8(kh + 8 * j + 8);
+                nal = ld8(kl + 8 * j + 8);
+                nbh = ld8(wh + 8 * j + 8);
+                nbl = ld8(wl + 8 * j + 8);
             }
-            if (pf && k4 / 2 < NPART) load_part(m - 1, k4 / 2);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bv.x, av.x, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv2.x, av2.x, acc2, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bv.y, av.y, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv2.y, av2.y, acc2, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bv.z, av.z, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv2.z, av2.z, acc2, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bv.w, av.w, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv2.w, av2.w, acc2, 0, 0, 0);
-            av = na; bv = nb; av2 = na2; bv2 = nb2;
+            if (pf && j < NPART) load_part(m - 1, j);
+            acc = mfma_bf32(ah, bh, acc);
+            acc2 = mfma_bf32(ah, bl, acc2);
+            acc3 = mfma_bf32(al, bh, acc3);
+            ah = nah; al = nal; bh = nbh; bl = nbl;
         }
 #pragma unroll
-        for (int pp = KK / 8; pp < NPART; pp++)
+        for (int pp = KB; pp < NPART; pp++)
             if (pf) load_part(m - 1, pp);
         // S7: the undo of every write at once: lane 128 w4 + 8 ui + g takes write ui, dims g + 8 (w4 + (D / 32) e).
-        // A 4-byte pass is 4 writes x 8 dims: the column accesses of the transposed keys (stride P per dim) land on
-        // 8 bank groups per write, offset by the writes' (different) rows; the kold and delta rows on 32 banks
-        // (both candidates for the key after each write are read, unconditionally, and selected)
+        // A pass of 32 lanes is 4 writes x 8 dims: the column accesses of the transposed key planes (stride P per
+        // dim) land on 8 bank groups per write, offset by the writes' (different) rows; the kold and delta rows on
+        // 32 banks (both candidates for the key after each write are read, unconditionally, and selected)
         const int ui = (int)((tidw >> 3) & 15), ud = (int)(tidw & 7) + 8 * (int)(tidw >> 7);
         auto udim = [&](int e) { return ud + 8 * (D / 32) * e; };
         const bool uev = ui < nt;
@@ -2178,7 +2220,7 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
                 const int d = udim(e);
                 ko[e] = sKO[ui * KOS + d];
                 kx[e] = sKO[nxc * KOS + d];
-                kt[e] = sKT[d * P + uai];
+                kt[e] = join_bf(sKT[0][d * P + uai], sKT[1][d * P + uai]);
             }
             keep(kn, ko[0], ko[1], ko[2], ko[3], kx[0], kx[1], kx[2], kx[3], kt[0], kt[1], kt[2], kt[3]);
 #pragma unroll
@@ -2191,12 +2233,17 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
         __syncthreads();                                                      // B3: every read of the window-end keys done
         if (ufirst) {
 #pragma unroll
-            for (int e = 0; e < DPT; e++) sKT[udim(e) * P + uai] = ux[e];
+            for (int e = 0; e < DPT; e += 2) {
+                u32 hi, lo;
+                split_bf2(ux[e], ux[e + 1], hi, lo);
+                st_kt(udim(e), uai, hi, lo);
+                st_kt(udim(e + 1), uai, hi >> 16, lo >> 16);
+            }
         }
         // S8: the rewritten rows' correction, sum_{s >= t} W[t][a_s] delta_s (rows of steps past the chain end
         // are zero deltas)
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[r] += acc2[r];
+        for (int r = 0; r < 4; r++) acc[r] += acc2[r] + acc3[r];
         float bv8[4];
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) bv8[kc] = sDel[(4 * kc + grpw) * DEL + d0 + cw];
