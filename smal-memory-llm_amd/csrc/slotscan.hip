@@ -1778,6 +1778,7 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     constexpr int EPU = 16 / (int)sizeof(TI);           // query elements per 16-byte piece
     constexpr int KLR = D / 4;                          // lanes per kold row in the prefetch (one float4 each)
     constexpr int QLR = D / EPU;                        // lanes per query row in the prefetch (one 16-byte piece)
+    constexpr int QL0 = NT - WIN * QLR;                 // the query rows' first lane (whole waves at the end)
     constexpr int UDN = (4 * NR + NT - 1) / NT;         // Dn float4 pieces per lane in the prefetch (4 per row)
     constexpr int Q4 = RPC / 4, R2 = (RPC % 4) / 2;     // softmax lane rows: Q4 groups of 4, then R2 pairs
     // Dn column swizzle: row n of step s sits at column n ^ 8 [s & 8].  The transposing publish stores rows n .. n + 7
@@ -1793,17 +1794,13 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
     __shared__ __align__(16) float sDel[WIN * DEL];     // undo deltas [write][dim]
     __shared__ __align__(16) float sKO[WIN * KOS];      // kold rows of the window's writes
     __shared__ __align__(16) float sQ[WIN * QS];        // query rows
-    __shared__ float sO[NR];                            // occupancy at the window end
     __shared__ u32 s_tkm[NR];                           // per row: bit s = occupied at window step s
-    __shared__ u32 s_scw[RPL + 1][4 * WIN];             // step scalars (address, oold, gate, fr; 16 each), one
-                                                        // copy per mask wave; wave 0's serves the whole block
-    u32* s_sc = s_scw[0];
+    __shared__ u32 s_sc[4 * WIN];                       // step scalars (address, oold, gate, fr; 16 each)
     __shared__ float s_kil[WIN], s_qi[WIN], s_pr[WIN];
     __shared__ float s_dgf[2][WIN];                     // per step: dgate and the per-token dfr, stored by wave 0
     __shared__ int s_nx[WIN], s_first[WIN];
     __shared__ float s_fin[2][NW];
     const int* s_am = reinterpret_cast<const int*>(s_sc);
-    const float* s_oo = reinterpret_cast<const float*>(s_sc + WIN);
     const float* s_g = reinterpret_cast<const float*>(s_sc + 2 * WIN);
     const float* s_fr = reinterpret_cast<const float*>(s_sc + 3 * WIN);
 
@@ -1863,9 +1860,12 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             st_kt(4 * l + 3, row, h23 >> 16, l23 >> 16);
         }
     }
-    for (int n = tid; n < NR; n += NT) {                // the occupancy at t_end, likewise
-        const int fw = n < N ? s_fw[n] : T;
-        sO[n] = n >= N ? 0.f : (fw < T ? a.oold[tok0 + (size_t)fw * H] : a.ofin[(size_t)bh * N + n]);
+    // the occupancy at t_end, likewise, held in a register by row n's mask lane (thread n; NR < NT): the mask loop
+    // below carries it from each window's end to its start
+    float o_row = 0.f;
+    if (tid < NR) {
+        const int fw = tid < N ? s_fw[tid] : T;
+        o_row = tid >= N ? 0.f : (fw < T ? a.oold[tok0 + (size_t)fw * H] : a.ofin[(size_t)bh * N + tid]);
     }
     __syncthreads();
 
@@ -1942,10 +1942,10 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             nko = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < nt) nko = ld4(a.kold + (tok0 + (size_t)(t0 + i) * H) * D + 4 * (tid % KLR));
         }
-        if (tid < WIN * QLR) {                          // whole waves
-            const int i = tid / QLR;
+        if (tid >= QL0) {                               // whole waves: the last ones (the first hold the step scalars)
+            const int i = (tid - QL0) / QLR;
             nq = make_uint4(0u, 0u, 0u, 0u);
-            if (i < nt) nq = *reinterpret_cast<const uint4*>(qp + (tok0 + (size_t)(t0 + i) * H) * D + EPU * (tid % QLR));
+            if (i < nt) nq = *reinterpret_cast<const uint4*>(qp + (tok0 + (size_t)(t0 + i) * H) * D + EPU * ((tid - QL0) % QLR));
         }
         if (tid < 64 * (RPL + 1)) {                     // the mask and link waves; one load per 16-lane kind (a
             const int kind = lane >> 4, i = lane & 15;  // per-lane choice of base pointer compiles to a load of it)
@@ -1988,8 +1988,8 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             const float ki = rsq_clamped(lanesum<KLR>(sq4(nko)));
             if (l == 0) s_kil[i] = ki;
         }
-        if (tidw < WIN * QLR) {                          // query rows and 1 / max(|q_t|, 1e-6), signed: negative
-            const int i = (int)(tidw / QLR), l = (int)(tidw % QLR);   // where |q_t|^2 < 1e-12 (no projection)
+        if (tidw >= (u32)QL0) {      // query rows and 1 / max(|q_t|, 1e-6), negative where |q_t|^2 < 1e-12 (no projection)
+            const int i = (int)((tidw - QL0) / QLR), l = (int)((tidw - QL0) % QLR);
             stage_store(&sQ[i * QS + EPU * l], nq, BF);
             float qq;
             if constexpr (BF) {
@@ -2008,31 +2008,27 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             qq = lanesum<QLR>(qq);
             if (l == 0) s_qi[i] = qq < 1e-12f ? -rsq_clamped(qq) : rsq_clamped(qq);
         }
-        if (tidw < 64 * (RPL + 1)) {                     // waves 0 .. RPL (whole waves): each publishes its copy of
-            const int wv = (int)(tidw >> 6);             // the step scalars and reads it back as broadcasts (its own
-            s_scw[wv][lanew] = nsc;                      // writes, in order: a wave barrier suffices)
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (tidw < 64 * (RPL + 1)) {                     // waves 0 .. RPL (whole waves) hold the step scalars: wave 0
+            const int wv = (int)(tidw >> 6);             // publishes the block's copy; each takes the addresses and
+            if (wv == 0) s_sc[lanew] = nsc;              // pre-write occupancies as scalars from its own lanes
             int ai[WIN];
             float oi[WIN];
 #pragma unroll
-            for (int k = 0; k < WIN / 4; k++) {
-                const int4 x = *reinterpret_cast<const int4*>(&s_scw[wv][4 * k]);
-                const float4 y = *reinterpret_cast<const float4*>(&s_scw[wv][WIN + 4 * k]);
-                ai[4 * k] = x.x; ai[4 * k + 1] = x.y; ai[4 * k + 2] = x.z; ai[4 * k + 3] = x.w;
-                oi[4 * k] = y.x; oi[4 * k + 1] = y.y; oi[4 * k + 2] = y.z; oi[4 * k + 3] = y.w;
+            for (int i = 0; i < WIN; i++) {
+                ai[i] = __builtin_amdgcn_readlane((int)nsc, i);
+                oi[i] = __int_as_float(__builtin_amdgcn_readlane((int)nsc, WIN + i));
             }
-            if (wv < RPL) {                              // occupancy masks, row 64 wave + lane: over the window's 16
-                const int n = 64 * wv + lanew;           // steps backwards from the window-end occupancy, o becomes
-                float o = sO[n];                         // the pre-write occupancy at each write to the row
-                u32 mk = 0u;
+            if (wv < RPL) {                              // occupancy masks, row n = 64 wave + lane: over the window's
+                const int n = (int)tidw;                 // 16 steps backwards from the window-end occupancy, o becomes
+                float o = o_row;                         // the pre-write occupancy at each write to the row, and at
+                u32 mk = 0u;                             // the end the window-start occupancy (the next window's end)
 #pragma unroll
                 for (int i = WIN - 1; i >= 0; i--) {
                     o = ai[i] == n ? oi[i] : o;
                     mk |= (n < N && o >= eps ? 1u : 0u) << i;
                 }
                 s_tkm[n] = mk;
+                o_row = o;
             } else if (lanew < WIN) {                    // per write: the next write to the same row inside the
                 const int i = lanew, me = (int)nsc;      // window, and whether it is the row's first
                 int nx = -1;
@@ -2047,10 +2043,14 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             }
         }
         __syncthreads();                                                      // B1
-        // S4: the softmax adjoint of every step: step s = lanes [NC s, NC s + NC), rows as in the prefetch
+        // S4: the softmax adjoint of every step: step s = lanes [NC s, NC s + NC), rows as in the prefetch.  The
+        // addresses S8 needs (steps 4 kc + grp) are read with S4's own operands, so that S8's W reads go out at once
+        int as8[4];
         {
             const int s = (int)(tidw / NC), r = (int)(tidw % NC);
             const bool live = s < nt;
+#pragma unroll
+            for (int kc = 0; kc < 4; kc++) as8[kc] = s_am[4 * kc + grpw];
             const float g = s_g[s], frv = frt ? s_fr[s] : fr_s;
             auto rowof = [&](int j) { return j < 4 * Q4 ? 4 * (r + NC * (j >> 2)) + (j & 3) : 4 * NC * Q4 + 2 * r + j - 4 * Q4; };
             float dw[RPC];
@@ -2067,6 +2067,7 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
                 const uint2 y = *reinterpret_cast<const uint2*>(&s_tkm[rowof(4 * Q4)]);
                 dw[4 * Q4] = x.x; dw[4 * Q4 + 1] = x.y; tkm[4 * Q4] = y.x; tkm[4 * Q4 + 1] = y.y;
             }
+            keep(as8[0], as8[1], as8[2], as8[3]);
             u32 tk = 0u, rows = 0u;                      // occupied at step s; below N
 #pragma unroll
             for (int j = 0; j < RPC; j++) {
@@ -2137,26 +2138,14 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             }
         }
         __syncthreads();                                                      // B2
-        if (tidw < WIN && s_first[tidw]) sO[s_am[tidw]] = s_oo[tidw];            // occupancy at the window start
-        if (tidw < 2 * WIN) {                            // the steps' dgate (and per-token dfr): one store each
-            const int i = lanew & 15, k = lanew >> 4;
-            const size_t ix = tok0 + (size_t)(t0 + i) * H;
-            const float v = s_dgf[k][i];
-            if (i < nt && k == 0) a.dg[ix] = v;
-            if (i < nt && k == 1 && frt) a.dfr[ix] = v;
-        }
         // S8's B operand, W[c][a_s] for s = 4 kc + grp >= c, and S9's operands (the query of step c at this lane's
         // four dims), read before B3: past it the next window's publish may overwrite them
         float av8[4], qsv, prv;
         float4 qv;
         {
-            int as8[4];
-#pragma unroll
-            for (int kc = 0; kc < 4; kc++) as8[kc] = s_am[4 * kc + grpw];
             qv = ld4(&sQ[cw * QS + d0 + 4 * grpw]);
             qsv = s_qi[cw];
             prv = s_pr[cw];
-            keep(as8[0], as8[1], as8[2], as8[3]);
 #pragma unroll
             for (int kc = 0; kc < 4; kc++) {
                 const int o = cw * SW + min(max(as8[kc], 0), NR - 1);
@@ -2231,6 +2220,13 @@ __global__ __launch_bounds__(4 * D) void chain_bwd_w(ChainBwdArgs a) {
             }
         }
         __syncthreads();                                                      // B3: every read of the window-end keys done
+        if (tidw >= NT - 64 && lanew < 2 * WIN) {       // the steps' dgate (and per-token dfr), one store each, by the
+            const int i = lanew & 15, k = lanew >> 4;   // last wave (the one with the shortest publish): read before
+            const size_t ix = tok0 + (size_t)(t0 + i) * H;   // it reaches the next B1, past which S4 rewrites them
+            const float v = s_dgf[k][i];
+            if (i < nt && k == 0) a.dg[ix] = v;
+            if (i < nt && k == 1 && frt) a.dfr[ix] = v;
+        }
         if (ufirst) {
 #pragma unroll
             for (int e = 0; e < DPT; e += 2) {
