@@ -334,6 +334,13 @@ __device__ __forceinline__ void gen_scores(const float (&K)[RPL][DPK], const flo
     }
 }
 
+// a <- fmaf(m, a, p), the result in a's own register.  The compiler's v_fmac form ties the destination to the
+// addend p, so a state updated that way in a loop moved to new registers every step and was copied back at the
+// loop's end (about 140 register moves per forward step at RPL 6).  The same single-rounding fma.
+__device__ __forceinline__ void fma_in(float& a, float m, float p) {
+    asm("v_fma_f32 %0, %1, %0, %2" : "+v"(a) : "v"(m), "v"(p));
+}
+
 template <int RPL, int DPK, int DPV>
 __device__ __forceinline__ void gen_update(float (&K)[RPL][DPK], float (&V)[RPL][DPV], float (&o)[RPL],
                                            const float (&wr)[RPL], const float* kt, const float* vt) {
@@ -341,9 +348,9 @@ __device__ __forceinline__ void gen_update(float (&K)[RPL][DPK], float (&V)[RPL]
     for (int j = 0; j < RPL; j++) {
         const float omw = 1.f - wr[j];
 #pragma unroll
-        for (int i = 0; i < DPK; i++) K[j][i] = fmaf(omw, K[j][i], wr[j] * kt[i]);
+        for (int i = 0; i < DPK; i++) fma_in(K[j][i], omw, wr[j] * kt[i]);
 #pragma unroll
-        for (int i = 0; i < DPV; i++) V[j][i] = fmaf(omw, V[j][i], wr[j] * vt[i]);
+        for (int i = 0; i < DPV; i++) fma_in(V[j][i], omw, wr[j] * vt[i]);
         o[j] = fmaf(omw, o[j], wr[j]);
     }
 }
@@ -405,22 +412,29 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
     float lo = 0.f, la = 0.f, ls = 0.f, lk = 0.f, lq = 0.f;
     float lw[RPL];
     int lbest = -1;
-    auto store_log = [&](int t) {
+    // nb, d, tid: this lane's nbase, dim-lane and thread index (taken from the step's opaque copy)
+    auto store_log = [&](int t, int nb, int d, uint32_t tid) {
         const size_t ti = tok(t);
-        if (a.hard && threadIdx.x == 0) a.am[ti] = lbest;
-        if (a.wb && dl == 0) {
+        if (a.hard && tid == 0) a.am[ti] = lbest;
+        if (a.wb && d == 0) {
 #pragma unroll
             for (int j = 0; j < RPL; j++)
-                if (nbase + j < a.N) a.wb[ti * a.N + nbase + j] = lw[j];
+                if (nb + j < a.N) a.wb[ti * a.N + nb + j] = lw[j];
         }
         if (a.rlog) {                         // dim-lane j < RPL stores row nbase + j
-            const int n = nbase + dl;
+            const int n = nb + d;
             float* rec = a.rlog + ((size_t)chain * a.T + t) * 4 * a.N;
-            if (dl < RPL && n < a.N) { rec[n] = lo; rec[a.N + n] = la; rec[2 * a.N + n] = ls; rec[3 * a.N + n] = lk; }
-            if (threadIdx.x == 0) a.rlog[(size_t)gridDim.x * a.T * 4 * a.N + (size_t)chain * a.T + t] = lq;
+            if (d < RPL && n < a.N) { rec[n] = lo; rec[a.N + n] = la; rec[2 * a.N + n] = ls; rec[3 * a.N + n] = lk; }
+            if (tid == 0) a.rlog[(size_t)gridDim.x * a.T * 4 * a.N + (size_t)chain * a.T + t] = lq;
         }
     };
     for (int t = 0; t < a.T; t++) {
+        // the lane indices re-derived from an opaque copy every step: comparisons on them are then not loop
+        // invariant, so the compiler does not hoist the per-row and per-lane masks into scalar registers
+        // (they had spilled to VGPR lanes, reloaded by readlane every step)
+        uint32_t tido;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(tido) : "v"((uint32_t)threadIdx.x));
+        const int lane_s = (int)(tido & 63u), dl_s = lane_s & 15, nb_s = w * RPW + (lane_s >> 4) * RPL;
         float kt[DPK], qt[DPK], vt[DPV];
         rk.cvt(kt); rq.cvt(qt); rv.cvt(vt);
         if (t > 0 && (t & 63) == 0) {
@@ -433,35 +447,35 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
             char* vb = (char*)(a.vbuf + slab * DV);
 #pragma unroll
             for (int j = 0; j < RPL; j++) {
-                if (nbase + j < a.N) {
+                if (nb_s + j < a.N) {
 #pragma unroll
                     for (int i = 0; i < DPK; i += 4)
                         *reinterpret_cast<float4*>(kb + sk_off + (j * DK + i) * 4) = make_float4(K[j][i], K[j][i + 1], K[j][i + 2], K[j][i + 3]);
 #pragma unroll
                     for (int i = 0; i < DPV; i += 4)
                         *reinterpret_cast<float4*>(vb + sv_off + (j * DV + i) * 4) = make_float4(V[j][i], V[j][i + 1], V[j][i + 2], V[j][i + 3]);
-                    if (dl == 0) a.obuf[slab + nbase + j] = o[j];
+                    if (dl_s == 0) a.obuf[slab + nb_s + j] = o[j];
                 }
             }
         }
-        if (t > 0) store_log(t - 1);
+        if (t > 0) store_log(t - 1, nb_s, dl_s, tido);
         if (t + 1 < a.T) { rk.load(krow(t + 1), tk_off); rq.load(qrow(t + 1), tk_off); rv.load(vrow(t + 1), tv_off); }
         const float g = steppar_g(spc, t);
         const float frt = steppar_f(spc, t);
         float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
         gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, a.pin, z, sr, knr, qinv);
-        lbest = gen_address<RPL>(z, o, nbase, a.N, a.eps, a.hard, -1, xf[t & 1], w, lane, as, ad);
+        lbest = gen_address<RPL>(z, o, nb_s, a.N, a.eps, a.hard, -1, xf[t & 1], w, lane_s, as, ad);
         lo = o[0]; la = as[0]; ls = sr[0]; lk = knr[0]; lq = qinv;
 #pragma unroll
         for (int j = 1; j < RPL; j++) {
-            const bool me = dl == j;
+            const bool me = dl_s == j;
             lo = me ? o[j] : lo; la = me ? as[j] : la; ls = me ? sr[j] : ls; lk = me ? knr[j] : lk;
         }
 #pragma unroll
         for (int j = 0; j < RPL; j++) { lw[j] = ad[j]; wr[j] = g * ad[j]; }
         gen_update<RPL, DPK, DPV>(K, V, o, wr, kt, vt);
     }
-    store_log(a.T - 1);
+    store_log(a.T - 1, nbase, dl, threadIdx.x);
 }
 
 // ------------------------------------------------------------------------------------------- backward
@@ -719,8 +733,8 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                     const float wr = g * ad[j];
                     const float omw = 1.f - wr;
 #pragma unroll
-                    for (int i = 0; i < DPK; i++) K[j][i] = fmaf(omw, K[j][i], wr * kt[i]);
-                    P[j] = fmaf(omw, P[j], wr * e[j]);
+                    for (int i = 0; i < DPK; i++) fma_in(K[j][i], omw, wr * kt[i]);
+                    fma_in(P[j], omw, wr * e[j]);
                 }
             }
         }
@@ -765,7 +779,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                         const float wr = gu * adu;
                         const float omw = 1.f - wr;
 #pragma unroll
-                        for (int i = 0; i < DPK; i++) K[j][i] = fmaf(omw, K[j][i], wr * ku[i]);
+                        for (int i = 0; i < DPK; i++) fma_in(K[j][i], omw, wr * ku[i]);
                     }
                 }
             };
