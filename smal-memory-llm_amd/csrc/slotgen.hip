@@ -678,6 +678,12 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             RawTok<TI, DPV> rv;
             rv.load((const char*)a.v + tok(t0) * DV * sizeof(TI), tv_off);
             for (int t = t0; t < t1; t++) {
+                // lane indices from an opaque copy every step: comparisons on them are then not loop invariant, so
+                // the compiler does not hoist the per-row and per-lane masks into (spilled) scalar registers
+                uint32_t tido;
+                asm volatile("v_mov_b32 %0, %1" : "=v"(tido) : "v"((uint32_t)threadIdx.x));
+                const int lane_s = (int)(tido & 63u), dl_s = lane_s & 15, rl_s = lane_s >> 4;
+                const int nb_s = w * RPW + rl_s * RPL;
                 const int s = t - t0;
                 float vt[DPV];
                 rv.cvt(vt);
@@ -698,13 +704,13 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 if (a.hard) {
                     const int amt = steppar_am(sp, t);
 #pragma unroll
-                    for (int j = 0; j < RPL; j++) ad[j] = nbase + j == amt ? 1.f : 0.f;
+                    for (int j = 0; j < RPL; j++) ad[j] = nb_s + j == amt ? 1.f : 0.f;
                 } else if (s < GL) {
 #pragma unroll
-                    for (int j = 0; j < RPL; j++) ad[j] = lsc[(s * 5 + 1) * NP + nbase + j];
+                    for (int j = 0; j < RPL; j++) ad[j] = lsc[(s * 5 + 1) * NP + nb_s + j];
                 } else {
 #pragma unroll
-                    for (int j = 0; j < RPL; j++) ad[j] = nbase + j < a.N ? rlog[((size_t)t * 4 + 1) * a.N + nbase + j] : 0.f;
+                    for (int j = 0; j < RPL; j++) ad[j] = nb_s + j < a.N ? rlog[((size_t)t * 4 + 1) * a.N + nb_s + j] : 0.f;
                 }
                 float e[RPL];
 #pragma unroll
@@ -718,10 +724,10 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                     }
                     e[j] = rowsum16(x);
                 }
-                if (dl == 0) {
+                if (dl_s == 0) {
 #pragma unroll
                     for (int j = 0; j < RPL; j++) {
-                        const int n = nbase + j;
+                        const int n = nb_s + j;
                         // explicit branches (s is uniform): a select between the LDS and the global pointer
                         // would make every access a flat one, which waits on both counters
                         if (s < GL) lsc[(s * 5 + 4) * NP + n] = e[j] - P[j];
@@ -744,11 +750,17 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
 #pragma unroll
         for (int j = 0; j < RPL; j++) cV[j] = 1.f;
         for (int t = t1 - 1; t >= t0; t--) {
+            // lane indices from an opaque copy every step: comparisons on them are then not loop invariant, so
+            // the compiler does not hoist the per-row and per-lane masks into (spilled) scalar registers
+            uint32_t tido;
+            asm volatile("v_mov_b32 %0, %1" : "=v"(tido) : "v"((uint32_t)threadIdx.x));
+            const int lane_s = (int)(tido & 63u), dl_s = lane_s & 15, rl_s = lane_s >> 4;
+            const int nb_s = w * RPW + rl_s * RPL;
             const int s = t - t0;
             const size_t ti = tok(t);
             // The pre-write keys of step s: the checkpoint at or before it, then the replay's updates of the
             // steps in between.  Built once per step and held across the step's barrier (with the addresses
-            // held as scalar bases and lane offsets there is room for them; rebuilding them after the barrier
+            // held as scalar bases and lane_s offsets there is room for them; rebuilding them after the barrier
             // cost more).
             auto load_K = [&](float (&K)[RPL][DPK]) {
                 const int c = (s / SC::GC) * SC::GC;
@@ -767,15 +779,15 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                     float asu[RPL];                                 // a_s of step u
                     if (u < GL) {
 #pragma unroll
-                        for (int j = 0; j < RPL; j++) asu[j] = lsc[(u * 5 + 1) * NP + nbase + j];
+                        for (int j = 0; j < RPL; j++) asu[j] = lsc[(u * 5 + 1) * NP + nb_s + j];
                     } else {
 #pragma unroll
                         for (int j = 0; j < RPL; j++)
-                            asu[j] = nbase + j < a.N ? rlog[((size_t)(t0 + u) * 4 + 1) * a.N + nbase + j] : 0.f;
+                            asu[j] = nb_s + j < a.N ? rlog[((size_t)(t0 + u) * 4 + 1) * a.N + nb_s + j] : 0.f;
                     }
 #pragma unroll
                     for (int j = 0; j < RPL; j++) {
-                        const float adu = a.hard ? (nbase + j == amu ? 1.f : 0.f) : asu[j];
+                        const float adu = a.hard ? (nb_s + j == amu ? 1.f : 0.f) : asu[j];
                         const float wr = gu * adu;
                         const float omw = 1.f - wr;
 #pragma unroll
@@ -787,14 +799,14 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             auto load_s = [&](float (&x)[RPL], int f) {
                 if (s < GL) {
 #pragma unroll
-                    for (int j = 0; j < RPL; j++) x[j] = lsc[(s * 5 + f) * NP + nbase + j];
+                    for (int j = 0; j < RPL; j++) x[j] = lsc[(s * 5 + f) * NP + nb_s + j];
                 } else if (f < 4) {                            // logged by the forward
 #pragma unroll
                     for (int j = 0; j < RPL; j++)
-                        x[j] = nbase + j < a.N ? rlog[((size_t)t * 4 + f) * a.N + nbase + j] : 0.f;
+                        x[j] = nb_s + j < a.N ? rlog[((size_t)t * 4 + f) * a.N + nb_s + j] : 0.f;
                 } else {
 #pragma unroll
-                    for (int j = 0; j < RPL; j++) x[j] = scr_e[(size_t)s * NP + nbase + j];
+                    for (int j = 0; j < RPL; j++) x[j] = scr_e[(size_t)s * NP + nb_s + j];
                 }
             };
             float kt[DPK];
@@ -816,7 +828,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             {
                 const int amt = a.hard ? steppar_am(sp, t) : -1;
 #pragma unroll
-                for (int j = 0; j < RPL; j++) ad[j] = a.hard ? (nbase + j == amt ? 1.f : 0.f) : as[j];
+                for (int j = 0; j < RPL; j++) ad[j] = a.hard ? (nb_s + j == amt ? 1.f : 0.f) : as[j];
             }
 #pragma unroll
             for (int j = 0; j < RPL; j++) {
@@ -857,13 +869,13 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 float yk[DPK / 4], yv[DPV / 4];
                 rows4_rs<DPK>(pk, yk);
                 rows4_rs<DPV>(pv, yv);
-                float* ok = q1 + w * P1W + dl * DPK + rows4_rs_base<DPK>(rl);
-                float* ov = q1 + w * P1W + DK + dl * DPV + rows4_rs_base<DPV>(rl);
+                float* ok = q1 + w * P1W + dl_s * DPK + rows4_rs_base<DPK>(rl_s);
+                float* ov = q1 + w * P1W + DK + dl_s * DPV + rows4_rs_base<DPV>(rl_s);
 #pragma unroll
                 for (int i = 0; i < DPK / 4; i++) ok[i] = yk[i];
 #pragma unroll
                 for (int i = 0; i < DPV / 4; i++) ov[i] = yv[i];
-                if (lane == 0) { q1[w * P1W + DK + DV] = pg; q1[w * P1W + DK + DV + 1] = pa; }
+                if (lane_s == 0) { q1[w * P1W + DK + DV] = pg; q1[w * P1W + DK + DV + 1] = pa; }
             }
             lds_barrier();
             if (pend_t >= 0) finish_q(pend_t, pend_t - t0, pend_qinv, p2[par ^ 1]);
@@ -872,18 +884,18 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             for (int ww = 0; ww < GEN_WAVES; ww++) { SG += q1[ww * P1W + DK + DV]; SA += q1[ww * P1W + DK + DV + 1]; }
             if (w == 0) {                     // dk_t, dv_t and dgate_t
                 constexpr int CK = DK / 4, CV = DV / 4;
-                if (lane < CK + CV) {
-                    const int off = lane < CK ? 4 * lane : DK + 4 * (lane - CK);
+                if (lane_s < CK + CV) {
+                    const int off = lane_s < CK ? 4 * lane_s : DK + 4 * (lane_s - CK);
                     float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
                     for (int ww = 0; ww < GEN_WAVES; ww++) {
                         const float4 f = *reinterpret_cast<const float4*>(q1 + ww * P1W + off);
                         r.x += f.x; r.y += f.y; r.z += f.z; r.w += f.w;
                     }
-                    if (lane < CK) sttok4<TI>(dkp + ti * DK + off, r);
+                    if (lane_s < CK) sttok4<TI>(dkp + ti * DK + off, r);
                     else sttok4<TI>(dvp + ti * DV + (off - DK), r);
                 }
-                if (lane == 0) a.dg[ti] = SG;
+                if (lane_s == 0) a.dg[ti] = SG;
             }
             // dz and the search-side partials
             float o[RPL], as[RPL], sr[RPL], knr[RPL], qt[DPK];
@@ -914,10 +926,10 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 }
                 float yq[DPK / 4];
                 rows4_rs<DPK>(pq, yq);
-                float* oq = q2 + w * P2W + dl * DPK + rows4_rs_base<DPK>(rl);
+                float* oq = q2 + w * P2W + dl_s * DPK + rows4_rs_base<DPK>(rl_s);
 #pragma unroll
                 for (int i = 0; i < DPK / 4; i++) oq[i] = yq[i];
-                if (lane == 0) { q2[w * P2W + DK] = sfo; q2[w * P2W + DK + 1] = sds; }
+                if (lane_s == 0) { q2[w * P2W + DK] = sfo; q2[w * P2W + DK + 1] = sds; }
             }
             pend_t = t;
             pend_qinv = qinv;

@@ -33,3 +33,15 @@ def test_proj_gemm_uses_no_scratch():
         assert d["ScratchSize [bytes/lane]"] == "0", f"{name} uses scratch: {d}"
         assert d["VGPRs Spill"] == "0", f"{name} spills: {d}"
         assert d["Dynamic Stack"] == "False", name
+
+
+def test_general_mode_kernels_use_no_scratch():
+    """gen_fwd / gen_bwd hold a chain's rows in registers at up to 256 VGPRs (RPL = 6: 6 rows x D / 16 dims of
+    K, V or their adjoints per lane).  A spill there is a scratch round trip inside the per-step loop; every
+    instantiation (token dtype x DK x DV x RPL) is kept free of it."""
+    rep = build.resource_report("slotgen.hip")
+    kern = {n: d for n, d in rep.items() if re.fullmatch(r"void gen_(fwd|bwd)<.*>", n)}
+    assert len(kern) == 48, sorted(kern)        # 2 dtypes x 2 DK x 2 DV x 3 RPL, forward and backward
+    for name, d in kern.items():
+        assert d["ScratchSize [bytes/lane]"] == "0", f"{name} uses scratch: {d}"
+        assert d["VGPRs Spill"] == "0", f"{name} spills: {d}"
