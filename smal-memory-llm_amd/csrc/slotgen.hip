@@ -214,10 +214,11 @@ template <int NV> __device__ __forceinline__ int rows4_rs_base(int rl) { return 
 // One step's address over the chain: every lane gets its rows' soft address a_s, the address a used for the
 // write (a_s, or the one-hot of `hard_row`), and the winning row of the hard argmax.  xf is the workgroup
 // exchange slot of this step: [wave][8] = {softmax max, sum, first-free index, its z, best z, best index}.
-template <int RPL>
+// shadow() runs between the wave's post and the barrier: work that no other wave waits for fills the wait.
+template <int RPL, typename F>
 __device__ __forceinline__ int gen_address(const float (&z)[RPL], const float (&o)[RPL], int nbase, int N,
                                            float eps, bool hard, int hard_row, float* xf, int w, int lane,
-                                           float (&as)[RPL], float (&ad)[RPL]) {
+                                           float (&as)[RPL], float (&ad)[RPL], F&& shadow) {
     // Short dependency chains: maxima first, then independent exponentials summed in trees (the lane's rows,
     // its 4 row-lanes, the 8 waves' posts), instead of an online softmax carried row by row.
     float m = -INFINITY;
@@ -264,6 +265,7 @@ __device__ __forceinline__ int gen_address(const float (&z)[RPL], const float (&
         p[0] = make_float4(m, s, __int_as_float(ff), zff);
         p[1] = make_float4(bz, __int_as_float(bi), 0.f, 0.f);
     }
+    shadow();
     lds_barrier();
     float4 p0[GEN_WAVES], p1[GEN_WAVES];
 #pragma unroll
@@ -341,17 +343,14 @@ __device__ __forceinline__ void fma_in(float& a, float m, float p) {
     asm("v_fma_f32 %0, %1, %0, %2" : "+v"(a) : "v"(m), "v"(p));
 }
 
-template <int RPL, int DPK, int DPV>
-__device__ __forceinline__ void gen_update(float (&K)[RPL][DPK], float (&V)[RPL][DPV], float (&o)[RPL],
-                                           const float (&wr)[RPL], const float* kt, const float* vt) {
+// The write of one step into this lane's rows: X <- (1 - wr) X + wr x (keys, or values), o likewise.
+template <int RPL, int DP>
+__device__ __forceinline__ void gen_update(float (&X)[RPL][DP], const float (&wr)[RPL], const float* x) {
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
         const float omw = 1.f - wr[j];
 #pragma unroll
-        for (int i = 0; i < DPK; i++) fma_in(K[j][i], omw, wr[j] * kt[i]);
-#pragma unroll
-        for (int i = 0; i < DPV; i++) fma_in(V[j][i], omw, wr[j] * vt[i]);
-        o[j] = fmaf(omw, o[j], wr[j]);
+        for (int i = 0; i < DP; i++) fma_in(X[j][i], omw, wr[j] * x[i]);
     }
 }
 
@@ -428,6 +427,14 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
             if (tid == 0) a.rlog[(size_t)gridDim.x * a.T * 4 * a.N + (size_t)chain * a.T + t] = lq;
         }
     };
+    // The value rows are not read by the step's scores: step t's value write is applied during step t + 1's
+    // address exchange (between the wave's post and the barrier), or before the snapshot when step t + 1
+    // emits one.  pvt, pwr: the pending write's value token and weights.
+    float pvt[DPV], pwr[RPL];
+#pragma unroll
+    for (int i = 0; i < DPV; i++) pvt[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < RPL; j++) pwr[j] = 0.f;
     for (int t = 0; t < a.T; t++) {
         // the lane indices re-derived from an opaque copy every step: comparisons on them are then not loop
         // invariant, so the compiler does not hoist the per-row and per-lane masks into scalar registers
@@ -441,7 +448,9 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
             spc = spn;
             spn = load_steppar(a.gate, a.fr, a.frt, nullptr, a.T, a.H, tok0, t + 64, lane);
         }
-        if (t % a.G == 0) {                   // emit the pre-write state
+        const bool snap = t % a.G == 0;
+        if (snap) {                           // emit the pre-write state
+            if (t > 0) gen_update<RPL, DPV>(V, pwr, pvt);
             const size_t slab = (((size_t)b * a.NB + t / a.G) * a.H + h) * a.N;
             char* kb = (char*)(a.kbuf + slab * DK);
             char* vb = (char*)(a.vbuf + slab * DV);
@@ -458,13 +467,17 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
                 }
             }
         }
-        if (t > 0) store_log(t - 1, nb_s, dl_s, tido);
         if (t + 1 < a.T) { rk.load(krow(t + 1), tk_off); rq.load(qrow(t + 1), tk_off); rv.load(vrow(t + 1), tv_off); }
         const float g = steppar_g(spc, t);
         const float frt = steppar_f(spc, t);
         float z[RPL], sr[RPL], knr[RPL], qinv, as[RPL], ad[RPL], wr[RPL];
         gen_scores<RPL, DPK>(K, o, qt, temp, frt, a.eps, a.occ_bin, a.pin, z, sr, knr, qinv);
-        lbest = gen_address<RPL>(z, o, nb_s, a.N, a.eps, a.hard, -1, xf[t & 1], w, lane_s, as, ad);
+        lbest = gen_address<RPL>(z, o, nb_s, a.N, a.eps, a.hard, -1, xf[t & 1], w, lane_s, as, ad, [&] {
+            if (t > 0) {                      // the previous step's log and (between snapshots) its value write
+                store_log(t - 1, nb_s, dl_s, tido);
+                if (!snap) gen_update<RPL, DPV>(V, pwr, pvt);
+            }
+        });
         lo = o[0]; la = as[0]; ls = sr[0]; lk = knr[0]; lq = qinv;
 #pragma unroll
         for (int j = 1; j < RPL; j++) {
@@ -473,7 +486,11 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < RPL; j++) { lw[j] = ad[j]; wr[j] = g * ad[j]; }
-        gen_update<RPL, DPK, DPV>(K, V, o, wr, kt, vt);
+        gen_update<RPL, DPK>(K, wr, kt);
+#pragma unroll
+        for (int j = 0; j < RPL; j++) { o[j] = fmaf(1.f - wr[j], o[j], wr[j]); pwr[j] = wr[j]; }
+#pragma unroll
+        for (int i = 0; i < DPV; i++) pvt[i] = vt[i];
     }
     store_log(a.T - 1, nbase, dl, threadIdx.x);
 }
