@@ -24,7 +24,8 @@ algorithmic HBM bytes per launch over its average launch time, measured with HIP
 library on the launch stream during the timed region; `step_roofline` applies the same formula to the
 whole step's algorithmic bytes.  Only the dominant kernel carries timing events during the timed steps (each
 timed launch costs its stream a few microseconds); `kernels_ms` times every kernel on the last warm-up
-step.  `hbm_measured` is the write-only and read-only bandwidth this box reaches with plain streaming
+step.  The forward-only read workloads (config4, config4_wo) run six identical layers per step and time the
+first layer's launches of each timed step only: a launch with completion events cannot overlap the next.  `hbm_measured` is the write-only and read-only bandwidth this box reaches with plain streaming
 kernels (torch fill_ and a column sum over 4 GiB), the practical ceilings beside the published 8 TB/s.
 `cpu_baseline` is the fp32 torch restatement of the reference's torch scan (oracle/torch_scan.py) timed with
 autograd on this host's cores: a B = 1 slice of the same workload, with config 1 beside it.
@@ -519,7 +520,7 @@ def bench_read_out(args, W):
             t_.requires_grad_()
         douts = [rn(B, T, DM).to(bf) for _ in range(layers)]
 
-    def step():
+    def step(probe=False):
         if bwd:
             for t_ in [K, V, kinv] + qs + scs + wos + deltas:
                 t_.grad = None                                  # time the op, not a gradient accumulation
@@ -528,16 +529,25 @@ def bench_read_out(args, W):
             torch.autograd.backward(outs, douts)
             return outs
         with torch.no_grad():
-            return [RH.slot_read_out(qs[i], K, V, kinv, valid, scs[i], G, wos[i], delta=deltas[i])
-                    for i in range(layers)]
+            outs = []
+            for i in range(layers):
+                if probe and i == 0:
+                    L.profile(True)
+                outs.append(RH.slot_read_out(qs[i], K, V, kinv, valid, scs[i], G, wos[i], delta=deltas[i]))
+                if probe and i == 0:
+                    L.profile(False)
+            return outs
 
+    # As bench_read: the forward-only workload times the first layer's launches of each timed step, the
+    # training workload every launch.
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    L.profile(True)
+    if bwd:
+        L.profile(True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        step(probe=not bwd)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     L.profile(False)
@@ -645,20 +655,35 @@ def bench_read(args, W):
             x.requires_grad_()
         drd = rn(B, T, H, NQ, D).to(torch.bfloat16)
 
-    def step():
+    def step(probe=False):
         if bwd:
             rd = RH.slot_read(qs[0], K, V, kinv, valid, scs[0], G)
             return torch.autograd.grad(rd, (qs[0], K, V, scs[0]), drd)
         with torch.no_grad():
-            return [RH.slot_read(qs[i], K, V, kinv, valid, scs[i], G) for i in range(layers)]
+            out = []
+            for i in range(layers):
+                if probe and i == 0:
+                    L.profile(True)
+                out.append(RH.slot_read(qs[i], K, V, kinv, valid, scs[i], G))
+                if probe and i == 0:
+                    L.profile(False)
+            return out
 
-    for _ in range(args.warmup):
+    # The forward-only workload times one layer's launch per timed step (a timed launch is dispatched with
+    # completion events, so it cannot overlap the launch after it; the layers are identical), the training
+    # workload every launch.  Every kernel is also timed on the last warm-up step.
+    for i in range(args.warmup):
+        if i == args.warmup - 1:
+            L.profile(True)
         step()
     torch.cuda.synchronize()
-    L.profile(True)
+    L.profile(False)
+    warm = L.profile_read()
+    if bwd:
+        L.profile(True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        step(probe=not bwd)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     L.profile(False)
@@ -686,8 +711,9 @@ def bench_read(args, W):
                                        "WRITE_SIZE passes, not measured in this run",
                      "algorithmic_bytes_per_launch": by, "avg_launch_ms": round(kms, 4),
                      "mfma_tflops": round(fl / (kms * 1e-3) / 1e12, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
-                     "mfma_frac": round(fl / (kms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
-        "kernels_ms": {n: round(x / c, 4) for n, (x, c) in prof.items()},
+                     "mfma_frac": round(fl / (kms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "timed_launches": cnt},
+        "kernels_ms": {n: round(x / c, 4) for n, (x, c) in (warm or prof).items()},
     }
     if bwd:
         bt, bc = prof["read_bwd"]
