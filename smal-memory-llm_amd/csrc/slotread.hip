@@ -340,6 +340,8 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 __device__ __forceinline__ uint2 ld_tr16(const unsigned char* p) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const lds_void*)p)));
 }
+// an empty use of a register: the load that produced it is waited for here, not later
+__device__ __forceinline__ void wide_keep(uint4& x) { asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w)); }
 // wait until at most n of this wave's vector-memory operations are outstanding.  The direct loads are not
 // tracked by the compiler; the kernel's other vector-memory operations -- query loads, output stores, any
 // scratch access -- are tracked by it or younger, so they can only make these waits longer, never shorter.
@@ -385,10 +387,15 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
     };
     // this wave's direct loads of one staged operand (keys: kpos, values: vpos): lane L of block b fills LDS
     // bytes 1024 b + 16 L, i.e. row (1024 b + 16 L) / ROWB at chunk position p, from the chunk stored there
+    // The per-lane source offsets are derived from an opaque copy of the lane index at every call: hoisted out of
+    // the unit loop they were spilled, and each reload's wait (the compiler cannot count the direct loads) then
+    // waited for every direct load issued before it, one round trip per load.
     auto stage = [&](const bf16_t* src, unsigned char* dst, bool val) {
+        uint32_t lo;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(lo) : "v"((uint32_t)lane));
 #pragma unroll
         for (int i = 0; i < S::PWD; i++) {
-            const int blk = w * S::PWD + i, byte = blk * 1024 + 16 * lane;
+            const int blk = w * S::PWD + i, byte = blk * 1024 + 16 * (int)lo;
             const int r = byte / S::ROWB, p = (byte % S::ROWB) / 16;
             const int cc = val ? vpos<D>(r, p) : kpos<D>(r, p);
             dma16(src + (size_t)min(r, N - 1) * D + 8 * cc, lds_addr(dst + blk * 1024));
@@ -579,6 +586,17 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
                         o[1][dt] = mfma_k32(va, pB[1][cc], o[1][dt]);
                     }
                     __builtin_amdgcn_sched_barrier(0);
+                }
+                if (t == TPW - 1) {
+                    // the next unit's first query registers, waited for here (their loads went out at this pair's
+                    // start, nothing else is in flight): the direct loads are invisible to the compiler's counts,
+                    // so its wait for these registers at the unit's turn would also wait for the unit's values
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+#pragma unroll
+                        for (int kk = 0; kk < KK; kk++) wide_keep(qn[e][kk]);
+                        asm volatile("" : "+v"(scn[e]));
+                    }
                 }
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
