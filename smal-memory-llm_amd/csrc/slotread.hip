@@ -364,25 +364,34 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int N = a.N;
-    const int nunits = a.slabs * a.parts;
-    const int TPW = (a.MC / 32 + WIDE_WAVES - 1) / WIDE_WAVES;   // 32-query tile pairs per wave and unit
+    // The work is the sequence of query chunks (slab, CH queries), a.parts chunks per slab; workgroup i takes the
+    // contiguous range [c0, c1) of it, so it crosses as few slab boundaries as it can (one per 1.5 slabs at
+    // config 4, against one per 512-query unit when the units were dealt round-robin): a unit is a maximal run of
+    // the range inside one slab, and only a change of unit restages the slot store behind two barriers.
+    constexpr int CH = 32 * WIDE_WAVES;                    // queries per chunk: one tile pair per wave
+    const int64_t nch = (int64_t)a.slabs * a.parts;
+    const int c0 = (int)(nch * blockIdx.x / gridDim.x), c1 = (int)(nch * (blockIdx.x + 1) / gridDim.x);
 
-    struct Unit { int slab, b, h, t0, mlo, mhi; };
+    struct Unit { int slab, b, h, t0, mlo, mhi, tpw, cnext; };
     auto unit = [&](int u) {
         Unit x;                                            // (every field wave-uniform: scalar registers)
         u = __builtin_amdgcn_readfirstlane(u);
         x.slab = u / a.parts;
-        const int part = u - x.slab * a.parts;
+        const int p0 = u - x.slab * a.parts;
+        const int p1 = min(a.parts, p0 + (c1 - u));        // this unit: chunks [p0, p1) of the slab
+        x.tpw = p1 - p0;                                   // tile pairs per wave
+        x.cnext = u + x.tpw;
         x.h = x.slab % a.H;
         const int j = (x.slab / a.H) % a.NB;
         x.b = x.slab / (a.H * a.NB);
         x.t0 = j * a.G;
         const int Mblk = min(a.G, a.T - x.t0) * a.NQ;
-        x.mlo = part * a.MC;
-        x.mhi = min(Mblk, x.mlo + a.MC);
+        x.mlo = p0 * CH;
+        x.mhi = min(Mblk, p1 * CH);
         x.slab = __builtin_amdgcn_readfirstlane(x.slab); x.b = __builtin_amdgcn_readfirstlane(x.b);
         x.h = __builtin_amdgcn_readfirstlane(x.h); x.t0 = __builtin_amdgcn_readfirstlane(x.t0);
         x.mlo = __builtin_amdgcn_readfirstlane(x.mlo); x.mhi = __builtin_amdgcn_readfirstlane(x.mhi);
+        x.tpw = __builtin_amdgcn_readfirstlane(x.tpw); x.cnext = __builtin_amdgcn_readfirstlane(x.cnext);
         return x;
     };
     // this wave's direct loads of one staged operand (keys: kpos, values: vpos): lane L of block b fills LDS
@@ -436,7 +445,7 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
     const int vch = (c & 3) >> 1, vhb = 8 * (c & 1);
 
     // ---- prologue: the first unit's keys, values, kinv / valid and first query tile pair
-    int u = blockIdx.x;
+    int u = c0;
     Unit cur = unit(u);
     stage(a.kb + (size_t)cur.slab * N * D, sKb[0], false);
     stage(a.vb + (size_t)cur.slab * N * D, sVb, true);
@@ -453,13 +462,14 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
     __syncthreads();
     int kb = 0;
     for (;;) {
-        const int un = u + gridDim.x;
-        const bool hasn = un < nunits;
+        const int un = cur.cnext;
+        const bool hasn = un < c1;
         Unit nx = cur;
         float kin = 0.f;
         uint32_t van = 0;
         if (hasn) nx = unit(un);
         const unsigned char* Kc = sKb[kb];
+        const int TPW = cur.tpw;
         for (int t = 0; t < TPW; t++) {
             // a pair of 16-query tiles, A = [m0, m0 + 16) and B = [m0 + 16, m0 + 32): every key and value operand
             // read from LDS feeds one MFMA of each
@@ -1077,9 +1087,6 @@ static int check_read(int64_t B, int64_t T, int64_t H, int64_t NQ, int64_t N, in
 #ifndef READ_TARGET_WGS
 #define READ_TARGET_WGS 768
 #endif
-#ifndef READ_WIDE_TARGET_WGS
-#define READ_WIDE_TARGET_WGS 512
-#endif
 #ifndef READ_WIDE_MIN_M
 #define READ_WIDE_MIN_M 256                      // queries per block from which the wide kernel is used
 #endif
@@ -1125,17 +1132,13 @@ extern "C" int slotread_fwd(const void* q, const void* kbuf, const void* vbuf, c
     {
         slothost::Scope sc(SLOTSCAN_K_READ_FWD, st);
         if (G * NQ >= READ_WIDE_MIN_M) {
-            // many queries per block: each workgroup takes a range of whole 16-query tiles for its 16 waves
-            const int64_t tiles = (G * NQ + 15) / 16;
-            int64_t split = (READ_WIDE_TARGET_WGS + slabs - 1) / slabs;
-            if (split > (tiles + WIDE_WAVES - 1) / WIDE_WAVES) split = (tiles + WIDE_WAVES - 1) / WIDE_WAVES;
-            if (split < 1) split = 1;
-            ra.MC = (int)(((tiles + split - 1) / split) * 16);
-            ra.MC = (ra.MC + 31) / 32 * 32;                   // whole 32-query tile pairs
-            ra.parts = (int)((G * NQ + ra.MC - 1) / ra.MC);
-            // persistent: one workgroup per CU (the 147 KB of LDS hold one), each walking about 3 units
-            const int64_t units = slabs * ra.parts;
-            dim3 wgrid((unsigned)std::min<int64_t>(units, cu_count())), wblock(WIDE_THREADS);
+            // many queries per block, persistent: one workgroup per CU (the 147 KB of LDS hold one), each walking
+            // a contiguous range of the query chunks (32 queries per wave)
+            ra.MC = 32 * WIDE_WAVES;
+            ra.parts = (int)((G * NQ + ra.MC - 1) / ra.MC);   // chunks per slab
+            const int64_t chunks = slabs * ra.parts;
+            if (chunks > 0x7fffffffLL) return fail(SLOTSCAN_ERR_SHAPE, "slotread_fwd: B*NB*H*ceil(G*NQ/256) must fit in int32");
+            dim3 wgrid((unsigned)std::min<int64_t>(chunks, cu_count())), wblock(WIDE_THREADS);
             if (D == 128) slothost::launch(read_fwd_wide<128>, wgrid, wblock, 0, st, ra);
             else slothost::launch(read_fwd_wide<64>, wgrid, wblock, 0, st, ra);
         } else {
