@@ -564,9 +564,11 @@ __global__ __launch_bounds__(WIDE_THREADS) void read_fwd_wide(ReadFwdArgs a) {
             if (t == 0) {
                 // this unit's values (their loads went out at the end of the previous unit, behind its last
                 // tile): wait for everything this wave issued, then the next unit's keys and kinv / valid go out,
-                // behind the rest of this unit
-                wide_wait_vm<0>();
-                __syncthreads();
+                // behind the rest of this unit.  The first unit's values were published by the prologue.
+                if (u != c0) {
+                    wide_wait_vm<0>();
+                    __syncthreads();
+                }
                 if (hasn) {
                     stage(a.kb + (size_t)nx.slab * N * D, sKb[kb ^ 1], false);
                     load_kv(nx, kin, van);
