@@ -83,6 +83,14 @@ struct ReadFwdArgs {
     int slabs, parts;             // read_fwd_wide: the work units are (slab, part of MC queries)
 };
 
+// a 16-byte streaming store: the backward's gradient rows are written once and not read by this layer again
+// (read_train 2.89 -> 2.80 ms/step A/B in one process, mostly from the dK / dV rows)
+__device__ __forceinline__ void st16_stream(bf16_t* p, uint4 v) {
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v y = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(y, reinterpret_cast<u32x4v*>(p));
+}
+
 template <int D>
 struct ReadSmem {
     static constexpr int VST = D + 8;   // staged value row stride (bf16): rows 4 apart land 16 banks apart
@@ -773,7 +781,7 @@ __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(AC
             uint4 v = *reinterpret_cast<const uint4*>(tw + row * RB + 16 * (ch ^ (x >> 1)));
             if (x & 1) v = make_uint4(v.z, v.w, v.x, v.y);
             const int n = w * TPW * 16 + row;
-            if (row < TPW * 16 && n < N) *reinterpret_cast<uint4*>(dst + (size_t)n * D + PD * hf + 8 * ch) = v;
+            if (row < TPW * 16 && n < N) st16_stream(dst + (size_t)n * D + PD * hf + 8 * ch, v);
         }
         wave_lds_sync();                                      // the reads are done before the next pass writes
     };
@@ -1043,7 +1051,7 @@ __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(AC
                 if constexpr (EPT == 8) {
                     uint4 x;
                     x.x = pack2(r[0], r[1]); x.y = pack2(r[2], r[3]); x.z = pack2(r[4], r[5]); x.w = pack2(r[6], r[7]);
-                    *reinterpret_cast<uint4*>(dst) = x;
+                    st16_stream(dst, x);
                 } else {
                     uint2 x;
                     x.x = pack2(r[0], r[1]); x.y = pack2(r[2], r[3]);

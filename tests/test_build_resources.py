@@ -45,3 +45,20 @@ def test_general_mode_kernels_use_no_scratch():
     for name, d in kern.items():
         assert d["ScratchSize [bytes/lane]"] == "0", f"{name} uses scratch: {d}"
         assert d["VGPRs Spill"] == "0", f"{name} spills: {d}"
+
+
+def test_read_and_window_kernels_use_no_scratch():
+    """read_fwd, read_fwd_wide and win_bwd stage operands with direct global -> LDS loads the compiler does not
+    track, so the wait the compiler puts before a spill reload cannot be narrowed to the reload: it waits for
+    every direct load in flight (one memory round trip per reload; read_fwd_wide lost about 9 k cycles per
+    unit that way before its staging offsets stopped spilling).  read_bwd runs at the register budget of three
+    waves per SIMD (168 VGPRs), where a spill is a scratch round trip inside its tile loop.  Every
+    instantiation of the read and window kernels is kept free of scratch."""
+    for src, n_kern in (("slotread.hip", 8), ("slotwin.hip", 4)):
+        rep = build.resource_report(src)
+        kern = {n: d for n, d in rep.items() if re.fullmatch(r"void (read_fwd_wide|read_fwd|read_bwd|win_fwd|win_bwd)<.*>", n)}
+        assert len(kern) == n_kern, (src, sorted(rep))
+        for name, d in kern.items():
+            assert d["ScratchSize [bytes/lane]"] == "0", f"{name} uses scratch: {d}"
+            assert d["VGPRs Spill"] == "0", f"{name} spills: {d}"
+            assert d["Dynamic Stack"] == "False", name
