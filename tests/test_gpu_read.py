@@ -109,6 +109,39 @@ def test_read_matches_oracle(case):
     run_case(*case, seed=3)
 
 
+WIDE_FULL_CASES = [  # B, T, H, N, D, G (NQ = 1), slabs checked against the oracle
+    # config 4's shape: 384 slabs x 4 chunks of 256 queries over 256 workgroups, 6 chunks each, so every
+    # other workgroup starts mid-slab and every one restages the store once; slabs 1, 2, 192, 193 and 383 are
+    # split between two workgroups or end a range
+    ((64, 1024, 6, 192, 128, 1024), (0, 1, 2, 3, 191, 192, 193, 382, 383)),
+    # ragged: 96 slabs x 4 chunks (the last of 232 queries) over 256 workgroups of 1 or 2 chunks each
+    ((16, 1000, 6, 192, 128, 1000), (0, 1, 2, 47, 48, 94, 95)),
+]
+
+
+@pytest.mark.parametrize("case", WIDE_FULL_CASES, ids=lambda c: "B{}T{}H{}N{}D{}G{}".format(*c[0]))
+def test_wide_read_full_size_sampled_slabs(case):
+    """The wide kernel at sizes where a workgroup walks several chunks and crosses slab boundaries (the
+    parity cases above give every workgroup one chunk at most): the whole launch at full size, then the
+    sampled slabs against the fp64 oracle, at the same bar as run_case."""
+    (B, T, H, N, D, G), slabs = case
+    q, K, V, kinv, valid, scale = make_read_inputs(B, T, H, 1, N, D, G, seed=3, sharp="softplus",
+                                                   empty_block0=False)
+    print(f"wide full-size read B{B} T{T} H{H} N{N} D{D} G{G}", flush=True)
+    c = lambda t: t.to(DEV)
+    rd = RH.slot_read(c(q), c(K), c(V), c(kinv), c(valid), c(scale), G).cpu()
+    torch.cuda.synchronize()
+    for s in slabs:
+        b, h = divmod(s, H)
+        sl = lambda t: t[b:b + 1, :, h:h + 1].contiguous()
+        ref = oracle_read(sl(q), sl(K), sl(V), sl(kinv), sl(valid), sl(scale), G)
+        got = sl(rd).double().numpy()
+        den = max(np.abs(ref).max(), 1e-30)
+        err = np.abs(got - ref)
+        assert err.max() <= 2e-2 * den, (s, err.max() / den)
+        assert err.mean() <= 2e-3 * den, (s, err.mean() / den)
+
+
 def test_read_softplus_sharpness_all_rows_valid():
     run_case(2, 128, 2, 1, 192, 128, 128, seed=4, sharp="softplus", empty_rows=0.0, empty_block0=False)
 
