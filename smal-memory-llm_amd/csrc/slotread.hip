@@ -79,8 +79,8 @@ struct ReadFwdArgs {
     const uint8_t* valid;
     const float* scale;
     bf16_t* rd;
-    int T, H, NQ, N, G, NB, MC;   // MC: query rows per workgroup / work unit (multiple of 16)
-    int slabs, parts;             // read_fwd_wide: the work units are (slab, part of MC queries)
+    int T, H, NQ, N, G, NB, MC;   // MC: query rows per workgroup (read_fwd, a multiple of 16) or per chunk (read_fwd_wide)
+    int slabs, parts;             // read_fwd_wide: parts chunks of MC queries per slab, slabs x parts chunks in all
 };
 
 // a 16-byte streaming store: the backward's gradient rows are written once and not read by this layer again
@@ -312,8 +312,9 @@ __global__ __launch_bounds__(READ_THREADS) __attribute__((amdgpu_waves_per_eu(3)
 //                   same 8 slots of one value dimension, read TRANSPOSED from the row-major value rows by two
 //                   ds_read_b64_tr_b16 (a 16-lane group reads 4 slot rows x 16 dims; lane l receives dim l);
 //   store           4 consecutive dims of one query per lane and tile (8 bytes), token-major.
-// The grid is persistent: one workgroup per CU walks the work units (a block's query range, about 3 per
-// workgroup) so that staging overlaps compute.  Keys are staged in two ping-pong buffers: the NEXT unit's
+// The grid is persistent: one workgroup per CU walks a contiguous range of the blocks' 256-query chunks (6 at
+// config 4: one and a half blocks), a unit being the part of the range inside one block, so that staging
+// overlaps compute and a workgroup restages the store only where its range crosses into the next block.  Keys are staged in two ping-pong buffers: the NEXT unit's
 // keys are fetched by direct global -> LDS loads (no registers) during the current unit, after its first
 // tile's softmax.  Values are staged row-major (as the keys: no transposition, so they too are direct loads)
 // into one buffer, fetched when every wave is done with the current unit's values; the next unit's first
