@@ -189,6 +189,14 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// rowsum16 whose result is materialised where it is formed: its last DPP add then folds into one
+// instruction (when the sum's uses sit in later blocks the compiler had sunk that add behind a separate DPP
+// move and a zero-initialised register)
+__device__ __forceinline__ float rowsum16p(float v) {
+    v = rowsum16(v);
+    asm volatile("" : "+v"(v));
+    return v;
+}
 // Sum over the 4 row-lanes (lanes c, c+16, c+32, c+48).
 __device__ __forceinline__ float rows4_sum(float x) { return sum4rows(x); }
 
@@ -318,15 +326,15 @@ __device__ __forceinline__ void gen_scores(const float (&K)[RPL][DPK], const flo
     float qq = 0.f;
 #pragma unroll
     for (int i = 0; i < DPK; i++) qq = fmaf(qt[i], qt[i], qq);
-    qq = rowsum16(qq);
+    qq = rowsum16p(qq);
     qinv = __builtin_amdgcn_rsqf(fmaxf(qq, GEN_NORM_EPS * GEN_NORM_EPS));   // 1 / max(|q|, 1e-6)
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
         float d = 0.f, n2 = 0.f;
 #pragma unroll
         for (int i = 0; i < DPK; i++) { d = fmaf(K[j][i], qt[i], d); n2 = fmaf(K[j][i], K[j][i], n2); }
-        d = rowsum16(d);
-        n2 = rowsum16(n2);
+        d = rowsum16p(d);
+        n2 = rowsum16p(n2);
         kn[j] = __builtin_amdgcn_sqrtf(n2);
         const float kinv = __builtin_amdgcn_rsqf(fmaxf(n2, GEN_NORM_EPS * GEN_NORM_EPS));   // 1 / max(|K|, 1e-6)
         sr[j] = temp * (d * kinv * qinv);
@@ -444,6 +452,13 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_fwd(GenArgs a) {
         const int lane_s = (int)(tido & 63u), dl_s = lane_s & 15, nb_s = w * RPW + (lane_s >> 4) * RPL;
         float kt[DPK], qt[DPK], vt[DPV];
         rk.cvt(kt); rq.cvt(qt); rv.cvt(vt);
+        // converted here, so that the raw words are dead before the next step's loads reuse their registers
+        // (converted where used, they were live across those loads, which then went to other registers and
+        // were copied back at the loop's end: 24 moves per step)
+#pragma unroll
+        for (int i = 0; i < DPK; i++) asm volatile("" : "+v"(kt[i]), "+v"(qt[i]));
+#pragma unroll
+        for (int i = 0; i < DPV; i++) asm volatile("" : "+v"(vt[i]));
         if (t > 0 && (t & 63) == 0) {
             spc = spn;
             spn = load_steppar(a.gate, a.fr, a.frt, nullptr, a.T, a.H, tok0, t + 64, lane);
@@ -616,8 +631,8 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
         float pr = 0.f, qq = 0.f;
 #pragma unroll
         for (int i = 0; i < DPK; i++) { pr = fmaf(qt[i] * qinv, dqn[i], pr); qq = fmaf(qt[i], qt[i], qq); }
-        pr = rowsum16(pr);
-        qq = rowsum16(qq);
+        pr = rowsum16p(pr);
+        qq = rowsum16p(qq);
         const bool small = qq < GEN_NORM_EPS * GEN_NORM_EPS;
         if (rl == 0) {
             float r[DPK];
@@ -689,7 +704,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                         x = fmaf(Vs[j][i], d.x, x); x = fmaf(Vs[j][i + 1], d.y, x);
                         x = fmaf(Vs[j][i + 2], d.z, x); x = fmaf(Vs[j][i + 3], d.w, x);
                     }
-                    P[j] = rowsum16(x);
+                    P[j] = rowsum16p(x);
                 }
             }
             RawTok<TI, DPV> rv;
@@ -739,7 +754,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                         x = fmaf(vt[i], d.x, x); x = fmaf(vt[i + 1], d.y, x);
                         x = fmaf(vt[i + 2], d.z, x); x = fmaf(vt[i + 3], d.w, x);
                     }
-                    e[j] = rowsum16(x);
+                    e[j] = rowsum16p(x);
                 }
                 if (dl_s == 0) {
 #pragma unroll
@@ -852,7 +867,7 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
                 float x = 0.f;
 #pragma unroll
                 for (int i = 0; i < DPK; i++) x = fmaf(kt[i] - K[j][i], dK[j][i], x);
-                x = rowsum16(x);
+                x = rowsum16p(x);
                 x = fmaf(cV[j], ep[j], x);              // <v_t - V(t), dV(t+)> = cV (e - P)
                 dw[j] = fmaf(1.f - o[j], dO[j], x);
                 wr[j] = g * ad[j];
