@@ -2580,10 +2580,15 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
         }
         if (e != hipSuccess) return hip_fail(e, "chain_fwd launch");
         hipStream_t rs = st;
-        if (nch > 1) {
+        if (nch > 1 && c + 1 < nch) {
             if ((e = hipEventRecord(ev[c], st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
             if ((e = hipStreamWaitEvent(side, ev[c], 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
             rs = side;
+        } else if (nch > 1) {
+            // the last chunk's replay follows its chain on the caller's stream, behind the side stream's
+            // replays (its value carry): no cross-stream wait between the chain and it, and no join after it
+            if ((e = hipEventRecord(ev[c], side)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+            if ((e = hipStreamWaitEvent(st, ev[c], 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
         }
         {
             slothost::Scope sc(SLOTSCAN_K_ROWS_FWD, rs);
@@ -2601,11 +2606,7 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
         }
         if (e != hipSuccess) return hip_fail(e, "rows_fwd launch");
     }
-    if (nch > 1) {                                       // join: the caller's stream sees every chunk
-        if ((e = hipEventRecord(ev[nch], side)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-        if ((e = hipStreamWaitEvent(st, ev[nch], 0)) != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
-    }
-    return 0;
+    return 0;                                            // the caller's stream has every chunk behind it
 }
 
 extern "C" int slotscan_fwd(const void* k, const void* q, const void* v, int dtype,
