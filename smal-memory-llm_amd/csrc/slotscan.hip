@@ -2538,7 +2538,8 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
                    k, k0, nullptr, o.bits, o.group, o.kbm, o.kinvm, o.validm, o.kcode, o.kscale, o.vcode, o.vscale};
     // Long sequences run as a two-stream pipeline over step chunks of a multiple of G: the key chain of
     // chunk c + 1 (latency-bound, caller's stream) overlaps the row replay of chunk c (HBM-bound, the
-    // library's side stream).  fp32 contract: the state crosses an inner chunk boundary te as the snapshot
+    // library's side stream); the last chunk's replay has no chain to overlap and runs on the caller's stream
+    // behind its chain, after the side stream's replays.  fp32 contract: the state crosses an inner chunk boundary te as the snapshot
     // of block te / G, which is exactly the state there -- a chunk ends by writing it (it is its next block's
     // PRE-write snapshot) and the next chunk starts from it without storing it again.  The other contracts
     // emit no fp32 state, so the chain carries its keys in kfin, the value replay its values in vfin, and a
