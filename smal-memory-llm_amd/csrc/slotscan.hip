@@ -464,7 +464,15 @@ void chain_fwd(ChainFwdArgs a) {
             }
             x[j] = kk;
         }
-        const float nsq0 = rs_reduce<P>(x, c);
+        // each row's norm summed over its 16 lanes in rowsum16's order, the order of the row update after a
+        // write: a chunk then starts from bitwise the kinv the previous chunk ended with, and the scan's
+        // results do not depend on where the pipeline cuts the sequence (at multiples of the 16-step window)
+        float nsq0 = 0.f;
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            const float sj = rowsum16(x[j]);
+            nsq0 = (c >> RS<P>::SH) == j ? sj : nsq0;
+        }
         kinv_me = rsq_clamped(nsq0);
         vld_me = nsq0 > 1e-12f;
         if (a.o0 && R.n_me < N) o_me = a.o0[(size_t)bh * N + R.n_me];
@@ -2492,6 +2500,46 @@ static int64_t fwd_chunk_len(int64_t T, int64_t G) {
     return T >= 512 ? ((std::max<int64_t>(128, T / 8) + G - 1) / G) * G : T;
 }
 
+// The forward pipeline's chunk boundaries b[0] = 0 < b[1] < ... < b[n] = T (inner ones multiples of G);
+// returns n (at most FWD_MAX_CHUNKS).  Equal chunks of fwd_chunk_len, unless the value replay fits one round
+// of workgroups (two per CU): it then takes well under half the chain's time per step (the chain is bound
+// by its step latency), and the chunks halve towards the end (..., 128, 64, 32, 32 steps at G = 8), so that
+// the tail the replay leaves exposed (the last chunk's) and the number of chunk starts are both small, while
+// each replay still hides behind the next chain chunk, half as long.
+#define FWD_MAX_CHUNKS 40
+static int fwd_chunks(int64_t B, int64_t T, int64_t H, int64_t N, int64_t G, int64_t* b) {
+    b[0] = 0;
+    const int64_t len = fwd_chunk_len(T, G);
+    if (len >= T) { b[1] = T; return 1; }
+    int n = 0;
+    if (B * H * ((N + 31) / 32) > 512) {
+        for (int64_t t = 0; t < T; t += len) b[++n] = std::min<int64_t>(T, t + len);
+        return n;
+    }
+    // on the whole blocks of T (the last chunk takes T % G too): the tail m, m, 2m, 4m, ... from the end while
+    // the rest is at least twice the next size, then the rest as one chunk, or two if it is over twice the tail's
+    // largest (a replay runs at well under half its chain's time per step, so each hides behind the next chunk)
+    const int64_t Tg = (T / G) * G;
+    const int64_t m = ((std::max<int64_t>(32, G) + G - 1) / G) * G;
+    int64_t tail[FWD_MAX_CHUNKS];
+    int nt = 0;
+    int64_t total = 0, next = m;
+    while (nt < FWD_MAX_CHUNKS - 3 && total + 2 * next <= Tg) {
+        tail[nt++] = next;
+        total += next;
+        if (nt >= 2) next *= 2;
+    }
+    const int64_t R = Tg - total;
+    if (nt > 0 && R > 2 * tail[nt - 1]) {
+        const int64_t r1 = std::max<int64_t>(G, (R / 2 / G) * G);
+        b[++n] = r1;
+    }
+    b[++n] = R;
+    for (int i = nt - 1; i >= 0; i--, n++) b[n + 1] = b[n] + tail[i];
+    b[n] = T;
+    return n;
+}
+
 static int check_q(int bits, int64_t group, int64_t D, bool codes) {
     if (codes ? (bits < 2 || bits > 8) : (bits != 0 && (bits < 2 || bits > 8)))
         return fail(SLOTSCAN_ERR_SHAPE, codes ? "bits must be 2..8" : "bits must be 0 or 2..8");
@@ -2511,8 +2559,8 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
     if (int r = check_common(B, T, H, N, D, G, dtype)) return r;
     const int mode = o.mode;
     const bool kr = mode == FE_MEMQ || mode == FE_CODES;         // the row replay emits the keys
-    const int64_t len = fwd_chunk_len(T, G);
-    const int nch = (int)((T + len - 1) / len);
+    int64_t cb[FWD_MAX_CHUNKS + 1];
+    const int nch = fwd_chunks(B, T, H, N, G, cb);
     if (!k || !q || !v || !gate || !fr || !temp || !am || !kfin || !vfin || !ofin ||
         (mode == FE_F32 && (!o.kbuf || !o.vbuf)) ||
         ((mode == FE_MEM || mode == FE_MEMQ) && (!o.kbm || !o.vbm || !o.kinvm || !o.validm)) ||
@@ -2552,8 +2600,8 @@ static int scan_fwd(const void* k, const void* q, const void* v, int dtype,
     dim3 grid((unsigned)(B * H), (unsigned)((N + 31) / 32)), block(512);
     hipError_t e;
     for (int c = 0; c < nch; c++) {
-        ca.ts = ra.ts = (int)(c * len);
-        ca.te = ra.te = (int)std::min<int64_t>(T, (c + 1) * len);
+        ca.ts = ra.ts = (int)cb[c];
+        ca.te = ra.te = (int)cb[c + 1];
         const bool inner_end = ca.te < T;
         if (c > 0) {
             ca.o0 = ofin;

@@ -129,7 +129,9 @@ def _fullsize_case(name, bs, mem=False, twice=False):
     idx = torch.tensor(bs, device=dev)
     ins_s = _slice(ins, bs)
     small = _run(W, ins_s, mem)
-    # 1. batch-slice consistency, bitwise
+    # 1. batch-slice consistency, bitwise.  At T >= 512 the two launches also cut the forward pipeline
+    # differently (the full batch in equal chunks, the 3-row slice, whose value replay fits one round of
+    # workgroups, in chunks halving towards the end): the scan's results do not depend on the cut
     H = W["H"]
     rows = torch.tensor([b * H + h for b in bs for h in range(H)], device=dev)
     for i, (x, y) in enumerate(zip(full[0], small[0])):
