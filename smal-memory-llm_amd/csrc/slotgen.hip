@@ -42,6 +42,8 @@
 // the same exchange.  The scratch is written and read in 16-byte units, each row by its 16 dim-lanes.
 // The step is bound by its VALU instruction count (2 waves per SIMD), so the clamped inverse norms and the
 // softmax normaliser use the hardware v_rsq / v_rcp / v_sqrt (1 ulp) instead of IEEE division sequences.
+#include <type_traits>
+
 #include "slot_common.h"
 #include "slotscan.h"
 #include "slot_host.h"
@@ -275,36 +277,46 @@ __device__ __forceinline__ int gen_address(const float (&z)[RPL], const float (&
     }
     shadow();
     lds_barrier();
-    float4 p0[GEN_WAVES], p1[GEN_WAVES];
-#pragma unroll
-    for (int ww = 0; ww < GEN_WAVES; ww++) {
-        p0[ww] = reinterpret_cast<const float4*>(xf + ww * 8)[0];
-        p1[ww] = reinterpret_cast<const float4*>(xf + ww * 8)[1];
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < GEN_WAVES; ww++) M = fmaxf(M, p0[ww].x);
-    int FF = INT_MAX; float Z = 0.f;
-    float BZ = 0.f; int BI = INT_MAX;
-#pragma unroll
-    for (int ww = 0; ww < GEN_WAVES; ww++) {   // waves in row order: the lowest index wins ties
-        idx_merge(FF, Z, __float_as_int(p0[ww].z), p0[ww].w, FF, Z);
-        best_merge(BZ, BI, p1[ww].x, __float_as_int(p1[ww].y), BZ, BI);
-    }
+    // The 8 waves' posts are merged across the lanes of each 8-lane group (lane l reads wave l & 7's post) and
+    // taken as scalars from lane 0: the maxima and the index selections are order-free, and the exponential
+    // sum uses the tree of a loop over the waves, ((0 + 4) + (2 + 6)) + ((1 + 5) + (3 + 7)), so the results
+    // are bitwise those of every lane merging all 8 posts (16 LDS reads and 8 exponentials per lane before)
+    static_assert(GEN_WAVES == 8, "one post per lane of an 8-lane group");
+    const int pw = lane & 7;
+    const float4 q0 = reinterpret_cast<const float4*>(xf + pw * 8)[0];
+    const float4 q1 = reinterpret_cast<const float4*>(xf + pw * 8)[1];
+    float mx = q0.x;
+    mx = fmaxf(mx, dppf<SLOT_DPP_XOR1>(mx));
+    mx = fmaxf(mx, dppf<SLOT_DPP_XOR2>(mx));
+    mx = fmaxf(mx, dppf<SLOT_DPP_HMIR>(mx));
+    int ffl = __float_as_int(q0.z), bil = __float_as_int(q1.y);
+    float zfl = q0.w, bzl = q1.x;
+    auto merge_stage = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        const int fi = (int)dppu<C>((uint32_t)ffl), bi1 = (int)dppu<C>((uint32_t)bil);
+        const float fz = dppf<C>(zfl), bz1 = dppf<C>(bzl);
+        idx_merge(ffl, zfl, fi, fz, ffl, zfl);
+        best_merge(bzl, bil, bz1, bi1, bzl, bil);
+    };
+    merge_stage(std::integral_constant<int, SLOT_DPP_XOR1>{});
+    merge_stage(std::integral_constant<int, SLOT_DPP_XOR2>{});
+    merge_stage(std::integral_constant<int, SLOT_DPP_HMIR>{});
+    float M = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mx)));
+    const int FF = __builtin_amdgcn_readfirstlane(ffl);
+    const float Z = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(zfl)));
+    float BZ = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bzl)));
+    int BI = __builtin_amdgcn_readfirstlane(bil);
     if (FF != INT_MAX) {                      // the first free row competes too
         M = fmaxf(M, Z);
         best_merge(BZ, BI, Z, FF, BZ, BI);
     }
     float S = FF != INT_MAX ? __expf(Z - M) : 0.f;
     {
-        float sw[GEN_WAVES];
-#pragma unroll
-        for (int ww = 0; ww < GEN_WAVES; ww++) sw[ww] = p0[ww].y > 0.f ? p0[ww].y * __expf(p0[ww].x - M) : 0.f;
-#pragma unroll
-        for (int st = GEN_WAVES / 2; st >= 1; st /= 2)
-#pragma unroll
-            for (int ww = 0; ww < st; ww++) sw[ww] += sw[ww + st];
-        S += sw[0];
+        float sw = q0.y > 0.f ? q0.y * __expf(q0.x - M) : 0.f;
+        sw += dppf<0x12C>(sw);                // row_ror:12: lanes 0..3 add the posts of waves 4..7
+        sw += dppf<SLOT_DPP_XOR2>(sw);        // lanes 0, 1 add lanes 2, 3
+        sw += dppf<SLOT_DPP_XOR1>(sw);        // lane 0 adds lane 1
+        S += __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sw)));
     }
     const float rS = __builtin_amdgcn_rcpf(S);
     const int row = hard ? (hard_row >= 0 ? hard_row : BI) : -1;
