@@ -631,7 +631,8 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
         for (int i = 0; i < DPK; i++) dqn[i] = 0.f;
         float sfo = 0.f, sds = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < GEN_WAVES; ww++) {
+        for (int u = 0; u < 2; u++) {           // row-lane rl sums waves 2 rl, 2 rl + 1; then over the 4 rows
+            const int ww = 2 * rl + u;
 #pragma unroll
             for (int i = 0; i < DPK; i += 4) {
                 const float4 f = *reinterpret_cast<const float4*>(q2 + ww * P2W + dl * DPK + i);
@@ -640,6 +641,10 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             sfo += q2[ww * P2W + DK];
             sds += q2[ww * P2W + DK + 1];
         }
+#pragma unroll
+        for (int i = 0; i < DPK; i++) dqn[i] = rows4_sum(dqn[i]);
+        sfo = rows4_sum(sfo);
+        sds = rows4_sum(sds);
         float pr = 0.f, qq = 0.f;
 #pragma unroll
         for (int i = 0; i < DPK; i++) { pr = fmaf(qt[i] * qinv, dqn[i], pr); qq = fmaf(qt[i], qt[i], qq); }
@@ -923,9 +928,16 @@ __global__ __launch_bounds__(GEN_THREADS) void gen_bwd(GenArgs a) {
             }
             lds_barrier();
             if (pend_t >= 0) finish_q(pend_t, pend_t - t0, pend_qinv, p2[par ^ 1]);
-            float SG = 0.f, SA = 0.f;
-#pragma unroll
-            for (int ww = 0; ww < GEN_WAVES; ww++) { SG += q1[ww * P1W + DK + DV]; SA += q1[ww * P1W + DK + DV + 1]; }
+            float SG, SA;
+            {                                 // the 8 waves' {sum a dw, sum a_s g dw}: lane l holds wave l & 7's
+                const float2 gp = *reinterpret_cast<const float2*>(q1 + (lane & 7) * P1W + DK + DV);
+                float sg = gp.x, sa = gp.y;
+                sg += dppf<SLOT_DPP_XOR1>(sg); sa += dppf<SLOT_DPP_XOR1>(sa);
+                sg += dppf<SLOT_DPP_XOR2>(sg); sa += dppf<SLOT_DPP_XOR2>(sa);
+                sg += dppf<SLOT_DPP_HMIR>(sg); sa += dppf<SLOT_DPP_HMIR>(sa);
+                SG = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sg)));
+                SA = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sa)));
+            }
             if (w == 0) {                     // dk_t, dv_t and dgate_t
                 constexpr int CK = DK / 4, CV = DV / 4;
                 if (lane_s < CK + CV) {
