@@ -123,8 +123,9 @@ def test_bwd_plan_untracked_rows_kernel_guard(T, H, N, D, G, mem, untracked):
 
 
 def test_integration_doc_stubs_match_the_bindings():
-    """Every `lib.<name>.argtypes = ...` line in INTEGRATION.md binds exactly the argument list of the C
-    prototype (the same types, in order, as slotscan_lib.SIGNATURES): a maintainer copies these stubs."""
+    """Every `lib.<name>.argtypes = ...` line of the integration guide at the repository root binds exactly
+    the argument list of the C prototype (the same types, in order, as slotscan_lib.SIGNATURES): a maintainer
+    copies these stubs."""
     txt = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     found = re.findall(r"^lib\.(\w+)\.argtypes = (.+)$", txt, flags=re.M)
     assert len(found) >= 5
